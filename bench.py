@@ -1,0 +1,248 @@
+#!/usr/bin/env python3
+"""Decode-attention benchmark on one MI355X (BASELINE.json metric).
+
+One step = one split-KV paged decode call (partial + combine kernels) over the
+whole synthetic batch of the named workload, inputs already resident in HBM.
+The KV pool is rotated across copies totalling >= 1 GB so the 256 MB Infinity
+Cache cannot serve repeated reads. Prints ONE JSON line:
+
+  value        effective KV GB/s = sum_b 4*L_b*HKV*HD / (median us per call)
+  roofline     split partial kernel alone: algorithmic bytes (KV + q + out +
+               used block-table entries + lengths) / its average duration,
+               HIP events on the launch stream, against 8 TB/s
+  cpu_baseline fp32 torch-CPU restatement of reference.attention_kvcache
+               (oracle.reference_port) on the host cores, bounded sample
+  cells        the six GQ x HD cells of config 2 and configs 1, 3, 4
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "decode-attn effective KV GB/s (% of HBM peak) + µs/call, B=32 GQ4 HD128 bf16"
+MAIN_WORKLOAD = "config2_qwen3_4b"
+ROTATE_BYTES = 1 << 30
+
+
+def parse_args() -> argparse.Namespace:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default=MAIN_WORKLOAD)
+    ap.add_argument("--no-cells", action="store_true", help="skip the per-cell table")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-reps", type=int, default=5)
+    return ap.parse_args()
+
+
+def build_pools(spec: dict, device: torch.device):
+    """One batch plus extra copies of its caches so the rotation covers >= 1 GB."""
+    from mxflashattn_amd.workloads import make_paged_batch
+
+    base = make_paged_batch(**spec, device=device)
+    cache_bytes = 2 * base.k_cache.numel() * base.k_cache.element_size()
+    copies = max(2, math.ceil(ROTATE_BYTES / max(1, cache_bytes)))
+    pools = [(base.k_cache, base.v_cache)]
+    for _ in range(copies - 1):
+        pools.append((base.k_cache.clone(), base.v_cache.clone()))
+    return base, pools
+
+
+def time_calls(fn, pools, steps: int, warmup: int, stream) -> tuple[float, float]:
+    """(median us per call from per-call events, mean us per call over the whole run)."""
+    for i in range(warmup):
+        fn(*pools[i % len(pools)])
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    first = torch.cuda.Event(enable_timing=True)
+    last = torch.cuda.Event(enable_timing=True)
+    first.record(stream)
+    for i in range(steps):
+        starts[i].record(stream)
+        fn(*pools[(warmup + i) % len(pools)])
+        ends[i].record(stream)
+    last.record(stream)
+    torch.cuda.synchronize()
+    per = [s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends)]
+    return statistics.median(per), first.elapsed_time(last) * 1e3 / steps
+
+
+def measure_workload(name: str, spec: dict, device, steps: int, warmup: int) -> dict:
+    from mxflashattn_amd import native
+
+    base, pools = build_pools(spec, device)
+    stream = torch.cuda.current_stream(device)
+    out = torch.empty_like(base.q)
+    hkv, ps, btw = base.kv_heads, base.page_size, base.block_table.shape[1]
+    ns, cl = native.split_heuristic(base.batch, hkv, ps, btw, native.num_cus(device.index or 0))
+
+    def call(kc, vc):
+        native.paged_decode_split(base.q, kc, vc, base.block_table, base.cache_seqlens,
+                                  base.scale, out=out, num_splits=ns, chunk_len=cl)
+
+    us_med, us_mean = time_calls(call, pools, steps, warmup, stream)
+
+    # Dominant kernel alone: the split partial (the whole call when ns == 1).
+    if ns > 1:
+        ws = torch.empty(native.workspace_size(base.batch, base.q_heads, base.head_dim, ns),
+                         dtype=torch.uint8, device=device)
+
+        def partial(kc, vc):
+            native.split_decode_partial(base.q, kc, vc, base.block_table, base.cache_seqlens,
+                                        base.scale, ws, ns, cl)
+
+        _, us_partial = time_calls(partial, pools, steps, warmup, stream)
+    else:
+        us_partial = us_mean
+    kv = base.kv_bytes()
+    alg = base.algorithmic_bytes()
+    gbs = kv / (us_med * 1e-6) / 1e9
+    res = {
+        "us_per_call": round(us_med, 3),
+        "us_per_call_mean": round(us_mean, 3),
+        "kv_gb_s": round(gbs, 1),
+        "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
+        "kv_bytes": kv,
+        "algorithmic_bytes": alg,
+        "num_splits": ns,
+        "chunk_len": cl,
+        "partial_kernel_us": round(us_partial, 3),
+        "partial_kernel_gb_s": round(alg / (us_partial * 1e-6) / 1e9, 1),
+        "rotation_copies": len(pools),
+    }
+    del pools, base
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline(spec: dict, reps: int) -> dict:
+    """Time the fp32 CPU restatement on the same batch (CPU tensors)."""
+    from mxflashattn_amd.workloads import make_paged_batch
+    from oracle import reference_port
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    b = make_paged_batch(**spec, device="cpu")
+    times = []
+    for i in range(reps + 1):
+        t0 = time.perf_counter()
+        reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache,
+                                         cache_seqlens=b.cache_seqlens.clone(),
+                                         block_table=b.block_table, softmax_scale=b.scale)
+        if i:
+            times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {
+        "value": round(b.kv_bytes() / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{MAIN_WORKLOAD} full batch (B={b.batch}, {b.total_tokens()} tokens), "
+                   f"median of {reps} calls after 1 warmup; {med * 1e3:.1f} ms per call"),
+        "ms_per_call": round(med * 1e3, 2),
+    }
+
+
+def load_traffic(workload: str) -> float | None:
+    path = REPO / "profiles" / f"traffic_{workload}.json"
+    if not path.exists():
+        return None
+    try:
+        return float(json.loads(path.read_text())["hbm_bytes_per_launch"])
+    except (KeyError, ValueError, json.JSONDecodeError):
+        return None
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported on this build "
+              "(the decode path shards by sequence or kv head with no exchange; see DESIGN.md)",
+              file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    from mxflashattn_amd import native
+    from mxflashattn_amd.workloads import CELLS, CONFIGS, DEFAULT_SEED
+
+    native.library()  # fail loudly when the HIP library is missing
+    device = torch.device("cuda", 0)
+    spec = {**CONFIGS, **CELLS}[args.workload]
+    print(f"[bench] workload {args.workload}: steps={args.steps} warmup={args.warmup}",
+          file=sys.stderr, flush=True)
+    main_res = measure_workload(args.workload, spec, device, args.steps, args.warmup)
+    print(f"[bench] {args.workload}: {main_res}", file=sys.stderr, flush=True)
+
+    cells = {}
+    if not args.no_cells:
+        for name, cspec in {**CELLS, **CONFIGS}.items():
+            if name == args.workload:
+                continue
+            cells[name] = measure_workload(name, cspec, device, 50, 5)
+            print(f"[bench] {name}: {cells[name]}", file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(spec, args.cpu_reps)
+
+    achieved = main_res["partial_kernel_gb_s"]
+    line = {
+        "metric": METRIC,
+        "value": main_res["kv_gb_s"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(main_res["us_per_call_mean"] / 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if spec["dtype"] == torch.bfloat16 else "f16",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"{args.workload}: B={spec['batch']} HQ={spec['q_heads']} "
+                         f"HKV={spec['kv_heads']} HD={spec['head_dim']} PS=16 "
+                         f"L={spec['lengths']} seed={DEFAULT_SEED}"),
+            "global_batch": spec["batch"],
+            "parallelism": "single_gpu",
+        },
+        "us_per_call": main_res["us_per_call"],
+        "pct_hbm_peak": main_res["pct_hbm_peak"],
+        "num_splits": main_res["num_splits"],
+        "chunk_len": main_res["chunk_len"],
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": load_traffic(args.workload),
+            "kernel": "split_partial_kernel",
+            "kernel_us": main_res["partial_kernel_us"],
+            "algorithmic_bytes": main_res["algorithmic_bytes"],
+        },
+        "cpu_baseline": cpu,
+        "cells": cells,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,158 @@
+/*
+ * mxfa_mi355x.h -- C ABI of the MI355X (gfx950) split-KV paged decode library.
+ *
+ * Library file: mxflashattn_amd/_lib/libmxfa_mi355x.so
+ *
+ * Every entry point is plain C: raw device pointers, element strides and sizes,
+ * an int return code and a hipStream_t passed as void*. Nothing here allocates
+ * device memory, synchronises the stream or throws. All launches are
+ * asynchronous on the given stream and are safe to record into a HIP graph
+ * (no host reads of device data, no memsets).
+ *
+ * Layouts (elements, not bytes; the last dimension of every tensor must be
+ * contiguous and every base pointer 16-byte aligned):
+ *   q        [B, HQ, HD]                 strides (q_stride_b, q_stride_h, 1)
+ *   cache    [num_pages, PS, HKV, HD]    strides (page, token, head, 1)
+ *   out      [B, HQ, HD]                 strides (out_stride_b, out_stride_h, 1)
+ *   block_table int32 [B, >=ceil(L/PS)]  row stride bt_stride
+ *   seqlens  int32 [B]; the attended length of sequence b is seqlens[b] + seqlen_add
+ * Query head h reads kv head h / (HQ / HKV).
+ * Page ids read from block_table are clamped to [0, num_pages) and lengths to
+ * block_table_width * PS, so malformed metadata yields wrong numbers, never an
+ * out-of-bounds access.
+ *
+ * Return codes: MXFA_OK (0) or one of the negative MXFA_E* values below.
+ */
+#ifndef MXFA_MI355X_H
+#define MXFA_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MXFA_ABI_VERSION 1
+
+/* Return codes. */
+#define MXFA_OK 0
+#define MXFA_EUNSUPPORTED (-1) /* shape/dtype outside the kernel contract (GQ, HD, dtype, PS) */
+#define MXFA_EINVAL (-2)       /* null pointer, non-positive size, misaligned pointer or stride */
+#define MXFA_EWORKSPACE (-3)   /* workspace missing or smaller than mxfa_split_decode_workspace_size */
+#define MXFA_ELAUNCH (-4)      /* the HIP runtime rejected a kernel launch */
+
+/* Element types. */
+#define MXFA_DTYPE_F16 0
+#define MXFA_DTYPE_BF16 1
+
+/* ABI version of the loaded library (MXFA_ABI_VERSION). No reference counterpart. */
+int mxfa_abi_version(void);
+
+/* Static text for a return code. No reference counterpart. */
+const char *mxfa_strerror(int code);
+
+/*
+ * Split-count heuristic for the launch below, sized for the device's CU count.
+ * Integer-only, reads no device data. Replaces the Python loop at
+ * integrations/vllm/vllm_plugin.py:271-276 (NP doubling until B*HKV*NP >= 2048,
+ * c_len = ceil(BTW*PS/NP)). Writes the number of splits and the per-split
+ * token count (a multiple of 64) through num_splits / chunk_len.
+ */
+int mxfa_split_heuristic(int batch, int kv_heads, int page_size, int block_table_width,
+                         int num_cus, int *num_splits, int *chunk_len);
+
+/*
+ * Bytes of caller-owned workspace the split launch needs for num_splits > 1
+ * (0 for num_splits == 1). Replaces the per-call at::empty of ows/mdws at
+ * csrc_native/m1_binding.cpp:94-96.
+ */
+int mxfa_split_decode_workspace_size(int batch, int q_heads, int head_dim, int num_splits,
+                                     size_t *bytes);
+
+/*
+ * Split-KV paged decode: out[b, h, :] = softmax(q[b,h]·K_b^T · scale) · V_b over the
+ * first seqlens[b] + seqlen_add tokens of sequence b, gathered through block_table.
+ * Launches the split partial kernel and, when num_splits > 1, the LSE combine
+ * kernel. A sequence of length 0 yields zeros.
+ * Replaces mxfa_paged_decode_split_launch (csrc_native/m1_kernel.cpp:1206-1211);
+ * same information plus explicit strides, seqlen_add and a sized workspace.
+ * Supported: HD in {64,128}, HQ/HKV in {2,4,8}, PS a power of two in [1, 4096],
+ * dtype F16/BF16 (q, caches and out share it).
+ */
+int mxfa_split_decode_launch(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                             const void *k_cache, const void *v_cache,
+                             int64_t cache_stride_page, int64_t cache_stride_token,
+                             int64_t cache_stride_head, const int32_t *block_table,
+                             int64_t bt_stride, const int32_t *seqlens, int seqlen_add,
+                             void *out, int64_t out_stride_b, int64_t out_stride_h,
+                             void *workspace, size_t workspace_bytes, float scale,
+                             int batch, int q_heads, int kv_heads, int head_dim,
+                             int page_size, int block_table_width, int num_pages, int dtype,
+                             int num_splits, int chunk_len, void *stream);
+
+/*
+ * Partial stage alone: writes per-split normalised outputs and base-2 LSEs into
+ * the workspace (layout documented in mxflashattn_amd/csrc/split_decode.hip).
+ * With the combine below it is the same computation as mxfa_split_decode_launch;
+ * separately it lets a caller time the dominant kernel or merge partials from
+ * several devices. Counterpart of the paged_decode_v3 launch inside launch_split
+ * (csrc_native/m1_kernel.cpp:985-999).
+ */
+int mxfa_split_decode_partial_launch(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                                     const void *k_cache, const void *v_cache,
+                                     int64_t cache_stride_page, int64_t cache_stride_token,
+                                     int64_t cache_stride_head, const int32_t *block_table,
+                                     int64_t bt_stride, const int32_t *seqlens,
+                                     int seqlen_add, void *workspace, size_t workspace_bytes,
+                                     float scale, int batch, int q_heads, int kv_heads,
+                                     int head_dim, int page_size, int block_table_width,
+                                     int num_pages, int dtype, int num_splits, int chunk_len,
+                                     void *stream);
+
+/*
+ * Combine stage alone (LSE merge of the partials). Counterpart of the
+ * split_combine launch (csrc_native/m1_kernel.cpp:1000-1001, kernel :861-888).
+ */
+int mxfa_split_decode_combine_launch(const void *workspace, size_t workspace_bytes,
+                                     const int32_t *seqlens, int seqlen_add, void *out,
+                                     int64_t out_stride_b, int64_t out_stride_h, int batch,
+                                     int q_heads, int head_dim, int dtype, int num_splits,
+                                     int chunk_len, void *stream);
+
+/*
+ * vLLM-style paged append: for token t with slot = slot_mapping[t] >= 0,
+ * cache[slot / PS, slot % PS, kvh, :] = key/value[t, kvh, :]; slot < 0 is skipped.
+ * Bit-exact copy. key/value are [num_tokens, HKV, HD] with strides (tok, head, 1).
+ * Replaces the vendor reshape_and_cache_flash the reference plugin binds
+ * (integrations/vllm/vllm_plugin.py:43-44, do_kv_cache_update :507-511).
+ */
+int mxfa_reshape_and_cache_launch(const void *key, const void *value,
+                                  int64_t kv_stride_token, int64_t kv_stride_head,
+                                  void *k_cache, void *v_cache, int64_t cache_stride_page,
+                                  int64_t cache_stride_token, int64_t cache_stride_head,
+                                  const int64_t *slot_mapping, int num_tokens, int kv_heads,
+                                  int head_dim, int page_size, int num_pages, int dtype,
+                                  void *stream);
+
+/*
+ * Block-table append used by flash_attn_with_kvcache(k=, v=): token t of
+ * sequence b goes to logical position seqlens[b] + t, i.e. page
+ * block_table[b, pos / PS], offset pos % PS. seqlens is not modified.
+ * k/v are [B, S_new, HKV, HD] with strides (b, tok, head, 1). Bit-exact copy.
+ * Replaces the append loop of mxflashattn/reference.py:117-122
+ * (csrc/mxmac/paged_kv.cpp:102-109 in the ATen backend).
+ */
+int mxfa_append_kv_launch(const void *k, const void *v, int64_t kv_stride_b,
+                          int64_t kv_stride_token, int64_t kv_stride_head, void *k_cache,
+                          void *v_cache, int64_t cache_stride_page, int64_t cache_stride_token,
+                          int64_t cache_stride_head, const int32_t *block_table,
+                          int64_t bt_stride, const int32_t *seqlens, int batch, int new_tokens,
+                          int kv_heads, int head_dim, int page_size, int block_table_width,
+                          int num_pages, int dtype, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MXFA_MI355X_H */

@@ -1,0 +1,416 @@
+"""ctypes binding of ``libmxfa_mi355x.so`` (C ABI: ``include/mxfa_mi355x.h``).
+
+This module is the thin host layer between torch tensors and the C entry
+points: it checks shapes, passes raw device pointers and element strides, keeps
+a per-(device, stream) workspace so steady-state calls allocate nothing, and
+launches on the caller's current HIP stream without synchronising.
+
+Reference counterpart: the pybind module ``mxmmain`` (``csrc_native/m1_binding.cpp``),
+``paged_decode_split`` at ``csrc_native/m1_binding.cpp:78-115``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import functools
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmxfa_mi355x.so"
+ABI_VERSION = 1
+
+MXFA_OK = 0
+MXFA_EUNSUPPORTED = -1
+MXFA_EINVAL = -2
+MXFA_EWORKSPACE = -3
+MXFA_ELAUNCH = -4
+
+DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
+
+SUPPORTED_HEAD_DIMS = (64, 128)
+SUPPORTED_GQA = (2, 4, 8)
+
+# Every entry point declared in include/mxfa_mi355x.h.
+EXPORTED_SYMBOLS = (
+    "mxfa_abi_version",
+    "mxfa_strerror",
+    "mxfa_split_heuristic",
+    "mxfa_split_decode_workspace_size",
+    "mxfa_split_decode_launch",
+    "mxfa_split_decode_partial_launch",
+    "mxfa_split_decode_combine_launch",
+    "mxfa_reshape_and_cache_launch",
+    "mxfa_append_kv_launch",
+)
+
+
+class NativeLibraryError(RuntimeError):
+    """The HIP library is missing, failed to load or has the wrong ABI."""
+
+
+class UnsupportedConfig(RuntimeError):
+    """The kernel contract does not cover this shape/dtype (MXFA_EUNSUPPORTED)."""
+
+
+_i = ctypes.c_int
+_i64 = ctypes.c_int64
+_p = ctypes.c_void_p
+_f = ctypes.c_float
+_sz = ctypes.c_size_t
+
+_SIGNATURES = {
+    "mxfa_abi_version": (_i, []),
+    "mxfa_strerror": (ctypes.c_char_p, [_i]),
+    "mxfa_split_heuristic": (_i, [_i, _i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
+    "mxfa_split_decode_workspace_size": (_i, [_i, _i, _i, _i, ctypes.POINTER(_sz)]),
+    "mxfa_split_decode_launch": (
+        _i,
+        [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _p, _i64, _i64, _p, _sz,
+         _f, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _p],
+    ),
+    "mxfa_split_decode_partial_launch": (
+        _i,
+        [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _p, _sz, _f, _i, _i, _i,
+         _i, _i, _i, _i, _i, _i, _i, _p],
+    ),
+    "mxfa_split_decode_combine_launch": (
+        _i,
+        [_p, _sz, _p, _i, _p, _i64, _i64, _i, _i, _i, _i, _i, _i, _p],
+    ),
+    "mxfa_reshape_and_cache_launch": (
+        _i,
+        [_p, _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i, _i, _i, _i, _i, _i, _p],
+    ),
+    "mxfa_append_kv_launch": (
+        _i,
+        [_p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _i, _i, _i,
+         _i, _i, _i, _i, _p],
+    ),
+}
+
+_load_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+_load_error: str | None = None
+
+
+def library() -> ctypes.CDLL:
+    """Load the library once; raise NativeLibraryError with the reason otherwise."""
+    global _lib, _load_error
+    if _lib is not None:
+        return _lib
+    with _load_lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            _load_error = (
+                f"native library not built: {LIB_PATH} is missing "
+                "(run python -m mxflashattn_amd._build)"
+            )
+            raise NativeLibraryError(_load_error)
+        try:
+            lib = ctypes.CDLL(str(LIB_PATH))
+        except OSError as exc:
+            _load_error = f"native library failed to load: {exc}"
+            raise NativeLibraryError(_load_error) from exc
+        for name, (restype, argtypes) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        version = lib.mxfa_abi_version()
+        if version != ABI_VERSION:
+            _load_error = f"native library ABI {version} does not match {ABI_VERSION}"
+            raise NativeLibraryError(_load_error)
+        _lib = lib
+        return lib
+
+
+def unavailable_reason() -> str | None:
+    """None when the library loads, else the reason it does not."""
+    try:
+        library()
+    except NativeLibraryError as exc:
+        return str(exc)
+    return None
+
+
+def _check(rc: int, what: str) -> None:
+    if rc == MXFA_OK:
+        return
+    text = library().mxfa_strerror(rc).decode()
+    if rc == MXFA_EUNSUPPORTED:
+        raise UnsupportedConfig(f"{what}: {text}")
+    raise RuntimeError(f"{what} failed ({rc}): {text}")
+
+
+@functools.lru_cache(maxsize=256)
+def split_heuristic(batch: int, kv_heads: int, page_size: int, block_table_width: int,
+                    num_cus: int) -> tuple[int, int]:
+    """(num_splits, chunk_len) for a launch; integer-only, no device access."""
+    ns, cl = _i(), _i()
+    _check(
+        library().mxfa_split_heuristic(batch, kv_heads, page_size, block_table_width, num_cus,
+                                       ctypes.byref(ns), ctypes.byref(cl)),
+        "mxfa_split_heuristic",
+    )
+    return ns.value, cl.value
+
+
+def workspace_size(batch: int, q_heads: int, head_dim: int, num_splits: int) -> int:
+    out = _sz()
+    _check(library().mxfa_split_decode_workspace_size(batch, q_heads, head_dim, num_splits,
+                                                       ctypes.byref(out)),
+           "mxfa_split_decode_workspace_size")
+    return out.value
+
+
+@functools.lru_cache(maxsize=16)
+def num_cus(device_index: int) -> int:
+    return int(torch.cuda.get_device_properties(device_index).multi_processor_count)
+
+
+class _Workspace:
+    """Grow-only fp32 scratch per (device, stream); reused across calls."""
+
+    def __init__(self) -> None:
+        self._buffers: dict[tuple[int, int], torch.Tensor] = {}
+        self._lock = threading.Lock()
+
+    def get(self, device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+        key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+        with self._lock:
+            buf = self._buffers.get(key)
+            if buf is None or buf.numel() < nbytes:
+                size = max(nbytes, 1 << 20)
+                if buf is not None:
+                    size = max(size, buf.numel() * 2)
+                buf = torch.empty(size, dtype=torch.uint8, device=device)
+                self._buffers[key] = buf
+            return buf
+
+    def clear(self) -> None:
+        with self._lock:
+            self._buffers.clear()
+
+
+WORKSPACE = _Workspace()
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    code = DTYPE_CODES.get(t.dtype)
+    if code is None:
+        raise UnsupportedConfig(f"dtype {t.dtype} is not float16/bfloat16")
+    return code
+
+
+def _int32_contig(t: torch.Tensor, name: str) -> torch.Tensor:
+    if t.dtype != torch.int32:
+        t = t.to(torch.int32)
+    if t.dim() == 2:
+        if t.stride(1) != 1:
+            t = t.contiguous()
+    elif not t.is_contiguous():
+        t = t.contiguous()
+    return t
+
+
+def _stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def check_decode_shapes(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
+    """Raise UnsupportedConfig when the kernel contract does not cover the call."""
+    if q.dim() not in (3, 4) or (q.dim() == 4 and q.shape[1] != 1):
+        raise UnsupportedConfig(f"q must be [B,1,HQ,HD] or [B,HQ,HD], got {tuple(q.shape)}")
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise UnsupportedConfig("caches must be [pages, page_size, kv_heads, head_dim]")
+    hq, hd = q.shape[-2], q.shape[-1]
+    hkv = k_cache.shape[2]
+    if hd not in SUPPORTED_HEAD_DIMS or k_cache.shape[3] != hd:
+        raise UnsupportedConfig(f"head_dim {hd} not in {SUPPORTED_HEAD_DIMS}")
+    if hkv <= 0 or hq % hkv or hq // hkv not in SUPPORTED_GQA:
+        raise UnsupportedConfig(f"GQA ratio {hq}/{hkv} not in {SUPPORTED_GQA}")
+    if q.dtype not in DTYPE_CODES or k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
+        raise UnsupportedConfig("q and caches must share float16 or bfloat16")
+    ps = k_cache.shape[1]
+    if ps <= 0 or ps & (ps - 1) or ps > 4096:
+        raise UnsupportedConfig(f"page size {ps} is not a power of two <= 4096")
+
+
+def paged_decode_split(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    cache_seqlens: torch.Tensor,
+    softmax_scale: float,
+    *,
+    out: torch.Tensor | None = None,
+    num_splits: int | None = None,
+    chunk_len: int | None = None,
+    seqlen_add: int = 0,
+) -> torch.Tensor:
+    """Split-KV paged decode on the current stream; returns ``out`` shaped like q.
+
+    q: [B, 1, HQ, HD] or [B, HQ, HD] (any strides with a contiguous last dim);
+    caches: [pages, PS, HKV, HD]; block_table: int32 [B, W]; cache_seqlens: int32 [B].
+    The attended length of sequence b is cache_seqlens[b] + seqlen_add.
+    """
+    check_decode_shapes(q, k_cache, v_cache)
+    lib = library()
+    device = q.device
+    batch, hq, hd = q.shape[0], q.shape[-2], q.shape[-1]
+    pages, ps, hkv = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    if k_cache.stride(-1) != 1 or v_cache.stride() != k_cache.stride():
+        raise UnsupportedConfig("k_cache and v_cache must share strides with a contiguous last dim")
+    block_table = _int32_contig(block_table, "block_table")
+    cache_seqlens = _int32_contig(cache_seqlens, "cache_seqlens")
+    if block_table.dim() != 2 or block_table.shape[0] != batch:
+        raise ValueError("block_table must be [batch, width]")
+    if cache_seqlens.numel() != batch:
+        raise ValueError("cache_seqlens must have one entry per sequence")
+    btw = block_table.shape[1]
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=device)
+    if out.shape != q.shape or out.dtype != q.dtype or out.stride(-1) != 1:
+        raise ValueError("out must match q's shape and dtype with a contiguous last dim")
+    if num_splits is None or chunk_len is None:
+        num_splits, chunk_len = split_heuristic(batch, hkv, ps, btw, num_cus(device.index or 0))
+    stream = _stream_handle(device)
+    ws_bytes = workspace_size(batch, hq, hd, num_splits)
+    ws_ptr = 0
+    if ws_bytes:
+        ws_ptr = WORKSPACE.get(device, stream, ws_bytes).data_ptr()
+    qs = q.stride()
+    os_ = out.stride()
+    cs = k_cache.stride()
+    rc = lib.mxfa_split_decode_launch(
+        q.data_ptr(), qs[0], qs[-2], k_cache.data_ptr(), v_cache.data_ptr(), cs[0], cs[1], cs[2],
+        block_table.data_ptr(), block_table.stride(0), cache_seqlens.data_ptr(), seqlen_add,
+        out.data_ptr(), os_[0], os_[-2], ws_ptr, ws_bytes, float(softmax_scale), batch, hq, hkv,
+        hd, ps, btw, pages, DTYPE_CODES[q.dtype], num_splits, chunk_len, stream,
+    )
+    _check(rc, "mxfa_split_decode_launch")
+    return out
+
+
+def split_decode_partial(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    cache_seqlens: torch.Tensor,
+    softmax_scale: float,
+    workspace: torch.Tensor,
+    num_splits: int,
+    chunk_len: int,
+    seqlen_add: int = 0,
+) -> None:
+    """Partial stage only: per-split normalised outputs and base-2 LSEs into ``workspace``.
+
+    ``workspace`` must hold at least ``workspace_size(B, HQ, HD, num_splits)`` bytes;
+    ``split_decode_combine`` finishes the computation. Inputs as for paged_decode_split.
+    """
+    check_decode_shapes(q, k_cache, v_cache)
+    batch, hq, hd = q.shape[0], q.shape[-2], q.shape[-1]
+    pages, ps, hkv = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
+    block_table = _int32_contig(block_table, "block_table")
+    cache_seqlens = _int32_contig(cache_seqlens, "cache_seqlens")
+    qs, cs = q.stride(), k_cache.stride()
+    rc = library().mxfa_split_decode_partial_launch(
+        q.data_ptr(), qs[0], qs[-2], k_cache.data_ptr(), v_cache.data_ptr(), cs[0], cs[1], cs[2],
+        block_table.data_ptr(), block_table.stride(0), cache_seqlens.data_ptr(), seqlen_add,
+        workspace.data_ptr(), workspace.numel() * workspace.element_size(), float(softmax_scale),
+        batch, hq, hkv, hd, ps, block_table.shape[1], pages, DTYPE_CODES[q.dtype], num_splits,
+        chunk_len, _stream_handle(q.device),
+    )
+    _check(rc, "mxfa_split_decode_partial_launch")
+
+
+def split_decode_combine(
+    workspace: torch.Tensor,
+    cache_seqlens: torch.Tensor,
+    out: torch.Tensor,
+    num_splits: int,
+    chunk_len: int,
+    seqlen_add: int = 0,
+) -> torch.Tensor:
+    """LSE merge of the partials in ``workspace`` into ``out`` ([B,1,HQ,HD] or [B,HQ,HD])."""
+    cache_seqlens = _int32_contig(cache_seqlens, "cache_seqlens")
+    batch, hq, hd = out.shape[0], out.shape[-2], out.shape[-1]
+    os_ = out.stride()
+    rc = library().mxfa_split_decode_combine_launch(
+        workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+        cache_seqlens.data_ptr(), seqlen_add, out.data_ptr(), os_[0], os_[-2], batch, hq, hd,
+        _dtype_code(out), num_splits, chunk_len, _stream_handle(out.device),
+    )
+    _check(rc, "mxfa_split_decode_combine_launch")
+    return out
+
+
+def reshape_and_cache(
+    key: torch.Tensor,
+    value: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+) -> None:
+    """vLLM-format paged append: row t -> slot_mapping[t] (skipped when < 0)."""
+    if key.dim() != 3 or value.shape != key.shape:
+        raise ValueError("key/value must be [num_tokens, kv_heads, head_dim]")
+    if key_cache.dim() != 4 or value_cache.shape != key_cache.shape:
+        raise ValueError("caches must be [pages, page_size, kv_heads, head_dim]")
+    if key.shape[1:] != key_cache.shape[2:]:
+        raise ValueError("key/value heads and head_dim must match the cache")
+    if key.dtype != key_cache.dtype or value.dtype != key.dtype or value_cache.dtype != key.dtype:
+        raise ValueError("key/value and caches must share a dtype")
+    if key.stride() != value.stride() or key.stride(-1) != 1:
+        key, value = key.contiguous(), value.contiguous()
+    if value_cache.stride() != key_cache.stride() or key_cache.stride(-1) != 1:
+        raise UnsupportedConfig("caches must share strides with a contiguous last dim")
+    slots = slot_mapping
+    if slots.dtype != torch.int64:
+        slots = slots.to(torch.int64)
+    slots = slots.contiguous()
+    n = key.shape[0]
+    if slots.numel() < n:
+        raise ValueError("slot_mapping must have one entry per token")
+    cs = key_cache.stride()
+    rc = library().mxfa_reshape_and_cache_launch(
+        key.data_ptr(), value.data_ptr(), key.stride(0), key.stride(1), key_cache.data_ptr(),
+        value_cache.data_ptr(), cs[0], cs[1], cs[2], slots.data_ptr(), n, key.shape[1],
+        key.shape[2], key_cache.shape[1], key_cache.shape[0], _dtype_code(key),
+        _stream_handle(key.device),
+    )
+    _check(rc, "mxfa_reshape_and_cache_launch")
+
+
+def append_kv(
+    k: torch.Tensor,
+    v: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    cache_seqlens: torch.Tensor,
+) -> None:
+    """Block-table append: k[b, t] -> position cache_seqlens[b] + t (seqlens unchanged)."""
+    if k.dim() != 4 or v.shape != k.shape:
+        raise ValueError("k/v must be [batch, new_tokens, kv_heads, head_dim]")
+    if k.stride() != v.stride() or k.stride(-1) != 1:
+        k, v = k.contiguous(), v.contiguous()
+    if v_cache.stride() != k_cache.stride() or k_cache.stride(-1) != 1:
+        raise UnsupportedConfig("caches must share strides with a contiguous last dim")
+    block_table = _int32_contig(block_table, "block_table")
+    cache_seqlens = _int32_contig(cache_seqlens, "cache_seqlens")
+    cs = k_cache.stride()
+    rc = library().mxfa_append_kv_launch(
+        k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), k.stride(2), k_cache.data_ptr(),
+        v_cache.data_ptr(), cs[0], cs[1], cs[2], block_table.data_ptr(), block_table.stride(0),
+        cache_seqlens.data_ptr(), k.shape[0], k.shape[1], k.shape[2], k.shape[3],
+        k_cache.shape[1], block_table.shape[1], k_cache.shape[0], _dtype_code(k),
+        _stream_handle(k.device),
+    )
+    _check(rc, "mxfa_append_kv_launch")

@@ -1,0 +1,156 @@
+"""Seeded synthetic paged-KV decode batches (the shapes of the benchmark configs).
+
+Inputs follow the reference kernel test's recipe (csrc_native/test_m1.py:40-47):
+q/k/v ~ N(0, 1), a random permutation of physical pages as the block table,
+scale 1/sqrt(head_dim). Generation runs on a torch.Generator of the target
+device (or the CPU), so the same seed gives the same batch on every box.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+DEFAULT_SEED = 20261007  # csrc_native/test_m1.py:40
+
+
+@dataclass
+class PagedBatch:
+    q: torch.Tensor             # [B, 1, HQ, HD]
+    k_cache: torch.Tensor       # [P, PS, HKV, HD]
+    v_cache: torch.Tensor       # [P, PS, HKV, HD]
+    block_table: torch.Tensor   # int32 [B, W]
+    cache_seqlens: torch.Tensor  # int32 [B]
+    scale: float
+
+    @property
+    def batch(self) -> int:
+        return self.q.shape[0]
+
+    @property
+    def q_heads(self) -> int:
+        return self.q.shape[2]
+
+    @property
+    def kv_heads(self) -> int:
+        return self.k_cache.shape[2]
+
+    @property
+    def head_dim(self) -> int:
+        return self.q.shape[3]
+
+    @property
+    def page_size(self) -> int:
+        return self.k_cache.shape[1]
+
+    def total_tokens(self) -> int:
+        return int(self.cache_seqlens.sum().item())
+
+    def kv_bytes(self) -> int:
+        """K and V bytes the call must read: sum_b 2 * L_b * HKV * HD * elem."""
+        return 2 * self.total_tokens() * self.kv_heads * self.head_dim * self.q.element_size()
+
+    def algorithmic_bytes(self) -> int:
+        """KV + q + out + used block-table entries + lengths."""
+        ps = self.page_size
+        pages = int(((self.cache_seqlens + ps - 1) // ps).sum().item())
+        qo = 2 * self.q.numel() * self.q.element_size()
+        return self.kv_bytes() + qo + 4 * pages + 4 * self.batch
+
+    def to(self, device: torch.device | str) -> "PagedBatch":
+        return PagedBatch(self.q.to(device), self.k_cache.to(device), self.v_cache.to(device),
+                          self.block_table.to(device), self.cache_seqlens.to(device), self.scale)
+
+
+def make_paged_batch(
+    batch: int,
+    q_heads: int,
+    kv_heads: int,
+    head_dim: int,
+    dtype: torch.dtype,
+    lengths: torch.Tensor | tuple[int, int] | int,
+    *,
+    page_size: int = 16,
+    pool_factor: float = 1.25,
+    num_pages: int | None = None,
+    block_table_width: int | None = None,
+    peaky_fraction: float = 0.0,
+    peaky_scale: float = 8.0,
+    seed: int = DEFAULT_SEED,
+    device: torch.device | str = "cpu",
+) -> PagedBatch:
+    """Build one synthetic decode batch.
+
+    lengths: a tensor of per-sequence lengths, an inclusive (lo, hi) range for
+    uniform integers, or one length for every sequence. The page pool holds
+    ceil(pool_factor * pages needed) pages unless num_pages is given; every
+    sequence gets distinct pages from a random permutation of the pool.
+    peaky_fraction of the K rows are multiplied by peaky_scale.
+    """
+    device = torch.device(device)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    if isinstance(lengths, torch.Tensor):
+        lens = lengths.to(torch.int64).cpu()
+    elif isinstance(lengths, tuple):
+        lo, hi = lengths
+        cpu_gen = torch.Generator().manual_seed(seed)
+        lens = torch.randint(lo, hi + 1, (batch,), generator=cpu_gen, dtype=torch.int64)
+    else:
+        lens = torch.full((batch,), int(lengths), dtype=torch.int64)
+    need = [(int(x) + page_size - 1) // page_size for x in lens]
+    total_need = sum(need)
+    if num_pages is None:
+        num_pages = max(1, math.ceil(pool_factor * total_need))
+    if num_pages < total_need:
+        raise ValueError(f"pool of {num_pages} pages cannot hold {total_need} pages")
+    width = block_table_width or max(1, max(need) if need else 1)
+    perm = torch.randperm(num_pages, generator=torch.Generator().manual_seed(seed + 1))
+    table = torch.zeros((batch, width), dtype=torch.int32)
+    cursor = 0
+    for b, n in enumerate(need):
+        table[b, :n] = perm[cursor:cursor + n].to(torch.int32)
+        cursor += n
+
+    def randn(*shape: int) -> torch.Tensor:
+        return torch.randn(*shape, generator=gen, device=device, dtype=torch.float32).to(dtype)
+
+    q = randn(batch, 1, q_heads, head_dim)
+    k_cache = randn(num_pages, page_size, kv_heads, head_dim)
+    v_cache = randn(num_pages, page_size, kv_heads, head_dim)
+    if peaky_fraction > 0:
+        rows = k_cache.view(-1, head_dim)
+        pick = torch.rand(rows.shape[0], generator=gen, device=device) < peaky_fraction
+        rows[pick] = (rows[pick].float() * peaky_scale).to(dtype)
+    return PagedBatch(
+        q=q,
+        k_cache=k_cache,
+        v_cache=v_cache,
+        block_table=table.to(device),
+        cache_seqlens=lens.to(torch.int32).to(device),
+        scale=head_dim ** -0.5,
+    )
+
+
+# The benchmark configurations of BASELINE.json (configs 1-4) and the six
+# GQ x HD cells of config 2, as keyword arguments of make_paged_batch.
+CONFIGS = {
+    "config1_cpu_ref": dict(batch=4, q_heads=8, kv_heads=2, head_dim=64, dtype=torch.float16,
+                            lengths=(1, 512), num_pages=128, block_table_width=32),
+    "config2_qwen3_4b": dict(batch=32, q_heads=32, kv_heads=8, head_dim=128,
+                             dtype=torch.bfloat16, lengths=(1024, 8192)),
+    "config3_highbatch_gq2_d64": dict(batch=128, q_heads=16, kv_heads=8, head_dim=64,
+                                      dtype=torch.float16, lengths=(1, 512)),
+    "config4_long_gq8_d128": dict(batch=16, q_heads=32, kv_heads=4, head_dim=128,
+                                  dtype=torch.bfloat16, lengths=16384, peaky_fraction=0.01),
+    "config4_long_gq8_d64": dict(batch=16, q_heads=32, kv_heads=4, head_dim=64,
+                                 dtype=torch.bfloat16, lengths=16384, peaky_fraction=0.01),
+}
+
+CELLS = {
+    f"cell_gq{32 // hkv}_d{hd}": dict(batch=32, q_heads=32, kv_heads=hkv, head_dim=hd,
+                                      dtype=torch.bfloat16, lengths=(1024, 8192))
+    for hkv in (16, 8, 4) for hd in (128, 64)
+}

@@ -1,0 +1,189 @@
+"""GPU parity of the HIP kernels against the CPU oracle (through the C ABI).
+
+Tolerances: max-abs error <= 2e-3 for fp16 and <= 1.6e-2
+for bf16 against the fp32-softmax oracle (oracle.reference_port); the block-table
+gather and both appends are bit-exact.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from mxflashattn_amd import native
+from mxflashattn_amd.workloads import make_paged_batch
+from oracle import c_oracle, reference_port
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float16: 2e-3, torch.bfloat16: 1.6e-2}
+
+
+def oracle_out(b) -> torch.Tensor:
+    """fp32 reference output [B, 1, HQ, HD] (float32) for a PagedBatch on any device."""
+    cpu = b.to("cpu")
+    out = reference_port.attention_kvcache(
+        cpu.q, cpu.k_cache, cpu.v_cache, cache_seqlens=cpu.cache_seqlens.clone(),
+        block_table=cpu.block_table, softmax_scale=cpu.scale,
+    )
+    return out.float()
+
+
+def max_err(actual: torch.Tensor, expected: torch.Tensor) -> float:
+    return (actual.float().cpu() - expected.float().cpu()).abs().max().item()
+
+
+def run_native(b, **kw) -> torch.Tensor:
+    out = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
+                                    b.scale, **kw)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("gq", [2, 4, 8])
+def test_cells_ragged_match_oracle(device, dtype, head_dim, gq):
+    lengths = torch.tensor([1, 15, 16, 17, 300, 1000])
+    b = make_paged_batch(6, 2 * gq, 2, head_dim, dtype, lengths, seed=11 + gq).to(device)
+    expected = oracle_out(b)
+    for ns_cl in (None, (1, 1024), (16, 64)):
+        kw = {} if ns_cl is None else dict(num_splits=ns_cl[0], chunk_len=ns_cl[1])
+        got = run_native(b, **kw)
+        assert torch.isfinite(got.float()).all()
+        assert max_err(got, expected) <= TOL[dtype], ns_cl
+
+
+@pytest.mark.parametrize("page_size", [1, 2, 4, 8, 32, 64, 256])
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_page_sizes(device, page_size, head_dim):
+    lengths = torch.tensor([3, 129, 517])
+    b = make_paged_batch(3, 8, 2, head_dim, torch.float16, lengths, page_size=page_size,
+                         seed=5).to(device)
+    expected = oracle_out(b)
+    assert max_err(run_native(b), expected) <= TOL[torch.float16]
+    assert max_err(run_native(b, num_splits=12, chunk_len=64), expected) <= TOL[torch.float16]
+
+
+def test_single_token_returns_v_row_exactly(device):
+    # One key: softmax weight is exactly 1, so the output is the V row bit for bit.
+    for dtype in (torch.float16, torch.bfloat16):
+        b = make_paged_batch(4, 16, 4, 128, dtype, 1, seed=3).to(device)
+        got = run_native(b).cpu()
+        cpu = b.to("cpu")
+        for i in range(4):
+            page = int(cpu.block_table[i, 0])
+            for h in range(16):
+                assert torch.equal(got[i, 0, h], cpu.v_cache[page, 0, h // 4])
+
+
+def test_uniform_scores_average_v(device):
+    # scale = 0 makes every score equal: the output is the mean of the V rows.
+    b = make_paged_batch(2, 8, 2, 64, torch.float16, torch.tensor([5, 70]), seed=9).to(device)
+    got = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
+                                    0.0)
+    torch.cuda.synchronize()
+    cpu = b.to("cpu")
+    for i, n in enumerate([5, 70]):
+        v = reference_port.gather_pages(cpu.v_cache, cpu.block_table[i].tolist(), n).float()
+        mean = v.mean(dim=0)  # [HKV, D]
+        for h in range(8):
+            assert (got[i, 0, h].float().cpu() - mean[h // 4]).abs().max() <= 2e-3
+
+
+def test_zero_length_sequence_gives_zeros(device):
+    b = make_paged_batch(3, 8, 2, 128, torch.bfloat16, torch.tensor([0, 40, 0]), seed=2).to(device)
+    for kw in ({}, dict(num_splits=4, chunk_len=64), dict(num_splits=1, chunk_len=64)):
+        got = run_native(b, **kw).cpu()
+        assert torch.equal(got[0], torch.zeros_like(got[0]))
+        assert torch.equal(got[2], torch.zeros_like(got[2]))
+        assert torch.isfinite(got.float()).all()
+
+
+def test_peaky_keys_long_context(device):
+    b = make_paged_batch(2, 32, 4, 128, torch.bfloat16, 16384, peaky_fraction=0.01,
+                         seed=4).to(device)
+    expected = oracle_out(b)
+    assert max_err(run_native(b), expected) <= TOL[torch.bfloat16]
+
+
+def test_large_scores_do_not_overflow(device):
+    # q x 400 (csrc_native/test_m1.py:148 "ovf" case): base-2 scores reach hundreds.
+    b = make_paged_batch(2, 8, 2, 128, torch.float16, torch.tensor([512, 300]), seed=6)
+    b.q = (b.q.float() * 400).clamp(-60000, 60000).to(torch.float16)
+    b = b.to(device)
+    got = run_native(b, num_splits=8, chunk_len=64)
+    assert torch.isfinite(got.float()).all()
+    expected = torch.from_numpy(c_oracle.paged_decode_f64(
+        b.q.cpu(), b.k_cache.cpu(), b.v_cache.cpu(), b.block_table.cpu(), b.cache_seqlens.cpu(),
+        b.scale)).reshape(got.shape)
+    assert max_err(got, expected) <= 2e-3
+
+
+def test_noncontiguous_q_and_out(device):
+    b = make_paged_batch(4, 16, 4, 128, torch.float16, torch.tensor([33, 64, 1, 200]),
+                         seed=8).to(device)
+    fused = torch.randn(4, 1, 48, 128, device=device, dtype=torch.float16)
+    fused[:, :, 16:32] = b.q
+    q_view = fused[:, :, 16:32]
+    assert not q_view.is_contiguous()
+    out_buf = torch.zeros(4, 1, 40, 128, device=device, dtype=torch.float16)
+    out_view = out_buf[:, :, 8:24]
+    native.paged_decode_split(q_view, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
+                              b.scale, out=out_view)
+    torch.cuda.synchronize()
+    assert max_err(out_view, oracle_out(b)) <= TOL[torch.float16]
+    assert torch.equal(out_buf[:, :, :8].cpu(), torch.zeros(4, 1, 8, 128, dtype=torch.float16))
+
+
+def test_config2_full_size_matches_oracle(device):
+    from mxflashattn_amd.workloads import CONFIGS
+
+    b = make_paged_batch(**CONFIGS["config2_qwen3_4b"], device=device)
+    got = run_native(b)
+    assert max_err(got, oracle_out(b)) <= TOL[torch.bfloat16]
+    # Split-count independence at full size: one split per sequence gives the same answer.
+    cap = b.block_table.shape[1] * b.page_size
+    one = run_native(b, num_splits=1, chunk_len=(cap + 63) // 64 * 64)
+    assert max_err(got, one) <= TOL[torch.bfloat16]
+
+
+def test_append_kv_bit_exact(device):
+    for dtype in (torch.float16, torch.bfloat16):
+        # Allocate pages for the appended rows too, so every destination is distinct.
+        b = make_paged_batch(3, 8, 2, 128, dtype, torch.tensor([8, 19, 33]), seed=12,
+                             block_table_width=4).to(device)
+        b.cache_seqlens = torch.tensor([5, 16, 30], dtype=torch.int32, device=device)
+        k_new = torch.randn(3, 3, 2, 128, device=device).to(dtype)
+        v_new = torch.randn(3, 3, 2, 128, device=device).to(dtype)
+        exp_k, exp_v = c_oracle.append_kv(k_new.cpu(), v_new.cpu(), b.k_cache.cpu(),
+                                          b.v_cache.cpu(), b.block_table.cpu(),
+                                          b.cache_seqlens.cpu())
+        kc, vc = b.k_cache.clone(), b.v_cache.clone()
+        native.append_kv(k_new, v_new, kc, vc, b.block_table, b.cache_seqlens)
+        torch.cuda.synchronize()
+        assert torch.equal(kc.cpu(), exp_k) and torch.equal(vc.cpu(), exp_v)
+
+
+def test_reshape_and_cache_bit_exact(device):
+    for dtype in (torch.float16, torch.bfloat16):
+        kc = torch.randn(6, 16, 4, 64, device=device).to(dtype)
+        vc = torch.randn(6, 16, 4, 64, device=device).to(dtype)
+        key = torch.randn(5, 4, 64, device=device).to(dtype)
+        value = torch.randn(5, 4, 64, device=device).to(dtype)
+        slots = torch.tensor([0, 17, -1, 95, 40], device=device, dtype=torch.int64)
+        exp_k, exp_v = c_oracle.reshape_and_cache(key.cpu(), value.cpu(), kc.cpu(), vc.cpu(),
+                                                  slots.cpu())
+        native.reshape_and_cache(key, value, kc, vc, slots)
+        torch.cuda.synchronize()
+        assert torch.equal(kc.cpu(), exp_k) and torch.equal(vc.cpu(), exp_v)
+
+
+def test_fp64_oracle_agrees_with_fp32_port_on_gpu_inputs(device):
+    # Cross-check of the two oracles on the data the kernels see.
+    b = make_paged_batch(3, 8, 2, 64, torch.float16, torch.tensor([7, 100, 333]), seed=13)
+    ref64 = c_oracle.paged_decode_f64(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
+                                      b.scale)
+    port = oracle_out(b).reshape(ref64.shape).numpy()
+    assert np.abs(port - ref64).max() <= 2e-3
