@@ -88,27 +88,23 @@ def measure_workload(name: str, spec: dict, device, steps: int, warmup: int) -> 
     base, pools = build_pools(spec, device)
     stream = torch.cuda.current_stream(device)
     out = torch.empty_like(base.q)
-    hkv, ps, btw = base.kv_heads, base.page_size, base.block_table.shape[1]
-    ns, cl = native.split_heuristic(base.batch, hkv, ps, btw, native.num_cus(device.index or 0))
+    ns = native.default_num_splits(base.q, base.k_cache, base.block_table)
 
     def call(kc, vc):
         native.paged_decode_split(base.q, kc, vc, base.block_table, base.cache_seqlens,
-                                  base.scale, out=out, num_splits=ns, chunk_len=cl)
+                                  base.scale, out=out, num_splits=ns)
 
     us_med, us_mean = time_calls(call, pools, steps, warmup, stream)
 
-    # Dominant kernel alone: the split partial (the whole call when ns == 1).
-    if ns > 1:
-        ws = torch.empty(native.workspace_size(base.batch, base.q_heads, base.head_dim, ns),
-                         dtype=torch.uint8, device=device)
+    # Dominant kernel alone: the split partial, same inputs and stream.
+    ws = torch.empty(native.workspace_size(base.batch, base.q_heads, base.head_dim, ns),
+                     dtype=torch.uint8, device=device)
 
-        def partial(kc, vc):
-            native.split_decode_partial(base.q, kc, vc, base.block_table, base.cache_seqlens,
-                                        base.scale, ws, ns, cl)
+    def partial(kc, vc):
+        native.split_decode_partial(base.q, kc, vc, base.block_table, base.cache_seqlens,
+                                    base.scale, out, ws, ns)
 
-        _, us_partial = time_calls(partial, pools, steps, warmup, stream)
-    else:
-        us_partial = us_mean
+    _, us_partial = time_calls(partial, pools, steps, warmup, stream)
     kv = base.kv_bytes()
     alg = base.algorithmic_bytes()
     gbs = kv / (us_med * 1e-6) / 1e9
@@ -120,7 +116,6 @@ def measure_workload(name: str, spec: dict, device, steps: int, warmup: int) -> 
         "kv_bytes": kv,
         "algorithmic_bytes": alg,
         "num_splits": ns,
-        "chunk_len": cl,
         "partial_kernel_us": round(us_partial, 3),
         "partial_kernel_gb_s": round(alg / (us_partial * 1e-6) / 1e9, 1),
         "rotation_copies": len(pools),
@@ -225,7 +220,6 @@ def main() -> int:
         "us_per_call": main_res["us_per_call"],
         "pct_hbm_peak": main_res["pct_hbm_peak"],
         "num_splits": main_res["num_splits"],
-        "chunk_len": main_res["chunk_len"],
         "roofline": {
             "bound": "hbm",
             "achieved": achieved,

@@ -9,6 +9,9 @@ namespace mxfa {
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf162_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 struct F16 {};
 struct BF16 {};
@@ -55,6 +58,7 @@ constexpr int kDppQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
 constexpr int kDppRowHalfMirror = 0x141;
 constexpr int kDppRowMirror = 0x140;
+constexpr int kDppRowNewBcast0 = 0x150;  // row_newbcast:n = 0x150 + n (lane n of each row)
 
 template <int Ctrl>
 __device__ __forceinline__ float dpp_f(float x) {

@@ -1,0 +1,152 @@
+"""Routes from the public API to the HIP split-KV decode (``mi355x_split_decode``).
+
+Each ``route_*`` function inspects a validated call and returns a
+``DecodeRoute``: ``reason`` names why the HIP path cannot take the call (then
+the dispatch chain continues), otherwise ``run`` launches it. Checks here read
+only shapes, dtypes and devices, never device data, so a qualifying call does
+not synchronise the stream.
+
+  flash_attn_with_kvcache  paged or dense cache, q_len 1, optional k/v append
+                           (append kernel, then decode over seqlens + S_new,
+                           then cache_seqlens += S_new on the device).
+  flash_attn_func          q_len 1: k/v [B, S, HKV, D] is a dense cache of S
+                           tokens per sequence.
+  flash_attn_varlen_func   every sequence has at most one query token: packed
+                           k/v are a cache of one-token pages whose block table
+                           row b is cu_seqlens_k[b] + arange(max_seqlen_k).
+
+A dense cache [B, S, HKV, D] is viewed as pages of P tokens, P the largest
+power of two dividing S (capped at 256), with block table row b =
+b * S/P + arange(S/P): the same bytes, no copy.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import native
+from .dispatch import DecodeRoute
+
+_ACCEL = {"cuda"}
+
+
+def _common_reason(q: torch.Tensor, kv_heads: int, head_dim: int) -> str | None:
+    if q.device.type not in _ACCEL:
+        return "requires_accelerator_tensor"
+    if q.dtype not in native.DTYPE_CODES:
+        return "supports_only_float16_and_bfloat16"
+    if head_dim not in native.SUPPORTED_HEAD_DIMS:
+        return f"head_dim_{head_dim}_not_in_{native.SUPPORTED_HEAD_DIMS}"
+    hq = q.shape[-2]
+    if kv_heads <= 0 or hq % kv_heads or hq // kv_heads not in native.SUPPORTED_GQA:
+        return f"gqa_ratio_{hq}/{kv_heads}_not_in_{native.SUPPORTED_GQA}"
+    return None
+
+
+def _dense_page_size(seq: int) -> int:
+    page = 1
+    while page < 256 and seq % (page * 2) == 0:
+        page *= 2
+    return page
+
+
+def _dense_as_pages(cache: torch.Tensor) -> torch.Tensor | None:
+    """[B, S, HKV, D] -> [B*S/P, P, HKV, D] view, or None when not viewable."""
+    b, s = cache.shape[0], cache.shape[1]
+    page = _dense_page_size(s)
+    try:
+        return cache.view(b * (s // page), page, cache.shape[2], cache.shape[3])
+    except RuntimeError:
+        return None
+
+
+def _dense_table(batch: int, pages_per_seq: int, device: torch.device) -> torch.Tensor:
+    base = torch.arange(batch, device=device, dtype=torch.int32).unsqueeze(1) * pages_per_seq
+    return base + torch.arange(pages_per_seq, device=device, dtype=torch.int32).unsqueeze(0)
+
+
+def route_kvcache(q, k_cache, v_cache, k, v, cache_seqlens, block_table, scale,
+                  causal) -> DecodeRoute:
+    reason = _common_reason(q, k_cache.shape[2], q.shape[-1])
+    if reason is not None:
+        return DecodeRoute(reason)
+    if q.shape[1] != 1:
+        return DecodeRoute(f"query_length_{q.shape[1]}_is_not_single_token_decode")
+    if k_cache.stride(-1) != 1 or v_cache.stride() != k_cache.stride():
+        return DecodeRoute("cache_layout_not_supported")
+    if block_table is None:
+        kc, vc = _dense_as_pages(k_cache), _dense_as_pages(v_cache)
+        if kc is None or vc is None:
+            return DecodeRoute("dense_cache_not_viewable_as_pages")
+    else:
+        ps = k_cache.shape[1]
+        if ps & (ps - 1) or ps > 4096:
+            return DecodeRoute(f"page_size_{ps}_not_a_power_of_two_up_to_4096")
+        kc, vc = k_cache, v_cache
+    if k is not None and (k.stride(-1) != 1 or v.stride(-1) != 1):
+        k, v = k.contiguous(), v.contiguous()
+
+    def run() -> torch.Tensor:
+        if block_table is None:
+            table = _dense_table(q.shape[0], kc.shape[0] // q.shape[0], q.device)
+        else:
+            table = block_table
+        new = 0 if k is None else k.shape[1]
+        if new:
+            native.append_kv(k, v, kc, vc, table, cache_seqlens)
+        out = native.paged_decode_split(q, kc, vc, table, cache_seqlens, scale, seqlen_add=new)
+        if new:
+            cache_seqlens.add_(new)
+        return out
+
+    return DecodeRoute(None, run)
+
+
+def route_dense(q, k, v, scale, causal) -> DecodeRoute:
+    reason = _common_reason(q, k.shape[2], q.shape[-1])
+    if reason is not None:
+        return DecodeRoute(reason)
+    if q.shape[1] != 1:
+        return DecodeRoute(f"query_length_{q.shape[1]}_is_not_single_token_decode")
+    kc, vc = _dense_as_pages(k), _dense_as_pages(v)
+    if kc is None or vc is None or kc.stride(-1) != 1 or vc.stride() != kc.stride():
+        return DecodeRoute("dense_kv_not_viewable_as_pages")
+
+    def run() -> torch.Tensor:
+        batch = q.shape[0]
+        table = _dense_table(batch, kc.shape[0] // batch, q.device)
+        lengths = torch.full((batch,), k.shape[1], dtype=torch.int32, device=q.device)
+        return native.paged_decode_split(q, kc, vc, table, lengths, scale)
+
+    return DecodeRoute(None, run)
+
+
+def route_varlen(q, k, v, q_offsets: list[int], k_offsets: list[int], max_seqlen_k: int, scale,
+                 causal) -> DecodeRoute:
+    reason = _common_reason(q, k.shape[1], q.shape[-1])
+    if reason is not None:
+        return DecodeRoute(reason)
+    q_lens = [b - a for a, b in zip(q_offsets, q_offsets[1:])]
+    if any(n > 1 for n in q_lens):
+        return DecodeRoute("varlen_query_length_above_one")
+    if k.stride(-1) != 1 or v.stride() != k.stride():
+        return DecodeRoute("kv_layout_not_supported")
+    # Sequences with a query row, in row order.
+    rows = [i for i, n in enumerate(q_lens) if n == 1]
+
+    def run() -> torch.Tensor:
+        device = q.device
+        starts = torch.tensor([k_offsets[i] for i in rows], dtype=torch.int32, device=device)
+        lengths = torch.tensor([k_offsets[i + 1] - k_offsets[i] for i in rows],
+                               dtype=torch.int32, device=device)
+        width = max(1, max_seqlen_k)
+        table = starts.unsqueeze(1) + torch.arange(width, dtype=torch.int32,
+                                                   device=device).unsqueeze(0)
+        kc = k.unsqueeze(1)  # [T, 1, HKV, D]: one token per page
+        vc = v.unsqueeze(1)
+        out = native.paged_decode_split(q.unsqueeze(1), kc, vc, table, lengths, scale)
+        return out.squeeze(1)
+
+    if not rows:
+        return DecodeRoute("varlen_without_query_rows")
+    return DecodeRoute(None, run)

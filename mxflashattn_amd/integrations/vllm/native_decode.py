@@ -1,0 +1,137 @@
+"""Decode routing inside vLLM's attention call, independent of vLLM itself.
+
+``try_native_decode`` replaces the reference's ``_try_native_decode``
+(integrations/vllm/vllm_plugin.py:199-317): behind MXFA_NATIVE_DECODE=1 it
+sends single-token paged decode straight to the HIP split-KV kernels.
+Unsupported calls are handed back (return None) by explicit guards, with no
+exception on the hot path: no block table or lengths, alibi, a positive
+window, a dtype other than fp16/bf16 or different from the cache's, q_len > 1,
+head dim outside {64, 128}, GQA ratio outside {2, 4, 8}, or a page size that is
+not a power of two. The caller then runs the original implementation.
+
+``mx_kvcache_compat`` replaces ``_mx_kvcache_compat`` (:319-349): it drops
+vLLM-only keyword arguments, tries the native route, else the original vendor
+function, else the public API. ``reshape_and_cache_flash`` is the cache write
+with vLLM's signature, on the HIP append kernel.
+"""
+
+from __future__ import annotations
+
+import os
+from typing import Any, Callable
+
+import torch
+
+from ... import api, native
+from .backend import record_event
+
+# Set by the vLLM plugin around a forward call: the vendor function the
+# compat wrapper hands unsupported calls back to.
+official_kvcache: Callable[..., Any] | None = None
+
+_VLLM_ONLY_KWARGS = ("s_aux", "return_softmax_lse", "scheduler_metadata", "fa_version",
+                     "q_descale", "k_descale", "v_descale")
+
+
+def _guard(args: tuple, kwargs: dict) -> tuple[str | None, tuple]:
+    """(reason, (q, k_cache, v_cache, block_table, seqlens)); reason None = take it."""
+    q = args[0] if args else kwargs.get("q")
+    if q is None or q.dim() not in (3, 4):
+        return "query_rank", ()
+    bt = kwargs.get("block_table")
+    sl = kwargs.get("cache_seqlens")
+    if bt is None or sl is None or sl.shape[0] != q.shape[0]:
+        return "block_table_or_seqlens", ()
+    if kwargs.get("alibi_slopes") is not None:
+        return "alibi", ()
+    window = kwargs.get("window_size")
+    if window is not None:
+        # (-1, -1) or -1 means no sliding window; a positive size needs masking.
+        try:
+            values = window if isinstance(window, (tuple, list)) else (window,)
+            if any(int(x) > 0 for x in values):
+                return "window", ()
+        except (TypeError, ValueError):
+            return "window", ()
+    k_cache = kwargs.get("k_cache", args[1] if len(args) > 1 else None)
+    v_cache = kwargs.get("v_cache", args[2] if len(args) > 2 else None)
+    if k_cache is None or v_cache is None:
+        return "caches", ()
+    if q.dtype not in native.DTYPE_CODES or k_cache.dtype != q.dtype:
+        return "dtype", ()
+    if q.dim() == 4 and q.shape[1] != 1:
+        return "query_length", ()
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        return "cache_rank", ()
+    hd, hq, hkv = q.shape[-1], q.shape[-2], k_cache.shape[2]
+    if hd not in native.SUPPORTED_HEAD_DIMS or k_cache.shape[3] != hd:
+        return "head_dim", ()
+    if hkv <= 0 or hq % hkv or hq // hkv not in native.SUPPORTED_GQA:
+        return "gqa_ratio", ()
+    ps = k_cache.shape[1]
+    if ps <= 0 or ps & (ps - 1) or ps > 4096:
+        return "page_size", ()
+    if q.device.type != "cuda":
+        return "device", ()
+    return None, (q, k_cache, v_cache, bt, sl)
+
+
+def try_native_decode(args: tuple, kwargs: dict) -> torch.Tensor | None:
+    """HIP decode of a vLLM flash_attn_with_kvcache call, or None to hand it back."""
+    if os.getenv("MXFA_NATIVE_DECODE", "0") != "1":
+        return None
+    reason, picked = _guard(args, kwargs)
+    if reason is not None:
+        record_event({"path": "native_decode", "fallback": "true",
+                      "fallback_reason": f"guard:{reason}"})
+        return None
+    q, k_cache, v_cache, bt, sl = picked
+    hq, hd = q.shape[-2], q.shape[-1]
+    scale = kwargs.get("softmax_scale") or hd ** -0.5
+    # vLLM passes q as [T, HQ, D] or [B, 1, HQ, D], possibly a strided slice of
+    # the fused QKV buffer: the kernel takes the strides as they are.
+    q4 = q.reshape(q.shape[0], 1, hq, hd) if q.dim() == 3 else q
+    provided = kwargs.get("out")
+    out = None
+    if provided is not None and provided.numel() == q4.numel() and provided.dtype == q.dtype:
+        view = provided.view(q4.shape) if provided.is_contiguous() else None
+        if view is not None:
+            out = view
+    ns = native.default_num_splits(q4, k_cache, bt)
+    result = native.paged_decode_split(q4, k_cache, v_cache, bt, sl, scale, out=out,
+                                       num_splits=ns)
+    if provided is not None and out is None:
+        provided.copy_(result.reshape_as(provided))
+        result = provided
+    elif provided is not None:
+        result = provided
+    else:
+        result = result.reshape(q.shape)
+    record_event({"path": "mi355x_split_decode", "operation": "paged_decode_split",
+                  "fallback": "false", "np": str(ns)})
+    return result
+
+
+def mx_kvcache_compat(*args, **kwargs):
+    """Stand-in for vLLM's flash_attn_with_kvcache inside its attention forward."""
+    for name in _VLLM_ONLY_KWARGS:
+        kwargs.pop(name, None)
+    result = try_native_decode(args, kwargs)
+    if result is not None:
+        return result
+    # Shapes the public API rejects must reach the original implementation
+    # instead of raising inside vLLM.
+    if official_kvcache is not None:
+        return official_kvcache(*args, **kwargs)
+    return api.flash_attn_with_kvcache(*args, **kwargs)
+
+
+def reshape_and_cache_flash(key: torch.Tensor, value: torch.Tensor, key_cache: torch.Tensor,
+                            value_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                            kv_cache_dtype: str = "auto", k_scale: Any = None,
+                            v_scale: Any = None) -> None:
+    """vLLM cache write (slot t -> page slot // PS, row slot % PS; slot < 0 skipped)."""
+    if kv_cache_dtype not in ("auto", None):
+        raise NotImplementedError(f"kv_cache_dtype {kv_cache_dtype!r} is not supported")
+    n = slot_mapping.shape[0]
+    native.reshape_and_cache(key[:n], value[:n], key_cache, value_cache, slot_mapping)

@@ -1,0 +1,113 @@
+"""vLLM attention backend classes (needs vLLM; import fails cleanly without it).
+
+Structure of integrations/vllm/vllm_plugin.py:351-511 of the reference:
+``MXFlashAttnImpl`` keeps vLLM's own FlashAttention metadata split and output
+write-back and swaps only the attention calls. With
+MXFLASHATTN_GRAPH_OFFICIAL_SPLIT=1 the implementation's module-level
+``flash_attn_with_kvcache`` is replaced by ``native_decode.mx_kvcache_compat``
+for the duration of the forward call (restored in ``finally``); an "invalid
+argument" failure is retried once with the untouched functions. Otherwise the
+forward runs ``decode_forward`` (public API) and falls back to vLLM for prefill.
+The KV-cache update uses the HIP append kernel (``reshape_and_cache_flash``).
+Classes live at module scope because vLLM resolves the backend by import path
+in its worker processes.
+"""
+
+from __future__ import annotations
+
+import os
+
+from vllm.v1.attention.backends.flash_attn import (  # noqa: F401  (requires vLLM)
+    FlashAttentionBackend,
+    FlashAttentionImpl,
+)
+
+from ...dispatch import get_last_dispatch_info
+from . import native_decode
+from .backend import record_event
+from .decoder_adapter import DecoderAdapterBlocked, decode_forward
+
+
+def _forward_official_split(impl, layer, query, key, value, kv_cache, metadata, output,
+                            output_scale, output_block_scale):
+    fn = FlashAttentionImpl.forward
+    glb = fn.__globals__
+    old_kv = glb.get("flash_attn_with_kvcache")
+    native_decode.official_kvcache = old_kv
+    glb["flash_attn_with_kvcache"] = native_decode.mx_kvcache_compat
+    event = {"path": "vendor_direct", "operation": "official_split_mx", "fallback": "false"}
+    try:
+        try:
+            result = super(MXFlashAttnImpl, impl).forward(
+                layer, query, key, value, kv_cache, metadata, output, output_scale,
+                output_block_scale)
+        except Exception as exc:
+            if "invalid argument" not in str(exc).lower():
+                raise
+            glb["flash_attn_with_kvcache"] = old_kv
+            result = super(MXFlashAttnImpl, impl).forward(
+                layer, query, key, value, kv_cache, metadata, output, output_scale,
+                output_block_scale)
+            event = {"path": "vendor_direct",
+                     "operation": "official_split_invalid_argument_fallback",
+                     "fallback": "true", "fallback_reason": "official_split_invalid_argument"}
+    finally:
+        glb["flash_attn_with_kvcache"] = old_kv
+        native_decode.official_kvcache = None
+    record_event(event)
+    return result
+
+
+class MXFlashAttnImpl(FlashAttentionImpl):
+    def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None,
+                output_scale=None, output_block_scale=None):
+        if attn_metadata is None:
+            if output is None:
+                raise ValueError("vLLM must provide an output buffer for profiling")
+            return output.fill_(0)
+        if os.getenv("MXFLASHATTN_SPLIT_PURE", "0") == "1":
+            return super().forward(layer, query, key, value, kv_cache, attn_metadata, output,
+                                   output_scale, output_block_scale)
+        if os.getenv("MXFLASHATTN_GRAPH_OFFICIAL_SPLIT", "0") == "1":
+            return _forward_official_split(self, layer, query, key, value, kv_cache,
+                                           attn_metadata, output, output_scale,
+                                           output_block_scale)
+        try:
+            result, _ = decode_forward(query, kv_cache, attn_metadata, softmax_scale=self.scale,
+                                       causal=bool(attn_metadata.causal))
+        except DecoderAdapterBlocked as exc:
+            record_event({"path": "vendor_prefill_or_blocked", "reason": str(exc)})
+            if "single_token_decode" in str(exc):
+                return super().forward(layer, query, key, value, kv_cache, attn_metadata,
+                                       output, output_scale, output_block_scale)
+            raise
+        info = get_last_dispatch_info()
+        if info is None:
+            raise RuntimeError("MXFlashAttn decoder returned without dispatch evidence")
+        record_event({"path": info.backend, "operation": info.operation,
+                      "fallback": "false" if info.fallback_reason is None else "true"})
+        if output is None:
+            raise ValueError("vLLM must provide an output buffer")
+        target = output[: result.shape[0]]
+        if target.numel() != result.numel():
+            raise RuntimeError(
+                f"MXFlashAttn decoder output size mismatch: target={tuple(target.shape)} "
+                f"result={tuple(result.shape)}")
+        target.copy_(result.reshape_as(target))
+        return output
+
+    def do_kv_cache_update(self, layer, key, value, kv_cache, slot_mapping):
+        key_cache, value_cache = kv_cache.unbind(0)
+        native_decode.reshape_and_cache_flash(key, value, key_cache, value_cache, slot_mapping,
+                                              self.kv_cache_dtype)
+
+
+class MXFlashAttnBackend(FlashAttentionBackend):
+    @staticmethod
+    def get_name() -> str:
+        # vLLM indexes its backend enum by this name.
+        return "FLASH_ATTN"
+
+    @staticmethod
+    def get_impl_cls():
+        return MXFlashAttnImpl

@@ -13,12 +13,17 @@ from __future__ import annotations
 
 import ctypes
 import functools
+import os
 import threading
 from pathlib import Path
 
 import torch
 
-LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmxfa_mi355x.so"
+# MXFLASHATTN_AMD_LIB points the binding at another build of the same C ABI.
+LIB_PATH = Path(
+    os.environ.get("MXFLASHATTN_AMD_LIB")
+    or Path(__file__).resolve().parent / "_lib" / "libmxfa_mi355x.so"
+)
 ABI_VERSION = 1
 
 MXFA_OK = 0
@@ -63,21 +68,21 @@ _sz = ctypes.c_size_t
 _SIGNATURES = {
     "mxfa_abi_version": (_i, []),
     "mxfa_strerror": (ctypes.c_char_p, [_i]),
-    "mxfa_split_heuristic": (_i, [_i, _i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
+    "mxfa_split_heuristic": (_i, [_i, _i, _i, _i, _i, _i, _i, ctypes.POINTER(_i)]),
     "mxfa_split_decode_workspace_size": (_i, [_i, _i, _i, _i, ctypes.POINTER(_sz)]),
     "mxfa_split_decode_launch": (
         _i,
         [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _p, _i64, _i64, _p, _sz,
-         _f, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _p],
+         _f, _i, _i, _i, _i, _i, _i, _i, _i, _i, _p],
     ),
     "mxfa_split_decode_partial_launch": (
         _i,
-        [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _p, _sz, _f, _i, _i, _i,
-         _i, _i, _i, _i, _i, _i, _i, _p],
+        [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _p, _i64, _i64, _p, _sz,
+         _f, _i, _i, _i, _i, _i, _i, _i, _i, _i, _p],
     ),
     "mxfa_split_decode_combine_launch": (
         _i,
-        [_p, _sz, _p, _i, _p, _i64, _i64, _i, _i, _i, _i, _i, _i, _p],
+        [_p, _sz, _p, _i64, _i64, _i, _i, _i, _i, _i, _p],
     ),
     "mxfa_reshape_and_cache_launch": (
         _i,
@@ -145,16 +150,16 @@ def _check(rc: int, what: str) -> None:
 
 
 @functools.lru_cache(maxsize=256)
-def split_heuristic(batch: int, kv_heads: int, page_size: int, block_table_width: int,
-                    num_cus: int) -> tuple[int, int]:
-    """(num_splits, chunk_len) for a launch; integer-only, no device access."""
-    ns, cl = _i(), _i()
+def split_heuristic(batch: int, q_heads: int, kv_heads: int, head_dim: int, page_size: int,
+                    block_table_width: int, num_cus: int) -> int:
+    """Balanced ranges per kv head for a launch; integer-only, no device access."""
+    ns = _i()
     _check(
-        library().mxfa_split_heuristic(batch, kv_heads, page_size, block_table_width, num_cus,
-                                       ctypes.byref(ns), ctypes.byref(cl)),
+        library().mxfa_split_heuristic(batch, q_heads, kv_heads, head_dim, page_size,
+                                       block_table_width, num_cus, ctypes.byref(ns)),
         "mxfa_split_heuristic",
     )
-    return ns.value, cl.value
+    return ns.value
 
 
 def workspace_size(batch: int, q_heads: int, head_dim: int, num_splits: int) -> int:
@@ -238,30 +243,23 @@ def check_decode_shapes(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
         raise UnsupportedConfig(f"page size {ps} is not a power of two <= 4096")
 
 
-def paged_decode_split(
-    q: torch.Tensor,
-    k_cache: torch.Tensor,
-    v_cache: torch.Tensor,
-    block_table: torch.Tensor,
-    cache_seqlens: torch.Tensor,
-    softmax_scale: float,
-    *,
-    out: torch.Tensor | None = None,
-    num_splits: int | None = None,
-    chunk_len: int | None = None,
-    seqlen_add: int = 0,
-) -> torch.Tensor:
-    """Split-KV paged decode on the current stream; returns ``out`` shaped like q.
-
-    q: [B, 1, HQ, HD] or [B, HQ, HD] (any strides with a contiguous last dim);
-    caches: [pages, PS, HKV, HD]; block_table: int32 [B, W]; cache_seqlens: int32 [B].
-    The attended length of sequence b is cache_seqlens[b] + seqlen_add.
-    """
-    check_decode_shapes(q, k_cache, v_cache)
-    lib = library()
-    device = q.device
+def _launch_args(q, k_cache, v_cache, block_table, cache_seqlens, out, workspace, ws_bytes,
+                 softmax_scale, num_splits, seqlen_add):
     batch, hq, hd = q.shape[0], q.shape[-2], q.shape[-1]
     pages, ps, hkv = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
+    qs, os_, cs = q.stride(), out.stride(), k_cache.stride()
+    return (
+        q.data_ptr(), qs[0], qs[-2], k_cache.data_ptr(), v_cache.data_ptr(), cs[0], cs[1], cs[2],
+        block_table.data_ptr(), block_table.stride(0), cache_seqlens.data_ptr(), seqlen_add,
+        out.data_ptr(), os_[0], os_[-2], workspace, ws_bytes, float(softmax_scale), batch, hq,
+        hkv, hd, ps, block_table.shape[1], pages, DTYPE_CODES[q.dtype], num_splits,
+        _stream_handle(q.device),
+    )
+
+
+def _prepare(q, k_cache, v_cache, block_table, cache_seqlens, out):
+    check_decode_shapes(q, k_cache, v_cache)
+    batch = q.shape[0]
     if q.stride(-1) != 1:
         q = q.contiguous()
     if k_cache.stride(-1) != 1 or v_cache.stride() != k_cache.stride():
@@ -272,27 +270,48 @@ def paged_decode_split(
         raise ValueError("block_table must be [batch, width]")
     if cache_seqlens.numel() != batch:
         raise ValueError("cache_seqlens must have one entry per sequence")
-    btw = block_table.shape[1]
     if out is None:
-        out = torch.empty(q.shape, dtype=q.dtype, device=device)
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     if out.shape != q.shape or out.dtype != q.dtype or out.stride(-1) != 1:
         raise ValueError("out must match q's shape and dtype with a contiguous last dim")
-    if num_splits is None or chunk_len is None:
-        num_splits, chunk_len = split_heuristic(batch, hkv, ps, btw, num_cus(device.index or 0))
-    stream = _stream_handle(device)
-    ws_bytes = workspace_size(batch, hq, hd, num_splits)
-    ws_ptr = 0
-    if ws_bytes:
-        ws_ptr = WORKSPACE.get(device, stream, ws_bytes).data_ptr()
-    qs = q.stride()
-    os_ = out.stride()
-    cs = k_cache.stride()
-    rc = lib.mxfa_split_decode_launch(
-        q.data_ptr(), qs[0], qs[-2], k_cache.data_ptr(), v_cache.data_ptr(), cs[0], cs[1], cs[2],
-        block_table.data_ptr(), block_table.stride(0), cache_seqlens.data_ptr(), seqlen_add,
-        out.data_ptr(), os_[0], os_[-2], ws_ptr, ws_bytes, float(softmax_scale), batch, hq, hkv,
-        hd, ps, btw, pages, DTYPE_CODES[q.dtype], num_splits, chunk_len, stream,
-    )
+    return q, block_table, cache_seqlens, out
+
+
+def default_num_splits(q: torch.Tensor, k_cache: torch.Tensor, block_table: torch.Tensor) -> int:
+    return split_heuristic(q.shape[0], q.shape[-2], k_cache.shape[2], q.shape[-1],
+                           k_cache.shape[1], block_table.shape[1], num_cus(q.device.index or 0))
+
+
+def paged_decode_split(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    cache_seqlens: torch.Tensor,
+    softmax_scale: float,
+    *,
+    out: torch.Tensor | None = None,
+    num_splits: int | None = None,
+    seqlen_add: int = 0,
+) -> torch.Tensor:
+    """Split-KV paged decode on the current stream; returns ``out`` shaped like q.
+
+    q: [B, 1, HQ, HD] or [B, HQ, HD] (any strides with a contiguous last dim);
+    caches: [pages, PS, HKV, HD]; block_table: int32 [B, W]; cache_seqlens: int32 [B].
+    The attended length of sequence b is cache_seqlens[b] + seqlen_add.
+    num_splits: balanced work ranges per kv head (default: split_heuristic).
+    """
+    q, block_table, cache_seqlens, out = _prepare(q, k_cache, v_cache, block_table,
+                                                  cache_seqlens, out)
+    lib = library()
+    if num_splits is None:
+        num_splits = default_num_splits(q, k_cache, block_table)
+    stream = _stream_handle(q.device)
+    ws_bytes = workspace_size(q.shape[0], q.shape[-2], q.shape[-1], num_splits)
+    ws = WORKSPACE.get(q.device, stream, ws_bytes)
+    rc = lib.mxfa_split_decode_launch(*_launch_args(q, k_cache, v_cache, block_table,
+                                                    cache_seqlens, out, ws.data_ptr(), ws_bytes,
+                                                    softmax_scale, num_splits, seqlen_add))
     _check(rc, "mxfa_split_decode_launch")
     return out
 
@@ -304,48 +323,29 @@ def split_decode_partial(
     block_table: torch.Tensor,
     cache_seqlens: torch.Tensor,
     softmax_scale: float,
+    out: torch.Tensor,
     workspace: torch.Tensor,
     num_splits: int,
-    chunk_len: int,
     seqlen_add: int = 0,
 ) -> None:
-    """Partial stage only: per-split normalised outputs and base-2 LSEs into ``workspace``.
-
-    ``workspace`` must hold at least ``workspace_size(B, HQ, HD, num_splits)`` bytes;
-    ``split_decode_combine`` finishes the computation. Inputs as for paged_decode_split.
-    """
-    check_decode_shapes(q, k_cache, v_cache)
-    batch, hq, hd = q.shape[0], q.shape[-2], q.shape[-1]
-    pages, ps, hkv = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
-    block_table = _int32_contig(block_table, "block_table")
-    cache_seqlens = _int32_contig(cache_seqlens, "cache_seqlens")
-    qs, cs = q.stride(), k_cache.stride()
+    """Partial stage only (sequences inside one range land in ``out``, pieces in
+    ``workspace``); ``split_decode_combine`` finishes the call."""
+    q, block_table, cache_seqlens, out = _prepare(q, k_cache, v_cache, block_table,
+                                                  cache_seqlens, out)
+    nbytes = workspace.numel() * workspace.element_size()
     rc = library().mxfa_split_decode_partial_launch(
-        q.data_ptr(), qs[0], qs[-2], k_cache.data_ptr(), v_cache.data_ptr(), cs[0], cs[1], cs[2],
-        block_table.data_ptr(), block_table.stride(0), cache_seqlens.data_ptr(), seqlen_add,
-        workspace.data_ptr(), workspace.numel() * workspace.element_size(), float(softmax_scale),
-        batch, hq, hkv, hd, ps, block_table.shape[1], pages, DTYPE_CODES[q.dtype], num_splits,
-        chunk_len, _stream_handle(q.device),
-    )
+        *_launch_args(q, k_cache, v_cache, block_table, cache_seqlens, out, workspace.data_ptr(),
+                      nbytes, softmax_scale, num_splits, seqlen_add))
     _check(rc, "mxfa_split_decode_partial_launch")
 
 
-def split_decode_combine(
-    workspace: torch.Tensor,
-    cache_seqlens: torch.Tensor,
-    out: torch.Tensor,
-    num_splits: int,
-    chunk_len: int,
-    seqlen_add: int = 0,
-) -> torch.Tensor:
-    """LSE merge of the partials in ``workspace`` into ``out`` ([B,1,HQ,HD] or [B,HQ,HD])."""
-    cache_seqlens = _int32_contig(cache_seqlens, "cache_seqlens")
+def split_decode_combine(workspace: torch.Tensor, out: torch.Tensor, num_splits: int) -> torch.Tensor:
+    """LSE merge of the pieces in ``workspace`` into ``out`` ([B,1,HQ,HD] or [B,HQ,HD])."""
     batch, hq, hd = out.shape[0], out.shape[-2], out.shape[-1]
     os_ = out.stride()
     rc = library().mxfa_split_decode_combine_launch(
-        workspace.data_ptr(), workspace.numel() * workspace.element_size(),
-        cache_seqlens.data_ptr(), seqlen_add, out.data_ptr(), os_[0], os_[-2], batch, hq, hd,
-        _dtype_code(out), num_splits, chunk_len, _stream_handle(out.device),
+        workspace.data_ptr(), workspace.numel() * workspace.element_size(), out.data_ptr(),
+        os_[0], os_[-2], batch, hq, hd, _dtype_code(out), num_splits, _stream_handle(out.device),
     )
     _check(rc, "mxfa_split_decode_combine_launch")
     return out

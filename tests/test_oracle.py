@@ -1,0 +1,318 @@
+"""Pins of the CPU oracle (oracle/) before it is trusted as the parity checker.
+
+The reference ships no golden vectors for this path (its kernel tests compare
+against the closed MetaX wheel on a C500). Each oracle function is pinned by
+checks that a plausible mistake would fail:
+
+  reference_port.attention_kvcache / attention_single
+    - paged read order through block table [1, 0] equals attention over the
+      manually gathered rows (reference tests/test_api.py:136-155)
+    - append writes the new row into page table[b][pos // PS], row pos % PS,
+      and advances cache_seqlens (tests/test_api.py:158-197, tests/test_c500.py:84-126)
+    - one key: output is the V row exactly (csrc_native/debug_m1.py:25-28)
+    - scale 0: output is the mean of the V rows
+    - causal with q longer than k: zeros, then V (tests/test_api.py:52-62)
+    - agreement with torch's scaled_dot_product_attention (a library routine)
+      on independently gathered K/V, per query head against kv head h // GQ
+    - GQA mapping: kv heads with constant, distinct V rows give every query head
+      exactly its group's constant
+  c_oracle.paged_decode_f64
+    - agreement with reference_port (fp32) and with a float64 SDPA
+    - a peaked query (q = 40 * k_j) returns V_j
+    - permuting physical pages together with the block table changes nothing
+  c_oracle.append_kv / reshape_and_cache
+    - bitwise against torch index assignment; slot < 0 and positions beyond
+      the table are skipped
+  split_model
+    - the LSE merge of any split of the keys, empty splits included, equals
+      unsplit attention (the invariant behind csrc_native/m1_kernel.cpp:861-888)
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from mxflashattn_amd.workloads import make_paged_batch
+from oracle import c_oracle, reference_port, split_model
+
+
+def gather_dense(cache: torch.Tensor, table_row: list[int], length: int) -> torch.Tensor:
+    """Rows 0..length-1 of a paged sequence by explicit per-token indexing."""
+    ps = cache.shape[1]
+    return torch.stack([cache[table_row[t // ps], t % ps] for t in range(length)])
+
+
+def sdpa_reference(q_row: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
+                   scale: float) -> torch.Tensor:
+    """Library attention for one query token: q_row [HQ, D], keys/values [L, HKV, D]."""
+    hq, hkv = q_row.shape[0], keys.shape[1]
+    group = hq // hkv
+    outs = []
+    for h in range(hq):
+        qh = q_row[h].double().view(1, 1, 1, -1)
+        kh = keys[:, h // group].double().unsqueeze(0).unsqueeze(0)
+        vh = values[:, h // group].double().unsqueeze(0).unsqueeze(0)
+        outs.append(F.scaled_dot_product_attention(qh, kh, vh, scale=scale).view(-1))
+    return torch.stack(outs)
+
+
+def test_paged_read_order_matches_manual_gather():
+    torch.manual_seed(0)
+    q = torch.randn(1, 1, 2, 64)
+    k_cache = torch.randn(2, 2, 1, 64)
+    v_cache = torch.randn_like(k_cache)
+    table = torch.tensor([[1, 0]], dtype=torch.int32)
+    seqlens = torch.tensor([3], dtype=torch.int32)
+    out = reference_port.attention_kvcache(q, k_cache, v_cache, cache_seqlens=seqlens,
+                                           block_table=table)
+    keys = torch.cat((k_cache[1], k_cache[0, :1]), dim=0)
+    values = torch.cat((v_cache[1], v_cache[0, :1]), dim=0)
+    expected = reference_port.attention_single(q[0], keys, values)
+    torch.testing.assert_close(out[0], expected)
+    lib = sdpa_reference(q[0, 0], keys, values, 64 ** -0.5)
+    torch.testing.assert_close(out[0, 0].double(), lib, atol=1e-5, rtol=1e-5)
+
+
+def test_paged_append_writes_slot_and_advances_lengths():
+    torch.manual_seed(1)
+    q = torch.randn(1, 1, 2, 64)
+    k_new = torch.randn(1, 1, 1, 64)
+    v_new = torch.randn(1, 1, 1, 64)
+    k_cache = torch.zeros(2, 2, 1, 64)
+    v_cache = torch.zeros_like(k_cache)
+    k_cache[0] = torch.randn_like(k_cache[0])
+    v_cache[0] = torch.randn_like(v_cache[0])
+    seqlens = torch.tensor([2], dtype=torch.int32)
+    out = reference_port.attention_kvcache(q, k_cache, v_cache, cache_seqlens=seqlens,
+                                           block_table=torch.tensor([[0, 1]], dtype=torch.int32),
+                                           k=k_new, v=v_new)
+    assert out.shape == q.shape
+    assert seqlens.tolist() == [3]
+    assert torch.equal(k_cache[1, 0], k_new[0, 0])
+    assert torch.equal(v_cache[1, 0], v_new[0, 0])
+    assert torch.equal(k_cache[1, 1], torch.zeros(1, 64))
+
+
+def test_dense_append_writes_row_and_advances_lengths():
+    torch.manual_seed(2)
+    q = torch.randn(1, 1, 2, 64)
+    k_new, v_new = torch.randn(1, 1, 1, 64), torch.randn(1, 1, 1, 64)
+    k_cache = torch.zeros(1, 4, 1, 64)
+    v_cache = torch.zeros_like(k_cache)
+    seqlens = torch.tensor([2], dtype=torch.int32)
+    reference_port.attention_kvcache(q, k_cache, v_cache, cache_seqlens=seqlens, block_table=None,
+                                     k=k_new, v=v_new)
+    assert seqlens.tolist() == [3]
+    assert torch.equal(k_cache[0, 2], k_new[0, 0]) and torch.equal(v_cache[0, 2], v_new[0, 0])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_single_key_returns_v_row_exactly(dtype):
+    b = make_paged_batch(3, 8, 2, 128, dtype, 1, seed=3)
+    out = reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache,
+                                           cache_seqlens=b.cache_seqlens.clone(),
+                                           block_table=b.block_table)
+    for i in range(3):
+        page = int(b.block_table[i, 0])
+        for h in range(8):
+            assert torch.equal(out[i, 0, h], b.v_cache[page, 0, h // 4])
+    f64 = c_oracle.paged_decode_f64(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
+                                    b.scale)
+    for i in range(3):
+        page = int(b.block_table[i, 0])
+        for h in range(8):
+            assert np.array_equal(f64[i, h], b.v_cache[page, 0, h // 4].double().numpy())
+
+
+def test_zero_scale_is_the_mean_of_v():
+    b = make_paged_batch(2, 4, 2, 64, torch.float32, torch.tensor([5, 37]), seed=4)
+    out = reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache,
+                                           cache_seqlens=b.cache_seqlens.clone(),
+                                           block_table=b.block_table, softmax_scale=0.0)
+    for i, n in enumerate([5, 37]):
+        rows = gather_dense(b.v_cache, b.block_table[i].tolist(), n)
+        mean = rows.double().mean(dim=0)
+        for h in range(4):
+            assert torch.allclose(out[i, 0, h].double(), mean[h // 2], atol=1e-6)
+
+
+def test_causal_query_longer_than_key_gives_zeros_then_v():
+    q = torch.randn(1, 3, 2, 64)
+    k = torch.randn(1, 1, 1, 64)
+    v = torch.randn_like(k)
+    out = reference_port.attention_batched(q, k, v, causal=True)
+    assert torch.isfinite(out).all()
+    torch.testing.assert_close(out[:, :2], torch.zeros_like(out[:, :2]))
+    torch.testing.assert_close(out[:, 2:], v.expand(-1, -1, 2, -1))
+
+
+def test_causal_is_a_no_op_for_one_query_token():
+    b = make_paged_batch(2, 8, 2, 64, torch.float32, torch.tensor([9, 40]), seed=5)
+    args = dict(cache_seqlens=b.cache_seqlens, block_table=b.block_table)
+    plain = reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache, **args)
+    causal = reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache, causal=True, **args)
+    torch.testing.assert_close(plain, causal)
+
+
+@pytest.mark.parametrize("gq,hd", [(2, 64), (4, 128), (8, 64)])
+def test_port_matches_library_attention_on_gathered_rows(gq, hd):
+    lengths = torch.tensor([1, 16, 33, 200])
+    b = make_paged_batch(4, 2 * gq, 2, hd, torch.float32, lengths, seed=6)
+    out = reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache,
+                                           cache_seqlens=b.cache_seqlens.clone(),
+                                           block_table=b.block_table)
+    for i, n in enumerate(lengths.tolist()):
+        row = b.block_table[i].tolist()
+        lib = sdpa_reference(b.q[i, 0], gather_dense(b.k_cache, row, n),
+                             gather_dense(b.v_cache, row, n), b.scale)
+        torch.testing.assert_close(out[i, 0].double(), lib, atol=2e-5, rtol=1e-5)
+
+
+def test_gqa_mapping_with_constant_v_per_kv_head():
+    hq, hkv, hd = 8, 2, 64
+    b = make_paged_batch(2, hq, hkv, hd, torch.float32, torch.tensor([20, 50]), seed=7)
+    b.v_cache[:, :, 0] = 3.0
+    b.v_cache[:, :, 1] = -5.0
+    out = reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache,
+                                           cache_seqlens=b.cache_seqlens.clone(),
+                                           block_table=b.block_table)
+    for h in range(hq):
+        expect = 3.0 if h < hq // hkv else -5.0
+        assert torch.allclose(out[:, 0, h], torch.full_like(out[:, 0, h], expect), atol=1e-5)
+    f64 = c_oracle.paged_decode_f64(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
+                                    b.scale)
+    assert np.allclose(f64[:, : hq // hkv], 3.0, atol=1e-12)
+    assert np.allclose(f64[:, hq // hkv:], -5.0, atol=1e-12)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fp64_oracle_matches_fp32_port(dtype):
+    lengths = torch.tensor([1, 15, 16, 17, 100, 513])
+    b = make_paged_batch(6, 16, 4, 128, dtype, lengths, seed=8)
+    f64 = c_oracle.paged_decode_f64(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
+                                    b.scale)
+    # fp32 math on the same widened inputs, before the final cast to dtype.
+    cpu32 = make_paged_batch(6, 16, 4, 128, dtype, lengths, seed=8)
+    port = reference_port.attention_kvcache(
+        cpu32.q.float(), cpu32.k_cache.float(), cpu32.v_cache.float(),
+        cache_seqlens=cpu32.cache_seqlens.clone(), block_table=cpu32.block_table,
+        softmax_scale=cpu32.scale).numpy()[:, 0]
+    assert np.abs(port - f64).max() < 2e-5
+
+
+def test_fp64_oracle_matches_double_library_attention():
+    lengths = torch.tensor([3, 64, 250])
+    b = make_paged_batch(3, 8, 2, 64, torch.float32, lengths, page_size=8, seed=9)
+    f64 = c_oracle.paged_decode_f64(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
+                                    b.scale)
+    for i, n in enumerate(lengths.tolist()):
+        row = b.block_table[i].tolist()
+        lib = sdpa_reference(b.q[i, 0], gather_dense(b.k_cache, row, n),
+                             gather_dense(b.v_cache, row, n), b.scale)
+        assert np.abs(f64[i] - lib.numpy()).max() < 1e-10
+
+
+def test_peaked_query_selects_one_value_row():
+    b = make_paged_batch(1, 4, 1, 64, torch.float32, torch.tensor([40]), seed=10)
+    row = b.block_table[0].tolist()
+    target = 23
+    k_t = b.k_cache[row[target // 16], target % 16, 0]
+    b.q[0, 0, :] = 40.0 * k_t / k_t.norm()
+    f64 = c_oracle.paged_decode_f64(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
+                                    1.0)
+    v_t = b.v_cache[row[target // 16], target % 16, 0].double().numpy()
+    assert np.abs(f64[0, 0] - v_t).max() < 1e-6
+
+
+def test_permuting_pages_with_the_table_changes_nothing():
+    b = make_paged_batch(3, 8, 2, 64, torch.float32, torch.tensor([10, 47, 90]), seed=11)
+    ref = c_oracle.paged_decode_f64(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
+                                    b.scale)
+    perm = torch.randperm(b.k_cache.shape[0], generator=torch.Generator().manual_seed(3))
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(perm.numel())
+    k2, v2 = b.k_cache[perm], b.v_cache[perm]            # new page i = old page perm[i]
+    table2 = inv[b.block_table.long()].to(torch.int32)  # old page p now lives at inv[p]
+    out = c_oracle.paged_decode_f64(b.q, k2, v2, table2, b.cache_seqlens, b.scale)
+    assert np.array_equal(ref, out)
+
+
+def test_empty_sequence_gives_zeros_in_fp64_oracle():
+    b = make_paged_batch(2, 4, 2, 64, torch.float16, torch.tensor([0, 5]), seed=12)
+    out = c_oracle.paged_decode_f64(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
+                                    b.scale)
+    assert np.array_equal(out[0], np.zeros_like(out[0]))
+    assert np.abs(out[1]).max() > 0
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_append_oracle_is_index_assignment(dtype):
+    torch.manual_seed(13)
+    b = make_paged_batch(3, 8, 2, 64, dtype, torch.tensor([9, 19, 33]), seed=13,
+                         block_table_width=4)
+    seqlens = torch.tensor([5, 16, 30], dtype=torch.int32)
+    k_new = torch.randn(3, 4, 2, 64).to(dtype)
+    v_new = torch.randn(3, 4, 2, 64).to(dtype)
+    got_k, got_v = c_oracle.append_kv(k_new, v_new, b.k_cache, b.v_cache, b.block_table, seqlens)
+    exp_k, exp_v = b.k_cache.clone(), b.v_cache.clone()
+    for i in range(3):
+        for t in range(4):
+            pos = int(seqlens[i]) + t
+            if pos // 16 >= b.block_table.shape[1]:
+                continue
+            page = int(b.block_table[i, pos // 16])
+            exp_k[page, pos % 16] = k_new[i, t]
+            exp_v[page, pos % 16] = v_new[i, t]
+    assert torch.equal(got_k, exp_k) and torch.equal(got_v, exp_v)
+
+
+def test_reshape_and_cache_oracle_skips_negative_slots():
+    torch.manual_seed(14)
+    kc = torch.randn(4, 16, 2, 64).to(torch.bfloat16)
+    vc = torch.randn(4, 16, 2, 64).to(torch.bfloat16)
+    key = torch.randn(5, 2, 64).to(torch.bfloat16)
+    value = torch.randn(5, 2, 64).to(torch.bfloat16)
+    slots = torch.tensor([0, 17, -1, 63, 40])
+    got_k, got_v = c_oracle.reshape_and_cache(key, value, kc, vc, slots)
+    exp_k, exp_v = kc.clone(), vc.clone()
+    for t, s in enumerate(slots.tolist()):
+        if s >= 0:
+            exp_k[s // 16, s % 16] = key[t]
+            exp_v[s // 16, s % 16] = value[t]
+    assert torch.equal(got_k, exp_k) and torch.equal(got_v, exp_v)
+    assert not torch.equal(got_k, kc)
+
+
+@pytest.mark.parametrize("length,chunk,splits", [(1, 64, 4), (100, 16, 8), (257, 64, 5),
+                                                 (1000, 512, 2), (64, 64, 1), (300, 7, 60)])
+def test_split_partials_merge_to_unsplit_attention(length, chunk, splits):
+    rng = np.random.default_rng(length + chunk)
+    q = rng.standard_normal(64)
+    k = rng.standard_normal((length, 64)) * np.where(rng.random((length, 1)) < 0.05, 8.0, 1.0)
+    v = rng.standard_normal((length, 64))
+    scale = 1 / math.sqrt(64)
+    whole = split_model.attention_f64(q, k, v, scale)
+    outs, lse = split_model.split_partials(q, k, v, scale, chunk, max(splits, -(-length // chunk)))
+    merged = split_model.lse_combine(outs, lse)
+    assert np.abs(merged - whole).max() < 1e-12
+    # Empty splits carry -inf and weigh nothing (the sum order may move the last ulp).
+    padded = split_model.lse_combine(np.vstack([outs, np.zeros((3, 64))]),
+                                     np.concatenate([lse, [-np.inf] * 3]))
+    assert np.abs(padded - merged).max() < 1e-14
+
+
+def test_split_model_matches_fp64_oracle():
+    b = make_paged_batch(1, 2, 1, 64, torch.float32, torch.tensor([333]), seed=15)
+    f64 = c_oracle.paged_decode_f64(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
+                                    b.scale)
+    row = b.block_table[0].tolist()
+    keys = gather_dense(b.k_cache, row, 333)[:, 0].double().numpy()
+    vals = gather_dense(b.v_cache, row, 333)[:, 0].double().numpy()
+    outs, lse = split_model.split_partials(b.q[0, 0, 0].double().numpy(), keys, vals, b.scale,
+                                           64, 6)
+    assert np.abs(split_model.lse_combine(outs, lse) - f64[0, 0]).max() < 1e-12
