@@ -45,7 +45,7 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--workload", default=MAIN_WORKLOAD)
     ap.add_argument("--no-cells", action="store_true", help="skip the per-cell table")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-reps", type=int, default=5)
+    ap.add_argument("--cpu-reps", type=int, default=15)
     return ap.parse_args()
 
 
@@ -130,7 +130,13 @@ def cpu_baseline(spec: dict, reps: int) -> dict:
     from mxflashattn_amd.workloads import make_paged_batch
     from oracle import reference_port
 
-    torch.set_num_threads(os.cpu_count() or 1)
+    # The host cores this process may use; a GPU box's share is capped by
+    # OMP_NUM_THREADS whatever os.cpu_count() reports.
+    cores = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    if cap.isdigit() and int(cap) > 0:
+        cores = min(cores, int(cap))
+    torch.set_num_threads(max(1, cores))
     b = make_paged_batch(**spec, device="cpu")
     times = []
     for i in range(reps + 1):

@@ -117,8 +117,12 @@ int mxfa_split_decode_partial_launch(const void *q, int64_t q_stride_b, int64_t 
 
 /*
  * Combine stage alone: LSE merge of the pieces of every sequence that crosses
- * a range end, and zeros for empty sequences. Counterpart of the split_combine
- * launch (csrc_native/m1_kernel.cpp:1000-1001, kernel :861-888).
+ * a range end, and zeros for empty sequences. The workspace must have been
+ * filled by mxfa_split_decode_partial_launch with the same batch, q_heads,
+ * head_dim and num_splits, earlier on the same stream; a workspace holding
+ * anything else gives wrong numbers (never an out-of-bounds access).
+ * Counterpart of the split_combine launch (csrc_native/m1_kernel.cpp:1000-1001,
+ * kernel :861-888).
  */
 int mxfa_split_decode_combine_launch(void *workspace, size_t workspace_bytes, void *out,
                                      int64_t out_stride_b, int64_t out_stride_h, int batch,

@@ -512,7 +512,10 @@ __global__ __launch_bounds__(256) void split_combine_kernel(CombineParams p) {
   const int NT = p.ws_s[p.batch];
   const int sb = p.ws_s[b], nt = p.ws_s[b + 1] - sb;
   uint2 *dst = reinterpret_cast<uint2 *>(p.out + b * p.o_sb + (int64_t)h * p.o_sh + t * 4);
-  if (nt <= 0) {
+  // The prefix sums come from the partial launch; prefix sums that do not
+  // describe tiles inside [0, NT) (a workspace the partial stage did not fill)
+  // give zeros, so every range index below stays in [0, R).
+  if (nt <= 0 || sb < 0 || NT <= 0 || sb + nt > NT) {
     *dst = make_uint2(0u, 0u);  // empty sequence: zero output
     return;
   }

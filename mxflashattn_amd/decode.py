@@ -139,7 +139,9 @@ def route_varlen(q, k, v, q_offsets: list[int], k_offsets: list[int], max_seqlen
         starts = torch.tensor([k_offsets[i] for i in rows], dtype=torch.int32, device=device)
         lengths = torch.tensor([k_offsets[i + 1] - k_offsets[i] for i in rows],
                                dtype=torch.int32, device=device)
-        width = max(1, max_seqlen_k)
+        # Table width from the offsets themselves: a max_seqlen_k smaller than a
+        # sequence would otherwise cut that sequence short.
+        width = max(1, max(k_offsets[i + 1] - k_offsets[i] for i in rows))
         table = starts.unsqueeze(1) + torch.arange(width, dtype=torch.int32,
                                                    device=device).unsqueeze(0)
         kc = k.unsqueeze(1)  # [T, 1, HKV, D]: one token per page

@@ -224,6 +224,24 @@ def _stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+def _require_device(*tensors: torch.Tensor) -> torch.device:
+    """All tensors on one GPU, which must be the current HIP device.
+
+    The kernels dereference raw pointers: a host tensor or a tensor of another
+    GPU would fault instead of raising, so this is checked before every launch.
+    """
+    device = tensors[0].device
+    if device.type != "cuda":
+        raise ValueError(f"MI355X kernels need GPU tensors, got a tensor on {device}")
+    for t in tensors[1:]:
+        if t.device != device:
+            raise ValueError(f"all tensors must be on {device}, got one on {t.device}")
+    if (device.index or 0) != torch.cuda.current_device():
+        raise ValueError(f"tensors are on {device} but the current device is "
+                         f"cuda:{torch.cuda.current_device()}; call under torch.cuda.device")
+    return device
+
+
 def check_decode_shapes(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
     """Raise UnsupportedConfig when the kernel contract does not cover the call."""
     if q.dim() not in (3, 4) or (q.dim() == 4 and q.shape[1] != 1):
@@ -264,16 +282,18 @@ def _prepare(q, k_cache, v_cache, block_table, cache_seqlens, out):
         q = q.contiguous()
     if k_cache.stride(-1) != 1 or v_cache.stride() != k_cache.stride():
         raise UnsupportedConfig("k_cache and v_cache must share strides with a contiguous last dim")
+    _require_device(q, k_cache, v_cache, block_table, cache_seqlens)
     block_table = _int32_contig(block_table, "block_table")
     cache_seqlens = _int32_contig(cache_seqlens, "cache_seqlens")
-    if block_table.dim() != 2 or block_table.shape[0] != batch:
-        raise ValueError("block_table must be [batch, width]")
+    if block_table.dim() != 2 or block_table.shape[0] != batch or block_table.shape[1] < 1:
+        raise ValueError("block_table must be [batch, width >= 1]")
     if cache_seqlens.numel() != batch:
         raise ValueError("cache_seqlens must have one entry per sequence")
     if out is None:
         out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     if out.shape != q.shape or out.dtype != q.dtype or out.stride(-1) != 1:
         raise ValueError("out must match q's shape and dtype with a contiguous last dim")
+    _require_device(q, out)
     return q, block_table, cache_seqlens, out
 
 
@@ -332,6 +352,9 @@ def split_decode_partial(
     ``workspace``); ``split_decode_combine`` finishes the call."""
     q, block_table, cache_seqlens, out = _prepare(q, k_cache, v_cache, block_table,
                                                   cache_seqlens, out)
+    _require_device(q, workspace)
+    if not workspace.is_contiguous():
+        raise ValueError("workspace must be contiguous")
     nbytes = workspace.numel() * workspace.element_size()
     rc = library().mxfa_split_decode_partial_launch(
         *_launch_args(q, k_cache, v_cache, block_table, cache_seqlens, out, workspace.data_ptr(),
@@ -341,6 +364,11 @@ def split_decode_partial(
 
 def split_decode_combine(workspace: torch.Tensor, out: torch.Tensor, num_splits: int) -> torch.Tensor:
     """LSE merge of the pieces in ``workspace`` into ``out`` ([B,1,HQ,HD] or [B,HQ,HD])."""
+    _require_device(out, workspace)
+    if not workspace.is_contiguous() or out.stride(-1) != 1:
+        raise ValueError("workspace must be contiguous and out's last dim contiguous")
+    if out.dim() not in (3, 4) or (out.dim() == 4 and out.shape[1] != 1):
+        raise ValueError(f"out must be [B,1,HQ,HD] or [B,HQ,HD], got {tuple(out.shape)}")
     batch, hq, hd = out.shape[0], out.shape[-2], out.shape[-1]
     os_ = out.stride()
     rc = library().mxfa_split_decode_combine_launch(
@@ -371,6 +399,7 @@ def reshape_and_cache(
         key, value = key.contiguous(), value.contiguous()
     if value_cache.stride() != key_cache.stride() or key_cache.stride(-1) != 1:
         raise UnsupportedConfig("caches must share strides with a contiguous last dim")
+    _require_device(key, value, key_cache, value_cache, slot_mapping)
     slots = slot_mapping
     if slots.dtype != torch.int64:
         slots = slots.to(torch.int64)
@@ -399,12 +428,23 @@ def append_kv(
     """Block-table append: k[b, t] -> position cache_seqlens[b] + t (seqlens unchanged)."""
     if k.dim() != 4 or v.shape != k.shape:
         raise ValueError("k/v must be [batch, new_tokens, kv_heads, head_dim]")
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise ValueError("caches must be [pages, page_size, kv_heads, head_dim]")
+    if k.shape[2:] != k_cache.shape[2:]:
+        raise ValueError("k/v heads and head_dim must match the cache")
+    if k.dtype != k_cache.dtype or v.dtype != k.dtype or v_cache.dtype != k.dtype:
+        raise ValueError("k/v and caches must share a dtype")
+    _require_device(k, v, k_cache, v_cache, block_table, cache_seqlens)
     if k.stride() != v.stride() or k.stride(-1) != 1:
         k, v = k.contiguous(), v.contiguous()
     if v_cache.stride() != k_cache.stride() or k_cache.stride(-1) != 1:
         raise UnsupportedConfig("caches must share strides with a contiguous last dim")
     block_table = _int32_contig(block_table, "block_table")
     cache_seqlens = _int32_contig(cache_seqlens, "cache_seqlens")
+    if block_table.dim() != 2 or block_table.shape[0] != k.shape[0] or block_table.shape[1] < 1:
+        raise ValueError("block_table must be [batch, width >= 1]")
+    if cache_seqlens.numel() != k.shape[0]:
+        raise ValueError("cache_seqlens must have one entry per sequence")
     cs = k_cache.stride()
     rc = library().mxfa_append_kv_launch(
         k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), k.stride(2), k_cache.data_ptr(),

@@ -1,0 +1,212 @@
+"""The C ABI without a GPU: the library loads, exports what the header declares,
+and its integer-only entry points and argument checks behave as documented.
+
+No kernel is launched here: every launch entry below is given arguments that
+its host-side checks reject before any HIP call (the checks run first in each
+entry point of csrc/split_decode.hip and csrc/kv_append.hip).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from mxflashattn_amd import native
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "mxfa_mi355x.h"
+
+
+def header_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return re.findall(r"^[A-Za-z_][\w \*]*?\b(mxfa_\w+)\s*\(", text, flags=re.M)
+
+
+def header_defines() -> dict[str, int]:
+    out = {}
+    for name, value in re.findall(r"#define (MXFA_\w+)\s+\(?(-?\d+)\)?", HEADER.read_text()):
+        out[name] = int(value)
+    return out
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return native.library()
+
+
+def test_library_loads_and_reports_header_abi(lib):
+    assert native.unavailable_reason() is None
+    assert lib.mxfa_abi_version() == header_defines()["MXFA_ABI_VERSION"]
+
+
+def test_every_header_function_is_exported_and_bound(lib):
+    declared = header_functions()
+    assert len(declared) == len(set(declared)) == 9
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(native.EXPORTED_SYMBOLS) == set(native._SIGNATURES)
+
+
+def test_return_codes_match_header():
+    d = header_defines()
+    assert (d["MXFA_OK"], d["MXFA_EUNSUPPORTED"], d["MXFA_EINVAL"], d["MXFA_EWORKSPACE"],
+            d["MXFA_ELAUNCH"]) == (native.MXFA_OK, native.MXFA_EUNSUPPORTED, native.MXFA_EINVAL,
+                                   native.MXFA_EWORKSPACE, native.MXFA_ELAUNCH)
+    assert native.DTYPE_CODES == {torch.float16: d["MXFA_DTYPE_F16"],
+                                  torch.bfloat16: d["MXFA_DTYPE_BF16"]}
+
+
+def test_strerror_is_distinct_per_code(lib):
+    texts = {code: lib.mxfa_strerror(code).decode() for code in (0, -1, -2, -3, -4)}
+    assert len(set(texts.values())) == 5
+    assert "unsupported" in texts[-1]
+    assert lib.mxfa_strerror(-99).decode()
+
+
+def heuristic_closed_form(b, hq, hkv, hd, ps, btw, cus):
+    cap = btw * ps
+    per_cu = 2 if (hd == 64 and hq // hkv >= 8) or cap < 2048 else 1
+    n = -(-(cus * per_cu) // hkv)
+    n = min(n, -(-(b * -(-cap // 16)) // 4))
+    return max(1, min(n, 65535))
+
+
+@pytest.mark.parametrize("args", [
+    (32, 32, 8, 128, 16, 512, 256),    # config 2: 256 CUs / 8 kv heads
+    (32, 32, 16, 128, 16, 512, 256),   # GQ2: 16 kv heads
+    (32, 32, 4, 64, 16, 512, 256),     # GQ8 HD64: two per CU
+    (1, 2, 1, 64, 16, 1, 256),         # one tile in total
+    (256, 16, 8, 64, 16, 64, 256),     # short tables: two per CU
+    (4, 32, 4, 128, 256, 128, 304),    # other CU count
+    (16384, 64, 8, 128, 16, 4096, 256),
+])
+def test_split_heuristic_closed_form(args):
+    assert native.split_heuristic(*args) == heuristic_closed_form(*args)
+
+
+def test_split_heuristic_known_values():
+    assert native.split_heuristic(32, 32, 8, 128, 16, 512, 256) == 32
+    assert native.split_heuristic(32, 32, 4, 64, 16, 512, 256) == 128
+    assert native.split_heuristic(1, 2, 1, 64, 16, 1, 256) == 1
+
+
+def test_split_heuristic_rejects_bad_sizes(lib):
+    ns = ctypes.c_int(-7)
+    for bad in [(0, 32, 8, 128, 16, 512, 256), (32, 32, 0, 128, 16, 512, 256),
+                (32, 32, 8, 128, 16, 0, 256), (32, 32, 8, 128, 16, 512, 0)]:
+        assert lib.mxfa_split_heuristic(*bad, ctypes.byref(ns)) == native.MXFA_EINVAL
+    assert lib.mxfa_split_heuristic(32, 32, 8, 128, 16, 512, 256, None) == native.MXFA_EINVAL
+    assert ns.value == -7
+
+
+@pytest.mark.parametrize("b,hq,hd,ns", [(32, 32, 128, 32), (1, 2, 64, 1), (700, 64, 64, 999)])
+def test_workspace_size_formula(b, hq, hd, ns):
+    expect = (hq * ns * 2 * hd + hq * ns * 2 + b + 1) * 4
+    assert native.workspace_size(b, hq, hd, ns) == expect
+
+
+def test_workspace_size_rejects_bad_sizes(lib):
+    out = ctypes.c_size_t(0)
+    assert lib.mxfa_split_decode_workspace_size(0, 32, 128, 4, ctypes.byref(out)) == -2
+    assert lib.mxfa_split_decode_workspace_size(1, 32, 128, 0, ctypes.byref(out)) == -2
+    assert lib.mxfa_split_decode_workspace_size(1, 32, 128, 4, None) == -2
+
+
+FAKE = 0x100000  # 16-byte aligned, never dereferenced: every case below fails a host check
+
+
+def decode_args(**over):
+    """A well-formed argument tuple for mxfa_split_decode_launch, with overrides."""
+    a = dict(q=FAKE, q_sb=32 * 128, q_sh=128, k=FAKE, v=FAKE, c_sp=16 * 8 * 128, c_st=8 * 128,
+             c_sh=128, bt=FAKE, bt_stride=64, seqlens=FAKE, seqlen_add=0, out=FAKE,
+             o_sb=32 * 128, o_sh=128, ws=FAKE, ws_bytes=1 << 30, scale=0.088, batch=32, hq=32,
+             hkv=8, hd=128, ps=16, btw=64, pages=4096, dtype=1, ns=32, stream=None)
+    a.update(over)
+    return tuple(a.values())
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(q=None), -2), (dict(k=None), -2), (dict(bt=None), -2), (dict(seqlens=None), -2),
+    (dict(out=None), -2), (dict(batch=0), -2), (dict(ns=0), -2), (dict(seqlen_add=-1), -2),
+    (dict(scale=float("nan")), -2), (dict(scale=float("inf")), -2),
+    (dict(hd=96), -1), (dict(hd=256), -1), (dict(hq=24), -1), (dict(hq=48, hkv=16), -1),
+    (dict(hq=36), -1), (dict(dtype=2), -1), (dict(ps=12), -1), (dict(ps=8192), -1),
+    (dict(ns=70000), -1), (dict(batch=20000), -1), (dict(btw=1 << 27, ps=16), -1),
+    (dict(q=FAKE + 2), -2), (dict(k=FAKE + 8), -2), (dict(q_sh=100), -2), (dict(c_st=1028), -2),
+    (dict(o_sh=130), -2), (dict(out=FAKE + 2), -2),
+    (dict(ws=None), -3), (dict(ws=FAKE + 8), -3), (dict(ws_bytes=1000), -3),
+])
+def test_decode_launch_rejects_before_launching(lib, over, code):
+    assert lib.mxfa_split_decode_launch(*decode_args(**over)) == code
+    assert lib.mxfa_split_decode_partial_launch(*decode_args(**over)) == code
+
+
+def test_decode_workspace_boundary_is_exact(lib):
+    need = native.workspace_size(32, 32, 128, 32)
+    assert lib.mxfa_split_decode_launch(*decode_args(ws_bytes=need - 1)) == -3
+
+
+def test_combine_rejects_before_launching(lib):
+    ws = native.workspace_size(4, 8, 64, 3)
+    f = lib.mxfa_split_decode_combine_launch
+    assert f(None, ws, FAKE, 512, 64, 4, 8, 64, 0, 3, None) in (-2, -3)
+    assert f(FAKE, ws - 4, FAKE, 512, 64, 4, 8, 64, 0, 3, None) == -3
+    assert f(FAKE, ws, FAKE, 512, 64, 4, 8, 96, 0, 3, None) == -1
+    assert f(FAKE, ws, FAKE, 512, 64, 4, 8, 64, 5, 3, None) == -1
+    assert f(FAKE, ws, FAKE, 512, 64, 0, 8, 64, 0, 3, None) == -2
+
+
+def test_append_entry_points_reject_before_launching(lib):
+    rc = lib.mxfa_reshape_and_cache_launch(FAKE, FAKE, 1024, 128, FAKE, FAKE, 16384, 1024, 128,
+                                           None, 4, 8, 128, 16, 100, 1, None)
+    assert rc == -2  # tokens but no slot mapping
+    rc = lib.mxfa_reshape_and_cache_launch(FAKE, FAKE, 1024, 128, FAKE, FAKE, 16384, 1024, 128,
+                                           FAKE, 4, 8, 100, 16, 100, 1, None)
+    assert rc == -1  # head dim not a multiple of 8
+    rc = lib.mxfa_reshape_and_cache_launch(FAKE, FAKE, 1024, 128, FAKE, FAKE, 16384, 1024, 128,
+                                           FAKE, 4, 8, 128, 16, 100, 7, None)
+    assert rc == -1  # dtype
+    rc = lib.mxfa_append_kv_launch(FAKE, FAKE, 4096, 1024, 128, FAKE, FAKE, 16384, 1024, 128,
+                                   None, 8, None, 2, 4, 8, 128, 16, 8, 100, 1, None)
+    assert rc == -2  # rows to write but no table
+    rc = lib.mxfa_append_kv_launch(FAKE, FAKE, 4096, 1024, 128, FAKE + 4, FAKE, 16384, 1024, 128,
+                                   FAKE, 8, FAKE, 2, 4, 8, 128, 16, 8, 100, 1, None)
+    assert rc == -2  # misaligned cache
+
+
+def test_empty_appends_are_no_ops(lib):
+    assert lib.mxfa_reshape_and_cache_launch(FAKE, FAKE, 1024, 128, FAKE, FAKE, 16384, 1024,
+                                             128, None, 0, 8, 128, 16, 100, 1, None) == 0
+    assert lib.mxfa_append_kv_launch(FAKE, FAKE, 4096, 1024, 128, FAKE, FAKE, 16384, 1024, 128,
+                                     None, 8, None, 0, 4, 8, 128, 16, 8, 100, 1, None) == 0
+
+
+def test_python_layer_refuses_host_tensors():
+    q = torch.zeros(2, 1, 8, 64, dtype=torch.float16)
+    cache = torch.zeros(4, 16, 2, 64, dtype=torch.float16)
+    bt = torch.zeros(2, 2, dtype=torch.int32)
+    sl = torch.ones(2, dtype=torch.int32)
+    with pytest.raises(ValueError, match="GPU tensors"):
+        native.paged_decode_split(q, cache, cache, bt, sl, 0.125)
+    with pytest.raises(ValueError, match="GPU tensors"):
+        native.reshape_and_cache(torch.zeros(3, 2, 64, dtype=torch.float16),
+                                 torch.zeros(3, 2, 64, dtype=torch.float16), cache, cache,
+                                 torch.arange(3))
+    with pytest.raises(ValueError, match="GPU tensors"):
+        native.append_kv(torch.zeros(2, 1, 2, 64, dtype=torch.float16),
+                         torch.zeros(2, 1, 2, 64, dtype=torch.float16), cache, cache, bt, sl)
+
+
+@pytest.mark.parametrize("hq,hkv,hd,dtype,ps,match", [
+    (8, 2, 96, torch.float16, 16, "head_dim"), (6, 2, 64, torch.float16, 16, "GQA"),
+    (16, 1, 64, torch.float16, 16, "GQA"), (8, 2, 64, torch.float32, 16, "float16"),
+    (8, 2, 64, torch.float16, 12, "page size"),
+])
+def test_python_shape_contract(hq, hkv, hd, dtype, ps, match):
+    q = torch.zeros(2, 1, hq, hd, dtype=dtype)
+    cache = torch.zeros(4, ps, hkv, hd, dtype=dtype)
+    with pytest.raises(native.UnsupportedConfig, match=match):
+        native.check_decode_shapes(q, cache, cache)

@@ -1,0 +1,153 @@
+"""vLLM-side routing without vLLM (mirrors tests/test_vllm_bridge.py and
+tests/test_vllm_official_split_fallback.py of the reference, for the parts that
+do not need vLLM installed): shape guards, the compat wrapper's hand-back,
+dispatch events and the backend registration result."""
+
+import json
+
+import pytest
+import torch
+
+import mxflashattn_amd.dispatch as dispatch
+from mxflashattn_amd.integrations.vllm import backend, native_decode
+from mxflashattn_amd.integrations.vllm.backend import attention_forward
+
+
+def kv_kwargs(q_heads=16, kv_heads=4, head_dim=128, dtype=torch.float16, page=16):
+    return {
+        "k_cache": torch.empty(1, page, kv_heads, head_dim, dtype=dtype),
+        "v_cache": torch.empty(1, page, kv_heads, head_dim, dtype=dtype),
+        "block_table": torch.zeros(1, 1, dtype=torch.int32),
+        "cache_seqlens": torch.ones(1, dtype=torch.int32),
+    }
+
+
+def test_dense_vllm_bridge_delegates_to_public_api(monkeypatch):
+    monkeypatch.setenv("MXFLASHATTN_ALLOW_FALLBACK", "1")
+    monkeypatch.setattr(dispatch, "_flash_attn_function", lambda operation: None)
+    monkeypatch.setattr(dispatch, "_native_extension", lambda: None)
+    q = torch.randn(3, 2, 64)
+    k = torch.randn(4, 1, 64)
+    v = torch.randn_like(k)
+    with pytest.warns(RuntimeWarning, match="native_backend_requires_accelerator_tensor"):
+        output = attention_forward(q, k, v, causal=True, scale=0.125)
+    assert output.shape == q.shape
+    assert torch.isfinite(output).all()
+
+
+@pytest.mark.parametrize("head_dim,q_heads,kv_heads", [(256, 16, 4), (128, 24, 8)])
+def test_official_kvcache_compat_falls_back_to_vendor_for_unsupported_shapes(
+        monkeypatch, head_dim, q_heads, kv_heads):
+    calls = []
+    expected = object()
+    args = (torch.empty(1, 1, q_heads, head_dim),)
+    kwargs = kv_kwargs(q_heads, kv_heads, head_dim, dtype=torch.float32)
+    monkeypatch.setenv("MXFA_NATIVE_DECODE", "1")
+    monkeypatch.setattr(native_decode, "official_kvcache",
+                        lambda *a, **k: calls.append((a, k)) or expected)
+    monkeypatch.setattr(native_decode.api, "flash_attn_with_kvcache",
+                        lambda *a, **k: pytest.fail("unsupported shape must not enter the MX API"))
+    assert native_decode.mx_kvcache_compat(*args, **kwargs) is expected
+    assert calls == [(args, kwargs)]
+
+
+def test_compat_drops_vllm_only_keywords(monkeypatch):
+    seen = {}
+    monkeypatch.setattr(native_decode, "official_kvcache",
+                        lambda *a, **k: seen.update(k) or "vendor")
+    kwargs = kv_kwargs()
+    kwargs.update(s_aux=None, scheduler_metadata=None, fa_version=3, q_descale=None,
+                  k_descale=None, v_descale=None, return_softmax_lse=False)
+    assert native_decode.mx_kvcache_compat(torch.empty(1, 1, 16, 128), **kwargs) == "vendor"
+    assert set(seen) == {"k_cache", "v_cache", "block_table", "cache_seqlens"}
+
+
+def q_of(q_heads=16, head_dim=128, dtype=torch.float16, rank=4):
+    return torch.empty((1, 1, q_heads, head_dim) if rank == 4 else (1, q_heads, head_dim),
+                       dtype=dtype)
+
+
+@pytest.mark.parametrize("case,reason", [
+    (dict(q_heads=16, kv_heads=4, head_dim=256), "head_dim"),
+    (dict(q_heads=24, kv_heads=8, head_dim=128), "gqa_ratio"),
+    (dict(q_heads=16, kv_heads=16, head_dim=128), "gqa_ratio"),
+    (dict(q_heads=64, kv_heads=4, head_dim=128), "gqa_ratio"),
+    (dict(q_heads=16, kv_heads=4, head_dim=128, dtype=torch.float32), "dtype"),
+    (dict(q_heads=16, kv_heads=4, head_dim=128, page=24), "page_size"),
+    (dict(q_heads=16, kv_heads=4, head_dim=128), "device"),
+])
+def test_native_guard_hands_back_unsupported_calls(case, reason):
+    dtype = case.get("dtype", torch.float16)
+    q = q_of(case["q_heads"], case["head_dim"], dtype)
+    kwargs = kv_kwargs(case["q_heads"], case["kv_heads"], case["head_dim"], dtype,
+                       case.get("page", 16))
+    got, picked = native_decode._guard((q,), kwargs)
+    assert got == reason and picked == ()
+
+
+@pytest.mark.parametrize("extra,reason", [
+    (dict(alibi_slopes=torch.zeros(16)), "alibi"),
+    (dict(window_size=(128, 0)), "window"),
+    (dict(block_table=None), "block_table_or_seqlens"),
+    (dict(cache_seqlens=torch.ones(3, dtype=torch.int32)), "block_table_or_seqlens"),
+])
+def test_native_guard_option_checks(extra, reason):
+    kwargs = kv_kwargs()
+    kwargs.update(extra)
+    assert native_decode._guard((q_of(),), kwargs)[0] == reason
+
+
+def test_native_guard_accepts_no_window_and_rank3_queries():
+    kwargs = kv_kwargs()
+    kwargs["window_size"] = (-1, -1)
+    # Host tensors reach the device check last: every shape check has passed.
+    assert native_decode._guard((q_of(rank=3),), kwargs)[0] == "device"
+    assert native_decode._guard((torch.empty(1, 2, 16, 128, dtype=torch.float16),),
+                                kwargs)[0] == "query_length"
+
+
+def test_native_decode_is_opt_in(monkeypatch):
+    monkeypatch.delenv("MXFA_NATIVE_DECODE", raising=False)
+    assert native_decode.try_native_decode((q_of(),), kv_kwargs()) is None
+
+
+def test_guard_failures_are_recorded_as_fallback_events(monkeypatch):
+    monkeypatch.setenv("MXFA_NATIVE_DECODE", "1")
+    backend.clear_dispatch_events(truncate_log=False)
+    assert native_decode.try_native_decode((q_of(head_dim=256),),
+                                           kv_kwargs(head_dim=256)) is None
+    assert backend.get_dispatch_events() == [{
+        "path": "native_decode", "fallback": "true", "fallback_reason": "guard:head_dim"}]
+
+
+def test_dispatch_log_sampling(monkeypatch, tmp_path):
+    log = tmp_path / "events.jsonl"
+    monkeypatch.setenv("MXFLASHATTN_DISPATCH_LOG", str(log))
+    monkeypatch.setenv("MXFLASHATTN_DISPATCH_SAMPLE", "3")
+    backend.clear_dispatch_events()
+    monkeypatch.setattr(backend, "_counter", 0)
+    for i in range(7):
+        backend.record_event({"path": "mi355x_split_decode", "i": str(i)})
+    lines = [json.loads(x) for x in log.read_text().splitlines()]
+    assert [x["i"] for x in lines] == ["0", "3", "6"]
+    assert len(backend.get_dispatch_events()) == 7
+
+
+def test_plugin_import_log_names_the_dispatch_log(monkeypatch, tmp_path):
+    monkeypatch.delenv("MXFLASHATTN_DISPATCH_LOG", raising=False)
+    monkeypatch.setenv("MXFLASHATTN_PLUGIN_IMPORT_LOG", str(tmp_path / "run.plugin.log"))
+    assert backend._log_path() == str(tmp_path / "run.dispatch.jsonl")
+
+
+def test_registration_reports_missing_vllm():
+    result = backend.register_vllm_v1_backend()
+    try:
+        import vllm  # noqa: F401
+    except ImportError:
+        assert result["registered"] == "false"
+        assert result["reason"].startswith("vllm_v1_api_unavailable")
+
+
+def test_reshape_and_cache_flash_rejects_fp8_caches():
+    with pytest.raises(NotImplementedError, match="fp8"):
+        native_decode.reshape_and_cache_flash(None, None, None, None, torch.zeros(1), "fp8")
