@@ -40,7 +40,7 @@ ROTATE_BYTES = 1 << 30
 def parse_args() -> argparse.Namespace:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default=MAIN_WORKLOAD)
     ap.add_argument("--no-cells", action="store_true", help="skip the per-cell table")
@@ -63,7 +63,10 @@ def build_pools(spec: dict, device: torch.device):
 
 
 def time_calls(fn, pools, steps: int, warmup: int, stream) -> tuple[float, float]:
-    """(median us per call from per-call events, mean us per call over the whole run)."""
+    """(median us per call from per-call events, mean us per call over the whole run).
+
+    Events are recorded on ``stream``, the stream the kernels are launched on.
+    """
     for i in range(warmup):
         fn(*pools[i % len(pools)])
     torch.cuda.synchronize()
@@ -80,6 +83,23 @@ def time_calls(fn, pools, steps: int, warmup: int, stream) -> tuple[float, float
     torch.cuda.synchronize()
     per = [s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends)]
     return statistics.median(per), first.elapsed_time(last) * 1e3 / steps
+
+
+def time_back_to_back(fn, pools, steps: int, warmup: int, stream) -> float:
+    """Mean us per launch of ``steps`` launches queued back to back between two
+    events on ``stream`` (no markers between launches, so the figure is the
+    kernel's own duration plus the dispatch gap)."""
+    for i in range(warmup):
+        fn(*pools[i % len(pools)])
+    torch.cuda.synchronize()
+    first = torch.cuda.Event(enable_timing=True)
+    last = torch.cuda.Event(enable_timing=True)
+    first.record(stream)
+    for i in range(steps):
+        fn(*pools[(warmup + i) % len(pools)])
+    last.record(stream)
+    torch.cuda.synchronize()
+    return first.elapsed_time(last) * 1e3 / steps
 
 
 def measure_workload(name: str, spec: dict, device, steps: int, warmup: int) -> dict:
@@ -104,7 +124,7 @@ def measure_workload(name: str, spec: dict, device, steps: int, warmup: int) -> 
         native.split_decode_partial(base.q, kc, vc, base.block_table, base.cache_seqlens,
                                     base.scale, out, ws, ns)
 
-    _, us_partial = time_calls(partial, pools, steps, warmup, stream)
+    us_partial = time_back_to_back(partial, pools, steps, warmup, stream)
     kv = base.kv_bytes()
     alg = base.algorithmic_bytes()
     gbs = kv / (us_med * 1e-6) / 1e9
@@ -194,7 +214,7 @@ def main() -> int:
         for name, cspec in {**CELLS, **CONFIGS}.items():
             if name == args.workload:
                 continue
-            cells[name] = measure_workload(name, cspec, device, 50, 5)
+            cells[name] = measure_workload(name, cspec, device, 100, 10)
             print(f"[bench] {name}: {cells[name]}", file=sys.stderr, flush=True)
 
     cpu = None
