@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MXFA_ABI_VERSION 1
+#define MXFA_ABI_VERSION 2
 
 /* Return codes. */
 #define MXFA_OK 0
@@ -55,9 +55,9 @@ const char *mxfa_strerror(int code);
 /*
  * Split count for the launch below, sized for the device's CU count. The
  * work split itself happens on the device: the 16-token tiles of all
- * sequences of a kv head are laid end to end and cut into num_splits equal
- * ranges, one workgroup each, so the per-CU load is even for any length mix.
- * Integer-only, reads no device data. Replaces the Python loop at
+ * sequences are laid end to end and cut into num_splits equal ranges (fewer
+ * when there are fewer tiles), and every (kv head, range) pair is one wave, so
+ * the per-CU load is even for any length mix. Integer-only, reads no device data. Replaces the Python loop at
  * integrations/vllm/vllm_plugin.py:271-276 (NP doubling until B*HKV*NP >= 2048,
  * c_len = ceil(BTW*PS/NP)).
  */
@@ -65,10 +65,11 @@ int mxfa_split_heuristic(int batch, int q_heads, int kv_heads, int head_dim, int
                          int block_table_width, int num_cus, int *num_splits);
 
 /*
- * Bytes of caller-owned workspace the split launch needs. Replaces the per-call
- * at::empty of ows/mdws at csrc_native/m1_binding.cpp:94-96. Layout: piece
- * outputs fp32 [HQ, num_splits, 2, HD], piece base-2 LSEs fp32
- * [HQ, num_splits, 2], tile prefix sums int32 [B + 1].
+ * Bytes of caller-owned workspace the split launch needs. Replaces the
+ * per-call at::empty of ows/mdws at csrc_native/m1_binding.cpp:94-96. Layout:
+ * piece outputs fp32 [HKV, num_splits, 2, GQ, HD], piece base-2 LSEs fp32
+ * [HKV, num_splits, 2, GQ] (HKV * GQ = q_heads), tile prefix sums int32
+ * [batch + 1]. Its contents between calls do not matter.
  */
 int mxfa_split_decode_workspace_size(int batch, int q_heads, int head_dim, int num_splits,
                                      size_t *bytes);
@@ -76,13 +77,19 @@ int mxfa_split_decode_workspace_size(int batch, int q_heads, int head_dim, int n
 /*
  * Split-KV paged decode: out[b, h, :] = softmax(q[b,h]·K_b^T · scale) · V_b over the
  * first seqlens[b] + seqlen_add tokens of sequence b, gathered through block_table.
- * Launches the split partial kernel, then the LSE combine kernel. A sequence of
- * length 0 yields zeros.
- * Replaces mxfa_paged_decode_split_launch (csrc_native/m1_kernel.cpp:1206-1211):
- * the same information plus explicit strides, seqlen_add and a sized workspace;
- * the per-split length c_len is gone because ranges are cut on the device.
+ * Two launches on `stream`: the split partial kernel (it writes every sequence
+ * that lies inside one work range, zero for empty sequences, and the pieces of
+ * the others to the workspace), then the LSE combine kernel. A sequence of
+ * length 0 yields zeros. Calls that share a workspace must not run concurrently.
+ *
+ * Replaces mxfa_paged_decode_split_launch (csrc_native/m1_kernel.cpp:1206-1211)
+ * and its two launches (partial, then split_combine, :985-1001): the same
+ * information plus explicit strides, seqlen_add and a sized workspace; the
+ * per-split length c_len is gone because ranges are cut on the device.
  * Supported: HD in {64,128}, HQ/HKV in {2,4,8}, PS a power of two in [1, 4096],
- * dtype F16/BF16 (q, caches and out share it), batch <= 16384.
+ * dtype F16/BF16 (q, caches and out share it), batch <= 16384, non-overlapping
+ * token rows (cache_stride_token >= HD when PS > 1) and query heads
+ * (q_stride_h >= HD).
  */
 int mxfa_split_decode_launch(const void *q, int64_t q_stride_b, int64_t q_stride_h,
                              const void *k_cache, const void *v_cache,
@@ -90,44 +97,10 @@ int mxfa_split_decode_launch(const void *q, int64_t q_stride_b, int64_t q_stride
                              int64_t cache_stride_head, const int32_t *block_table,
                              int64_t bt_stride, const int32_t *seqlens, int seqlen_add,
                              void *out, int64_t out_stride_b, int64_t out_stride_h,
-                             void *workspace, size_t workspace_bytes, float scale,
-                             int batch, int q_heads, int kv_heads, int head_dim,
-                             int page_size, int block_table_width, int num_pages, int dtype,
-                             int num_splits, void *stream);
-
-/*
- * Partial stage alone: writes the output of every sequence that lies inside
- * one range, and the normalised output and base-2 LSE of every piece of a
- * sequence that crosses a range end into the workspace. Followed by
- * mxfa_split_decode_combine_launch it is the same computation as
- * mxfa_split_decode_launch; alone it lets a caller time the dominant kernel.
- * Counterpart of the paged_decode_v3 launch inside launch_split
- * (csrc_native/m1_kernel.cpp:985-999).
- */
-int mxfa_split_decode_partial_launch(const void *q, int64_t q_stride_b, int64_t q_stride_h,
-                                     const void *k_cache, const void *v_cache,
-                                     int64_t cache_stride_page, int64_t cache_stride_token,
-                                     int64_t cache_stride_head, const int32_t *block_table,
-                                     int64_t bt_stride, const int32_t *seqlens, int seqlen_add,
-                                     void *out, int64_t out_stride_b, int64_t out_stride_h,
-                                     void *workspace, size_t workspace_bytes, float scale,
-                                     int batch, int q_heads, int kv_heads, int head_dim,
-                                     int page_size, int block_table_width, int num_pages,
-                                     int dtype, int num_splits, void *stream);
-
-/*
- * Combine stage alone: LSE merge of the pieces of every sequence that crosses
- * a range end, and zeros for empty sequences. The workspace must have been
- * filled by mxfa_split_decode_partial_launch with the same batch, q_heads,
- * head_dim and num_splits, earlier on the same stream; a workspace holding
- * anything else gives wrong numbers (never an out-of-bounds access).
- * Counterpart of the split_combine launch (csrc_native/m1_kernel.cpp:1000-1001,
- * kernel :861-888).
- */
-int mxfa_split_decode_combine_launch(void *workspace, size_t workspace_bytes, void *out,
-                                     int64_t out_stride_b, int64_t out_stride_h, int batch,
-                                     int q_heads, int head_dim, int dtype, int num_splits,
-                                     void *stream);
+                             void *workspace, size_t workspace_bytes, float scale, int batch,
+                             int q_heads, int kv_heads, int head_dim, int page_size,
+                             int block_table_width, int num_pages, int dtype, int num_splits,
+                             void *stream);
 
 /*
  * vLLM-style paged append: for token t with slot = slot_mapping[t] >= 0,

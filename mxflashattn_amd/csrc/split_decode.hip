@@ -1,41 +1,51 @@
 // Split-KV paged decode attention for MI355X (gfx950, wave64).
 //
 // Work split (sized on the device, no host sync). Every sequence b is cut into
-// ceil(L_b / 16) tiles of 16 tokens; for each kv head the tiles of all
-// sequences are laid end to end (tile index t = S_b + j, S = exclusive prefix
-// sum) and cut into `num_splits` equal ranges. Workgroup (kv head, r) streams
-// range r: [floor(r*NT/R), floor((r+1)*NT/R)). A range covers whole sequences
-// and at most two pieces of sequences that cross its ends. Every workgroup
-// therefore gets the same number of tiles whatever the length mix, which is
-// what keeps all 256 CUs busy to the end of the call.
+// ceil(L_b / 16) tiles of 16 tokens; the tiles of all sequences are laid end to
+// end (tile index t = S_b + j, S = exclusive prefix sum) and cut into R equal
+// ranges [floor(r*NT/R), floor((r+1)*NT/R)), R = min(num_splits, NT). Every
+// (kv head, range) pair is the work of one wave, so every wave streams the same
+// number of tiles whatever the length mix.
 //
-// Partial kernel, per workgroup (4 waves) and per sequence piece of its range:
-//   waves take the piece's tiles round-robin; per tile of 16 tokens
-//   QK   on the matrix cores: S^T[16 tokens x 16 heads] = K[16 x HD] . Q^T[HD x 16]
-//        (v_mfma_f32_16x16x32, HD/32 steps; query heads >= GQ are zero columns).
-//        K is loaded token-per-lane for the A operand: lane l reads 64
-//        contiguous bytes of token l%16 per step. Result layout: lane
-//        (r = l/16, h = l%16) holds the scores of tokens 4r+i, i = 0..3, head h.
-//   softmax on that layout in the base-2 domain: one exp per (token, head).
-//        The reference max m of each head is shared by the wave and only moves
-//        (wave-uniform branch) when a score passes it by kRescaleLog2, so
-//        p = 2^(x - m) <= 2^kRescaleLog2 and rescales are rare.
-//   PV   on the VALU: V is loaded row-per-DPP-row (lane (r, c) holds dims
-//        [c*VD, c*VD+VD) of token 4r+u for load u), so the probability of
-//        token 4r+u and head h sits in lane (r, h), register u, of the same DPP
-//        row and reaches every lane through a row_newbcast:h operand.
-//   Rows, then waves (through LDS) are merged per piece. A piece that is a
-//   whole sequence writes the final output; a piece of a longer sequence
-//   writes its normalised output and base-2 log-sum-exp to the workspace.
+// Workgroups: 8 waves = KH kv heads x S sub-ranges (KH = min(HKV, 8), S = 8/KH).
+// The waves of a workgroup read the same pages at the same time, all kv heads
+// of each token row together, so the HBM sees whole pages instead of
+// 128/256-byte slivers spread over the run (measured: +8-15% read bandwidth on
+// MI355X against one kv head per workgroup).
 //
-// Combine kernel: for every sequence that crosses a range end, merge its pieces
-// with the LSE weights; it also writes the zero output of empty sequences.
+// Per wave, over the tiles of its range in order, with no break between
+// sequences (the load pipeline runs straight across sequence ends):
+//   loads  per tile, a buffer descriptor whose base is the tile's first row in
+//          its page (head offset folded in) and whose size covers exactly the
+//          valid rows, so rows past the sequence end and the padding tile past
+//          the range end read as zeros and cost no memory traffic. K and V
+//          carry the nontemporal hint (read once per call).
+//   QK     on the matrix cores: S^T[16 tokens x 16 heads] = K[16 x HD].Q^T[HD x 16]
+//          (v_mfma_f32_16x16x32, HD/32 steps; query heads >= GQ are zero
+//          columns). Lane l holds K bytes [64c + 16(l/16), +16) of token l%16.
+//          Result: lane (r = l/16, h = l%16) holds tokens 4r+i, i = 0..3, head h.
+//   softmax base 2; the reference max m of each head is shared by the wave and
+//          only moves (wave-uniform branch) when a score passes it by
+//          kRescaleLog2, so p = 2^(x - m) <= 2^kRescaleLog2 and rescales are rare.
+//   PV     on the VALU: lane (r, c) holds dims [c*VD, c*VD + VD) of token 4r+u
+//          for load u; the probability of token 4r+u and head h sits in lane
+//          (r, h), register u, of the same DPP row and reaches the whole row
+//          through a row_newbcast:h operand.
+//   piece end: the 4 DPP rows are summed (permlane swaps). A sequence that lies
+//          whole inside the range writes its output. A piece of a longer
+//          sequence writes its normalised output and base-2 log-sum-exp to the
+//          workspace.
 //
-// Workspace (fp32 unless noted), R = num_splits:
-//   ws_o   [HQ, R, 2, HD]  piece outputs; slot 0 = first piece of the range,
-//                          slot 1 = last piece (when it differs)
-//   ws_lse [HQ, R, 2]      piece log-sum-exp (base 2)
-//   ws_s   int32 [B + 1]   tile prefix sums S (written by workgroup (0, 0))
+// Combine kernel (second launch; the kernel boundary makes the pieces visible
+// across the XCDs' separate L2s): one thread per float4 of every (sequence,
+// head) output; sequences that cross a range end fold their pieces in range
+// order with online base-2 LSE weights, eight pieces in flight per step.
+// Merging inside the partial kernel was measured slower: its device-scope
+// counters and write-through stores cost more than the second launch.
+//
+// Workspace (fp32 unless noted), R = num_splits: ws_o [HKV, R, 2, GQ, HD] piece
+// outputs (slot 0 = first piece of a range, slot 1 = last piece when it
+// differs), ws_lse [HKV, R, 2, GQ], ws_s int32 [B + 1] tile prefix sums.
 //
 // Reference counterpart: paged_decode_v3 split mode and split_combine
 // (csrc_native/m1_kernel.cpp:553-888) with the split count of
@@ -47,50 +57,57 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 #include "mxfa_device.h"
 #include "mxfa_mi355x.h"
 
 namespace mxfa {
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr int kTile = 16;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleLog2 = 8.0f;
 constexpr int kMaxBatch = 16384;  // tile prefix sums live in LDS
+constexpr int kMaxHeadsPerWg = 8;
+constexpr uint32_t kSrdWord3 = 0x00020000u;  // raw 32-bit buffer, gfx9 family
+constexpr int kAuxStream = 2;                // nt: no temporal reuse expected
+constexpr int kOffOut = 0x40000000;          // a lane offset no descriptor covers
+
+// Tile flags.
+constexpr int kFirst = 1;        // first tile of a piece (range start or sequence start)
+constexpr int kLast = 2;         // last tile of a piece (range end or sequence end)
+constexpr int kSeqStart = 4;     // first tile of its sequence
+constexpr int kSeqEnd = 8;       // last tile of its sequence
+constexpr int kRangeStart = 16;  // first tile of the range
 
 struct DecodeParams {
-  const uint16_t *q;
-  int64_t q_sb, q_sh;
-  const uint16_t *k;
-  const uint16_t *v;
-  int64_t c_sp, c_st, c_sh;
+  const char *q;
+  int64_t q_sb, q_sh;  // bytes
+  const char *k;
+  const char *v;
+  int64_t sp_bytes;   // page stride
+  uint32_t st_bytes;  // token stride
+  uint32_t sh_bytes;  // head stride
   const int32_t *bt;
   int64_t bt_stride;
   const int32_t *seqlens;
-  uint16_t *out;
-  int64_t o_sb, o_sh;
+  char *out;
+  int64_t o_sb, o_sh;  // bytes
   float *ws_o;
   float *ws_lse;
   int32_t *ws_s;
   float scale_log2;
   int seqlen_add;
   int batch;
-  int hq;
+  int hkv;
+  int heads_per_wg;
+  int subs;
   int ps_log2;
   int max_len;  // block_table_width * page_size
   int num_pages;
-  int num_ranges;
-};
-
-struct CombineParams {
-  const float *ws_o;
-  const float *ws_lse;
-  const int32_t *ws_s;
-  uint16_t *out;
-  int64_t o_sb, o_sh;
-  int batch;
-  int hq;
   int num_ranges;
 };
 
@@ -100,6 +117,8 @@ struct CombineParams {
 typedef const __attribute__((address_space(4))) int32_t *ConstI32;
 
 __device__ __forceinline__ ConstI32 as_const(const int32_t *p) { return (ConstI32)p; }
+
+__device__ __forceinline__ int rfl(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
 __device__ __forceinline__ int seq_len_of(const int32_t *seqlens, int b, int add, int max_len) {
   int L = as_const(seqlens)[b] + add;
@@ -113,6 +132,10 @@ __device__ __forceinline__ int range_lo(int r, int R, int NT) {
 }
 __device__ __forceinline__ int range_of(int t, int R, int NT) {
   return (int)((((int64_t)t + 1) * R - 1) / NT);
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_srd(const char *base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(base), (short)0, bytes, kSrdWord3);
 }
 
 template <typename T>
@@ -132,17 +155,27 @@ struct Mfma<BF16> {
   }
 };
 
+template <int Aux>
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, int off) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, Aux);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+template <int Aux>
+__device__ __forceinline__ uint2 buf_load8(__amdgpu_buffer_rsrc_t r, int off) {
+  const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, Aux);
+  return make_uint2(v.x, v.y);
+}
+
 // V fragment of one lane: 8 elements (HD128, 16 B) or 4 elements (HD64, 8 B).
 template <int VD>
 struct VFrag;
 template <>
 struct VFrag<8> {
   uint4 w;
-  static __device__ __forceinline__ VFrag load(const char *ptr) {
-    VFrag f;
-    f.w = *reinterpret_cast<const uint4 *>(ptr);
-    return f;
+  __device__ __forceinline__ void load_buf(__amdgpu_buffer_rsrc_t r, int off) {
+    w = buf_load16<kAuxStream>(r, off);
   }
+  __device__ __forceinline__ void load_ptr(const char *ptr) { w = load_stream16(ptr); }
   template <typename E>
   __device__ __forceinline__ void widen(float (&v)[8]) const {
     v[0] = E::lo(w.x);
@@ -158,11 +191,10 @@ struct VFrag<8> {
 template <>
 struct VFrag<4> {
   uint2 w;
-  static __device__ __forceinline__ VFrag load(const char *ptr) {
-    VFrag f;
-    f.w = *reinterpret_cast<const uint2 *>(ptr);
-    return f;
+  __device__ __forceinline__ void load_buf(__amdgpu_buffer_rsrc_t r, int off) {
+    w = buf_load8<kAuxStream>(r, off);
   }
+  __device__ __forceinline__ void load_ptr(const char *ptr) { w = load_stream8(ptr); }
   template <typename E>
   __device__ __forceinline__ void widen(float (&v)[4]) const {
     v[0] = E::lo(w.x);
@@ -171,6 +203,16 @@ struct VFrag<4> {
     v[3] = E::hi(w.y);
   }
 };
+
+// f(std::integral_constant<int, I>) for I = 0 .. N-1, unrolled at compile time.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 template <int H>
 __device__ __forceinline__ float row_bcast(float x) {
@@ -233,35 +275,94 @@ __device__ __forceinline__ void tile_prefix(const DecodeParams &p, int32_t *s, i
   __syncthreads();
 }
 
-// kLanePages: page size below the 16-token tile, so every lane looks up its own
-// tokens' pages. Otherwise a tile lies in one page: one scalar lookup per tile.
+// Empty sequences (no tiles) get zero output; sequence b is cleared by the
+// workgroups with blockIdx.y == b % gridDim.y, each for its own kv heads.
+template <int HD, int GQ>
+__device__ __forceinline__ void zero_empty(const DecodeParams &p, const int32_t *s) {
+  const int kv0 = blockIdx.x * p.heads_per_wg;
+  const int kv1 = min(kv0 + p.heads_per_wg, p.hkv);
+  const int nh = (kv1 - kv0) * GQ;
+  constexpr int F = HD / 4;  // 8-byte pieces per head row
+  for (int b = blockIdx.y; b < p.batch; b += gridDim.y) {
+    if (s[b + 1] != s[b]) continue;
+    char *row = p.out + b * p.o_sb + (int64_t)kv0 * GQ * p.o_sh;
+    for (int i = threadIdx.x; i < nh * F; i += kThreads)
+      *reinterpret_cast<uint2 *>(row + (i / F) * p.o_sh + (i % F) * 8) = make_uint2(0u, 0u);
+  }
+}
+
+// Sum / max over the 4 DPP rows of the wave (lanes l, l^16, l^32, l^48); every
+// lane receives the result.
+__device__ __forceinline__ float rows_sum(float x) {
+  const auto a =
+      __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto c =
+      __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+  return __uint_as_float(c[0]) + __uint_as_float(c[1]);
+}
+__device__ __forceinline__ float rows_max(float x) {
+  const auto a =
+      __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto c =
+      __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+  return fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
+}
+
+// VD fp32 values times `scale`, rounded once to the element type, to 8-byte aligned dst.
+template <int VD, typename E>
+__device__ __forceinline__ void store_row(char *dst, const float (&v)[VD], float scale) {
+  uint32_t w[VD / 2];
+#pragma unroll
+  for (int j = 0; j < VD / 2; ++j)
+    w[j] = (uint32_t)E::narrow(v[2 * j] * scale) |
+           ((uint32_t)E::narrow(v[2 * j + 1] * scale) << 16);
+#pragma unroll
+  for (int j = 0; j < VD / 4; ++j)
+    *reinterpret_cast<uint2 *>(dst + 8 * j) = make_uint2(w[2 * j], w[2 * j + 1]);
+}
+
+// Scalar description of one tile, built two tiles ahead of the math.
+struct Tile {
+  int b;      // sequence
+  int tok0;   // first token of the tile within the sequence
+  int valid;  // tokens of the tile that exist (0: padding past the range end)
+  int flags;
+  int pg;  // page id (block-table entry), page-uniform tiles only
+};
+
+// One wave: the tiles [lo, hi) of kv head kvh, range rr of R.
 template <int HD, int GQ, typename T, bool kLanePages>
-__global__ __launch_bounds__(kThreads) void split_partial_kernel(DecodeParams p) {
+__device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *s_tiles, int kvh,
+                                          int rr, int R, int NT, int lo, int hi) {
   using E = Elem<T>;
   constexpr int NCH = HD / 32;  // MFMA steps over the head dim
   constexpr int VD = HD / 16;   // V elements per lane
   constexpr int U = 4;          // V loads per tile (token 4r+u in DPP row r)
-
-  extern __shared__ int32_t s_tiles[];  // [B + 1]
-  __shared__ int s_wave_tot[kWaves];
-  __shared__ float sm_m[kWaves][GQ];
-  __shared__ float sm_d[kWaves][GQ];
-  __shared__ float sm_o[kWaves][GQ][HD];
-
-  const int kvh = blockIdx.x;
-  const int r = blockIdx.y;
-  const int R = p.num_ranges;
-  tile_prefix(p, s_tiles, s_wave_tot);
+  constexpr int NPG = kLanePages ? 1 + U : 1;
   const int B = p.batch;
-  const int NT = s_tiles[B];
-  if (kvh == 0 && r == 0) {
-    for (int i = threadIdx.x; i <= B; i += kThreads) p.ws_s[i] = s_tiles[i];
-  }
-  const int lo = range_lo(r, R, NT), hi = range_lo(r + 1, R, NT);
-  if (lo >= hi) return;
+
+  const int lane = threadIdx.x & 63;
+  const int row = lane >> 4;  // DPP row
+  const int col = lane & 15;  // head (score layout) / V column
+  const int ps_mask = (1 << p.ps_log2) - 1;
+  const uint32_t st = p.st_bytes;
+  const uint64_t head_off = (uint64_t)kvh * p.sh_bytes;
+  const float c = p.scale_log2;
+  const int ns = p.num_ranges;  // workspace stride
+
+  // Lane offsets inside a tile: K in the MFMA A layout, V row-contiguous, q as
+  // the MFMA B operand (columns >= GQ read nothing).
+  const int k_off = col * (int)st + row * 16;
+  int v_off[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) v_off[u] = (4 * row + u) * (int)st + col * (VD * 2);
+  const int q_off = col < GQ ? col * (int)p.q_sh + row * 16 : kOffOut;
+  const int q_bytes = (GQ - 1) * (int)p.q_sh + HD * 2;
 
   // Sequence holding tile lo: largest b with s[b] <= lo (then s[b+1] > lo).
-  int b;
+  int pb;
   {
     int a = 0, z = B - 1;
     while (a < z) {
@@ -269,296 +370,351 @@ __global__ __launch_bounds__(kThreads) void split_partial_kernel(DecodeParams p)
       if (s_tiles[mid] <= lo) a = mid;
       else z = mid - 1;
     }
-    b = __builtin_amdgcn_readfirstlane(a);
+    pb = rfl(a);
   }
+  // Cursor of the tile builder (runs two tiles ahead of the math).
+  int p_start = rfl(s_tiles[pb]);
+  int p_end = rfl(s_tiles[pb + 1]);
+  int p_len = seq_len_of(p.seqlens, pb, p.seqlen_add, p.max_len);
+  ConstI32 p_bt = as_const(p.bt + (int64_t)pb * p.bt_stride);
 
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int row = lane >> 4;  // DPP row
-  const int col = lane & 15;  // head (score layout) / V column
-  const int h0 = kvh * GQ;
-
-  const char *__restrict__ kbase = reinterpret_cast<const char *>(p.k);
-  const char *__restrict__ vbase = reinterpret_cast<const char *>(p.v);
-  const int ps_mask = (1 << p.ps_log2) - 1;
-  const uint32_t st_bytes = (uint32_t)p.c_st * 2u;
-  const uint64_t sp_bytes = (uint64_t)p.c_sp * 2u;
-  const uint32_t head_bytes = (uint32_t)kvh * ((uint32_t)p.c_sh * 2u);
-  const uint32_t k_lane_bytes = head_bytes + (uint32_t)row * 16u;  // + 64c
-  const uint32_t v_lane_bytes = head_bytes + (uint32_t)col * (VD * 2u);
-  const float c = p.scale_log2;
-
-  bool first_piece = true;
-  for (; b < B && s_tiles[b] < hi; ++b) {
-    const int sb = s_tiles[b], se = s_tiles[b + 1];
-    const int t0 = (lo > sb ? lo : sb) - sb;  // piece = tiles [t0, t1) of sequence b
-    const int t1 = (hi < se ? hi : se) - sb;
-    if (t1 <= t0) continue;
-    const int L = seq_len_of(p.seqlens, b, p.seqlen_add, p.max_len);
-    const int c_start = t0 * kTile;
-    const int sl = (t1 * kTile < L ? t1 * kTile : L) - c_start;  // tokens in the piece
-    const int ntiles = t1 - t0;
-    const ConstI32 btrow = as_const(p.bt + (int64_t)b * p.bt_stride);
-
-    // B operand of the QK MFMA: lane (row, col) holds q[head col][32c + 8row, +8).
-    uint4 qf[NCH];
+  auto make_tile = [&](int t, Tile &d, int (&lpg)[NPG]) {
+    if (t >= hi) {
+      d.b = pb;
+      d.tok0 = 0;
+      d.valid = 0;
+      d.flags = 0;
+      d.pg = 0;
 #pragma unroll
-    for (int cc = 0; cc < NCH; ++cc) {
-      qf[cc] = make_uint4(0u, 0u, 0u, 0u);
-      if (col < GQ)
-        qf[cc] = *reinterpret_cast<const uint4 *>(p.q + b * p.q_sb + (int64_t)(h0 + col) * p.q_sh +
-                                                   cc * 32 + row * 8);
+      for (int i = 0; i < NPG; ++i) lpg[i] = 0;
+      return;
     }
+    if (t >= p_end) {  // next sequence with tiles (rare, wave-uniform)
+      do {
+        ++pb;
+        p_start = p_end;
+        p_end = rfl(s_tiles[pb + 1]);
+      } while (t >= p_end);
+      p_len = seq_len_of(p.seqlens, pb, p.seqlen_add, p.max_len);
+      p_bt = as_const(p.bt + (int64_t)pb * p.bt_stride);
+    }
+    d.b = pb;
+    d.tok0 = (t - p_start) * kTile;
+    d.valid = min(kTile, p_len - d.tok0);
+    const bool seq_start = d.tok0 == 0, seq_end = d.tok0 + kTile >= p_len;
+    d.flags = ((t == lo || seq_start) ? kFirst : 0) | ((t == hi - 1 || seq_end) ? kLast : 0) |
+              (seq_start ? kSeqStart : 0) | (seq_end ? kSeqEnd : 0) | (t == lo ? kRangeStart : 0);
+    if constexpr (kLanePages) {
+      // Per-lane page ids: [0] for this lane's K token, [1+u] for its V tokens.
+      // Token positions clamp to the last valid token.
+      const int last = d.valid - 1;
+      lpg[0] = p_bt[(d.tok0 + min(col, last)) >> p.ps_log2];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        lpg[1 + u] = p_bt[(d.tok0 + min(4 * row + u, last)) >> p.ps_log2];
+      d.pg = 0;
+    } else {
+      d.pg = p_bt[d.tok0 >> p.ps_log2];
+    }
+  };
 
-    float m = -INFINITY;  // reference max (base 2) of head `col`, same in every row
-    float d = 0.f;        // partial denominator of head `col` over this row's tokens
-    float o[GQ][VD];
+  auto clamp_page = [&](int pg) -> int {
+    pg = pg < 0 ? 0 : pg;
+    return pg >= p.num_pages ? p.num_pages - 1 : pg;
+  };
+
+  struct Set {
+    uint4 k[NCH];
+    VFrag<VD> v[U];
+    uint4 q[NCH];
+    int lpg[NPG];
+    Tile d;
+  };
+
+  auto issue = [&](Set &s) {
+    const Tile &d = s.d;
+    const __amdgpu_buffer_rsrc_t rq =
+        make_srd(p.q + (int64_t)d.b * p.q_sb + (int64_t)kvh * GQ * p.q_sh,
+                 (d.flags & kFirst) ? q_bytes : 0);
+#pragma unroll
+    for (int cc = 0; cc < NCH; ++cc) s.q[cc] = buf_load16<0>(rq, q_off + cc * 64);
+    if constexpr (!kLanePages) {
+      const uint64_t tile_off = (uint64_t)(uint32_t)clamp_page(d.pg) * (uint64_t)p.sp_bytes +
+                                (uint64_t)(d.tok0 & ps_mask) * st + head_off;
+      const int bytes = d.valid > 0 ? (d.valid - 1) * (int)st + HD * 2 : 0;
+      const __amdgpu_buffer_rsrc_t rk = make_srd(p.k + tile_off, bytes);
+      const __amdgpu_buffer_rsrc_t rv = make_srd(p.v + tile_off, bytes);
+#pragma unroll
+      for (int cc = 0; cc < NCH; ++cc) s.k[cc] = buf_load16<kAuxStream>(rk, k_off + cc * 64);
+#pragma unroll
+      for (int u = 0; u < U; ++u) s.v[u].load_buf(rv, v_off[u]);
+    } else {
+      // Lane pages: every lane addresses its own page; positions past the
+      // sequence end were clamped to its last token (their scores are masked).
+      const int last = d.valid > 0 ? d.valid - 1 : 0;
+      {
+        const int pos = d.tok0 + min(col, last);
+        const uint64_t off = (uint64_t)(uint32_t)clamp_page(s.lpg[0]) * (uint64_t)p.sp_bytes +
+                             (uint64_t)(pos & ps_mask) * st + head_off + row * 16;
+#pragma unroll
+        for (int cc = 0; cc < NCH; ++cc) s.k[cc] = load_stream16(p.k + off + cc * 64);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int pos = d.tok0 + min(4 * row + u, last);
+        const uint64_t off = (uint64_t)(uint32_t)clamp_page(s.lpg[1 + u]) * (uint64_t)p.sp_bytes +
+                             (uint64_t)(pos & ps_mask) * st + head_off + col * (VD * 2);
+        s.v[u].load_ptr(p.v + off);
+      }
+    }
+  };
+
+  // Running state of the current piece.
+  float m = -INFINITY;  // reference max (base 2) of head `col`, same in every row
+  float dsum = 0.f;     // partial denominator of head `col` over this row's tokens
+  float o[GQ][VD];
+  uint4 qf[NCH];
+#pragma unroll
+  for (int g = 0; g < GQ; ++g)
+#pragma unroll
+    for (int j = 0; j < VD; ++j) o[g][j] = 0.f;
+#pragma unroll
+  for (int cc = 0; cc < NCH; ++cc) qf[cc] = make_uint4(0u, 0u, 0u, 0u);
+  bool piece_from_start = false;
+  bool piece_first_in_range = false;
+
+  auto finalize = [&](const Tile &d) {
+    const float dt = rows_sum(dsum);
 #pragma unroll
     for (int g = 0; g < GQ; ++g)
 #pragma unroll
-      for (int j = 0; j < VD; ++j) o[g][j] = 0.f;
-
-    auto clamp_page = [&](int pg) -> int {
-      pg = pg < 0 ? 0 : pg;
-      return pg >= p.num_pages ? p.num_pages - 1 : pg;
-    };
-    // Token positions clamp to the last valid token, so every address is a
-    // real row of this sequence (and in the tile's own page).
-    auto pos_of = [&](int tile, int t) -> int {
-      t += tile * kTile;
-      return c_start + (t < sl ? t : sl - 1);
-    };
-
-    // Per tile: page ids (scalar: [0] for the whole tile; lane: [0] K, [1+u] V).
-    constexpr int NPG = kLanePages ? 1 + U : 1;
-    int pg_a[NPG], pg_b[NPG];
-    uint4 ka[NCH], kb[NCH];
-    VFrag<VD> va[U], vb[U];
-
-    auto load_pages = [&](int tile, int (&pg)[NPG]) {
-      if constexpr (kLanePages) {
-        pg[0] = btrow[pos_of(tile, col) >> p.ps_log2];
-#pragma unroll
-        for (int u = 0; u < U; ++u) pg[1 + u] = btrow[pos_of(tile, 4 * row + u) >> p.ps_log2];
-      } else {
-        pg[0] = btrow[__builtin_amdgcn_readfirstlane(pos_of(tile, 0) >> p.ps_log2)];
-      }
-    };
-    auto load_kv = [&](int tile, const int (&pg)[NPG], uint4 (&kr)[NCH], VFrag<VD> (&vr)[U]) {
-      {
-        const int pos = pos_of(tile, col);
-        const uint64_t page_off = (uint64_t)(uint32_t)clamp_page(pg[0]) * sp_bytes;
-        const uint32_t off = (uint32_t)(pos & ps_mask) * st_bytes + k_lane_bytes;
-#pragma unroll
-        for (int cc = 0; cc < NCH; ++cc)
-          kr[cc] = *reinterpret_cast<const uint4 *>(kbase + page_off + off + cc * 64u);
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int pos = pos_of(tile, 4 * row + u);
-        const int pgv = kLanePages ? pg[kLanePages ? 1 + u : 0] : pg[0];
-        const uint64_t page_off = (uint64_t)(uint32_t)clamp_page(pgv) * sp_bytes;
-        const uint32_t off = (uint32_t)(pos & ps_mask) * st_bytes + v_lane_bytes;
-        vr[u] = VFrag<VD>::load(vbase + page_off + off);
-      }
-    };
-    // Lane-page ids (VMEM) are fetched before the K/V loads that follow them so
-    // waiting for an id never waits for K/V data; scalar ids (SMEM, unordered)
-    // after the K/V loads that consume the previous ids.
-    auto advance = [&](int tile, const int (&pg_next)[NPG], int (&pg_after)[NPG],
-                       uint4 (&kr)[NCH], VFrag<VD> (&vr)[U]) {
-      if constexpr (kLanePages) {
-        load_pages(tile + 2 * kWaves, pg_after);
-        load_kv(tile + kWaves, pg_next, kr, vr);
-      } else {
-        load_kv(tile + kWaves, pg_next, kr, vr);
-        load_pages(tile + 2 * kWaves, pg_after);
-      }
-    };
-    auto compute = [&](int tile, const uint4 (&kr)[NCH], const VFrag<VD> (&vr)[U]) {
-      // QK on the matrix cores; two accumulators halve the MFMA dependency chain.
-      f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int cc = 0; cc < NCH; cc += 2) {
-        acc0 = Mfma<T>::run(kr[cc], qf[cc], acc0);
-        acc1 = Mfma<T>::run(kr[cc + 1], qf[cc + 1], acc1);
-      }
-      float x[4];
-      bool need = false;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const bool valid = (col < GQ) & (tile * kTile + 4 * row + i < sl);
-        x[i] = valid ? (acc0[i] + acc1[i]) * c : -INFINITY;
-        need |= x[i] > m + kRescaleLog2;
-      }
-      if (__builtin_amdgcn_ballot_w64(need) != 0) {
-        // Rare, wave-uniform: move the reference of each head to the wave's
-        // tile maximum when it passed the reference by more than kRescaleLog2.
-        float mt = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-        mt = fmaxf(mt, xor_shfl(mt, 16));
-        mt = fmaxf(mt, xor_shfl(mt, 32));
-        const float mn = mt > m + kRescaleLog2 ? mt : m;
-        const float f = (mn == m) ? 1.f : fast_exp2(m - mn);  // m = -inf: f = 0
-        d *= f;
-        rescale_rows<GQ, VD>(o, f);
-        m = mn;
-      }
-      // m = -inf: this head has seen no valid token, its scores here are -inf too.
-      const float mr = m == -INFINITY ? 0.f : m;
-      float pr[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(x[i] - mr);
-      d += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        float v[VD];
-        vr[u].template widen<E>(v);
-        pv_accumulate<GQ, VD>(o, pr[u], v);
-      }
-    };
-
-    // Software pipeline over this wave's tiles of the piece: wave, wave +
-    // kWaves, ... Page ids run two tiles ahead of the math and K/V loads one
-    // tile ahead; two register sets (a/b) alternate so no copies are needed.
-    // The loop body runs two tiles and exits only at its latch, so the loads
-    // crossing the back edge are always the a-set of the next tile and the
-    // compiler never has to drain the load queue at the loop head. Loads past
-    // the wave's last tile clamp to the last valid token (cache hits).
-    const int ntw = wave < ntiles ? (ntiles - wave + kWaves - 1) / kWaves : 0;
-    if (ntw > 0) {
-      int tile = wave;
-      load_pages(tile, pg_a);
-      load_kv(tile, pg_a, ka, va);
-      load_pages(tile + kWaves, pg_b);
-      for (int i = 0; i + 1 < ntw; i += 2) {
-        advance(tile, pg_b, pg_a, kb, vb);
-        compute(tile, ka, va);
-        tile += kWaves;
-        advance(tile, pg_a, pg_b, ka, va);
-        compute(tile, kb, vb);
-        tile += kWaves;
-      }
-      if (ntw & 1) compute(tile, ka, va);
+      for (int j = 0; j < VD; ++j) o[g][j] = rows_sum(o[g][j]);
+    const int b = d.b;
+    if (piece_from_start && (d.flags & kSeqEnd)) {  // the whole sequence
+      static_for<GQ>([&](auto gc) {
+        constexpr int g = decltype(gc)::value;
+        const float Dg = row_bcast<g>(dt);
+        if ((g & 3) == row) {
+          const int h = kvh * GQ + g;
+          store_row<VD, E>(p.out + b * p.o_sb + h * p.o_sh + col * (VD * 2), o[g],
+                           Dg > 0.f ? 1.f / Dg : 0.f);
+        }
+      });
+      return;
     }
-
-    // Merge the four DPP rows of the wave (same reference max, different tokens).
-    d += xor_shfl(d, 16);
-    d += xor_shfl(d, 32);
+    // A piece: normalised output and base-2 LSE of each head to its slot.
+    const int slot = piece_first_in_range ? 0 : 1;
+    const int64_t pbase = ((int64_t)(kvh * ns + rr) * 2 + slot) * GQ;
+    static_for<GQ>([&](auto gc) {
+      constexpr int g = decltype(gc)::value;
+      const float Dg = row_bcast<g>(dt);
+      const float Mg = row_bcast<g>(m);
+      if ((g & 3) == row) {
+        const float inv = Dg > 0.f ? 1.f / Dg : 0.f;
+        float4 *dst = reinterpret_cast<float4 *>(p.ws_o + (pbase + g) * HD + col * VD);
 #pragma unroll
-    for (int g = 0; g < GQ; ++g) {
-#pragma unroll
-      for (int j = 0; j < VD; ++j) {
-        float t = o[g][j];
-        t += xor_shfl(t, 16);
-        t += xor_shfl(t, 32);
-        o[g][j] = t;
+        for (int j = 0; j < VD / 4; ++j)
+          dst[j] = make_float4(o[g][4 * j] * inv, o[g][4 * j + 1] * inv, o[g][4 * j + 2] * inv,
+                               o[g][4 * j + 3] * inv);
+        if (col == 0) p.ws_lse[pbase + g] = Dg > 0.f ? Mg + __log2f(Dg) : -INFINITY;
       }
-    }
-    if (row == 0) {
+    });
+  };
+
+  auto compute = [&](Set &s) {
+    const Tile &d = s.d;
+    if (d.flags & kFirst) {
+      m = -INFINITY;
+      dsum = 0.f;
 #pragma unroll
       for (int g = 0; g < GQ; ++g)
 #pragma unroll
-        for (int j = 0; j < VD; ++j) sm_o[wave][g][col * VD + j] = o[g][j];
-      if (col < GQ) {
-        sm_m[wave][col] = m;
-        sm_d[wave][col] = d;
-      }
+        for (int j = 0; j < VD; ++j) o[g][j] = 0.f;
+#pragma unroll
+      for (int cc = 0; cc < NCH; ++cc) qf[cc] = s.q[cc];
+      piece_from_start = (d.flags & kSeqStart) != 0;
+      piece_first_in_range = (d.flags & kRangeStart) != 0;
     }
-    __syncthreads();
+    // QK on the matrix cores; two accumulators halve the MFMA dependency chain.
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int cc = 0; cc < NCH; cc += 2) {
+      acc0 = Mfma<T>::run(s.k[cc], qf[cc], acc0);
+      acc1 = Mfma<T>::run(s.k[cc + 1], qf[cc + 1], acc1);
+    }
+    float x[4];
+    bool need = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool valid = (col < GQ) & (4 * row + i < d.valid);
+      x[i] = valid ? (acc0[i] + acc1[i]) * c : -INFINITY;
+      need |= x[i] > m + kRescaleLog2;
+    }
+    if (__builtin_amdgcn_ballot_w64(need) != 0) {
+      // Rare, wave-uniform: move the reference of each head to the wave's
+      // tile maximum when it passed the reference by more than kRescaleLog2.
+      const float mt = rows_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
+      const float mn = mt > m + kRescaleLog2 ? mt : m;
+      const float f = (mn == m) ? 1.f : fast_exp2(m - mn);  // m = -inf: f = 0
+      dsum *= f;
+      rescale_rows<GQ, VD>(o, f);
+      m = mn;
+    }
+    // m = -inf: this head has seen no valid token, its scores here are -inf too.
+    const float mr = m == -INFINITY ? 0.f : m;
+    float pr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(x[i] - mr);
+    dsum += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float v[VD];
+      s.v[u].template widen<E>(v);
+      pv_accumulate<GQ, VD>(o, pr[u], v);
+    }
+    if (d.flags & kLast) finalize(d);
+  };
 
-    // Merge the waves; a whole sequence writes its output, a piece its partial.
-    const bool whole = (t0 == 0) && (t1 == se - sb);
-    const int slot = first_piece ? 0 : 1;
-    for (int idx = threadIdx.x; idx < GQ * HD; idx += kThreads) {
-      const int g = idx / HD, dim = idx % HD;
-      float M = -INFINITY;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w][g]);
-      float D = 0.f, O = 0.f;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        const float mw = sm_m[w][g];
-        const float f = (mw == -INFINITY) ? 0.f : fast_exp2(mw - M);
-        D = fmaf(sm_d[w][g], f, D);
-        O = fmaf(sm_o[w][g][dim], f, O);
-      }
-      const float res = D > 0.f ? O / D : 0.f;
-      const int h = h0 + g;
-      if (whole) {
-        p.out[b * p.o_sb + (int64_t)h * p.o_sh + dim] = E::narrow(res);
-      } else {
-        const int64_t ps = ((int64_t)h * R + r) * 2 + slot;
-        p.ws_o[ps * HD + dim] = res;
-        if (dim == 0) p.ws_lse[ps] = D > 0.f ? M + __log2f(D) : -INFINITY;
-      }
+  // Software pipeline over the range: tile descriptors (and page ids) are
+  // built two tiles ahead of the math, K/V/q loads issued one tile ahead into
+  // the other register set. The body runs two tiles and exits only at its
+  // latch, so the loads crossing the back edge are always the a-set of the
+  // next tile. The descriptor of the padding tile past the range end covers
+  // no bytes, so its loads cost nothing.
+  Set sa, sb;
+  Tile dn;
+  int lpg_n[NPG];
+  make_tile(lo, sa.d, sa.lpg);
+  issue(sa);
+  make_tile(lo + 1, sb.d, sb.lpg);
+  const int ntiles = hi - lo;
+  int t = lo;
+  auto step = [&](Set &cur, Set &nxt) {
+    // nxt.d (tile t+1) is ready: issue its loads, build tile t+2, then the math of tile t.
+    if constexpr (kLanePages) {
+      make_tile(t + 2, dn, lpg_n);
+      issue(nxt);
+    } else {
+      issue(nxt);
+      make_tile(t + 2, dn, lpg_n);
     }
-    first_piece = false;
-    __syncthreads();  // sm_* are reused by the next piece
+    compute(cur);
+    cur.d = dn;
+#pragma unroll
+    for (int i = 0; i < NPG; ++i) cur.lpg[i] = lpg_n[i];
+    ++t;
+  };
+  for (int i = 0; i + 1 < ntiles; i += 2) {
+    step(sa, sb);
+    step(sb, sa);
   }
+  if (ntiles & 1) compute(sa);
 }
 
-// LSE combine: HD/4 threads per (sequence, head), float4 per thread. Sequences
-// that lie inside one range were written by the partial kernel and are skipped.
+template <int HD, int GQ, typename T, bool kLanePages, int kMinWgPerCu>
+__global__ __launch_bounds__(kThreads, kMinWgPerCu) void split_partial_kernel(DecodeParams p) {
+  extern __shared__ int32_t s_tiles[];  // [B + 1]
+  __shared__ int s_wave_tot[kWaves];
+
+  tile_prefix(p, s_tiles, s_wave_tot);  // ends with a barrier
+  zero_empty<HD, GQ>(p, s_tiles);
+  const int B = p.batch;
+  if (blockIdx.x == 0 && blockIdx.y == 0) {
+    for (int i = threadIdx.x; i <= B; i += kThreads) p.ws_s[i] = s_tiles[i];
+  }
+
+  const int wave = rfl(threadIdx.x >> 6);
+  const int KH = p.heads_per_wg;
+  const int kh = wave % KH, sub = wave / KH;
+  const int kvh = blockIdx.x * KH + kh;
+  const int NT = rfl(s_tiles[B]);
+  const int R = min(p.num_ranges, NT);  // every range holds >= 1 tile
+  const int rr = blockIdx.y * p.subs + sub;
+  if (sub >= p.subs || kvh >= p.hkv || rr >= R) return;
+  const int lo = range_lo(rr, R, NT), hi = range_lo(rr + 1, R, NT);
+  run_range<HD, GQ, T, kLanePages>(p, s_tiles, kvh, rr, R, NT, lo, hi);
+}
+
+struct CombineParams {
+  const float *ws_o;
+  const float *ws_lse;
+  const int32_t *ws_s;
+  char *out;
+  int64_t o_sb, o_sh;  // bytes
+  int batch;
+  int hq;
+  int gq;
+  int num_ranges;
+};
+
+// LSE combine: HD/4 threads per (sequence, head), one float4 of the output
+// each. Sequences that lie inside one range were written by the partial kernel
+// and are skipped, as are empty ones (zero-filled there). Pieces are folded in
+// range order, eight loads in flight per step, so the result does not depend
+// on timing.
 template <int HD, typename T>
 __global__ __launch_bounds__(256) void split_combine_kernel(CombineParams p) {
   using E = Elem<T>;
   constexpr int TPH = HD / 4;
-  constexpr int HPB = 256 / TPH;
-  const int hid = blockIdx.x * HPB + threadIdx.x / TPH;
+  constexpr int kUnroll = 8;
+  const int gid = blockIdx.x * 256 + threadIdx.x;
+  const int hid = gid / TPH;
   if (hid >= p.batch * p.hq) return;
-  const int t = threadIdx.x % TPH;
+  const int c = gid % TPH;
   const int b = hid / p.hq, h = hid % p.hq;
-  const int R = p.num_ranges;
+  const int kvh = h / p.gq, g = h % p.gq;
   const int NT = p.ws_s[p.batch];
-  const int sb = p.ws_s[b], nt = p.ws_s[b + 1] - sb;
-  uint2 *dst = reinterpret_cast<uint2 *>(p.out + b * p.o_sb + (int64_t)h * p.o_sh + t * 4);
-  // The prefix sums come from the partial launch; prefix sums that do not
-  // describe tiles inside [0, NT) (a workspace the partial stage did not fill)
-  // give zeros, so every range index below stays in [0, R).
-  if (nt <= 0 || sb < 0 || NT <= 0 || sb + nt > NT) {
-    *dst = make_uint2(0u, 0u);  // empty sequence: zero output
-    return;
-  }
-  const int ra = range_of(sb, R, NT), rb = range_of(sb + nt - 1, R, NT);
-  if (ra == rb) return;  // whole sequence inside one range: already written
-
-  // Pieces, walked range by range over the sequence's tiles: range ra holds
-  // slot 0 when the sequence starts that range (else slot 1); every later
-  // range holds slot 0. Two passes: the LSE maximum, then the weighted sum.
+  const int sb = p.ws_s[b], se = p.ws_s[b + 1];
+  // Prefix sums that do not describe tiles inside [0, NT) (a workspace the
+  // partial kernel did not fill) are skipped, so every index stays in range.
+  if (se <= sb || sb < 0 || se > NT) return;
+  const int R = min(p.num_ranges, NT);
+  const int ra = range_of(sb, R, NT), rb = range_of(se - 1, R, NT);
+  if (ra == rb) return;
   const int slot_a = (range_lo(ra, R, NT) == sb) ? 0 : 1;
-  const int tend = sb + nt;
-  float M = -INFINITY;
-  for (int tt = sb; tt < tend;) {
-    const int q = range_of(tt, R, NT);
-    const int64_t ps = ((int64_t)h * R + q) * 2 + (q == ra ? slot_a : 0);
-    M = fmaxf(M, p.ws_lse[ps]);
-    tt = range_lo(q + 1, R, NT);
-  }
+  const int ns = p.num_ranges;
+  float M = -INFINITY, W = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  float wsum = 0.f;
-  if (M != -INFINITY) {
-    for (int tt = sb; tt < tend;) {
-      const int q = range_of(tt, R, NT);
-      const int64_t ps = ((int64_t)h * R + q) * 2 + (q == ra ? slot_a : 0);
-      const float l = p.ws_lse[ps];
-      const float w = (l == -INFINITY) ? 0.f : fast_exp2(l - M);
-      const float4 v = reinterpret_cast<const float4 *>(p.ws_o + ps * HD)[t];
-      acc.x = fmaf(w, v.x, acc.x);
-      acc.y = fmaf(w, v.y, acc.y);
-      acc.z = fmaf(w, v.z, acc.z);
-      acc.w = fmaf(w, v.w, acc.w);
-      wsum += w;
-      tt = range_lo(q + 1, R, NT);
+  for (int q0 = ra; q0 <= rb; q0 += kUnroll) {
+    float l[kUnroll];
+    float4 ov[kUnroll];
+#pragma unroll
+    for (int i = 0; i < kUnroll; ++i) {
+      const int q = min(q0 + i, rb);
+      const int64_t ps = ((int64_t)(kvh * ns + q) * 2 + (q == ra ? slot_a : 0)) * p.gq + g;
+      l[i] = (q0 + i <= rb) ? p.ws_lse[ps] : -INFINITY;
+      ov[i] = reinterpret_cast<const float4 *>(p.ws_o + ps * HD)[c];
     }
+    float mx = l[0];
+#pragma unroll
+    for (int i = 1; i < kUnroll; ++i) mx = fmaxf(mx, l[i]);
+    const float Mn = fmaxf(M, mx);
+    if (Mn == -INFINITY) continue;
+    const float fo = (M == -INFINITY) ? 0.f : fast_exp2(M - Mn);
+    W *= fo;
+    acc.x *= fo;
+    acc.y *= fo;
+    acc.z *= fo;
+    acc.w *= fo;
+#pragma unroll
+    for (int i = 0; i < kUnroll; ++i) {
+      const float w = (l[i] == -INFINITY) ? 0.f : fast_exp2(l[i] - Mn);
+      W += w;
+      acc.x = fmaf(w, ov[i].x, acc.x);
+      acc.y = fmaf(w, ov[i].y, acc.y);
+      acc.z = fmaf(w, ov[i].z, acc.z);
+      acc.w = fmaf(w, ov[i].w, acc.w);
+    }
+    M = Mn;
   }
-  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
-  const uint16_t r0 = E::narrow(acc.x * inv), r1 = E::narrow(acc.y * inv);
-  const uint16_t r2 = E::narrow(acc.z * inv), r3 = E::narrow(acc.w * inv);
-  *dst = make_uint2((uint32_t)r0 | ((uint32_t)r1 << 16), (uint32_t)r2 | ((uint32_t)r3 << 16));
+  const float inv = W > 0.f ? 1.f / W : 0.f;
+  const uint32_t w0 = (uint32_t)E::narrow(acc.x * inv) | ((uint32_t)E::narrow(acc.y * inv) << 16);
+  const uint32_t w1 = (uint32_t)E::narrow(acc.z * inv) | ((uint32_t)E::narrow(acc.w * inv) << 16);
+  *reinterpret_cast<uint2 *>(p.out + b * p.o_sb + h * p.o_sh + c * 8) = make_uint2(w0, w1);
 }
 
 // ---------------------------------------------------------------------------
-// Host side: argument checks, template selection, launches.
+// Host side: argument checks, template selection, launch.
 
 static bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
@@ -614,7 +770,7 @@ static int check_split_args(const SplitArgs &a) {
   if (a.num_splits > 65535 || a.batch > kMaxBatch || a.hkv > 65535) return MXFA_EUNSUPPORTED;
   const int64_t max_len = (int64_t)a.btw * a.ps;
   if (max_len > (int64_t)1 << 30) return MXFA_EUNSUPPORTED;
-  // Total tiles per kv head must fit int32: B * ceil(max_len / 16).
+  // Total tiles must fit int32: B * ceil(max_len / 16).
   if ((int64_t)a.batch * ((max_len + kTile - 1) / kTile) >= ((int64_t)1 << 31))
     return MXFA_EUNSUPPORTED;
   // 16-byte fragments: pointers and every stride must keep 8-element alignment.
@@ -622,10 +778,14 @@ static int check_split_args(const SplitArgs &a) {
   if ((a.q_sb | a.q_sh | a.c_sp | a.c_st | a.c_sh) & 7) return MXFA_EINVAL;
   if (a.q_sb < 0 || a.q_sh < 0 || a.c_sp < 0 || a.c_st < 0 || a.c_sh < 0 || a.bt_stride < 0)
     return MXFA_EINVAL;
-  // In-page byte offsets are 32-bit: (PS-1)*token + (HKV-1)*head + HD elements.
-  if (((int64_t)(a.ps - 1) * a.c_st + (int64_t)(a.hkv - 1) * a.c_sh + a.hd) * 2 >=
-      ((int64_t)1 << 32))
+  // Rows must not overlap: the per-tile descriptors cover whole rows.
+  if ((a.ps > 1 && a.c_st < a.hd) || (gq > 1 && a.q_sh < a.hd)) return MXFA_EINVAL;
+  // Byte offsets inside a tile and inside a q group are 32-bit.
+  if (((int64_t)(kTile - 1) * a.c_st + a.hd) * 2 >= ((int64_t)1 << 30))
     return MXFA_EUNSUPPORTED;
+  if ((int64_t)(a.ps - 1) * a.c_st * 2 >= ((int64_t)1 << 32) || a.c_sh * 2 >= ((int64_t)1 << 32))
+    return MXFA_EUNSUPPORTED;
+  if (((int64_t)(gq - 1) * a.q_sh + a.hd) * 2 >= ((int64_t)1 << 30)) return MXFA_EUNSUPPORTED;
   if (((uintptr_t)a.out & 7u) || ((a.o_sb | a.o_sh) & 3) || a.o_sb < 0 || a.o_sh < 0)
     return MXFA_EINVAL;
   if (!a.ws || !aligned16(a.ws)) return MXFA_EWORKSPACE;
@@ -633,30 +793,45 @@ static int check_split_args(const SplitArgs &a) {
   return MXFA_OK;
 }
 
-static DecodeParams make_params(const SplitArgs &a) {
+struct Grid {
+  int heads_per_wg, subs, gx, gy;
+};
+
+static Grid grid_for(int hkv, int num_splits) {
+  Grid g;
+  g.heads_per_wg = hkv < kMaxHeadsPerWg ? hkv : kMaxHeadsPerWg;
+  g.subs = kWaves / g.heads_per_wg;
+  g.gx = (hkv + g.heads_per_wg - 1) / g.heads_per_wg;
+  g.gy = (num_splits + g.subs - 1) / g.subs;
+  return g;
+}
+
+static DecodeParams make_params(const SplitArgs &a, const Grid &g) {
   const WsLayout w = ws_layout(a.batch, a.hq, a.hd, a.num_splits);
   DecodeParams p;
-  p.q = (const uint16_t *)a.q;
-  p.q_sb = a.q_sb;
-  p.q_sh = a.q_sh;
-  p.k = (const uint16_t *)a.k;
-  p.v = (const uint16_t *)a.v;
-  p.c_sp = a.c_sp;
-  p.c_st = a.c_st;
-  p.c_sh = a.c_sh;
+  p.q = (const char *)a.q;
+  p.q_sb = a.q_sb * 2;
+  p.q_sh = a.q_sh * 2;
+  p.k = (const char *)a.k;
+  p.v = (const char *)a.v;
+  p.sp_bytes = a.c_sp * 2;
+  p.st_bytes = (uint32_t)(a.c_st * 2);
+  p.sh_bytes = (uint32_t)(a.c_sh * 2);
   p.bt = a.bt;
   p.bt_stride = a.bt_stride;
   p.seqlens = a.seqlens;
-  p.out = (uint16_t *)a.out;
-  p.o_sb = a.o_sb;
-  p.o_sh = a.o_sh;
+  p.out = (char *)a.out;
+  p.o_sb = a.o_sb * 2;
+  p.o_sh = a.o_sh * 2;
   p.ws_o = (float *)a.ws;
   p.ws_lse = (float *)a.ws + w.o_floats;
   p.ws_s = (int32_t *)((float *)a.ws + w.o_floats + w.lse_floats);
   p.scale_log2 = a.scale * kLog2e;
   p.seqlen_add = a.seqlen_add;
   p.batch = a.batch;
-  p.hq = a.hq;
+  p.hkv = a.hkv;
+  p.heads_per_wg = g.heads_per_wg;
+  p.subs = g.subs;
   p.ps_log2 = ilog2_exact(a.ps);
   p.max_len = a.btw * a.ps;
   p.num_pages = a.num_pages;
@@ -664,36 +839,32 @@ static DecodeParams make_params(const SplitArgs &a) {
   return p;
 }
 
+// Workgroups per CU the kernel is compiled for: HD 64 keeps under 128 VGPRs so
+// two workgroups (16 waves) share a CU; HD 128 runs one (8 waves, 256 VGPRs).
+template <int HD>
+constexpr int kWgPerCu = HD == 64 ? 2 : 1;
+
 template <int HD, int GQ, typename T>
-static int launch_partial_t(const DecodeParams &p, int hkv, hipStream_t st) {
-  dim3 grid(hkv, p.num_ranges);
+static int launch_t(const DecodeParams &p, const Grid &g, hipStream_t st) {
+  dim3 grid(g.gx, g.gy);
   const size_t lds = (size_t)(p.batch + 1) * sizeof(int32_t);
-  if ((1 << p.ps_log2) >= kTile)
-    hipLaunchKernelGGL((split_partial_kernel<HD, GQ, T, false>), grid, dim3(kThreads), lds, st, p);
+  if (p.ps_log2 >= 4)
+    hipLaunchKernelGGL((split_partial_kernel<HD, GQ, T, false, kWgPerCu<HD>>), grid,
+                       dim3(kThreads), lds, st, p);
   else
-    hipLaunchKernelGGL((split_partial_kernel<HD, GQ, T, true>), grid, dim3(kThreads), lds, st, p);
+    hipLaunchKernelGGL((split_partial_kernel<HD, GQ, T, true, kWgPerCu<HD>>), grid,
+                       dim3(kThreads), lds, st, p);
   return hipGetLastError() == hipSuccess ? MXFA_OK : MXFA_ELAUNCH;
 }
 
 template <int HD, typename T>
-static int launch_partial_gq(const DecodeParams &p, int gq, int hkv, hipStream_t st) {
+static int launch_gq(const DecodeParams &p, const Grid &g, int gq, hipStream_t st) {
   switch (gq) {
-    case 2: return launch_partial_t<HD, 2, T>(p, hkv, st);
-    case 4: return launch_partial_t<HD, 4, T>(p, hkv, st);
-    case 8: return launch_partial_t<HD, 8, T>(p, hkv, st);
+    case 2: return launch_t<HD, 2, T>(p, g, st);
+    case 4: return launch_t<HD, 4, T>(p, g, st);
+    case 8: return launch_t<HD, 8, T>(p, g, st);
   }
   return MXFA_EUNSUPPORTED;
-}
-
-static int launch_partial(const SplitArgs &a, hipStream_t st) {
-  const DecodeParams p = make_params(a);
-  const int gq = a.hq / a.hkv;
-  if (a.dtype == MXFA_DTYPE_BF16) {
-    return a.hd == 128 ? launch_partial_gq<128, BF16>(p, gq, a.hkv, st)
-                       : launch_partial_gq<64, BF16>(p, gq, a.hkv, st);
-  }
-  return a.hd == 128 ? launch_partial_gq<128, F16>(p, gq, a.hkv, st)
-                     : launch_partial_gq<64, F16>(p, gq, a.hkv, st);
 }
 
 template <int HD, typename T>
@@ -705,22 +876,30 @@ static int launch_combine_t(const CombineParams &c, hipStream_t st) {
   return hipGetLastError() == hipSuccess ? MXFA_OK : MXFA_ELAUNCH;
 }
 
-static int launch_combine(void *ws, void *out, int64_t o_sb, int64_t o_sh, int batch, int hq,
-                          int hd, int dtype, int ns, hipStream_t st) {
-  const WsLayout w = ws_layout(batch, hq, hd, ns);
+static int launch(const SplitArgs &a, hipStream_t st) {
+  const Grid g = grid_for(a.hkv, a.num_splits);
+  const DecodeParams p = make_params(a, g);
+  const int gq = a.hq / a.hkv;
+  int rc;
+  if (a.dtype == MXFA_DTYPE_BF16)
+    rc = a.hd == 128 ? launch_gq<128, BF16>(p, g, gq, st) : launch_gq<64, BF16>(p, g, gq, st);
+  else
+    rc = a.hd == 128 ? launch_gq<128, F16>(p, g, gq, st) : launch_gq<64, F16>(p, g, gq, st);
+  if (rc != MXFA_OK) return rc;
   CombineParams c;
-  c.ws_o = (const float *)ws;
-  c.ws_lse = (const float *)ws + w.o_floats;
-  c.ws_s = (const int32_t *)((const float *)ws + w.o_floats + w.lse_floats);
-  c.out = (uint16_t *)out;
-  c.o_sb = o_sb;
-  c.o_sh = o_sh;
-  c.batch = batch;
-  c.hq = hq;
-  c.num_ranges = ns;
-  if (dtype == MXFA_DTYPE_BF16)
-    return hd == 128 ? launch_combine_t<128, BF16>(c, st) : launch_combine_t<64, BF16>(c, st);
-  return hd == 128 ? launch_combine_t<128, F16>(c, st) : launch_combine_t<64, F16>(c, st);
+  c.ws_o = p.ws_o;
+  c.ws_lse = p.ws_lse;
+  c.ws_s = p.ws_s;
+  c.out = p.out;
+  c.o_sb = p.o_sb;
+  c.o_sh = p.o_sh;
+  c.batch = a.batch;
+  c.hq = a.hq;
+  c.gq = gq;
+  c.num_ranges = a.num_splits;
+  if (a.dtype == MXFA_DTYPE_BF16)
+    return a.hd == 128 ? launch_combine_t<128, BF16>(c, st) : launch_combine_t<64, BF16>(c, st);
+  return a.hd == 128 ? launch_combine_t<128, F16>(c, st) : launch_combine_t<64, F16>(c, st);
 }
 
 }  // namespace mxfa
@@ -734,7 +913,8 @@ int mxfa_abi_version(void) { return MXFA_ABI_VERSION; }
 const char *mxfa_strerror(int code) {
   switch (code) {
     case MXFA_OK: return "ok";
-    case MXFA_EUNSUPPORTED: return "unsupported configuration (head dim, GQA ratio, dtype or page size)";
+    case MXFA_EUNSUPPORTED:
+      return "unsupported configuration (head dim, GQA ratio, dtype or page size)";
     case MXFA_EINVAL: return "invalid argument (null pointer, size, alignment or stride)";
     case MXFA_EWORKSPACE: return "workspace missing or too small";
     case MXFA_ELAUNCH: return "kernel launch failed";
@@ -748,18 +928,15 @@ int mxfa_split_heuristic(int batch, int q_heads, int kv_heads, int head_dim, int
   if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || page_size <= 0 ||
       block_table_width <= 0 || num_cus <= 0)
     return MXFA_EINVAL;
-  // One workgroup (one wave per SIMD) per CU streams fastest (measured on
-  // MI355X across the GQ x HD cells); a second one per CU pays where the math
-  // per byte is highest (HD 64 with GQ 8) and where block tables are short
-  // (many short sequences, so more pieces to merge per range).
+  // One range per wave: kWgPerCu workgroups of 8 waves fill every CU, and each
+  // wave streams one (kv head, range). The kernel lowers the count to the real
+  // tile total on the device.
+  const Grid g = grid_for(kv_heads, 1);
+  const int64_t per_cu = head_dim == 64 ? kWgPerCu<64> : kWgPerCu<128>;
+  int64_t n = (int64_t)num_cus * per_cu * g.subs / g.gx;
   const int64_t cap = (int64_t)block_table_width * page_size;
-  const int gq = q_heads / kv_heads;
-  const int64_t per_cu = ((head_dim == 64 && gq >= 8) || cap < 2048) ? 2 : 1;
-  const int64_t kMinTiles = 4;
   const int64_t cap_tiles = (int64_t)batch * ((cap + kTile - 1) / kTile);
-  int64_t n = ((int64_t)num_cus * per_cu + kv_heads - 1) / kv_heads;
-  const int64_t by_tiles = (cap_tiles + kMinTiles - 1) / kMinTiles;
-  if (n > by_tiles) n = by_tiles;
+  if (n > cap_tiles) n = cap_tiles;
   if (n < 1) n = 1;
   if (n > 65535) n = 65535;
   *num_splits = (int)n;
@@ -781,61 +958,40 @@ int mxfa_split_decode_launch(const void *q, int64_t q_stride_b, int64_t q_stride
                              int64_t bt_stride, const int32_t *seqlens, int seqlen_add,
                              void *out, int64_t out_stride_b, int64_t out_stride_h,
                              void *workspace, size_t workspace_bytes_, float scale, int batch,
-                             int q_heads, int kv_heads, int head_dim, int page_size,
-                             int block_table_width, int num_pages, int dtype, int num_splits,
-                             void *stream) {
-  SplitArgs a{q,         q_stride_b,       q_stride_h,   k_cache,      v_cache,
-              cache_stride_page, cache_stride_token, cache_stride_head, block_table, bt_stride,
-              seqlens,   seqlen_add,       out,          out_stride_b, out_stride_h,
-              workspace, workspace_bytes_, scale,        batch,        q_heads,
-              kv_heads,  head_dim,         page_size,    block_table_width, num_pages,
-              dtype,     num_splits};
-  int rc = check_split_args(a);
+                             int q_heads,
+                             int kv_heads, int head_dim, int page_size, int block_table_width,
+                             int num_pages, int dtype, int num_splits, void *stream) {
+  SplitArgs a;
+  a.q = q;
+  a.q_sb = q_stride_b;
+  a.q_sh = q_stride_h;
+  a.k = k_cache;
+  a.v = v_cache;
+  a.c_sp = cache_stride_page;
+  a.c_st = cache_stride_token;
+  a.c_sh = cache_stride_head;
+  a.bt = block_table;
+  a.bt_stride = bt_stride;
+  a.seqlens = seqlens;
+  a.seqlen_add = seqlen_add;
+  a.out = out;
+  a.o_sb = out_stride_b;
+  a.o_sh = out_stride_h;
+  a.ws = workspace;
+  a.ws_bytes = workspace_bytes_;
+  a.scale = scale;
+  a.batch = batch;
+  a.hq = q_heads;
+  a.hkv = kv_heads;
+  a.hd = head_dim;
+  a.ps = page_size;
+  a.btw = block_table_width;
+  a.num_pages = num_pages;
+  a.dtype = dtype;
+  a.num_splits = num_splits;
+  const int rc = check_split_args(a);
   if (rc != MXFA_OK) return rc;
-  hipStream_t st = (hipStream_t)stream;
-  rc = launch_partial(a, st);
-  if (rc != MXFA_OK) return rc;
-  return launch_combine(workspace, out, out_stride_b, out_stride_h, batch, q_heads, head_dim,
-                        dtype, num_splits, st);
-}
-
-int mxfa_split_decode_partial_launch(const void *q, int64_t q_stride_b, int64_t q_stride_h,
-                                     const void *k_cache, const void *v_cache,
-                                     int64_t cache_stride_page, int64_t cache_stride_token,
-                                     int64_t cache_stride_head, const int32_t *block_table,
-                                     int64_t bt_stride, const int32_t *seqlens, int seqlen_add,
-                                     void *out, int64_t out_stride_b, int64_t out_stride_h,
-                                     void *workspace, size_t workspace_bytes_, float scale,
-                                     int batch, int q_heads, int kv_heads, int head_dim,
-                                     int page_size, int block_table_width, int num_pages,
-                                     int dtype, int num_splits, void *stream) {
-  SplitArgs a{q,         q_stride_b,       q_stride_h,   k_cache,      v_cache,
-              cache_stride_page, cache_stride_token, cache_stride_head, block_table, bt_stride,
-              seqlens,   seqlen_add,       out,          out_stride_b, out_stride_h,
-              workspace, workspace_bytes_, scale,        batch,        q_heads,
-              kv_heads,  head_dim,         page_size,    block_table_width, num_pages,
-              dtype,     num_splits};
-  int rc = check_split_args(a);
-  if (rc != MXFA_OK) return rc;
-  return launch_partial(a, (hipStream_t)stream);
-}
-
-int mxfa_split_decode_combine_launch(void *workspace, size_t workspace_bytes_, void *out,
-                                     int64_t out_stride_b, int64_t out_stride_h, int batch,
-                                     int q_heads, int head_dim, int dtype, int num_splits,
-                                     void *stream) {
-  if (!workspace || !out) return MXFA_EINVAL;
-  if (batch <= 0 || q_heads <= 0 || num_splits <= 0) return MXFA_EINVAL;
-  if (head_dim != 64 && head_dim != 128) return MXFA_EUNSUPPORTED;
-  if (dtype != MXFA_DTYPE_F16 && dtype != MXFA_DTYPE_BF16) return MXFA_EUNSUPPORTED;
-  if (batch > kMaxBatch || num_splits > 65535) return MXFA_EUNSUPPORTED;
-  if (!aligned16(workspace) || ((uintptr_t)out & 7u) || ((out_stride_b | out_stride_h) & 3) ||
-      out_stride_b < 0 || out_stride_h < 0)
-    return MXFA_EINVAL;
-  if (workspace_bytes_ < ws_layout(batch, q_heads, head_dim, num_splits).bytes)
-    return MXFA_EWORKSPACE;
-  return launch_combine(workspace, out, out_stride_b, out_stride_h, batch, q_heads, head_dim,
-                        dtype, num_splits, (hipStream_t)stream);
+  return launch(a, (hipStream_t)stream);
 }
 
 }  // extern "C"

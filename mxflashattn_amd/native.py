@@ -2,8 +2,8 @@
 
 This module is the thin host layer between torch tensors and the C entry
 points: it checks shapes, passes raw device pointers and element strides, keeps
-a per-(device, stream) workspace so steady-state calls allocate nothing, and
-launches on the caller's current HIP stream without synchronising.
+a per-(device, stream) workspace so steady-state calls allocate nothing, and launches on the caller's current HIP stream without
+synchronising.
 
 Reference counterpart: the pybind module ``mxmmain`` (``csrc_native/m1_binding.cpp``),
 ``paged_decode_split`` at ``csrc_native/m1_binding.cpp:78-115``.
@@ -24,7 +24,7 @@ LIB_PATH = Path(
     os.environ.get("MXFLASHATTN_AMD_LIB")
     or Path(__file__).resolve().parent / "_lib" / "libmxfa_mi355x.so"
 )
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 MXFA_OK = 0
 MXFA_EUNSUPPORTED = -1
@@ -44,8 +44,6 @@ EXPORTED_SYMBOLS = (
     "mxfa_split_heuristic",
     "mxfa_split_decode_workspace_size",
     "mxfa_split_decode_launch",
-    "mxfa_split_decode_partial_launch",
-    "mxfa_split_decode_combine_launch",
     "mxfa_reshape_and_cache_launch",
     "mxfa_append_kv_launch",
 )
@@ -74,15 +72,6 @@ _SIGNATURES = {
         _i,
         [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _p, _i64, _i64, _p, _sz,
          _f, _i, _i, _i, _i, _i, _i, _i, _i, _i, _p],
-    ),
-    "mxfa_split_decode_partial_launch": (
-        _i,
-        [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _p, _i64, _i64, _p, _sz,
-         _f, _i, _i, _i, _i, _i, _i, _i, _i, _i, _p],
-    ),
-    "mxfa_split_decode_combine_launch": (
-        _i,
-        [_p, _sz, _p, _i64, _i64, _i, _i, _i, _i, _i, _p],
     ),
     "mxfa_reshape_and_cache_launch": (
         _i,
@@ -176,7 +165,11 @@ def num_cus(device_index: int) -> int:
 
 
 class _Workspace:
-    """Grow-only fp32 scratch per (device, stream); reused across calls."""
+    """Grow-only scratch per (device, stream), reused across calls.
+
+    A launch on one stream never shares its workspace with another stream's
+    launches, so calls on different streams cannot race on it.
+    """
 
     def __init__(self) -> None:
         self._buffers: dict[tuple[int, int], torch.Tensor] = {}
@@ -269,19 +262,22 @@ def _launch_args(q, k_cache, v_cache, block_table, cache_seqlens, out, workspace
     return (
         q.data_ptr(), qs[0], qs[-2], k_cache.data_ptr(), v_cache.data_ptr(), cs[0], cs[1], cs[2],
         block_table.data_ptr(), block_table.stride(0), cache_seqlens.data_ptr(), seqlen_add,
-        out.data_ptr(), os_[0], os_[-2], workspace, ws_bytes, float(softmax_scale), batch, hq,
-        hkv, hd, ps, block_table.shape[1], pages, DTYPE_CODES[q.dtype], num_splits,
-        _stream_handle(q.device),
+        out.data_ptr(), os_[0], os_[-2], workspace, ws_bytes,
+        float(softmax_scale), batch, hq, hkv, hd, ps, block_table.shape[1], pages,
+        DTYPE_CODES[q.dtype], num_splits, _stream_handle(q.device),
     )
 
 
 def _prepare(q, k_cache, v_cache, block_table, cache_seqlens, out):
     check_decode_shapes(q, k_cache, v_cache)
     batch = q.shape[0]
-    if q.stride(-1) != 1:
+    hd = q.shape[-1]
+    if q.stride(-1) != 1 or (q.shape[-2] > 1 and q.stride(-2) < hd):
         q = q.contiguous()
     if k_cache.stride(-1) != 1 or v_cache.stride() != k_cache.stride():
         raise UnsupportedConfig("k_cache and v_cache must share strides with a contiguous last dim")
+    if k_cache.shape[1] > 1 and k_cache.stride(1) < hd:
+        raise UnsupportedConfig("cache token rows overlap (token stride < head_dim)")
     _require_device(q, k_cache, v_cache, block_table, cache_seqlens)
     block_table = _int32_contig(block_table, "block_table")
     cache_seqlens = _int32_contig(cache_seqlens, "cache_seqlens")
@@ -333,49 +329,6 @@ def paged_decode_split(
                                                     cache_seqlens, out, ws.data_ptr(), ws_bytes,
                                                     softmax_scale, num_splits, seqlen_add))
     _check(rc, "mxfa_split_decode_launch")
-    return out
-
-
-def split_decode_partial(
-    q: torch.Tensor,
-    k_cache: torch.Tensor,
-    v_cache: torch.Tensor,
-    block_table: torch.Tensor,
-    cache_seqlens: torch.Tensor,
-    softmax_scale: float,
-    out: torch.Tensor,
-    workspace: torch.Tensor,
-    num_splits: int,
-    seqlen_add: int = 0,
-) -> None:
-    """Partial stage only (sequences inside one range land in ``out``, pieces in
-    ``workspace``); ``split_decode_combine`` finishes the call."""
-    q, block_table, cache_seqlens, out = _prepare(q, k_cache, v_cache, block_table,
-                                                  cache_seqlens, out)
-    _require_device(q, workspace)
-    if not workspace.is_contiguous():
-        raise ValueError("workspace must be contiguous")
-    nbytes = workspace.numel() * workspace.element_size()
-    rc = library().mxfa_split_decode_partial_launch(
-        *_launch_args(q, k_cache, v_cache, block_table, cache_seqlens, out, workspace.data_ptr(),
-                      nbytes, softmax_scale, num_splits, seqlen_add))
-    _check(rc, "mxfa_split_decode_partial_launch")
-
-
-def split_decode_combine(workspace: torch.Tensor, out: torch.Tensor, num_splits: int) -> torch.Tensor:
-    """LSE merge of the pieces in ``workspace`` into ``out`` ([B,1,HQ,HD] or [B,HQ,HD])."""
-    _require_device(out, workspace)
-    if not workspace.is_contiguous() or out.stride(-1) != 1:
-        raise ValueError("workspace must be contiguous and out's last dim contiguous")
-    if out.dim() not in (3, 4) or (out.dim() == 4 and out.shape[1] != 1):
-        raise ValueError(f"out must be [B,1,HQ,HD] or [B,HQ,HD], got {tuple(out.shape)}")
-    batch, hq, hd = out.shape[0], out.shape[-2], out.shape[-1]
-    os_ = out.stride()
-    rc = library().mxfa_split_decode_combine_launch(
-        workspace.data_ptr(), workspace.numel() * workspace.element_size(), out.data_ptr(),
-        os_[0], os_[-2], batch, hq, hd, _dtype_code(out), num_splits, _stream_handle(out.device),
-    )
-    _check(rc, "mxfa_split_decode_combine_launch")
     return out
 
 

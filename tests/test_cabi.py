@@ -44,7 +44,7 @@ def test_library_loads_and_reports_header_abi(lib):
 
 def test_every_header_function_is_exported_and_bound(lib):
     declared = header_functions()
-    assert len(declared) == len(set(declared)) == 9
+    assert len(declared) == len(set(declared)) == 7
     for name in declared:
         assert hasattr(lib, name), name
     assert set(declared) == set(native.EXPORTED_SYMBOLS) == set(native._SIGNATURES)
@@ -67,29 +67,36 @@ def test_strerror_is_distinct_per_code(lib):
 
 
 def heuristic_closed_form(b, hq, hkv, hd, ps, btw, cus):
-    cap = btw * ps
-    per_cu = 2 if (hd == 64 and hq // hkv >= 8) or cap < 2048 else 1
-    n = -(-(cus * per_cu) // hkv)
-    n = min(n, -(-(b * -(-cap // 16)) // 4))
+    # One wave per (kv head, range): workgroups of 8 waves hold min(HKV, 8) kv
+    # heads x 8 // that sub-ranges; HD64 fits two workgroups per CU, HD128 one.
+    kh = min(hkv, 8)
+    subs = 8 // kh
+    gx = -(-hkv // kh)
+    per_cu = 2 if hd == 64 else 1
+    n = cus * per_cu * subs // gx
+    n = min(n, b * -(-(btw * ps) // 16))
     return max(1, min(n, 65535))
 
 
 @pytest.mark.parametrize("args", [
-    (32, 32, 8, 128, 16, 512, 256),    # config 2: 256 CUs / 8 kv heads
-    (32, 32, 16, 128, 16, 512, 256),   # GQ2: 16 kv heads
-    (32, 32, 4, 64, 16, 512, 256),     # GQ8 HD64: two per CU
+    (32, 32, 8, 128, 16, 512, 256),    # config 2: 256 CUs x 8 waves / 8 kv heads
+    (32, 32, 16, 128, 16, 512, 256),   # GQ2: 16 kv heads, two workgroups per range
+    (32, 32, 4, 64, 16, 512, 256),     # GQ8 HD64: two sub-ranges per workgroup, 2 per CU
     (1, 2, 1, 64, 16, 1, 256),         # one tile in total
-    (256, 16, 8, 64, 16, 64, 256),     # short tables: two per CU
+    (256, 16, 8, 64, 16, 64, 256),
     (4, 32, 4, 128, 256, 128, 304),    # other CU count
     (16384, 64, 8, 128, 16, 4096, 256),
+    (8, 24, 3, 128, 16, 64, 256),      # kv heads not a power of two
+    (8, 96, 12, 128, 16, 64, 256),
 ])
 def test_split_heuristic_closed_form(args):
     assert native.split_heuristic(*args) == heuristic_closed_form(*args)
 
 
 def test_split_heuristic_known_values():
-    assert native.split_heuristic(32, 32, 8, 128, 16, 512, 256) == 32
-    assert native.split_heuristic(32, 32, 4, 64, 16, 512, 256) == 128
+    assert native.split_heuristic(32, 32, 8, 128, 16, 512, 256) == 256
+    assert native.split_heuristic(32, 32, 4, 64, 16, 512, 256) == 1024
+    assert native.split_heuristic(32, 32, 16, 128, 16, 512, 256) == 128
     assert native.split_heuristic(1, 2, 1, 64, 16, 1, 256) == 1
 
 
@@ -137,26 +144,16 @@ def decode_args(**over):
     (dict(ns=70000), -1), (dict(batch=20000), -1), (dict(btw=1 << 27, ps=16), -1),
     (dict(q=FAKE + 2), -2), (dict(k=FAKE + 8), -2), (dict(q_sh=100), -2), (dict(c_st=1028), -2),
     (dict(o_sh=130), -2), (dict(out=FAKE + 2), -2),
+    (dict(c_st=64), -2), (dict(q_sh=64), -2),  # overlapping rows
     (dict(ws=None), -3), (dict(ws=FAKE + 8), -3), (dict(ws_bytes=1000), -3),
 ])
 def test_decode_launch_rejects_before_launching(lib, over, code):
     assert lib.mxfa_split_decode_launch(*decode_args(**over)) == code
-    assert lib.mxfa_split_decode_partial_launch(*decode_args(**over)) == code
 
 
 def test_decode_workspace_boundary_is_exact(lib):
     need = native.workspace_size(32, 32, 128, 32)
     assert lib.mxfa_split_decode_launch(*decode_args(ws_bytes=need - 1)) == -3
-
-
-def test_combine_rejects_before_launching(lib):
-    ws = native.workspace_size(4, 8, 64, 3)
-    f = lib.mxfa_split_decode_combine_launch
-    assert f(None, ws, FAKE, 512, 64, 4, 8, 64, 0, 3, None) in (-2, -3)
-    assert f(FAKE, ws - 4, FAKE, 512, 64, 4, 8, 64, 0, 3, None) == -3
-    assert f(FAKE, ws, FAKE, 512, 64, 4, 8, 96, 0, 3, None) == -1
-    assert f(FAKE, ws, FAKE, 512, 64, 4, 8, 64, 5, 3, None) == -1
-    assert f(FAKE, ws, FAKE, 512, 64, 0, 8, 64, 0, 3, None) == -2
 
 
 def test_append_entry_points_reject_before_launching(lib):

@@ -188,3 +188,61 @@ def test_fp64_oracle_agrees_with_fp32_port_on_gpu_inputs(device):
                                       b.scale)
     port = oracle_out(b).reshape(ref64.shape).numpy()
     assert np.abs(port - ref64).max() <= 2e-3
+
+
+@pytest.mark.parametrize("hq,hkv,head_dim", [
+    (2, 1, 128), (8, 1, 64), (6, 3, 128), (24, 12, 64), (32, 16, 128), (64, 16, 64),
+])
+def test_kv_head_counts(device, hq, hkv, head_dim):
+    # Workgroups hold min(HKV, 8) kv heads x 8 // that sub-ranges: one kv head
+    # with eight sub-ranges, three heads with two, and two head groups.
+    lengths = torch.tensor([1, 40, 700, 16, 33])
+    b = make_paged_batch(5, hq, hkv, head_dim, torch.bfloat16, lengths, seed=21).to(device)
+    expected = oracle_out(b)
+    for ns in (None, 1, 2, 5, 64):
+        kw = {} if ns is None else dict(num_splits=ns)
+        assert max_err(run_native(b, **kw), expected) <= TOL[torch.bfloat16], ns
+
+
+def test_back_to_back_calls_of_changing_shapes_share_the_workspace(device):
+    # Every call on a stream reuses one workspace; calls of other shapes in
+    # between must not leave anything a later call reads.
+    shapes = [
+        (6, 32, 8, 128, torch.bfloat16, torch.tensor([900, 17, 2048, 1, 300, 64]), 40),
+        (3, 16, 4, 64, torch.float16, torch.tensor([4000, 5, 129]), 200),
+        (6, 32, 8, 128, torch.bfloat16, torch.tensor([900, 17, 2048, 1, 300, 64]), 7),
+    ]
+    batches = [make_paged_batch(*s[:6], seed=30 + i).to(device) for i, s in enumerate(shapes)]
+    expected = [oracle_out(b) for b in batches]
+    for _ in range(3):
+        for b, exp, s in zip(batches, expected, shapes):
+            got = run_native(b, num_splits=s[6])
+            assert max_err(got, exp) <= TOL[b.q.dtype]
+
+
+def test_head_major_cache_layout(device):
+    # Cache stored [pages, HKV, PS, HD] and viewed as [pages, PS, HKV, HD]: the
+    # head stride exceeds the token stride.
+    b = make_paged_batch(3, 16, 4, 128, torch.float16, torch.tensor([50, 300, 17]), seed=41)
+    expected = oracle_out(b)
+    kc = b.k_cache.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+    vc = b.v_cache.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+    assert kc.stride(2) > kc.stride(1)
+    b = b.to(device)
+    out = native.paged_decode_split(b.q, kc.to(device), vc.to(device), b.block_table,
+                                    b.cache_seqlens, b.scale, num_splits=9)
+    torch.cuda.synchronize()
+    assert max_err(out, expected) <= TOL[torch.float16]
+
+
+@pytest.mark.parametrize("dtype,head_dim,gq", [(torch.bfloat16, 128, 4), (torch.float16, 64, 8)])
+def test_repeated_calls_are_bitwise_reproducible(device, dtype, head_dim, gq):
+    # Every piece is computed the same way on every call and the combine walks
+    # the pieces in range order, so the output must not change by a single bit
+    # from call to call. A combine that read a stale piece would break this.
+    lengths = torch.tensor([3000, 1, 4500, 700, 2048, 17, 6000, 333])
+    b = make_paged_batch(8, 8 * gq, 8, head_dim, dtype, lengths, seed=55).to(device)
+    first = run_native(b).clone()
+    assert max_err(first, oracle_out(b)) <= TOL[dtype]
+    for _ in range(40):
+        assert torch.equal(run_native(b), first)
