@@ -155,6 +155,48 @@ struct Mfma<BF16> {
   }
 };
 
+// PV on the matrix cores, v_mfma_f32_16x16x16: A = P[head][token] is the QK
+// result layout itself (lane (r, h) holds tokens 4r..4r+3 of head h), packed to
+// the element type; B = V[token][dim], lane (r, c) supplying tokens 4r..4r+3 of
+// one dim per block; D = O[head][dim]. Element packing keeps k order: the low
+// half of the first register is token 4r.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct PvMfma;
+template <>
+struct PvMfma<BF16> {
+  static __device__ __forceinline__ f32x4 run(uint2 a, uint2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                      __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint16_t round(float x) {
+    return __builtin_bit_cast(uint16_t, (__bf16)x);
+  }
+  static __device__ __forceinline__ float widen(uint16_t h) {
+    return __uint_as_float((uint32_t)h << 16);
+  }
+};
+template <>
+struct PvMfma<F16> {
+  static __device__ __forceinline__ f32x4 run(uint2 a, uint2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
+                                                 __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint16_t round(float x) {
+    return __builtin_bit_cast(uint16_t, (_Float16)x);
+  }
+  static __device__ __forceinline__ float widen(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+  }
+};
+
+// 16-bit element j of a V fragment word list, paired from two tokens.
+__device__ __forceinline__ uint32_t pair_halves(uint32_t lo_tok, uint32_t hi_tok, int odd) {
+  return __builtin_amdgcn_perm(hi_tok, lo_tok, odd ? 0x07060302u : 0x05040100u);
+}
+
 template <int Aux>
 __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, int off) {
   const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, Aux);
@@ -176,6 +218,9 @@ struct VFrag<8> {
     w = buf_load16<kAuxStream>(r, off);
   }
   __device__ __forceinline__ void load_ptr(const char *ptr) { w = load_stream16(ptr); }
+  __device__ __forceinline__ uint32_t word(int i) const {
+    return i == 0 ? w.x : i == 1 ? w.y : i == 2 ? w.z : w.w;
+  }
   template <typename E>
   __device__ __forceinline__ void widen(float (&v)[8]) const {
     v[0] = E::lo(w.x);
@@ -195,6 +240,7 @@ struct VFrag<4> {
     w = buf_load8<kAuxStream>(r, off);
   }
   __device__ __forceinline__ void load_ptr(const char *ptr) { w = load_stream8(ptr); }
+  __device__ __forceinline__ uint32_t word(int i) const { return i == 0 ? w.x : w.y; }
   template <typename E>
   __device__ __forceinline__ void widen(float (&v)[4]) const {
     v[0] = E::lo(w.x);
@@ -239,6 +285,17 @@ __device__ __forceinline__ void rescale_rows(float (&o)[GQ][VD], float f) {
     for (int j = 0; j < VD; ++j) o[H][j] *= fh;
     rescale_rows<GQ, VD, H + 1>(o, f);
   }
+}
+
+// Value of head 4*row + I from a per-head quantity held by column h of every
+// DPP row (the score layout). Only rows whose heads exist (row < GQ/4) get a
+// meaningful value. DPP moves only: no LDS round trip, so no wait on the
+// scalar page-id loads in flight.
+template <int GQ, int I>
+__device__ __forceinline__ float head_of_row(float x, int row) {
+  float v = row_bcast<I>(x);
+  if constexpr (GQ > 4) v = row == 1 ? row_bcast<4 + I>(x) : v;
+  return v;
 }
 
 // Exclusive prefix sum of per-sequence tile counts into s[0..B] (LDS), all threads.
@@ -332,8 +389,11 @@ struct Tile {
   int pg;  // page id (block-table entry), page-uniform tiles only
 };
 
-// One wave: the tiles [lo, hi) of kv head kvh, range rr of R.
-template <int HD, int GQ, typename T, bool kLanePages>
+// One wave: the tiles [lo, hi) of kv head kvh, range rr of R. kPvMfma: PV on
+// the matrix cores (accumulator lane (r, c) holds heads 4r..4r+3, dims
+// c*VD + jb in block jb), else on the VALU (o[g][j], g = head, dims c*VD + j,
+// one partial per DPP row).
+template <int HD, int GQ, typename T, bool kLanePages, bool kPvMfma, int NBUF>
 __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *s_tiles, int kvh,
                                           int rr, int R, int NT, int lo, int hi) {
   using E = Elem<T>;
@@ -472,18 +532,60 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   // Running state of the current piece.
   float m = -INFINITY;  // reference max (base 2) of head `col`, same in every row
   float dsum = 0.f;     // partial denominator of head `col` over this row's tokens
-  float o[GQ][VD];
+  float o[kPvMfma ? 1 : GQ][VD];  // VALU PV accumulators
+  f32x4 oacc[kPvMfma ? VD : 1];     // MFMA PV accumulators
   uint4 qf[NCH];
+  auto clear_acc = [&]() {
+    if constexpr (kPvMfma) {
 #pragma unroll
-  for (int g = 0; g < GQ; ++g)
+      for (int j = 0; j < VD; ++j) oacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    } else {
 #pragma unroll
-    for (int j = 0; j < VD; ++j) o[g][j] = 0.f;
+      for (int g = 0; g < GQ; ++g)
+#pragma unroll
+        for (int j = 0; j < VD; ++j) o[g][j] = 0.f;
+    }
+  };
+  clear_acc();
 #pragma unroll
   for (int cc = 0; cc < NCH; ++cc) qf[cc] = make_uint4(0u, 0u, 0u, 0u);
   bool piece_from_start = false;
   bool piece_first_in_range = false;
 
+  auto finalize_mfma = [&](const Tile &d) {
+    const float dt = rows_sum(dsum);  // lane (any row, h): denominator of head h
+    const int b = d.b;
+    const bool whole = piece_from_start && (d.flags & kSeqEnd);
+    const int slot = piece_first_in_range ? 0 : 1;
+    const int64_t pbase = ((int64_t)(kvh * ns + rr) * 2 + slot) * GQ;
+    static_for<4>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      const int hh = 4 * row + i;  // head of accumulator element i in this lane
+      const float Dh = head_of_row<GQ, i>(dt, row);
+      const float Mh = head_of_row<GQ, i>(m, row);
+      if (hh >= GQ) return;
+      const float inv = Dh > 0.f ? 1.f / Dh : 0.f;
+      float v[VD];
+#pragma unroll
+      for (int j = 0; j < VD; ++j) v[j] = oacc[j][i];
+      if (whole) {
+        store_row<VD, E>(p.out + b * p.o_sb + (kvh * GQ + hh) * p.o_sh + col * (VD * 2), v, inv);
+      } else {
+        float4 *dst = reinterpret_cast<float4 *>(p.ws_o + (pbase + hh) * HD + col * VD);
+#pragma unroll
+        for (int j = 0; j < VD / 4; ++j)
+          dst[j] = make_float4(v[4 * j] * inv, v[4 * j + 1] * inv, v[4 * j + 2] * inv,
+                               v[4 * j + 3] * inv);
+        if (col == 0) p.ws_lse[pbase + hh] = Dh > 0.f ? Mh + __log2f(Dh) : -INFINITY;
+      }
+    });
+  };
+
   auto finalize = [&](const Tile &d) {
+    if constexpr (kPvMfma) {
+      finalize_mfma(d);
+      return;
+    }
     const float dt = rows_sum(dsum);
 #pragma unroll
     for (int g = 0; g < GQ; ++g)
@@ -526,10 +628,7 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
     if (d.flags & kFirst) {
       m = -INFINITY;
       dsum = 0.f;
-#pragma unroll
-      for (int g = 0; g < GQ; ++g)
-#pragma unroll
-        for (int j = 0; j < VD; ++j) o[g][j] = 0.f;
+      clear_acc();
 #pragma unroll
       for (int cc = 0; cc < NCH; ++cc) qf[cc] = s.q[cc];
       piece_from_start = (d.flags & kSeqStart) != 0;
@@ -557,7 +656,16 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
       const float mn = mt > m + kRescaleLog2 ? mt : m;
       const float f = (mn == m) ? 1.f : fast_exp2(m - mn);  // m = -inf: f = 0
       dsum *= f;
-      rescale_rows<GQ, VD>(o, f);
+      if constexpr (kPvMfma) {
+        static_for<4>([&](auto ic) {
+          constexpr int i = decltype(ic)::value;
+          const float fi = head_of_row<GQ, i>(f, row);
+#pragma unroll
+          for (int j = 0; j < VD; ++j) oacc[j][i] *= fi;
+        });
+      } else {
+        rescale_rows<GQ, VD>(o, f);
+      }
       m = mn;
     }
     // m = -inf: this head has seen no valid token, its scores here are -inf too.
@@ -565,53 +673,77 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
     float pr[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(x[i] - mr);
-    dsum += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+    if constexpr (kPvMfma) {
+      // P rounded to the element type once; the denominator sums the same
+      // rounded weights, so the output stays a convex combination of V rows.
+      uint16_t ph[4];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float v[VD];
-      s.v[u].template widen<E>(v);
-      pv_accumulate<GQ, VD>(o, pr[u], v);
+      for (int i = 0; i < 4; ++i) ph[i] = PvMfma<T>::round(pr[i]);
+      dsum += (PvMfma<T>::widen(ph[0]) + PvMfma<T>::widen(ph[1])) +
+              (PvMfma<T>::widen(ph[2]) + PvMfma<T>::widen(ph[3]));
+      const uint2 a = make_uint2((uint32_t)ph[0] | ((uint32_t)ph[1] << 16),
+                                 (uint32_t)ph[2] | ((uint32_t)ph[3] << 16));
+#pragma unroll
+      for (int jb = 0; jb < VD; ++jb) {
+        const int wi = jb >> 1, odd = jb & 1;
+        const uint2 bv = make_uint2(pair_halves(s.v[0].word(wi), s.v[1].word(wi), odd),
+                                    pair_halves(s.v[2].word(wi), s.v[3].word(wi), odd));
+        oacc[jb] = PvMfma<T>::run(a, bv, oacc[jb]);
+      }
+    } else {
+      dsum += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float v[VD];
+        s.v[u].template widen<E>(v);
+        pv_accumulate<GQ, VD>(o, pr[u], v);
+      }
     }
     if (d.flags & kLast) finalize(d);
   };
 
-  // Software pipeline over the range: tile descriptors (and page ids) are
-  // built two tiles ahead of the math, K/V/q loads issued one tile ahead into
-  // the other register set. The body runs two tiles and exits only at its
-  // latch, so the loads crossing the back edge are always the a-set of the
-  // next tile. The descriptor of the padding tile past the range end covers
-  // no bytes, so its loads cost nothing.
-  Set sa, sb;
+  // Software pipeline over the range with NBUF register sets: tile
+  // descriptors (and page ids) are built NBUF tiles ahead of the math, K/V/q
+  // loads issued NBUF-1 tiles ahead. The body runs NBUF tiles and exits only at
+  // its latch, so the loads crossing the back edge always land in the same
+  // sets. The descriptor of a padding tile past the range end covers no
+  // bytes, so its loads cost nothing.
+  Set sets[NBUF];
   Tile dn;
   int lpg_n[NPG];
-  make_tile(lo, sa.d, sa.lpg);
-  issue(sa);
-  make_tile(lo + 1, sb.d, sb.lpg);
+  static_for<NBUF>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    make_tile(lo + i, sets[i].d, sets[i].lpg);
+    if constexpr (i < NBUF - 1) issue(sets[i]);
+  });
   const int ntiles = hi - lo;
   int t = lo;
-  auto step = [&](Set &cur, Set &nxt) {
-    // nxt.d (tile t+1) is ready: issue its loads, build tile t+2, then the math of tile t.
+  auto step = [&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    constexpr int kn = (k + NBUF - 1) % NBUF;  // holds tile t + NBUF - 1
     if constexpr (kLanePages) {
-      make_tile(t + 2, dn, lpg_n);
-      issue(nxt);
+      make_tile(t + NBUF, dn, lpg_n);
+      issue(sets[kn]);
     } else {
-      issue(nxt);
-      make_tile(t + 2, dn, lpg_n);
+      issue(sets[kn]);
+      make_tile(t + NBUF, dn, lpg_n);
     }
-    compute(cur);
-    cur.d = dn;
+    compute(sets[k]);
+    sets[k].d = dn;
 #pragma unroll
-    for (int i = 0; i < NPG; ++i) cur.lpg[i] = lpg_n[i];
+    for (int i = 0; i < NPG; ++i) sets[k].lpg[i] = lpg_n[i];
     ++t;
   };
-  for (int i = 0; i + 1 < ntiles; i += 2) {
-    step(sa, sb);
-    step(sb, sa);
-  }
-  if (ntiles & 1) compute(sa);
+  int done = 0;
+  for (; done + NBUF <= ntiles; done += NBUF) static_for<NBUF>(step);
+  const int rest = ntiles - done;  // < NBUF tiles, already issued into sets[0 .. rest-1]
+  static_for<NBUF - 1>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    if (j < rest) compute(sets[j]);
+  });
 }
 
-template <int HD, int GQ, typename T, bool kLanePages, int kMinWgPerCu>
+template <int HD, int GQ, typename T, bool kLanePages, bool kPvMfma, int NBUF, int kMinWgPerCu>
 __global__ __launch_bounds__(kThreads, kMinWgPerCu) void split_partial_kernel(DecodeParams p) {
   extern __shared__ int32_t s_tiles[];  // [B + 1]
   __shared__ int s_wave_tot[kWaves];
@@ -632,7 +764,7 @@ __global__ __launch_bounds__(kThreads, kMinWgPerCu) void split_partial_kernel(De
   const int rr = blockIdx.y * p.subs + sub;
   if (sub >= p.subs || kvh >= p.hkv || rr >= R) return;
   const int lo = range_lo(rr, R, NT), hi = range_lo(rr + 1, R, NT);
-  run_range<HD, GQ, T, kLanePages>(p, s_tiles, kvh, rr, R, NT, lo, hi);
+  run_range<HD, GQ, T, kLanePages, kPvMfma, NBUF>(p, s_tiles, kvh, rr, R, NT, lo, hi);
 }
 
 struct CombineParams {
@@ -839,20 +971,35 @@ static DecodeParams make_params(const SplitArgs &a, const Grid &g) {
   return p;
 }
 
-// Workgroups per CU the kernel is compiled for: HD 64 keeps under 128 VGPRs so
-// two workgroups (16 waves) share a CU; HD 128 runs one (8 waves, 256 VGPRs).
+// One workgroup (8 waves, two per SIMD) per CU; measured on MI355X against two
+// per CU (16 waves): HD 128 loses 3% with two, HD 64 loses 5-17% (twice as
+// many ranges, so twice the pieces to merge and half the tiles per wave).
 template <int HD>
-constexpr int kWgPerCu = HD == 64 ? 2 : 1;
+constexpr int kWgPerCu = 1;
+// Register sets of the tile pipeline: HD 64 tiles are half the bytes, so a
+// third set keeps as many bytes in flight per wave as HD 128 does with two.
+template <int HD>
+constexpr int kNbuf = HD == 64 ? 3 : 2;
+
+// PV on the matrix cores from this many query heads per kv head up. Measured
+// on MI355X (config-2 shape, one call): against DPP-broadcast FMAs on the VALU
+// the matrix cores are even at GQ 2 and faster at GQ 4 (2-3%) and GQ 8 (6% at
+// HD 128, 14% at HD 64), so every supported GQ uses them.
+constexpr int kPvMfmaMinGq = 2;
 
 template <int HD, int GQ, typename T>
 static int launch_t(const DecodeParams &p, const Grid &g, hipStream_t st) {
   dim3 grid(g.gx, g.gy);
   const size_t lds = (size_t)(p.batch + 1) * sizeof(int32_t);
   if (p.ps_log2 >= 4)
-    hipLaunchKernelGGL((split_partial_kernel<HD, GQ, T, false, kWgPerCu<HD>>), grid,
+    hipLaunchKernelGGL((split_partial_kernel<HD, GQ, T, false, (GQ >= kPvMfmaMinGq), kNbuf<HD>,
+                                             kWgPerCu<HD>>),
+                       grid,
                        dim3(kThreads), lds, st, p);
   else
-    hipLaunchKernelGGL((split_partial_kernel<HD, GQ, T, true, kWgPerCu<HD>>), grid,
+    hipLaunchKernelGGL((split_partial_kernel<HD, GQ, T, true, (GQ >= kPvMfmaMinGq), 2,
+                                             kWgPerCu<HD>>),
+                       grid,
                        dim3(kThreads), lds, st, p);
   return hipGetLastError() == hipSuccess ? MXFA_OK : MXFA_ELAUNCH;
 }

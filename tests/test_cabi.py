@@ -68,12 +68,11 @@ def test_strerror_is_distinct_per_code(lib):
 
 def heuristic_closed_form(b, hq, hkv, hd, ps, btw, cus):
     # One wave per (kv head, range): workgroups of 8 waves hold min(HKV, 8) kv
-    # heads x 8 // that sub-ranges; HD64 fits two workgroups per CU, HD128 one.
+    # heads x 8 // that sub-ranges, one workgroup per CU.
     kh = min(hkv, 8)
     subs = 8 // kh
     gx = -(-hkv // kh)
-    per_cu = 2 if hd == 64 else 1
-    n = cus * per_cu * subs // gx
+    n = cus * subs // gx
     n = min(n, b * -(-(btw * ps) // 16))
     return max(1, min(n, 65535))
 
@@ -81,7 +80,7 @@ def heuristic_closed_form(b, hq, hkv, hd, ps, btw, cus):
 @pytest.mark.parametrize("args", [
     (32, 32, 8, 128, 16, 512, 256),    # config 2: 256 CUs x 8 waves / 8 kv heads
     (32, 32, 16, 128, 16, 512, 256),   # GQ2: 16 kv heads, two workgroups per range
-    (32, 32, 4, 64, 16, 512, 256),     # GQ8 HD64: two sub-ranges per workgroup, 2 per CU
+    (32, 32, 4, 64, 16, 512, 256),     # GQ8 HD64: two sub-ranges per workgroup
     (1, 2, 1, 64, 16, 1, 256),         # one tile in total
     (256, 16, 8, 64, 16, 64, 256),
     (4, 32, 4, 128, 256, 128, 304),    # other CU count
@@ -95,7 +94,7 @@ def test_split_heuristic_closed_form(args):
 
 def test_split_heuristic_known_values():
     assert native.split_heuristic(32, 32, 8, 128, 16, 512, 256) == 256
-    assert native.split_heuristic(32, 32, 4, 64, 16, 512, 256) == 1024
+    assert native.split_heuristic(32, 32, 4, 64, 16, 512, 256) == 512
     assert native.split_heuristic(32, 32, 16, 128, 16, 512, 256) == 128
     assert native.split_heuristic(1, 2, 1, 64, 16, 1, 256) == 1
 
