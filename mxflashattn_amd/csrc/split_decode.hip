@@ -496,8 +496,10 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
     const __amdgpu_buffer_rsrc_t rq =
         make_srd(p.q + (int64_t)d.b * p.q_sb + (int64_t)kvh * GQ * p.q_sh,
                  (d.flags & kFirst) ? q_bytes : 0);
+    if (d.flags & kFirst) {  // wave-uniform; q is loaded once per piece
 #pragma unroll
-    for (int cc = 0; cc < NCH; ++cc) s.q[cc] = buf_load16<0>(rq, q_off + cc * 64);
+      for (int cc = 0; cc < NCH; ++cc) s.q[cc] = buf_load16<0>(rq, q_off + cc * 64);
+    }
     if constexpr (!kLanePages) {
       const uint64_t tile_off = (uint64_t)(uint32_t)clamp_page(d.pg) * (uint64_t)p.sp_bytes +
                                 (uint64_t)(d.tok0 & ps_mask) * st + head_off;
@@ -777,24 +779,49 @@ struct CombineParams {
   int hq;
   int gq;
   int num_ranges;
+  int chunk_blocks;  // blocks per (sequence, kv head) pair, a power of two
 };
 
-// LSE combine: HD/4 threads per (sequence, head), one float4 of the output
-// each. Sequences that lie inside one range were written by the partial kernel
-// and are skipped, as are empty ones (zero-filled there). Pieces are folded in
-// range order, eight loads in flight per step, so the result does not depend
-// on timing.
-template <int HD, typename T>
-__global__ __launch_bounds__(256) void split_combine_kernel(CombineParams p) {
+// Merge of two partial states (max, weight, accumulator) in the base-2 domain.
+__device__ __forceinline__ void lse_fold(float &M, float &W, float4 &A, float m2, float w2,
+                                         const float4 &a2) {
+  const float Mn = fmaxf(M, m2);
+  if (Mn == -INFINITY) return;
+  const float f1 = (M == -INFINITY) ? 0.f : fast_exp2(M - Mn);
+  const float f2 = (m2 == -INFINITY) ? 0.f : fast_exp2(m2 - Mn);
+  W = W * f1 + w2 * f2;
+  A.x = A.x * f1 + a2.x * f2;
+  A.y = A.y * f1 + a2.y * f2;
+  A.z = A.z * f1 + a2.z * f2;
+  A.w = A.w * f1 + a2.w * f2;
+  M = Mn;
+}
+
+// LSE combine: F = chunk_blocks blocks of kCombineThreads per (sequence b,
+// kv head) pair; block f takes CB = C / F of the pair's C float4 chunks of the
+// GQ x HD output and splits the pieces over G = kCombineThreads / CB groups.
+// Thread (g, c) folds pieces ra+g, ra+g+G, ... of chunk c, eight loads in
+// flight per step; the G groups are then merged by an LDS tree and the output
+// rounded once. The fold order depends on F only (a host choice), never on
+// timing. Pairs whose sequence lies inside one range (written by the partial
+// kernel) or is empty (zero-filled there) leave at once.
+constexpr int kCombineThreads = 256;
+
+template <int HD, int GQ, typename T>
+__global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(CombineParams p) {
   using E = Elem<T>;
-  constexpr int TPH = HD / 4;
+  constexpr int C = GQ * HD / 4;  // float4 chunks per pair
+  static_assert(C <= kCombineThreads && kCombineThreads % C == 0, "chunks per pair");
   constexpr int kUnroll = 8;
-  const int gid = blockIdx.x * 256 + threadIdx.x;
-  const int hid = gid / TPH;
-  if (hid >= p.batch * p.hq) return;
-  const int c = gid % TPH;
-  const int b = hid / p.hq, h = hid % p.hq;
-  const int kvh = h / p.gq, g = h % p.gq;
+  __shared__ float s_red[kCombineThreads * 6];
+  const int hkv = p.hq / GQ;
+  const int F = p.chunk_blocks;
+  const int CB = C / F;
+  const int groups = kCombineThreads / CB;
+  const int pair = blockIdx.x / F;
+  const int b = pair / hkv, kvh = pair % hkv;
+  const int g = threadIdx.x / CB;
+  const int c = (blockIdx.x % F) * CB + threadIdx.x % CB;
   const int NT = p.ws_s[p.batch];
   const int sb = p.ws_s[b], se = p.ws_s[b + 1];
   // Prefix sums that do not describe tiles inside [0, NT) (a workspace the
@@ -805,44 +832,55 @@ __global__ __launch_bounds__(256) void split_combine_kernel(CombineParams p) {
   if (ra == rb) return;
   const int slot_a = (range_lo(ra, R, NT) == sb) ? 0 : 1;
   const int ns = p.num_ranges;
+  const int cc = c;
+  const int head = cc / (HD / 4);
   float M = -INFINITY, W = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int q0 = ra; q0 <= rb; q0 += kUnroll) {
+  for (int q0 = ra + g; q0 <= rb; q0 += kUnroll * groups) {
     float l[kUnroll];
     float4 ov[kUnroll];
 #pragma unroll
     for (int i = 0; i < kUnroll; ++i) {
-      const int q = min(q0 + i, rb);
-      const int64_t ps = ((int64_t)(kvh * ns + q) * 2 + (q == ra ? slot_a : 0)) * p.gq + g;
-      l[i] = (q0 + i <= rb) ? p.ws_lse[ps] : -INFINITY;
-      ov[i] = reinterpret_cast<const float4 *>(p.ws_o + ps * HD)[c];
+      const int q = min(q0 + i * groups, rb);
+      const int64_t ps = ((int64_t)(kvh * ns + q) * 2 + (q == ra ? slot_a : 0)) * GQ + head;
+      l[i] = (q0 + i * groups <= rb) ? p.ws_lse[ps] : -INFINITY;
+      ov[i] = reinterpret_cast<const float4 *>(p.ws_o + ps * HD)[cc % (HD / 4)];
     }
-    float mx = l[0];
 #pragma unroll
-    for (int i = 1; i < kUnroll; ++i) mx = fmaxf(mx, l[i]);
-    const float Mn = fmaxf(M, mx);
-    if (Mn == -INFINITY) continue;
-    const float fo = (M == -INFINITY) ? 0.f : fast_exp2(M - Mn);
-    W *= fo;
-    acc.x *= fo;
-    acc.y *= fo;
-    acc.z *= fo;
-    acc.w *= fo;
-#pragma unroll
-    for (int i = 0; i < kUnroll; ++i) {
-      const float w = (l[i] == -INFINITY) ? 0.f : fast_exp2(l[i] - Mn);
-      W += w;
-      acc.x = fmaf(w, ov[i].x, acc.x);
-      acc.y = fmaf(w, ov[i].y, acc.y);
-      acc.z = fmaf(w, ov[i].z, acc.z);
-      acc.w = fmaf(w, ov[i].w, acc.w);
-    }
-    M = Mn;
+    for (int i = 0; i < kUnroll; ++i) lse_fold(M, W, acc, l[i], 1.f, ov[i]);
   }
-  const float inv = W > 0.f ? 1.f / W : 0.f;
-  const uint32_t w0 = (uint32_t)E::narrow(acc.x * inv) | ((uint32_t)E::narrow(acc.y * inv) << 16);
-  const uint32_t w1 = (uint32_t)E::narrow(acc.z * inv) | ((uint32_t)E::narrow(acc.w * inv) << 16);
-  *reinterpret_cast<uint2 *>(p.out + b * p.o_sb + h * p.o_sh + c * 8) = make_uint2(w0, w1);
+  float *red = s_red + threadIdx.x * 6;
+  red[0] = M;
+  red[1] = W;
+  red[2] = acc.x;
+  red[3] = acc.y;
+  red[4] = acc.z;
+  red[5] = acc.w;
+  __syncthreads();
+#pragma unroll
+  for (int stride = groups / 2; stride >= 1; stride >>= 1) {  // groups is a power of two
+    if (g < stride) {
+      const float *o2 = s_red + (threadIdx.x + stride * CB) * 6;
+      lse_fold(M, W, acc, o2[0], o2[1], make_float4(o2[2], o2[3], o2[4], o2[5]));
+      red[0] = M;
+      red[1] = W;
+      red[2] = acc.x;
+      red[3] = acc.y;
+      red[4] = acc.z;
+      red[5] = acc.w;
+    }
+    __syncthreads();
+  }
+  if (g == 0) {
+    const float inv = W > 0.f ? 1.f / W : 0.f;
+    const uint32_t w0 =
+        (uint32_t)E::narrow(acc.x * inv) | ((uint32_t)E::narrow(acc.y * inv) << 16);
+    const uint32_t w1 =
+        (uint32_t)E::narrow(acc.z * inv) | ((uint32_t)E::narrow(acc.w * inv) << 16);
+    const int h = kvh * GQ + head;
+    *reinterpret_cast<uint2 *>(p.out + b * p.o_sb + h * p.o_sh + (cc % (HD / 4)) * 8) =
+        make_uint2(w0, w1);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1014,13 +1052,34 @@ static int launch_gq(const DecodeParams &p, const Grid &g, int gq, hipStream_t s
   return MXFA_EUNSUPPORTED;
 }
 
-template <int HD, typename T>
-static int launch_combine_t(const CombineParams &c, hipStream_t st) {
-  constexpr int HPB = 256 / (HD / 4);
-  const int heads = c.batch * c.hq;
-  dim3 grid((heads + HPB - 1) / HPB);
-  hipLaunchKernelGGL((split_combine_kernel<HD, T>), grid, dim3(256), 0, st, c);
+// Blocks per pair: enough piece groups that a sequence of typical length
+// (num_splits / batch ranges, +1 for the range ends) folds its pieces in one
+// step of eight loads per thread; at most C / 16 (16 chunks per block).
+template <int HD, int GQ>
+static int combine_chunk_blocks(int batch, int num_splits) {
+  constexpr int C = GQ * HD / 4;
+  const int pieces = (num_splits + batch - 1) / batch + 1;
+  int f = 1;
+  while (f < C / 16 && (kCombineThreads * f / C) * 8 < pieces) f *= 2;
+  return f;
+}
+
+template <int HD, int GQ, typename T>
+static int launch_combine_t(CombineParams c, hipStream_t st) {
+  c.chunk_blocks = combine_chunk_blocks<HD, GQ>(c.batch, c.num_ranges);
+  dim3 grid(c.batch * (c.hq / GQ) * c.chunk_blocks);
+  hipLaunchKernelGGL((split_combine_kernel<HD, GQ, T>), grid, dim3(kCombineThreads), 0, st, c);
   return hipGetLastError() == hipSuccess ? MXFA_OK : MXFA_ELAUNCH;
+}
+
+template <int HD, typename T>
+static int launch_combine_gq(const CombineParams &c, hipStream_t st) {
+  switch (c.gq) {
+    case 2: return launch_combine_t<HD, 2, T>(c, st);
+    case 4: return launch_combine_t<HD, 4, T>(c, st);
+    case 8: return launch_combine_t<HD, 8, T>(c, st);
+  }
+  return MXFA_EUNSUPPORTED;
 }
 
 static int launch(const SplitArgs &a, hipStream_t st) {
@@ -1045,8 +1104,8 @@ static int launch(const SplitArgs &a, hipStream_t st) {
   c.gq = gq;
   c.num_ranges = a.num_splits;
   if (a.dtype == MXFA_DTYPE_BF16)
-    return a.hd == 128 ? launch_combine_t<128, BF16>(c, st) : launch_combine_t<64, BF16>(c, st);
-  return a.hd == 128 ? launch_combine_t<128, F16>(c, st) : launch_combine_t<64, F16>(c, st);
+    return a.hd == 128 ? launch_combine_gq<128, BF16>(c, st) : launch_combine_gq<64, BF16>(c, st);
+  return a.hd == 128 ? launch_combine_gq<128, F16>(c, st) : launch_combine_gq<64, F16>(c, st);
 }
 
 }  // namespace mxfa
