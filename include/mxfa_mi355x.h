@@ -103,6 +103,42 @@ int mxfa_split_decode_launch(const void *q, int64_t q_stride_b, int64_t q_stride
                              void *stream);
 
 /*
+ * Partial stage alone: the first of the two launches of mxfa_split_decode_launch,
+ * same arguments. It writes every sequence that lies inside one work range
+ * (and zeros for empty sequences) to out, and the normalised output and base-2
+ * LSE of every piece of the other sequences, with the tile prefix sums, to the
+ * workspace. Followed by mxfa_split_decode_combine_launch on the same stream it
+ * is the same computation as mxfa_split_decode_launch; alone it lets a caller
+ * time the dominant kernel or schedule the two stages itself.
+ * Counterpart of the paged_decode_v3 launch inside launch_split
+ * (csrc_native/m1_kernel.cpp:985-999).
+ */
+int mxfa_split_decode_partial_launch(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                                     const void *k_cache, const void *v_cache,
+                                     int64_t cache_stride_page, int64_t cache_stride_token,
+                                     int64_t cache_stride_head, const int32_t *block_table,
+                                     int64_t bt_stride, const int32_t *seqlens, int seqlen_add,
+                                     void *out, int64_t out_stride_b, int64_t out_stride_h,
+                                     void *workspace, size_t workspace_bytes, float scale,
+                                     int batch, int q_heads, int kv_heads, int head_dim,
+                                     int page_size, int block_table_width, int num_pages,
+                                     int dtype, int num_splits, void *stream);
+
+/*
+ * Combine stage alone: LSE merge of the pieces of every sequence that crosses
+ * a work range end. The workspace must have been filled by
+ * mxfa_split_decode_partial_launch with the same batch, heads, head_dim and
+ * num_splits, earlier on the same stream; a workspace holding anything else
+ * gives wrong numbers (never an out-of-bounds access).
+ * Counterpart of the split_combine launch (csrc_native/m1_kernel.cpp:1000-1001,
+ * kernel :861-888).
+ */
+int mxfa_split_decode_combine_launch(void *workspace, size_t workspace_bytes, void *out,
+                                     int64_t out_stride_b, int64_t out_stride_h, int batch,
+                                     int q_heads, int kv_heads, int head_dim, int dtype,
+                                     int num_splits, void *stream);
+
+/*
  * vLLM-style paged append: for token t with slot = slot_mapping[t] >= 0,
  * cache[slot / PS, slot % PS, kvh, :] = key/value[t, kvh, :]; slot < 0 is skipped.
  * Bit-exact copy. key/value are [num_tokens, HKV, HD] with strides (tok, head, 1).

@@ -1082,30 +1082,71 @@ static int launch_combine_gq(const CombineParams &c, hipStream_t st) {
   return MXFA_EUNSUPPORTED;
 }
 
-static int launch(const SplitArgs &a, hipStream_t st) {
+static int launch_partial(const SplitArgs &a, hipStream_t st) {
   const Grid g = grid_for(a.hkv, a.num_splits);
   const DecodeParams p = make_params(a, g);
   const int gq = a.hq / a.hkv;
-  int rc;
   if (a.dtype == MXFA_DTYPE_BF16)
-    rc = a.hd == 128 ? launch_gq<128, BF16>(p, g, gq, st) : launch_gq<64, BF16>(p, g, gq, st);
-  else
-    rc = a.hd == 128 ? launch_gq<128, F16>(p, g, gq, st) : launch_gq<64, F16>(p, g, gq, st);
-  if (rc != MXFA_OK) return rc;
+    return a.hd == 128 ? launch_gq<128, BF16>(p, g, gq, st) : launch_gq<64, BF16>(p, g, gq, st);
+  return a.hd == 128 ? launch_gq<128, F16>(p, g, gq, st) : launch_gq<64, F16>(p, g, gq, st);
+}
+
+static int launch_combine(void *ws, void *out, int64_t o_sb, int64_t o_sh, int batch, int hq,
+                          int hkv, int hd, int dtype, int ns, hipStream_t st) {
+  const WsLayout w = ws_layout(batch, hq, hd, ns);
   CombineParams c;
-  c.ws_o = p.ws_o;
-  c.ws_lse = p.ws_lse;
-  c.ws_s = p.ws_s;
-  c.out = p.out;
-  c.o_sb = p.o_sb;
-  c.o_sh = p.o_sh;
-  c.batch = a.batch;
-  c.hq = a.hq;
-  c.gq = gq;
-  c.num_ranges = a.num_splits;
-  if (a.dtype == MXFA_DTYPE_BF16)
-    return a.hd == 128 ? launch_combine_gq<128, BF16>(c, st) : launch_combine_gq<64, BF16>(c, st);
-  return a.hd == 128 ? launch_combine_gq<128, F16>(c, st) : launch_combine_gq<64, F16>(c, st);
+  c.ws_o = (const float *)ws;
+  c.ws_lse = (const float *)ws + w.o_floats;
+  c.ws_s = (const int32_t *)((const float *)ws + w.o_floats + w.lse_floats);
+  c.out = (char *)out;
+  c.o_sb = o_sb * 2;
+  c.o_sh = o_sh * 2;
+  c.batch = batch;
+  c.hq = hq;
+  c.gq = hq / hkv;
+  c.num_ranges = ns;
+  if (dtype == MXFA_DTYPE_BF16)
+    return hd == 128 ? launch_combine_gq<128, BF16>(c, st) : launch_combine_gq<64, BF16>(c, st);
+  return hd == 128 ? launch_combine_gq<128, F16>(c, st) : launch_combine_gq<64, F16>(c, st);
+}
+
+static SplitArgs split_args(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                            const void *k_cache, const void *v_cache, int64_t cache_stride_page,
+                            int64_t cache_stride_token, int64_t cache_stride_head,
+                            const int32_t *block_table, int64_t bt_stride, const int32_t *seqlens,
+                            int seqlen_add, void *out, int64_t out_stride_b, int64_t out_stride_h,
+                            void *workspace, size_t workspace_bytes, float scale, int batch,
+                            int q_heads, int kv_heads, int head_dim, int page_size,
+                            int block_table_width, int num_pages, int dtype, int num_splits) {
+  SplitArgs a;
+  a.q = q;
+  a.q_sb = q_stride_b;
+  a.q_sh = q_stride_h;
+  a.k = k_cache;
+  a.v = v_cache;
+  a.c_sp = cache_stride_page;
+  a.c_st = cache_stride_token;
+  a.c_sh = cache_stride_head;
+  a.bt = block_table;
+  a.bt_stride = bt_stride;
+  a.seqlens = seqlens;
+  a.seqlen_add = seqlen_add;
+  a.out = out;
+  a.o_sb = out_stride_b;
+  a.o_sh = out_stride_h;
+  a.ws = workspace;
+  a.ws_bytes = workspace_bytes;
+  a.scale = scale;
+  a.batch = batch;
+  a.hq = q_heads;
+  a.hkv = kv_heads;
+  a.hd = head_dim;
+  a.ps = page_size;
+  a.btw = block_table_width;
+  a.num_pages = num_pages;
+  a.dtype = dtype;
+  a.num_splits = num_splits;
+  return a;
 }
 
 }  // namespace mxfa
@@ -1157,47 +1198,56 @@ int mxfa_split_decode_workspace_size(int batch, int q_heads, int head_dim, int n
   return MXFA_OK;
 }
 
-int mxfa_split_decode_launch(const void *q, int64_t q_stride_b, int64_t q_stride_h,
-                             const void *k_cache, const void *v_cache,
-                             int64_t cache_stride_page, int64_t cache_stride_token,
-                             int64_t cache_stride_head, const int32_t *block_table,
-                             int64_t bt_stride, const int32_t *seqlens, int seqlen_add,
-                             void *out, int64_t out_stride_b, int64_t out_stride_h,
-                             void *workspace, size_t workspace_bytes_, float scale, int batch,
-                             int q_heads,
-                             int kv_heads, int head_dim, int page_size, int block_table_width,
-                             int num_pages, int dtype, int num_splits, void *stream) {
-  SplitArgs a;
-  a.q = q;
-  a.q_sb = q_stride_b;
-  a.q_sh = q_stride_h;
-  a.k = k_cache;
-  a.v = v_cache;
-  a.c_sp = cache_stride_page;
-  a.c_st = cache_stride_token;
-  a.c_sh = cache_stride_head;
-  a.bt = block_table;
-  a.bt_stride = bt_stride;
-  a.seqlens = seqlens;
-  a.seqlen_add = seqlen_add;
-  a.out = out;
-  a.o_sb = out_stride_b;
-  a.o_sh = out_stride_h;
-  a.ws = workspace;
-  a.ws_bytes = workspace_bytes_;
-  a.scale = scale;
-  a.batch = batch;
-  a.hq = q_heads;
-  a.hkv = kv_heads;
-  a.hd = head_dim;
-  a.ps = page_size;
-  a.btw = block_table_width;
-  a.num_pages = num_pages;
-  a.dtype = dtype;
-  a.num_splits = num_splits;
+#define MXFA_SPLIT_PARAMS                                                                    \
+  const void *q, int64_t q_stride_b, int64_t q_stride_h, const void *k_cache,               \
+      const void *v_cache, int64_t cache_stride_page, int64_t cache_stride_token,           \
+      int64_t cache_stride_head, const int32_t *block_table, int64_t bt_stride,             \
+      const int32_t *seqlens, int seqlen_add, void *out, int64_t out_stride_b,              \
+      int64_t out_stride_h, void *workspace, size_t workspace_bytes, float scale, int batch, \
+      int q_heads, int kv_heads, int head_dim, int page_size, int block_table_width,        \
+      int num_pages, int dtype, int num_splits, void *stream
+#define MXFA_SPLIT_ARGS                                                                      \
+  q, q_stride_b, q_stride_h, k_cache, v_cache, cache_stride_page, cache_stride_token,       \
+      cache_stride_head, block_table, bt_stride, seqlens, seqlen_add, out, out_stride_b,    \
+      out_stride_h, workspace, workspace_bytes, scale, batch, q_heads, kv_heads, head_dim,  \
+      page_size, block_table_width, num_pages, dtype, num_splits
+
+int mxfa_split_decode_launch(MXFA_SPLIT_PARAMS) {
+  const SplitArgs a = split_args(MXFA_SPLIT_ARGS);
+  int rc = check_split_args(a);
+  if (rc != MXFA_OK) return rc;
+  rc = launch_partial(a, (hipStream_t)stream);
+  if (rc != MXFA_OK) return rc;
+  return launch_combine(a.ws, a.out, a.o_sb, a.o_sh, a.batch, a.hq, a.hkv, a.hd, a.dtype,
+                        a.num_splits, (hipStream_t)stream);
+}
+
+int mxfa_split_decode_partial_launch(MXFA_SPLIT_PARAMS) {
+  const SplitArgs a = split_args(MXFA_SPLIT_ARGS);
   const int rc = check_split_args(a);
   if (rc != MXFA_OK) return rc;
-  return launch(a, (hipStream_t)stream);
+  return launch_partial(a, (hipStream_t)stream);
+}
+
+int mxfa_split_decode_combine_launch(void *workspace, size_t workspace_bytes, void *out,
+                                     int64_t out_stride_b, int64_t out_stride_h, int batch,
+                                     int q_heads, int kv_heads, int head_dim, int dtype,
+                                     int num_splits, void *stream) {
+  if (!workspace || !out) return MXFA_EINVAL;
+  if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || num_splits <= 0) return MXFA_EINVAL;
+  if (head_dim != 64 && head_dim != 128) return MXFA_EUNSUPPORTED;
+  if (q_heads % kv_heads != 0) return MXFA_EUNSUPPORTED;
+  const int gq = q_heads / kv_heads;
+  if (gq != 2 && gq != 4 && gq != 8) return MXFA_EUNSUPPORTED;
+  if (dtype != MXFA_DTYPE_F16 && dtype != MXFA_DTYPE_BF16) return MXFA_EUNSUPPORTED;
+  if (batch > kMaxBatch || num_splits > 65535) return MXFA_EUNSUPPORTED;
+  if (!aligned16(workspace) || ((uintptr_t)out & 7u) || ((out_stride_b | out_stride_h) & 3) ||
+      out_stride_b < 0 || out_stride_h < 0)
+    return MXFA_EINVAL;
+  if (workspace_bytes < ws_layout(batch, q_heads, head_dim, num_splits).bytes)
+    return MXFA_EWORKSPACE;
+  return launch_combine(workspace, out, out_stride_b, out_stride_h, batch, q_heads, kv_heads,
+                        head_dim, dtype, num_splits, (hipStream_t)stream);
 }
 
 }  // extern "C"

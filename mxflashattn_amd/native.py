@@ -44,6 +44,8 @@ EXPORTED_SYMBOLS = (
     "mxfa_split_heuristic",
     "mxfa_split_decode_workspace_size",
     "mxfa_split_decode_launch",
+    "mxfa_split_decode_partial_launch",
+    "mxfa_split_decode_combine_launch",
     "mxfa_reshape_and_cache_launch",
     "mxfa_append_kv_launch",
 )
@@ -72,6 +74,15 @@ _SIGNATURES = {
         _i,
         [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _p, _i64, _i64, _p, _sz,
          _f, _i, _i, _i, _i, _i, _i, _i, _i, _i, _p],
+    ),
+    "mxfa_split_decode_partial_launch": (
+        _i,
+        [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _p, _i64, _i64, _p, _sz,
+         _f, _i, _i, _i, _i, _i, _i, _i, _i, _i, _p],
+    ),
+    "mxfa_split_decode_combine_launch": (
+        _i,
+        [_p, _sz, _p, _i64, _i64, _i, _i, _i, _i, _i, _i, _p],
     ),
     "mxfa_reshape_and_cache_launch": (
         _i,
@@ -329,6 +340,51 @@ def paged_decode_split(
                                                     cache_seqlens, out, ws.data_ptr(), ws_bytes,
                                                     softmax_scale, num_splits, seqlen_add))
     _check(rc, "mxfa_split_decode_launch")
+    return out
+
+
+def split_decode_partial(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    cache_seqlens: torch.Tensor,
+    softmax_scale: float,
+    out: torch.Tensor,
+    workspace: torch.Tensor,
+    num_splits: int,
+    seqlen_add: int = 0,
+) -> None:
+    """Partial stage only: sequences inside one work range land in ``out``, the
+    pieces of the others in ``workspace``; ``split_decode_combine`` finishes."""
+    q, block_table, cache_seqlens, out = _prepare(q, k_cache, v_cache, block_table,
+                                                  cache_seqlens, out)
+    _require_device(q, workspace)
+    if not workspace.is_contiguous():
+        raise ValueError("workspace must be contiguous")
+    nbytes = workspace.numel() * workspace.element_size()
+    rc = library().mxfa_split_decode_partial_launch(
+        *_launch_args(q, k_cache, v_cache, block_table, cache_seqlens, out, workspace.data_ptr(),
+                      nbytes, softmax_scale, num_splits, seqlen_add))
+    _check(rc, "mxfa_split_decode_partial_launch")
+
+
+def split_decode_combine(workspace: torch.Tensor, out: torch.Tensor, kv_heads: int,
+                         num_splits: int) -> torch.Tensor:
+    """LSE merge of the pieces in ``workspace`` into ``out`` ([B,1,HQ,HD] or [B,HQ,HD])."""
+    _require_device(out, workspace)
+    if not workspace.is_contiguous() or out.stride(-1) != 1:
+        raise ValueError("workspace must be contiguous and out's last dim contiguous")
+    if out.dim() not in (3, 4) or (out.dim() == 4 and out.shape[1] != 1):
+        raise ValueError(f"out must be [B,1,HQ,HD] or [B,HQ,HD], got {tuple(out.shape)}")
+    batch, hq, hd = out.shape[0], out.shape[-2], out.shape[-1]
+    os_ = out.stride()
+    rc = library().mxfa_split_decode_combine_launch(
+        workspace.data_ptr(), workspace.numel() * workspace.element_size(), out.data_ptr(),
+        os_[0], os_[-2], batch, hq, kv_heads, hd, _dtype_code(out), num_splits,
+        _stream_handle(out.device),
+    )
+    _check(rc, "mxfa_split_decode_combine_launch")
     return out
 
 

@@ -44,7 +44,7 @@ def test_library_loads_and_reports_header_abi(lib):
 
 def test_every_header_function_is_exported_and_bound(lib):
     declared = header_functions()
-    assert len(declared) == len(set(declared)) == 7
+    assert len(declared) == len(set(declared)) == 9
     for name in declared:
         assert hasattr(lib, name), name
     assert set(declared) == set(native.EXPORTED_SYMBOLS) == set(native._SIGNATURES)
@@ -148,6 +148,19 @@ def decode_args(**over):
 ])
 def test_decode_launch_rejects_before_launching(lib, over, code):
     assert lib.mxfa_split_decode_launch(*decode_args(**over)) == code
+    assert lib.mxfa_split_decode_partial_launch(*decode_args(**over)) == code
+
+
+def test_combine_rejects_before_launching(lib):
+    ws = native.workspace_size(4, 8, 64, 3)
+    f = lib.mxfa_split_decode_combine_launch
+    assert f(None, ws, FAKE, 512, 64, 4, 8, 2, 64, 0, 3, None) == -2
+    assert f(FAKE, ws - 4, FAKE, 512, 64, 4, 8, 2, 64, 0, 3, None) == -3
+    assert f(FAKE, ws, FAKE, 512, 64, 4, 8, 2, 96, 0, 3, None) == -1
+    assert f(FAKE, ws, FAKE, 512, 64, 4, 8, 3, 64, 0, 3, None) == -1  # GQ not an integer
+    assert f(FAKE, ws, FAKE, 512, 64, 4, 8, 2, 64, 5, 3, None) == -1
+    assert f(FAKE, ws, FAKE, 512, 64, 0, 8, 2, 64, 0, 3, None) == -2
+    assert f(FAKE, ws, FAKE + 2, 512, 64, 4, 8, 2, 64, 0, 3, None) == -2
 
 
 def test_decode_workspace_boundary_is_exact(lib):

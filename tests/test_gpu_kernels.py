@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from mxflashattn_amd import native
-from mxflashattn_amd.workloads import make_paged_batch
+from mxflashattn_amd.workloads import PagedBatch, make_paged_batch
 from oracle import c_oracle, reference_port
 
 pytestmark = pytest.mark.gpu
@@ -246,3 +246,25 @@ def test_repeated_calls_are_bitwise_reproducible(device, dtype, head_dim, gq):
     assert max_err(first, oracle_out(b)) <= TOL[dtype]
     for _ in range(40):
         assert torch.equal(run_native(b), first)
+
+
+def test_partial_then_combine_equals_one_launch(device):
+    # The two stages launched separately through the C ABI give the same bits
+    # as mxfa_split_decode_launch, including sequences inside one range, pieces
+    # of longer ones and an empty sequence.
+    lengths = torch.tensor([5000, 0, 33, 1200, 16, 7000])
+    b = make_paged_batch(6, 32, 8, 128, torch.bfloat16, lengths, seed=61).to(device)
+    ns = 40
+    one = run_native(b, num_splits=ns).clone()
+    ws = torch.empty(native.workspace_size(6, 32, 128, ns), dtype=torch.uint8, device=device)
+    out = torch.full_like(b.q, float("nan"))
+    native.split_decode_partial(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
+                                b.scale, out, ws, ns)
+    native.split_decode_combine(ws, out, 8, ns)
+    torch.cuda.synchronize()
+    assert torch.equal(out, one)
+    assert torch.equal(one[1], torch.zeros_like(one[1]))  # the empty sequence
+    keep = torch.tensor([0, 2, 3, 4, 5], device=device)
+    sub = PagedBatch(b.q[keep], b.k_cache, b.v_cache, b.block_table[keep], b.cache_seqlens[keep],
+                     b.scale)
+    assert max_err(one[keep], oracle_out(sub)) <= TOL[torch.bfloat16]
