@@ -18,6 +18,9 @@ Prints ONE JSON line:
   cpu_baseline fp32 torch-CPU restatement of reference.attention_kvcache
                (oracle.reference_port) on the host cores, bounded sample
   cells        the six GQ x HD cells of config 2 and configs 1, 3, 4
+  decode_step  config 5: decode tok/s of a 36-layer random-init Qwen3-4B-shaped
+               model whose attention runs through the vLLM backend path
+               (HIP-graph replayed steps), and attention's share of the step
 """
 
 from __future__ import annotations
@@ -50,6 +53,7 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--workload", default=MAIN_WORKLOAD)
     ap.add_argument("--no-cells", action="store_true", help="skip the per-cell table")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode-step", action="store_true", help="skip config 5")
     ap.add_argument("--cpu-reps", type=int, default=15)
     return ap.parse_args()
 
@@ -242,6 +246,19 @@ def main() -> int:
             cells[name] = measure_workload(name, cspec, device, 100, 10)
             print(f"[bench] {name}: {cells[name]}", file=sys.stderr, flush=True)
 
+    decode = None
+    if not args.no_decode_step:
+        from mxflashattn_amd.integrations.vllm import decode_step
+
+        print("[bench] config5 decode step", file=sys.stderr, flush=True)
+        try:
+            decode = decode_step.run(device=device)
+        except Exception as exc:  # reported in the line, the main metric still prints
+            print(f"[bench] config5 decode step failed: {exc!r}", file=sys.stderr, flush=True)
+            decode = {"error": repr(exc)}
+        print(f"[bench] config5: {decode}", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+
     cpu = None
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
@@ -286,6 +303,7 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
         "cells": cells,
+        "decode_step": decode,
     }
     print(json.dumps(line))
     return 0

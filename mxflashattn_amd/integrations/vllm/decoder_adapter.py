@@ -16,6 +16,9 @@ from typing import Any
 import torch
 
 from ... import api
+from ...dispatch import get_last_dispatch_info
+from .backend import record_event
+from .native_decode import reshape_and_cache_flash
 
 # inspect_layout() reads query_start_loc / seq_lens back to the host (a device
 # sync per layer per step); it runs only when MXFLASHATTN_STRICT_LAYOUT=1.
@@ -215,3 +218,34 @@ def _decode_forward_graph(query: torch.Tensor, kv_cache: torch.Tensor, attn_meta
         block_table=block_table.contiguous(), softmax_scale=softmax_scale, causal=causal,
     )
     return result.reshape(q.shape[0] * q.shape[1], -1), None
+
+
+def forward_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: Any,
+                   output: torch.Tensor, *, softmax_scale: float) -> torch.Tensor:
+    """The decode body of the backend's ``forward``: one-token paged decode into
+    vLLM's output buffer, with the dispatch event the reference plugin records
+    (integrations/vllm/vllm_plugin.py:297-299,399-431). Raises
+    DecoderAdapterBlocked for calls outside the adapter contract (prefill,
+    cascade), which the backend hands to vLLM."""
+    result, _ = decode_forward(query, kv_cache, attn_metadata, softmax_scale=softmax_scale,
+                               causal=bool(attn_metadata.causal))
+    info = get_last_dispatch_info()
+    if info is None:
+        raise RuntimeError("MXFlashAttn decoder returned without dispatch evidence")
+    record_event({"path": info.backend, "operation": info.operation,
+                  "fallback": "false" if info.fallback_reason is None else "true"})
+    target = output[: result.shape[0]]
+    if target.numel() != result.numel():
+        raise RuntimeError(
+            f"MXFlashAttn decoder output size mismatch: target={tuple(target.shape)} "
+            f"result={tuple(result.shape)}")
+    target.copy_(result.reshape_as(target))
+    return output
+
+
+def kv_cache_update(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
+                    slot_mapping: torch.Tensor, kv_cache_dtype: str = "auto") -> None:
+    """The backend's ``do_kv_cache_update``: new K/V rows of [tokens, HKV, HD]
+    into the [2, blocks, PS, HKV, HD] cache at slot_mapping (vllm_plugin.py:507-511)."""
+    key_cache, value_cache = kv_cache.unbind(0)
+    reshape_and_cache_flash(key, value, key_cache, value_cache, slot_mapping, kv_cache_dtype)

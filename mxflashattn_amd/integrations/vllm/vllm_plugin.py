@@ -22,10 +22,9 @@ from vllm.v1.attention.backends.flash_attn import (  # noqa: F401  (requires vLL
     FlashAttentionImpl,
 )
 
-from ...dispatch import get_last_dispatch_info
 from . import native_decode
 from .backend import record_event
-from .decoder_adapter import DecoderAdapterBlocked, decode_forward
+from .decoder_adapter import DecoderAdapterBlocked, forward_decode, kv_cache_update
 
 
 def _forward_official_split(impl, layer, query, key, value, kv_cache, metadata, output,
@@ -72,34 +71,20 @@ class MXFlashAttnImpl(FlashAttentionImpl):
             return _forward_official_split(self, layer, query, key, value, kv_cache,
                                            attn_metadata, output, output_scale,
                                            output_block_scale)
+        if output is None:
+            raise ValueError("vLLM must provide an output buffer")
         try:
-            result, _ = decode_forward(query, kv_cache, attn_metadata, softmax_scale=self.scale,
-                                       causal=bool(attn_metadata.causal))
+            return forward_decode(query, kv_cache, attn_metadata, output,
+                                  softmax_scale=self.scale)
         except DecoderAdapterBlocked as exc:
             record_event({"path": "vendor_prefill_or_blocked", "reason": str(exc)})
             if "single_token_decode" in str(exc):
                 return super().forward(layer, query, key, value, kv_cache, attn_metadata,
                                        output, output_scale, output_block_scale)
             raise
-        info = get_last_dispatch_info()
-        if info is None:
-            raise RuntimeError("MXFlashAttn decoder returned without dispatch evidence")
-        record_event({"path": info.backend, "operation": info.operation,
-                      "fallback": "false" if info.fallback_reason is None else "true"})
-        if output is None:
-            raise ValueError("vLLM must provide an output buffer")
-        target = output[: result.shape[0]]
-        if target.numel() != result.numel():
-            raise RuntimeError(
-                f"MXFlashAttn decoder output size mismatch: target={tuple(target.shape)} "
-                f"result={tuple(result.shape)}")
-        target.copy_(result.reshape_as(target))
-        return output
 
     def do_kv_cache_update(self, layer, key, value, kv_cache, slot_mapping):
-        key_cache, value_cache = kv_cache.unbind(0)
-        native_decode.reshape_and_cache_flash(key, value, key_cache, value_cache, slot_mapping,
-                                              self.kv_cache_dtype)
+        kv_cache_update(key, value, kv_cache, slot_mapping, self.kv_cache_dtype)
 
 
 class MXFlashAttnBackend(FlashAttentionBackend):
