@@ -65,8 +65,7 @@ class DecodeMetadata:
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    xf = x.float()
-    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype) * weight
+    return torch.nn.functional.rms_norm(x, (x.shape[-1],), weight, eps)
 
 
 class DecoderModel:
@@ -110,11 +109,15 @@ class DecoderModel:
             n += sum(t.numel() for t in layer.values())
         return n * self.embed.element_size()
 
-    def rope(self, x: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
-        """Rotary positions (rotate-half form) on [B, heads, head_dim], in fp32."""
+    def rope_tables(self, positions: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """cos/sin [B, 1, head_dim] of the step's positions (shared by all layers)."""
         freqs = positions.float()[:, None] * self.inv_freq[None, :]      # [B, HD/2]
-        cos = torch.cat([freqs.cos(), freqs.cos()], dim=-1)[:, None, :]
-        sin = torch.cat([freqs.sin(), freqs.sin()], dim=-1)[:, None, :]
+        emb = torch.cat([freqs, freqs], dim=-1)[:, None, :]
+        return emb.cos(), emb.sin()
+
+    @staticmethod
+    def rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+        """Rotary positions (rotate-half form) on [B, heads, head_dim], in fp32."""
         xf = x.float()
         half = xf.shape[-1] // 2
         rotated = torch.cat([-xf[..., half:], xf[..., :half]], dim=-1)
@@ -133,6 +136,7 @@ class DecoderModel:
         bsz = tokens.shape[0]
         nq, nkv = s.q_heads * s.head_dim, s.kv_heads * s.head_dim
         x = self.embed[tokens]
+        cos, sin = self.rope_tables(positions)
         attn_out = torch.empty(bsz, nq, device=self.device, dtype=self.dtype)
         for i, layer in enumerate(self.layers):
             h = rms_norm(x, layer["ln1"], s.eps)
@@ -140,8 +144,8 @@ class DecoderModel:
             q = qkv[:, :nq].view(bsz, s.q_heads, s.head_dim)
             k = qkv[:, nq:nq + nkv].view(bsz, s.kv_heads, s.head_dim)
             v = qkv[:, nq + nkv:].view(bsz, s.kv_heads, s.head_dim)
-            q = self.rope(rms_norm(q, layer["q_norm"], s.eps), positions)
-            k = self.rope(rms_norm(k, layer["k_norm"], s.eps), positions)
+            q = self.rope(rms_norm(q, layer["q_norm"], s.eps), cos, sin)
+            k = self.rope(rms_norm(k, layer["k_norm"], s.eps), cos, sin)
             self.attention(i, q, k, v, kv_caches[i], meta, attn_out)
             x = x + attn_out @ layer["o"].t()
             h = rms_norm(x, layer["ln2"], s.eps)
