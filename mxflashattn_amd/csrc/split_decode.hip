@@ -65,13 +65,10 @@
 
 namespace mxfa {
 
-constexpr int kWaves = 8;
-constexpr int kThreads = kWaves * 64;
 constexpr int kTile = 16;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleLog2 = 8.0f;
 constexpr int kMaxBatch = 16384;  // tile prefix sums live in LDS
-constexpr int kMaxHeadsPerWg = 8;
 constexpr uint32_t kSrdWord3 = 0x00020000u;  // raw 32-bit buffer, gfx9 family
 constexpr int kAuxStream = 2;                // nt: no temporal reuse expected
 constexpr int kOffOut = 0x40000000;          // a lane offset no descriptor covers
@@ -299,6 +296,7 @@ __device__ __forceinline__ float head_of_row(float x, int row) {
 }
 
 // Exclusive prefix sum of per-sequence tile counts into s[0..B] (LDS), all threads.
+template <int kThreads>
 __device__ __forceinline__ void tile_prefix(const DecodeParams &p, int32_t *s, int *wave_tot) {
   const int B = p.batch;
   const int per = (B + kThreads - 1) / kThreads;
@@ -334,7 +332,7 @@ __device__ __forceinline__ void tile_prefix(const DecodeParams &p, int32_t *s, i
 
 // Empty sequences (no tiles) get zero output; sequence b is cleared by the
 // workgroups with blockIdx.y == b % gridDim.y, each for its own kv heads.
-template <int HD, int GQ>
+template <int HD, int GQ, int kThreads>
 __device__ __forceinline__ void zero_empty(const DecodeParams &p, const int32_t *s) {
   const int kv0 = blockIdx.x * p.heads_per_wg;
   const int kv1 = min(kv0 + p.heads_per_wg, p.hkv);
@@ -745,13 +743,15 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   });
 }
 
-template <int HD, int GQ, typename T, bool kLanePages, bool kPvMfma, int NBUF, int kMinWgPerCu>
-__global__ __launch_bounds__(kThreads, kMinWgPerCu) void split_partial_kernel(DecodeParams p) {
+template <int HD, int GQ, typename T, bool kLanePages, bool kPvMfma, int NBUF, int WAVES,
+          int kMinWgPerCu>
+__global__ __launch_bounds__(WAVES * 64, kMinWgPerCu) void split_partial_kernel(DecodeParams p) {
+  constexpr int kThreads = WAVES * 64;
   extern __shared__ int32_t s_tiles[];  // [B + 1]
-  __shared__ int s_wave_tot[kWaves];
+  __shared__ int s_wave_tot[WAVES];
 
-  tile_prefix(p, s_tiles, s_wave_tot);  // ends with a barrier
-  zero_empty<HD, GQ>(p, s_tiles);
+  tile_prefix<kThreads>(p, s_tiles, s_wave_tot);  // ends with a barrier
+  zero_empty<HD, GQ, kThreads>(p, s_tiles);
   const int B = p.batch;
   if (blockIdx.x == 0 && blockIdx.y == 0) {
     for (int i = threadIdx.x; i <= B; i += kThreads) p.ws_s[i] = s_tiles[i];
@@ -967,10 +967,11 @@ struct Grid {
   int heads_per_wg, subs, gx, gy;
 };
 
-static Grid grid_for(int hkv, int num_splits) {
+// Workgroups of `waves` waves: min(HKV, waves) kv heads x waves / that sub-ranges.
+static Grid grid_for(int hkv, int num_splits, int waves) {
   Grid g;
-  g.heads_per_wg = hkv < kMaxHeadsPerWg ? hkv : kMaxHeadsPerWg;
-  g.subs = kWaves / g.heads_per_wg;
+  g.heads_per_wg = hkv < waves ? hkv : waves;
+  g.subs = waves / g.heads_per_wg;
   g.gx = (hkv + g.heads_per_wg - 1) / g.heads_per_wg;
   g.gy = (num_splits + g.subs - 1) / g.subs;
   return g;
@@ -1009,9 +1010,26 @@ static DecodeParams make_params(const SplitArgs &a, const Grid &g) {
   return p;
 }
 
-// One workgroup (8 waves, two per SIMD) per CU; measured on MI355X against two
-// per CU (16 waves): HD 128 loses 3% with two, HD 64 loses 5-17% (twice as
-// many ranges, so twice the pieces to merge and half the tiles per wave).
+// Waves per workgroup: one wave per kv head (KH = min(HKV, max) kv heads per
+// workgroup), at least 4 waves (S = 4 / KH sub-ranges when HKV < 4), at most
+// 8 at HD 64 and 4 at HD 128; one workgroup per CU. Measured on MI355X
+// (one call, config-2 lengths): at HD 128 eight-wave workgroups run as two
+// generations of four waves per CU (the second wave on each SIMD issues its
+// first loads only when the first finishes, since four waves already fill
+// the CU's vector-memory queue), which leaves a drain tail: four-wave
+// workgroups are 3% (GQ4) to 10% (GQ8) faster. At HD 64 all eight waves run
+// together; eight beat four by 2-3% at 8 kv heads, four beat two sub-ranges of
+// eight by 10% at 4 kv heads; two workgroups per CU lose 2-15% everywhere.
+template <int HD>
+constexpr int kMaxWaves = HD == 64 ? 8 : 4;
+constexpr int kMinWaves = 4;
+
+static int waves_for(int hd, int hkv) {
+  const int most = hd == 64 ? kMaxWaves<64> : kMaxWaves<128>;
+  const int kh = hkv < most ? hkv : most;
+  return kh >= kMinWaves ? kh : kMinWaves;
+}
+
 template <int HD>
 constexpr int kWgPerCu = 1;
 // Register sets of the tile pipeline: HD 64 tiles are half the bytes, so a
@@ -1025,21 +1043,27 @@ constexpr int kNbuf = HD == 64 ? 3 : 2;
 // HD 128, 14% at HD 64), so every supported GQ uses them.
 constexpr int kPvMfmaMinGq = 2;
 
-template <int HD, int GQ, typename T>
-static int launch_t(const DecodeParams &p, const Grid &g, hipStream_t st) {
+template <int HD, int GQ, typename T, int WAVES>
+static int launch_w(const DecodeParams &p, const Grid &g, hipStream_t st) {
   dim3 grid(g.gx, g.gy);
   const size_t lds = (size_t)(p.batch + 1) * sizeof(int32_t);
+  constexpr bool kMfma = GQ >= kPvMfmaMinGq;
   if (p.ps_log2 >= 4)
-    hipLaunchKernelGGL((split_partial_kernel<HD, GQ, T, false, (GQ >= kPvMfmaMinGq), kNbuf<HD>,
+    hipLaunchKernelGGL((split_partial_kernel<HD, GQ, T, false, kMfma, kNbuf<HD>, WAVES,
                                              kWgPerCu<HD>>),
-                       grid,
-                       dim3(kThreads), lds, st, p);
+                       grid, dim3(WAVES * 64), lds, st, p);
   else
-    hipLaunchKernelGGL((split_partial_kernel<HD, GQ, T, true, (GQ >= kPvMfmaMinGq), 2,
-                                             kWgPerCu<HD>>),
-                       grid,
-                       dim3(kThreads), lds, st, p);
+    hipLaunchKernelGGL((split_partial_kernel<HD, GQ, T, true, kMfma, 2, WAVES, kWgPerCu<HD>>),
+                       grid, dim3(WAVES * 64), lds, st, p);
   return hipGetLastError() == hipSuccess ? MXFA_OK : MXFA_ELAUNCH;
+}
+
+template <int HD, int GQ, typename T>
+static int launch_t(const DecodeParams &p, const Grid &g, hipStream_t st) {
+  if constexpr (kMaxWaves<HD> == 8) {
+    if (g.heads_per_wg * g.subs == 8) return launch_w<HD, GQ, T, 8>(p, g, st);
+  }
+  return launch_w<HD, GQ, T, 4>(p, g, st);
 }
 
 template <int HD, typename T>
@@ -1083,7 +1107,7 @@ static int launch_combine_gq(const CombineParams &c, hipStream_t st) {
 }
 
 static int launch_partial(const SplitArgs &a, hipStream_t st) {
-  const Grid g = grid_for(a.hkv, a.num_splits);
+  const Grid g = grid_for(a.hkv, a.num_splits, waves_for(a.hd, a.hkv));
   const DecodeParams p = make_params(a, g);
   const int gq = a.hq / a.hkv;
   if (a.dtype == MXFA_DTYPE_BF16)
@@ -1175,10 +1199,10 @@ int mxfa_split_heuristic(int batch, int q_heads, int kv_heads, int head_dim, int
   if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || page_size <= 0 ||
       block_table_width <= 0 || num_cus <= 0)
     return MXFA_EINVAL;
-  // One range per wave: kWgPerCu workgroups of 8 waves fill every CU, and each
-  // wave streams one (kv head, range). The kernel lowers the count to the real
-  // tile total on the device.
-  const Grid g = grid_for(kv_heads, 1);
+  // One range per wave: one workgroup (waves_for waves) fills every CU, and
+  // each wave streams one (kv head, range). The kernel lowers the count to the
+  // real tile total on the device.
+  const Grid g = grid_for(kv_heads, 1, waves_for(head_dim, kv_heads));
   const int64_t per_cu = head_dim == 64 ? kWgPerCu<64> : kWgPerCu<128>;
   int64_t n = (int64_t)num_cus * per_cu * g.subs / g.gx;
   const int64_t cap = (int64_t)block_table_width * page_size;

@@ -67,10 +67,12 @@ def test_strerror_is_distinct_per_code(lib):
 
 
 def heuristic_closed_form(b, hq, hkv, hd, ps, btw, cus):
-    # One wave per (kv head, range): workgroups of 8 waves hold min(HKV, 8) kv
-    # heads x 8 // that sub-ranges, one workgroup per CU.
-    kh = min(hkv, 8)
-    subs = 8 // kh
+    # One wave per (kv head, range): a workgroup has max(4, min(HKV, 8 at HD64,
+    # 4 at HD128)) waves = min(HKV, waves) kv heads x waves // that sub-ranges,
+    # one workgroup per CU.
+    waves = max(4, min(hkv, 8 if hd == 64 else 4))
+    kh = min(hkv, waves)
+    subs = waves // kh
     gx = -(-hkv // kh)
     n = cus * subs // gx
     n = min(n, b * -(-(btw * ps) // 16))
@@ -86,6 +88,8 @@ def heuristic_closed_form(b, hq, hkv, hd, ps, btw, cus):
     (4, 32, 4, 128, 256, 128, 304),    # other CU count
     (16384, 64, 8, 128, 16, 4096, 256),
     (8, 24, 3, 128, 16, 64, 256),      # kv heads not a power of two
+    (4, 8, 2, 64, 16, 128, 256),       # config 1: two sub-ranges of two kv heads
+    (32, 32, 8, 64, 16, 512, 256),     # GQ4 HD64: eight waves
     (8, 96, 12, 128, 16, 64, 256),
 ])
 def test_split_heuristic_closed_form(args):
@@ -93,9 +97,11 @@ def test_split_heuristic_closed_form(args):
 
 
 def test_split_heuristic_known_values():
-    assert native.split_heuristic(32, 32, 8, 128, 16, 512, 256) == 256
-    assert native.split_heuristic(32, 32, 4, 64, 16, 512, 256) == 512
-    assert native.split_heuristic(32, 32, 16, 128, 16, 512, 256) == 128
+    assert native.split_heuristic(32, 32, 8, 128, 16, 512, 256) == 128
+    assert native.split_heuristic(32, 32, 4, 64, 16, 512, 256) == 256
+    assert native.split_heuristic(32, 32, 8, 64, 16, 512, 256) == 256
+    assert native.split_heuristic(32, 32, 16, 128, 16, 512, 256) == 64
+    assert native.split_heuristic(4, 8, 2, 64, 16, 128, 256) == 512
     assert native.split_heuristic(1, 2, 1, 64, 16, 1, 256) == 1
 
 

@@ -268,3 +268,29 @@ def test_partial_then_combine_equals_one_launch(device):
     sub = PagedBatch(b.q[keep], b.k_cache, b.v_cache, b.block_table[keep], b.cache_seqlens[keep],
                      b.scale)
     assert max_err(one[keep], oracle_out(sub)) <= TOL[torch.bfloat16]
+
+
+def test_graph_replays_match_eager(device):
+    # One decode call captured in a HIP graph (the workspace allocated by an
+    # eager call on the capture stream first) and replayed several times with
+    # unrelated eager work between replays: every replay equals the eager call.
+    b = make_paged_batch(5, 16, 4, 64, torch.float16, torch.tensor([700, 3, 1500, 64, 0]),
+                         seed=71).to(device)
+    stream = torch.cuda.Stream(device)
+    out = torch.empty_like(b.q)
+    with torch.cuda.stream(stream):
+        native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
+                                  b.scale, out=out)
+        eager = out.clone()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
+                                  b.scale, out=out)
+    for i in range(4):
+        out.fill_(float("nan"))
+        with torch.cuda.stream(stream):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), i
+        _ = (torch.randn(4096, device=device) * i).sum().item()
