@@ -10,7 +10,8 @@
  * (no host reads of device data, no memsets).
  *
  * Layouts (elements, not bytes; the last dimension of every tensor must be
- * contiguous and every base pointer 16-byte aligned):
+ * contiguous and every base pointer 16-byte aligned; an fp8 cache's element is
+ * one byte):
  *   q        [B, HQ, HD]                 strides (q_stride_b, q_stride_h, 1)
  *   cache    [num_pages, PS, HKV, HD]    strides (page, token, head, 1)
  *   out      [B, HQ, HD]                 strides (out_stride_b, out_stride_h, 1)
@@ -33,7 +34,7 @@
 extern "C" {
 #endif
 
-#define MXFA_ABI_VERSION 2
+#define MXFA_ABI_VERSION 3
 
 /* Return codes. */
 #define MXFA_OK 0
@@ -86,10 +87,11 @@ int mxfa_split_decode_workspace_size(int batch, int q_heads, int head_dim, int n
  * and its two launches (partial, then split_combine, :985-1001): the same
  * information plus explicit strides, seqlen_add and a sized workspace; the
  * per-split length c_len is gone because ranges are cut on the device.
- * Supported: HD in {64,128}, HQ/HKV in {2,4,8}, PS a power of two in [1, 4096],
- * dtype F16/BF16 (q, caches and out share it), batch <= 16384, non-overlapping
- * token rows (cache_stride_token >= HD when PS > 1) and query heads
- * (q_stride_h >= HD).
+ * Supported: HD in {64,128,256}, HQ/HKV in 1..16, PS a power of two in
+ * [1, 4096], dtype F16/BF16 (q, caches and out share it), batch <= 16384,
+ * non-overlapping token rows (cache_stride_token >= HD when PS > 1) and query
+ * heads (q_stride_h >= HD). The reference supports HD {64,128} and HQ/HKV
+ * {2,4,8} only (integrations/vllm/vllm_plugin.py:220-261 hands the rest back).
  */
 int mxfa_split_decode_launch(const void *q, int64_t q_stride_b, int64_t q_stride_h,
                              const void *k_cache, const void *v_cache,
@@ -139,6 +141,48 @@ int mxfa_split_decode_combine_launch(void *workspace, size_t workspace_bytes, vo
                                      int num_splits, void *stream);
 
 /*
+ * Split-KV paged decode over an fp8 KV cache (OCP e4m3fn, one byte per
+ * element): out = softmax(q.(k_scale*K)^T * scale) . (v_scale*V). Arguments as
+ * mxfa_split_decode_launch, with cache strides in bytes (multiples of 16) and
+ * `dtype` naming q and out (F16/BF16); k_scale and v_scale point to one fp32
+ * each in device memory (nullptr: 1.0), read by the kernel, so a captured
+ * graph sees later updates. K and V are widened exactly to dtype on the
+ * device; the scales fold into the score scale and the output normalisation.
+ * Uses the same workspace size and combine as the 16-bit launch.
+ * No reference counterpart: the reference has no fp8 cache
+ * (docs/support-matrix.md:27). For callers with an fp8 vLLM cache
+ * (kv_cache_dtype "fp8"/"fp8_e4m3").
+ */
+int mxfa_split_decode_fp8_launch(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                                 const void *k_cache, const void *v_cache,
+                                 int64_t cache_stride_page, int64_t cache_stride_token,
+                                 int64_t cache_stride_head, const int32_t *block_table,
+                                 int64_t bt_stride, const int32_t *seqlens, int seqlen_add,
+                                 void *out, int64_t out_stride_b, int64_t out_stride_h,
+                                 void *workspace, size_t workspace_bytes, float scale, int batch,
+                                 int q_heads, int kv_heads, int head_dim, int page_size,
+                                 int block_table_width, int num_pages, int dtype, int num_splits,
+                                 const float *k_scale, const float *v_scale, void *stream);
+
+/*
+ * Partial stage alone of mxfa_split_decode_fp8_launch (same arguments);
+ * followed by mxfa_split_decode_combine_launch it is the same computation.
+ * No reference counterpart (see mxfa_split_decode_fp8_launch).
+ */
+int mxfa_split_decode_fp8_partial_launch(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                                         const void *k_cache, const void *v_cache,
+                                         int64_t cache_stride_page, int64_t cache_stride_token,
+                                         int64_t cache_stride_head, const int32_t *block_table,
+                                         int64_t bt_stride, const int32_t *seqlens,
+                                         int seqlen_add, void *out, int64_t out_stride_b,
+                                         int64_t out_stride_h, void *workspace,
+                                         size_t workspace_bytes, float scale, int batch,
+                                         int q_heads, int kv_heads, int head_dim, int page_size,
+                                         int block_table_width, int num_pages, int dtype,
+                                         int num_splits, const float *k_scale,
+                                         const float *v_scale, void *stream);
+
+/*
  * vLLM-style paged append: for token t with slot = slot_mapping[t] >= 0,
  * cache[slot / PS, slot % PS, kvh, :] = key/value[t, kvh, :]; slot < 0 is skipped.
  * Bit-exact copy. key/value are [num_tokens, HKV, HD] with strides (tok, head, 1).
@@ -152,6 +196,26 @@ int mxfa_reshape_and_cache_launch(const void *key, const void *value,
                                   const int64_t *slot_mapping, int num_tokens, int kv_heads,
                                   int head_dim, int page_size, int num_pages, int dtype,
                                   void *stream);
+
+/*
+ * vLLM-style paged append into an fp8 cache (kv_cache_dtype "fp8"): as
+ * mxfa_reshape_and_cache_launch, but each element becomes
+ * e4m3fn_rne(saturate(x / scale, +-448)) with x widened exactly from dtype,
+ * the division correctly rounded in fp32, scale = *k_scale for K and *v_scale
+ * for V (device pointers, nullptr: 1.0), NaN kept NaN. Cache strides in bytes,
+ * multiples of 16; HD a multiple of 16. Counterpart of the vendor
+ * reshape_and_cache_flash called with an fp8 kv_cache_dtype and the layer's
+ * scales: the reference plugin reuses the vendor's do_kv_cache_update
+ * (integrations/vllm/vllm_plugin.py:507-511), and its decode path has no fp8
+ * support (docs/support-matrix.md:27). For fp8 vLLM caches.
+ */
+int mxfa_reshape_and_cache_fp8_launch(const void *key, const void *value,
+                                      int64_t kv_stride_token, int64_t kv_stride_head,
+                                      void *k_cache, void *v_cache, int64_t cache_stride_page,
+                                      int64_t cache_stride_token, int64_t cache_stride_head,
+                                      const int64_t *slot_mapping, int num_tokens, int kv_heads,
+                                      int head_dim, int page_size, int num_pages, int dtype,
+                                      const float *k_scale, const float *v_scale, void *stream);
 
 /*
  * Block-table append used by flash_attn_with_kvcache(k=, v=): token t of

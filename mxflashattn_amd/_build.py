@@ -7,6 +7,7 @@ mxflashattn_amd._build`` or ``__graft_entry__.build()``.
 
 from __future__ import annotations
 
+import concurrent.futures
 import os
 import shutil
 import subprocess
@@ -20,16 +21,18 @@ INCLUDE_DIR = REPO_DIR / "include"
 LIB_DIR = PACKAGE_DIR / "_lib"
 LIB_NAME = "libmxfa_mi355x.so"
 LIB_PATH = LIB_DIR / LIB_NAME
-SOURCES = ("split_decode.hip", "kv_append.hip")
+SOURCES = ("split_decode.hip", "split_hd64.hip", "split_hd128.hip", "split_hd256.hip",
+           "kv_append.hip")
 ARCH = "gfx950"
 
-# Packed-fp32 VALU forms are disabled for every device pass.
+# Packed-fp32 VALU forms are disabled for every device pass: hipcc forms them
+# from plain float code, and some of their forms have given wrong results on
+# MI355X boxes with no error raised.
 HIPCC_FLAGS = (
     f"--offload-arch={ARCH}",
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     "-mcode-object-version=5",
     "-Xclang",
     "-target-feature",
@@ -49,31 +52,41 @@ def hipcc_path() -> str:
     return found
 
 
-def build_command(output: Path = LIB_PATH, extra: tuple[str, ...] = ()) -> list[str]:
-    return [
-        hipcc_path(),
-        *HIPCC_FLAGS,
-        *extra,
-        f"-I{INCLUDE_DIR}",
-        f"-I{CSRC_DIR}",
-        *(str(CSRC_DIR / name) for name in SOURCES),
-        "-o",
-        str(output),
-    ]
+def compile_command(source: Path, obj: Path, extra: tuple[str, ...] = ()) -> list[str]:
+    return [hipcc_path(), *HIPCC_FLAGS, *extra, f"-I{INCLUDE_DIR}", f"-I{CSRC_DIR}", "-c",
+            str(source), "-o", str(obj)]
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile the library; always recompiles. Returns the library path."""
-    LIB_DIR.mkdir(parents=True, exist_ok=True)
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = build_command(tmp)
-    if verbose:
-        print(" ".join(cmd), flush=True)
+def link_command(objs: list[Path], output: Path) -> list[str]:
+    return [hipcc_path(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o",
+            str(output)]
+
+
+def _run(cmd: list[str]) -> None:
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
         raise RuntimeError(
-            f"hipcc failed ({result.returncode}):\n{result.stdout}\n{result.stderr}"
+            f"hipcc failed ({result.returncode}): {' '.join(cmd)}\n{result.stdout}\n{result.stderr}"
         )
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile the library; always recompiles (one hipcc per source, in
+    parallel, then one link). Returns the library path."""
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    obj_dir = LIB_DIR / "obj"
+    obj_dir.mkdir(exist_ok=True)
+    objs = [obj_dir / (Path(name).stem + ".o") for name in SOURCES]
+    cmds = [compile_command(CSRC_DIR / name, obj) for name, obj in zip(SOURCES, objs)]
+    if verbose:
+        for cmd in cmds:
+            print(" ".join(cmd), flush=True)
+    workers = jobs or min(len(cmds), os.cpu_count() or 1)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
+        for future in [pool.submit(_run, cmd) for cmd in cmds]:
+            future.result()
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    _run(link_command(objs, tmp))
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

@@ -8,10 +8,16 @@
 //     logical position seqlens[b] + t, page block_table[b, pos / PS].
 // Destinations outside the cache (page id out of range, position beyond the
 // block table) are skipped, never written.
+//
+// fp8 caches (slot form): each element is divided by its tensor's scale in
+// fp32 (correctly rounded), saturated to the finite e4m3fn range [-448, 448]
+// (NaN stays NaN) and rounded to nearest-even OCP e4m3fn by v_cvt_pk_fp8_f32;
+// a thread turns 16 bytes of K (and of V) into 8.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "mxfa_device.h"
 #include "mxfa_mi355x.h"
 
 namespace mxfa {
@@ -67,6 +73,70 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
     const int64_t dst = page * p.c_sp + off * p.c_st + (int64_t)h * p.c_sh + f * 8;
     *reinterpret_cast<uint4 *>(p.kc + dst) = *reinterpret_cast<const uint4 *>(p.k + src);
     *reinterpret_cast<uint4 *>(p.vc + dst) = *reinterpret_cast<const uint4 *>(p.v + src);
+  }
+}
+
+struct QuantAppendParams {
+  const uint16_t *k;
+  const uint16_t *v;
+  int64_t s_t, s_h;  // source strides (token, head), elements
+  uint8_t *kc;
+  uint8_t *vc;
+  int64_t c_sp, c_st, c_sh;  // cache strides, bytes
+  const int64_t *slots;
+  const float *k_scale;
+  const float *v_scale;
+  int rows;
+  int hkv;
+  int frags;  // 8-element fragments per head row (HD / 8)
+  int ps;
+  int num_pages;
+};
+
+__device__ __forceinline__ float fp8_saturate(float y) {
+  return y != y ? y : fminf(fmaxf(y, -448.f), 448.f);
+}
+
+// Eight 16-bit elements divided by s, as eight e4m3fn bytes (byte i = element i).
+template <typename T>
+__device__ __forceinline__ uint2 quantize8(const uint4 w, float s) {
+  using E = Elem<T>;
+  const uint32_t in[4] = {w.x, w.y, w.z, w.w};
+  uint32_t out[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const float a = fp8_saturate(__fdiv_rn(E::lo(in[2 * j]), s));
+    const float b = fp8_saturate(__fdiv_rn(E::hi(in[2 * j]), s));
+    const float c = fp8_saturate(__fdiv_rn(E::lo(in[2 * j + 1]), s));
+    const float d = fp8_saturate(__fdiv_rn(E::hi(in[2 * j + 1]), s));
+    int r = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    r = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, r, true);
+    out[j] = (uint32_t)r;
+  }
+  return make_uint2(out[0], out[1]);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void kv_quant_append_kernel(QuantAppendParams p) {
+  const float ks = p.k_scale ? p.k_scale[0] : 1.f;
+  const float vs = p.v_scale ? p.v_scale[0] : 1.f;
+  const int64_t total = (int64_t)p.rows * p.hkv * p.frags;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int f = (int)(i % p.frags);
+    const int64_t rh = i / p.frags;
+    const int h = (int)(rh % p.hkv);
+    const int r = (int)(rh / p.hkv);
+    const int64_t slot = p.slots[r];
+    if (slot < 0) continue;
+    const int64_t page = slot / p.ps, off = slot % p.ps;
+    if (page >= p.num_pages) continue;
+    const int64_t src = (int64_t)r * p.s_t + (int64_t)h * p.s_h + f * 8;
+    const int64_t dst = page * p.c_sp + off * p.c_st + (int64_t)h * p.c_sh + f * 8;
+    *reinterpret_cast<uint2 *>(p.kc + dst) =
+        quantize8<T>(*reinterpret_cast<const uint4 *>(p.k + src), ks);
+    *reinterpret_cast<uint2 *>(p.vc + dst) =
+        quantize8<T>(*reinterpret_cast<const uint4 *>(p.v + src), vs);
   }
 }
 
@@ -132,6 +202,58 @@ int mxfa_reshape_and_cache_launch(const void *key, const void *value, int64_t kv
   p.ps = page_size;
   p.num_pages = num_pages;
   return launch_append<false>(p, (hipStream_t)stream);
+}
+
+int mxfa_reshape_and_cache_fp8_launch(const void *key, const void *value,
+                                      int64_t kv_stride_token, int64_t kv_stride_head,
+                                      void *k_cache, void *v_cache, int64_t cache_stride_page,
+                                      int64_t cache_stride_token, int64_t cache_stride_head,
+                                      const int64_t *slot_mapping, int num_tokens, int kv_heads,
+                                      int head_dim, int page_size, int num_pages, int dtype,
+                                      const float *k_scale, const float *v_scale, void *stream) {
+  if (num_tokens < 0) return MXFA_EINVAL;
+  if (num_tokens > 0 && !slot_mapping) return MXFA_EINVAL;
+  if (!key || !value || !k_cache || !v_cache) return MXFA_EINVAL;
+  if (kv_heads <= 0 || page_size <= 0 || num_pages <= 0) return MXFA_EINVAL;
+  if (head_dim <= 0 || head_dim % 16 != 0 || head_dim > 4096) return MXFA_EUNSUPPORTED;
+  if (dtype != MXFA_DTYPE_F16 && dtype != MXFA_DTYPE_BF16) return MXFA_EUNSUPPORTED;
+  if (!al16(key) || !al16(value) || !al16(k_cache) || !al16(v_cache)) return MXFA_EINVAL;
+  if (((uintptr_t)k_scale & 3u) || ((uintptr_t)v_scale & 3u)) return MXFA_EINVAL;
+  if ((kv_stride_token | kv_stride_head) & 7) return MXFA_EINVAL;
+  if ((cache_stride_page | cache_stride_token | cache_stride_head) & 15) return MXFA_EINVAL;
+  if (kv_stride_token < 0 || kv_stride_head < 0 || cache_stride_page < 0 ||
+      cache_stride_token < 0 || cache_stride_head < 0)
+    return MXFA_EINVAL;
+  QuantAppendParams p{};
+  p.k = (const uint16_t *)key;
+  p.v = (const uint16_t *)value;
+  p.s_t = kv_stride_token;
+  p.s_h = kv_stride_head;
+  p.kc = (uint8_t *)k_cache;
+  p.vc = (uint8_t *)v_cache;
+  p.c_sp = cache_stride_page;
+  p.c_st = cache_stride_token;
+  p.c_sh = cache_stride_head;
+  p.slots = slot_mapping;
+  p.k_scale = k_scale;
+  p.v_scale = v_scale;
+  p.rows = num_tokens;
+  p.hkv = kv_heads;
+  p.frags = head_dim / 8;
+  p.ps = page_size;
+  p.num_pages = num_pages;
+  const int64_t total = (int64_t)p.rows * p.hkv * p.frags;
+  if (total == 0) return MXFA_OK;
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == MXFA_DTYPE_BF16)
+    hipLaunchKernelGGL((kv_quant_append_kernel<BF16>), dim3((unsigned)blocks), dim3(256), 0, st,
+                       p);
+  else
+    hipLaunchKernelGGL((kv_quant_append_kernel<F16>), dim3((unsigned)blocks), dim3(256), 0, st,
+                       p);
+  return hipGetLastError() == hipSuccess ? MXFA_OK : MXFA_ELAUNCH;
 }
 
 int mxfa_append_kv_launch(const void *k, const void *v, int64_t kv_stride_b,

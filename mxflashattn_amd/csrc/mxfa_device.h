@@ -90,6 +90,9 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
+__device__ __forceinline__ uint32_t load_stream4(const void *p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p));
+}
 __device__ __forceinline__ uint4 load_stream16(const void *p) {
   const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
   return make_uint4(v.x, v.y, v.z, v.w);

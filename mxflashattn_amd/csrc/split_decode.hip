@@ -1,890 +1,23 @@
-// Split-KV paged decode attention for MI355X (gfx950, wave64).
+// C ABI of the split-KV paged decode kernels (include/mxfa_mi355x.h): argument
+// checks, launch shapes, workspace layout and the split-count heuristic. The
+// kernels live in split_kernels.h and are compiled per head dim
+// (split_hd64.hip, split_hd128.hip, split_hd256.hip).
 //
-// Work split (sized on the device, no host sync). Every sequence b is cut into
-// ceil(L_b / 16) tiles of 16 tokens; the tiles of all sequences are laid end to
-// end (tile index t = S_b + j, S = exclusive prefix sum) and cut into R equal
-// ranges [floor(r*NT/R), floor((r+1)*NT/R)), R = min(num_splits, NT). Every
-// (kv head, range) pair is the work of one wave, so every wave streams the same
-// number of tiles whatever the length mix.
-//
-// Workgroups: 8 waves = KH kv heads x S sub-ranges (KH = min(HKV, 8), S = 8/KH).
-// The waves of a workgroup read the same pages at the same time, all kv heads
-// of each token row together, so the HBM sees whole pages instead of
-// 128/256-byte slivers spread over the run (measured: +8-15% read bandwidth on
-// MI355X against one kv head per workgroup).
-//
-// Per wave, over the tiles of its range in order, with no break between
-// sequences (the load pipeline runs straight across sequence ends):
-//   loads  per tile, a buffer descriptor whose base is the tile's first row in
-//          its page (head offset folded in) and whose size covers exactly the
-//          valid rows, so rows past the sequence end and the padding tile past
-//          the range end read as zeros and cost no memory traffic. K and V
-//          carry the nontemporal hint (read once per call).
-//   QK     on the matrix cores: S^T[16 tokens x 16 heads] = K[16 x HD].Q^T[HD x 16]
-//          (v_mfma_f32_16x16x32, HD/32 steps; query heads >= GQ are zero
-//          columns). Lane l holds K bytes [64c + 16(l/16), +16) of token l%16.
-//          Result: lane (r = l/16, h = l%16) holds tokens 4r+i, i = 0..3, head h.
-//   softmax base 2; the reference max m of each head is shared by the wave and
-//          only moves (wave-uniform branch) when a score passes it by
-//          kRescaleLog2, so p = 2^(x - m) <= 2^kRescaleLog2 and rescales are rare.
-//   PV     on the VALU: lane (r, c) holds dims [c*VD, c*VD + VD) of token 4r+u
-//          for load u; the probability of token 4r+u and head h sits in lane
-//          (r, h), register u, of the same DPP row and reaches the whole row
-//          through a row_newbcast:h operand.
-//   piece end: the 4 DPP rows are summed (permlane swaps). A sequence that lies
-//          whole inside the range writes its output. A piece of a longer
-//          sequence writes its normalised output and base-2 log-sum-exp to the
-//          workspace.
-//
-// Combine kernel (second launch; the kernel boundary makes the pieces visible
-// across the XCDs' separate L2s): one thread per float4 of every (sequence,
-// head) output; sequences that cross a range end fold their pieces in range
-// order with online base-2 LSE weights, eight pieces in flight per step.
-// Merging inside the partial kernel was measured slower: its device-scope
-// counters and write-through stores cost more than the second launch.
-//
-// Workspace (fp32 unless noted), R = num_splits: ws_o [HKV, R, 2, GQ, HD] piece
-// outputs (slot 0 = first piece of a range, slot 1 = last piece when it
-// differs), ws_lse [HKV, R, 2, GQ], ws_s int32 [B + 1] tile prefix sums.
-//
-// Reference counterpart: paged_decode_v3 split mode and split_combine
-// (csrc_native/m1_kernel.cpp:553-888) with the split count of
-// integrations/vllm/vllm_plugin.py:271-276; the algorithm (split partials +
-// LSE merge) is the same, the work split, data path and numerics are this
-// file's own.
+// Reference counterpart: the C launcher mxfa_paged_decode_split_launch and
+// launch_split (csrc_native/m1_kernel.cpp:970-1003,1206-1222), the binding's
+// workspace allocation (csrc_native/m1_binding.cpp:94-97) and the split count
+// of integrations/vllm/vllm_plugin.py:271-276.
 
-#include <hip/hip_runtime.h>
-#include <math.h>
-#include <stdint.h>
-
-#include <type_traits>
-#include <utility>
-
-#include "mxfa_device.h"
-#include "mxfa_mi355x.h"
+#include "split_kernels.h"
 
 namespace mxfa {
 
-constexpr int kTile = 16;
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kRescaleLog2 = 8.0f;
-constexpr int kMaxBatch = 16384;  // tile prefix sums live in LDS
-constexpr uint32_t kSrdWord3 = 0x00020000u;  // raw 32-bit buffer, gfx9 family
-constexpr int kAuxStream = 2;                // nt: no temporal reuse expected
-constexpr int kOffOut = 0x40000000;          // a lane offset no descriptor covers
-
-// Tile flags.
-constexpr int kFirst = 1;        // first tile of a piece (range start or sequence start)
-constexpr int kLast = 2;         // last tile of a piece (range end or sequence end)
-constexpr int kSeqStart = 4;     // first tile of its sequence
-constexpr int kSeqEnd = 8;       // last tile of its sequence
-constexpr int kRangeStart = 16;  // first tile of the range
-
-struct DecodeParams {
-  const char *q;
-  int64_t q_sb, q_sh;  // bytes
-  const char *k;
-  const char *v;
-  int64_t sp_bytes;   // page stride
-  uint32_t st_bytes;  // token stride
-  uint32_t sh_bytes;  // head stride
-  const int32_t *bt;
-  int64_t bt_stride;
-  const int32_t *seqlens;
-  char *out;
-  int64_t o_sb, o_sh;  // bytes
-  float *ws_o;
-  float *ws_lse;
-  int32_t *ws_s;
-  float scale_log2;
-  int seqlen_add;
-  int batch;
-  int hkv;
-  int heads_per_wg;
-  int subs;
-  int ps_log2;
-  int max_len;  // block_table_width * page_size
-  int num_pages;
-  int num_ranges;
-};
-
-// Block tables and lengths are read-only for the whole call; reading them
-// through the constant address space lets wave-uniform lookups use scalar
-// (SMEM) loads even inside loops that also store results.
-typedef const __attribute__((address_space(4))) int32_t *ConstI32;
-
-__device__ __forceinline__ ConstI32 as_const(const int32_t *p) { return (ConstI32)p; }
-
-__device__ __forceinline__ int rfl(int x) { return __builtin_amdgcn_readfirstlane(x); }
-
-__device__ __forceinline__ int seq_len_of(const int32_t *seqlens, int b, int add, int max_len) {
-  int L = as_const(seqlens)[b] + add;
-  L = L < 0 ? 0 : L;
-  return L > max_len ? max_len : L;
-}
-
-// First tile of range r out of R over NT tiles, and the range holding tile t.
-__device__ __forceinline__ int range_lo(int r, int R, int NT) {
-  return (int)(((int64_t)r * NT) / R);
-}
-__device__ __forceinline__ int range_of(int t, int R, int NT) {
-  return (int)((((int64_t)t + 1) * R - 1) / NT);
-}
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_srd(const char *base, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(base), (short)0, bytes, kSrdWord3);
-}
-
-template <typename T>
-struct Mfma;
-template <>
-struct Mfma<F16> {
-  static __device__ __forceinline__ f32x4 run(const uint4 &a, const uint4 &b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-  }
-};
-template <>
-struct Mfma<BF16> {
-  static __device__ __forceinline__ f32x4 run(const uint4 &a, const uint4 &b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  }
-};
-
-// PV on the matrix cores, v_mfma_f32_16x16x16: A = P[head][token] is the QK
-// result layout itself (lane (r, h) holds tokens 4r..4r+3 of head h), packed to
-// the element type; B = V[token][dim], lane (r, c) supplying tokens 4r..4r+3 of
-// one dim per block; D = O[head][dim]. Element packing keeps k order: the low
-// half of the first register is token 4r.
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-
-template <typename T>
-struct PvMfma;
-template <>
-struct PvMfma<BF16> {
-  static __device__ __forceinline__ f32x4 run(uint2 a, uint2 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
-                                                      __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ uint16_t round(float x) {
-    return __builtin_bit_cast(uint16_t, (__bf16)x);
-  }
-  static __device__ __forceinline__ float widen(uint16_t h) {
-    return __uint_as_float((uint32_t)h << 16);
-  }
-};
-template <>
-struct PvMfma<F16> {
-  static __device__ __forceinline__ f32x4 run(uint2 a, uint2 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
-                                                 __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ uint16_t round(float x) {
-    return __builtin_bit_cast(uint16_t, (_Float16)x);
-  }
-  static __device__ __forceinline__ float widen(uint16_t h) {
-    return (float)__builtin_bit_cast(_Float16, h);
-  }
-};
-
-// 16-bit element j of a V fragment word list, paired from two tokens.
-__device__ __forceinline__ uint32_t pair_halves(uint32_t lo_tok, uint32_t hi_tok, int odd) {
-  return __builtin_amdgcn_perm(hi_tok, lo_tok, odd ? 0x07060302u : 0x05040100u);
-}
-
-template <int Aux>
-__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, int off) {
-  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, Aux);
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
-template <int Aux>
-__device__ __forceinline__ uint2 buf_load8(__amdgpu_buffer_rsrc_t r, int off) {
-  const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, Aux);
-  return make_uint2(v.x, v.y);
-}
-
-// V fragment of one lane: 8 elements (HD128, 16 B) or 4 elements (HD64, 8 B).
-template <int VD>
-struct VFrag;
-template <>
-struct VFrag<8> {
-  uint4 w;
-  __device__ __forceinline__ void load_buf(__amdgpu_buffer_rsrc_t r, int off) {
-    w = buf_load16<kAuxStream>(r, off);
-  }
-  __device__ __forceinline__ void load_ptr(const char *ptr) { w = load_stream16(ptr); }
-  __device__ __forceinline__ uint32_t word(int i) const {
-    return i == 0 ? w.x : i == 1 ? w.y : i == 2 ? w.z : w.w;
-  }
-  template <typename E>
-  __device__ __forceinline__ void widen(float (&v)[8]) const {
-    v[0] = E::lo(w.x);
-    v[1] = E::hi(w.x);
-    v[2] = E::lo(w.y);
-    v[3] = E::hi(w.y);
-    v[4] = E::lo(w.z);
-    v[5] = E::hi(w.z);
-    v[6] = E::lo(w.w);
-    v[7] = E::hi(w.w);
-  }
-};
-template <>
-struct VFrag<4> {
-  uint2 w;
-  __device__ __forceinline__ void load_buf(__amdgpu_buffer_rsrc_t r, int off) {
-    w = buf_load8<kAuxStream>(r, off);
-  }
-  __device__ __forceinline__ void load_ptr(const char *ptr) { w = load_stream8(ptr); }
-  __device__ __forceinline__ uint32_t word(int i) const { return i == 0 ? w.x : w.y; }
-  template <typename E>
-  __device__ __forceinline__ void widen(float (&v)[4]) const {
-    v[0] = E::lo(w.x);
-    v[1] = E::hi(w.x);
-    v[2] = E::lo(w.y);
-    v[3] = E::hi(w.y);
-  }
-};
-
-// f(std::integral_constant<int, I>) for I = 0 .. N-1, unrolled at compile time.
-template <typename F, int... I>
-__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
-  (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F &&f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
-template <int H>
-__device__ __forceinline__ float row_bcast(float x) {
-  return __int_as_float(
-      __builtin_amdgcn_update_dpp(0, __float_as_int(x), kDppRowNewBcast0 + H, 0xf, 0xf, false));
-}
-
-// o[h][j] += p(token of this lane's row, head h) * v[j] for every head of the group.
-template <int GQ, int VD, int H = 0>
-__device__ __forceinline__ void pv_accumulate(float (&o)[GQ][VD], float p, const float (&v)[VD]) {
-  if constexpr (H < GQ) {
-    const float ph = row_bcast<H>(p);
-#pragma unroll
-    for (int j = 0; j < VD; ++j) o[H][j] = fmaf(ph, v[j], o[H][j]);
-    pv_accumulate<GQ, VD, H + 1>(o, p, v);
-  }
-}
-
-template <int GQ, int VD, int H = 0>
-__device__ __forceinline__ void rescale_rows(float (&o)[GQ][VD], float f) {
-  if constexpr (H < GQ) {
-    const float fh = row_bcast<H>(f);
-#pragma unroll
-    for (int j = 0; j < VD; ++j) o[H][j] *= fh;
-    rescale_rows<GQ, VD, H + 1>(o, f);
-  }
-}
-
-// Value of head 4*row + I from a per-head quantity held by column h of every
-// DPP row (the score layout). Only rows whose heads exist (row < GQ/4) get a
-// meaningful value. DPP moves only: no LDS round trip, so no wait on the
-// scalar page-id loads in flight.
-template <int GQ, int I>
-__device__ __forceinline__ float head_of_row(float x, int row) {
-  float v = row_bcast<I>(x);
-  if constexpr (GQ > 4) v = row == 1 ? row_bcast<4 + I>(x) : v;
-  return v;
-}
-
-// Exclusive prefix sum of per-sequence tile counts into s[0..B] (LDS), all threads.
-template <int kThreads>
-__device__ __forceinline__ void tile_prefix(const DecodeParams &p, int32_t *s, int *wave_tot) {
-  const int B = p.batch;
-  const int per = (B + kThreads - 1) / kThreads;
-  const int b0 = threadIdx.x * per;
-  int local = 0;
-  for (int i = 0; i < per; ++i) {
-    const int b = b0 + i;
-    if (b < B) local += (seq_len_of(p.seqlens, b, p.seqlen_add, p.max_len) + kTile - 1) / kTile;
-  }
-  // Inclusive scan of `local` across the workgroup.
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int x = local;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(x, off, 64);
-    if (lane >= off) x += y;
-  }
-  if (lane == 63) wave_tot[wave] = x;
-  __syncthreads();
-  int base = 0;
-  for (int w = 0; w < wave; ++w) base += wave_tot[w];
-  int run = base + x - local;  // exclusive prefix of this thread's first element
-  for (int i = 0; i < per; ++i) {
-    const int b = b0 + i;
-    if (b < B) {
-      s[b] = run;
-      run += (seq_len_of(p.seqlens, b, p.seqlen_add, p.max_len) + kTile - 1) / kTile;
-    }
-  }
-  if (threadIdx.x == kThreads - 1) s[B] = base + x;
-  __syncthreads();
-}
-
-// Empty sequences (no tiles) get zero output; sequence b is cleared by the
-// workgroups with blockIdx.y == b % gridDim.y, each for its own kv heads.
-template <int HD, int GQ, int kThreads>
-__device__ __forceinline__ void zero_empty(const DecodeParams &p, const int32_t *s) {
-  const int kv0 = blockIdx.x * p.heads_per_wg;
-  const int kv1 = min(kv0 + p.heads_per_wg, p.hkv);
-  const int nh = (kv1 - kv0) * GQ;
-  constexpr int F = HD / 4;  // 8-byte pieces per head row
-  for (int b = blockIdx.y; b < p.batch; b += gridDim.y) {
-    if (s[b + 1] != s[b]) continue;
-    char *row = p.out + b * p.o_sb + (int64_t)kv0 * GQ * p.o_sh;
-    for (int i = threadIdx.x; i < nh * F; i += kThreads)
-      *reinterpret_cast<uint2 *>(row + (i / F) * p.o_sh + (i % F) * 8) = make_uint2(0u, 0u);
-  }
-}
-
-// Sum / max over the 4 DPP rows of the wave (lanes l, l^16, l^32, l^48); every
-// lane receives the result.
-__device__ __forceinline__ float rows_sum(float x) {
-  const auto a =
-      __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  const auto c =
-      __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
-  return __uint_as_float(c[0]) + __uint_as_float(c[1]);
-}
-__device__ __forceinline__ float rows_max(float x) {
-  const auto a =
-      __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  const auto c =
-      __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
-  return fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
-}
-
-// VD fp32 values times `scale`, rounded once to the element type, to 8-byte aligned dst.
-template <int VD, typename E>
-__device__ __forceinline__ void store_row(char *dst, const float (&v)[VD], float scale) {
-  uint32_t w[VD / 2];
-#pragma unroll
-  for (int j = 0; j < VD / 2; ++j)
-    w[j] = (uint32_t)E::narrow(v[2 * j] * scale) |
-           ((uint32_t)E::narrow(v[2 * j + 1] * scale) << 16);
-#pragma unroll
-  for (int j = 0; j < VD / 4; ++j)
-    *reinterpret_cast<uint2 *>(dst + 8 * j) = make_uint2(w[2 * j], w[2 * j + 1]);
-}
-
-// Scalar description of one tile, built two tiles ahead of the math.
-struct Tile {
-  int b;      // sequence
-  int tok0;   // first token of the tile within the sequence
-  int valid;  // tokens of the tile that exist (0: padding past the range end)
-  int flags;
-  int pg;  // page id (block-table entry), page-uniform tiles only
-};
-
-// One wave: the tiles [lo, hi) of kv head kvh, range rr of R. kPvMfma: PV on
-// the matrix cores (accumulator lane (r, c) holds heads 4r..4r+3, dims
-// c*VD + jb in block jb), else on the VALU (o[g][j], g = head, dims c*VD + j,
-// one partial per DPP row).
-template <int HD, int GQ, typename T, bool kLanePages, bool kPvMfma, int NBUF>
-__device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *s_tiles, int kvh,
-                                          int rr, int R, int NT, int lo, int hi) {
-  using E = Elem<T>;
-  constexpr int NCH = HD / 32;  // MFMA steps over the head dim
-  constexpr int VD = HD / 16;   // V elements per lane
-  constexpr int U = 4;          // V loads per tile (token 4r+u in DPP row r)
-  constexpr int NPG = kLanePages ? 1 + U : 1;
-  const int B = p.batch;
-
-  const int lane = threadIdx.x & 63;
-  const int row = lane >> 4;  // DPP row
-  const int col = lane & 15;  // head (score layout) / V column
-  const int ps_mask = (1 << p.ps_log2) - 1;
-  const uint32_t st = p.st_bytes;
-  const uint64_t head_off = (uint64_t)kvh * p.sh_bytes;
-  const float c = p.scale_log2;
-  const int ns = p.num_ranges;  // workspace stride
-
-  // Lane offsets inside a tile: K in the MFMA A layout, V row-contiguous, q as
-  // the MFMA B operand (columns >= GQ read nothing).
-  const int k_off = col * (int)st + row * 16;
-  int v_off[U];
-#pragma unroll
-  for (int u = 0; u < U; ++u) v_off[u] = (4 * row + u) * (int)st + col * (VD * 2);
-  const int q_off = col < GQ ? col * (int)p.q_sh + row * 16 : kOffOut;
-  const int q_bytes = (GQ - 1) * (int)p.q_sh + HD * 2;
-
-  // Sequence holding tile lo: largest b with s[b] <= lo (then s[b+1] > lo).
-  int pb;
-  {
-    int a = 0, z = B - 1;
-    while (a < z) {
-      const int mid = (a + z + 1) >> 1;
-      if (s_tiles[mid] <= lo) a = mid;
-      else z = mid - 1;
-    }
-    pb = rfl(a);
-  }
-  // Cursor of the tile builder (runs two tiles ahead of the math).
-  int p_start = rfl(s_tiles[pb]);
-  int p_end = rfl(s_tiles[pb + 1]);
-  int p_len = seq_len_of(p.seqlens, pb, p.seqlen_add, p.max_len);
-  ConstI32 p_bt = as_const(p.bt + (int64_t)pb * p.bt_stride);
-
-  auto make_tile = [&](int t, Tile &d, int (&lpg)[NPG]) {
-    if (t >= hi) {
-      d.b = pb;
-      d.tok0 = 0;
-      d.valid = 0;
-      d.flags = 0;
-      d.pg = 0;
-#pragma unroll
-      for (int i = 0; i < NPG; ++i) lpg[i] = 0;
-      return;
-    }
-    if (t >= p_end) {  // next sequence with tiles (rare, wave-uniform)
-      do {
-        ++pb;
-        p_start = p_end;
-        p_end = rfl(s_tiles[pb + 1]);
-      } while (t >= p_end);
-      p_len = seq_len_of(p.seqlens, pb, p.seqlen_add, p.max_len);
-      p_bt = as_const(p.bt + (int64_t)pb * p.bt_stride);
-    }
-    d.b = pb;
-    d.tok0 = (t - p_start) * kTile;
-    d.valid = min(kTile, p_len - d.tok0);
-    const bool seq_start = d.tok0 == 0, seq_end = d.tok0 + kTile >= p_len;
-    d.flags = ((t == lo || seq_start) ? kFirst : 0) | ((t == hi - 1 || seq_end) ? kLast : 0) |
-              (seq_start ? kSeqStart : 0) | (seq_end ? kSeqEnd : 0) | (t == lo ? kRangeStart : 0);
-    if constexpr (kLanePages) {
-      // Per-lane page ids: [0] for this lane's K token, [1+u] for its V tokens.
-      // Token positions clamp to the last valid token.
-      const int last = d.valid - 1;
-      lpg[0] = p_bt[(d.tok0 + min(col, last)) >> p.ps_log2];
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-        lpg[1 + u] = p_bt[(d.tok0 + min(4 * row + u, last)) >> p.ps_log2];
-      d.pg = 0;
-    } else {
-      d.pg = p_bt[d.tok0 >> p.ps_log2];
-    }
-  };
-
-  auto clamp_page = [&](int pg) -> int {
-    pg = pg < 0 ? 0 : pg;
-    return pg >= p.num_pages ? p.num_pages - 1 : pg;
-  };
-
-  struct Set {
-    uint4 k[NCH];
-    VFrag<VD> v[U];
-    uint4 q[NCH];
-    int lpg[NPG];
-    Tile d;
-  };
-
-  auto issue = [&](Set &s) {
-    const Tile &d = s.d;
-    const __amdgpu_buffer_rsrc_t rq =
-        make_srd(p.q + (int64_t)d.b * p.q_sb + (int64_t)kvh * GQ * p.q_sh,
-                 (d.flags & kFirst) ? q_bytes : 0);
-    if (d.flags & kFirst) {  // wave-uniform; q is loaded once per piece
-#pragma unroll
-      for (int cc = 0; cc < NCH; ++cc) s.q[cc] = buf_load16<0>(rq, q_off + cc * 64);
-    }
-    if constexpr (!kLanePages) {
-      const uint64_t tile_off = (uint64_t)(uint32_t)clamp_page(d.pg) * (uint64_t)p.sp_bytes +
-                                (uint64_t)(d.tok0 & ps_mask) * st + head_off;
-      const int bytes = d.valid > 0 ? (d.valid - 1) * (int)st + HD * 2 : 0;
-      const __amdgpu_buffer_rsrc_t rk = make_srd(p.k + tile_off, bytes);
-      const __amdgpu_buffer_rsrc_t rv = make_srd(p.v + tile_off, bytes);
-#pragma unroll
-      for (int cc = 0; cc < NCH; ++cc) s.k[cc] = buf_load16<kAuxStream>(rk, k_off + cc * 64);
-#pragma unroll
-      for (int u = 0; u < U; ++u) s.v[u].load_buf(rv, v_off[u]);
-    } else {
-      // Lane pages: every lane addresses its own page; positions past the
-      // sequence end were clamped to its last token (their scores are masked).
-      const int last = d.valid > 0 ? d.valid - 1 : 0;
-      {
-        const int pos = d.tok0 + min(col, last);
-        const uint64_t off = (uint64_t)(uint32_t)clamp_page(s.lpg[0]) * (uint64_t)p.sp_bytes +
-                             (uint64_t)(pos & ps_mask) * st + head_off + row * 16;
-#pragma unroll
-        for (int cc = 0; cc < NCH; ++cc) s.k[cc] = load_stream16(p.k + off + cc * 64);
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int pos = d.tok0 + min(4 * row + u, last);
-        const uint64_t off = (uint64_t)(uint32_t)clamp_page(s.lpg[1 + u]) * (uint64_t)p.sp_bytes +
-                             (uint64_t)(pos & ps_mask) * st + head_off + col * (VD * 2);
-        s.v[u].load_ptr(p.v + off);
-      }
-    }
-  };
-
-  // Running state of the current piece.
-  float m = -INFINITY;  // reference max (base 2) of head `col`, same in every row
-  float dsum = 0.f;     // partial denominator of head `col` over this row's tokens
-  float o[kPvMfma ? 1 : GQ][VD];  // VALU PV accumulators
-  f32x4 oacc[kPvMfma ? VD : 1];     // MFMA PV accumulators
-  uint4 qf[NCH];
-  auto clear_acc = [&]() {
-    if constexpr (kPvMfma) {
-#pragma unroll
-      for (int j = 0; j < VD; ++j) oacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    } else {
-#pragma unroll
-      for (int g = 0; g < GQ; ++g)
-#pragma unroll
-        for (int j = 0; j < VD; ++j) o[g][j] = 0.f;
-    }
-  };
-  clear_acc();
-#pragma unroll
-  for (int cc = 0; cc < NCH; ++cc) qf[cc] = make_uint4(0u, 0u, 0u, 0u);
-  bool piece_from_start = false;
-  bool piece_first_in_range = false;
-
-  auto finalize_mfma = [&](const Tile &d) {
-    const float dt = rows_sum(dsum);  // lane (any row, h): denominator of head h
-    const int b = d.b;
-    const bool whole = piece_from_start && (d.flags & kSeqEnd);
-    const int slot = piece_first_in_range ? 0 : 1;
-    const int64_t pbase = ((int64_t)(kvh * ns + rr) * 2 + slot) * GQ;
-    static_for<4>([&](auto ic) {
-      constexpr int i = decltype(ic)::value;
-      const int hh = 4 * row + i;  // head of accumulator element i in this lane
-      const float Dh = head_of_row<GQ, i>(dt, row);
-      const float Mh = head_of_row<GQ, i>(m, row);
-      if (hh >= GQ) return;
-      const float inv = Dh > 0.f ? 1.f / Dh : 0.f;
-      float v[VD];
-#pragma unroll
-      for (int j = 0; j < VD; ++j) v[j] = oacc[j][i];
-      if (whole) {
-        store_row<VD, E>(p.out + b * p.o_sb + (kvh * GQ + hh) * p.o_sh + col * (VD * 2), v, inv);
-      } else {
-        float4 *dst = reinterpret_cast<float4 *>(p.ws_o + (pbase + hh) * HD + col * VD);
-#pragma unroll
-        for (int j = 0; j < VD / 4; ++j)
-          dst[j] = make_float4(v[4 * j] * inv, v[4 * j + 1] * inv, v[4 * j + 2] * inv,
-                               v[4 * j + 3] * inv);
-        if (col == 0) p.ws_lse[pbase + hh] = Dh > 0.f ? Mh + __log2f(Dh) : -INFINITY;
-      }
-    });
-  };
-
-  auto finalize = [&](const Tile &d) {
-    if constexpr (kPvMfma) {
-      finalize_mfma(d);
-      return;
-    }
-    const float dt = rows_sum(dsum);
-#pragma unroll
-    for (int g = 0; g < GQ; ++g)
-#pragma unroll
-      for (int j = 0; j < VD; ++j) o[g][j] = rows_sum(o[g][j]);
-    const int b = d.b;
-    if (piece_from_start && (d.flags & kSeqEnd)) {  // the whole sequence
-      static_for<GQ>([&](auto gc) {
-        constexpr int g = decltype(gc)::value;
-        const float Dg = row_bcast<g>(dt);
-        if ((g & 3) == row) {
-          const int h = kvh * GQ + g;
-          store_row<VD, E>(p.out + b * p.o_sb + h * p.o_sh + col * (VD * 2), o[g],
-                           Dg > 0.f ? 1.f / Dg : 0.f);
-        }
-      });
-      return;
-    }
-    // A piece: normalised output and base-2 LSE of each head to its slot.
-    const int slot = piece_first_in_range ? 0 : 1;
-    const int64_t pbase = ((int64_t)(kvh * ns + rr) * 2 + slot) * GQ;
-    static_for<GQ>([&](auto gc) {
-      constexpr int g = decltype(gc)::value;
-      const float Dg = row_bcast<g>(dt);
-      const float Mg = row_bcast<g>(m);
-      if ((g & 3) == row) {
-        const float inv = Dg > 0.f ? 1.f / Dg : 0.f;
-        float4 *dst = reinterpret_cast<float4 *>(p.ws_o + (pbase + g) * HD + col * VD);
-#pragma unroll
-        for (int j = 0; j < VD / 4; ++j)
-          dst[j] = make_float4(o[g][4 * j] * inv, o[g][4 * j + 1] * inv, o[g][4 * j + 2] * inv,
-                               o[g][4 * j + 3] * inv);
-        if (col == 0) p.ws_lse[pbase + g] = Dg > 0.f ? Mg + __log2f(Dg) : -INFINITY;
-      }
-    });
-  };
-
-  auto compute = [&](Set &s) {
-    const Tile &d = s.d;
-    if (d.flags & kFirst) {
-      m = -INFINITY;
-      dsum = 0.f;
-      clear_acc();
-#pragma unroll
-      for (int cc = 0; cc < NCH; ++cc) qf[cc] = s.q[cc];
-      piece_from_start = (d.flags & kSeqStart) != 0;
-      piece_first_in_range = (d.flags & kRangeStart) != 0;
-    }
-    // QK on the matrix cores; two accumulators halve the MFMA dependency chain.
-    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int cc = 0; cc < NCH; cc += 2) {
-      acc0 = Mfma<T>::run(s.k[cc], qf[cc], acc0);
-      acc1 = Mfma<T>::run(s.k[cc + 1], qf[cc + 1], acc1);
-    }
-    float x[4];
-    bool need = false;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const bool valid = (col < GQ) & (4 * row + i < d.valid);
-      x[i] = valid ? (acc0[i] + acc1[i]) * c : -INFINITY;
-      need |= x[i] > m + kRescaleLog2;
-    }
-    if (__builtin_amdgcn_ballot_w64(need) != 0) {
-      // Rare, wave-uniform: move the reference of each head to the wave's
-      // tile maximum when it passed the reference by more than kRescaleLog2.
-      const float mt = rows_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
-      const float mn = mt > m + kRescaleLog2 ? mt : m;
-      const float f = (mn == m) ? 1.f : fast_exp2(m - mn);  // m = -inf: f = 0
-      dsum *= f;
-      if constexpr (kPvMfma) {
-        static_for<4>([&](auto ic) {
-          constexpr int i = decltype(ic)::value;
-          const float fi = head_of_row<GQ, i>(f, row);
-#pragma unroll
-          for (int j = 0; j < VD; ++j) oacc[j][i] *= fi;
-        });
-      } else {
-        rescale_rows<GQ, VD>(o, f);
-      }
-      m = mn;
-    }
-    // m = -inf: this head has seen no valid token, its scores here are -inf too.
-    const float mr = m == -INFINITY ? 0.f : m;
-    float pr[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(x[i] - mr);
-    if constexpr (kPvMfma) {
-      // P rounded to the element type once; the denominator sums the same
-      // rounded weights, so the output stays a convex combination of V rows.
-      uint16_t ph[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) ph[i] = PvMfma<T>::round(pr[i]);
-      dsum += (PvMfma<T>::widen(ph[0]) + PvMfma<T>::widen(ph[1])) +
-              (PvMfma<T>::widen(ph[2]) + PvMfma<T>::widen(ph[3]));
-      const uint2 a = make_uint2((uint32_t)ph[0] | ((uint32_t)ph[1] << 16),
-                                 (uint32_t)ph[2] | ((uint32_t)ph[3] << 16));
-#pragma unroll
-      for (int jb = 0; jb < VD; ++jb) {
-        const int wi = jb >> 1, odd = jb & 1;
-        const uint2 bv = make_uint2(pair_halves(s.v[0].word(wi), s.v[1].word(wi), odd),
-                                    pair_halves(s.v[2].word(wi), s.v[3].word(wi), odd));
-        oacc[jb] = PvMfma<T>::run(a, bv, oacc[jb]);
-      }
-    } else {
-      dsum += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        float v[VD];
-        s.v[u].template widen<E>(v);
-        pv_accumulate<GQ, VD>(o, pr[u], v);
-      }
-    }
-    if (d.flags & kLast) finalize(d);
-  };
-
-  // Software pipeline over the range with NBUF register sets: tile
-  // descriptors (and page ids) are built NBUF tiles ahead of the math, K/V/q
-  // loads issued NBUF-1 tiles ahead. The body runs NBUF tiles and exits only at
-  // its latch, so the loads crossing the back edge always land in the same
-  // sets. The descriptor of a padding tile past the range end covers no
-  // bytes, so its loads cost nothing.
-  Set sets[NBUF];
-  Tile dn;
-  int lpg_n[NPG];
-  static_for<NBUF>([&](auto ic) {
-    constexpr int i = decltype(ic)::value;
-    make_tile(lo + i, sets[i].d, sets[i].lpg);
-    if constexpr (i < NBUF - 1) issue(sets[i]);
-  });
-  const int ntiles = hi - lo;
-  int t = lo;
-  auto step = [&](auto kc) {
-    constexpr int k = decltype(kc)::value;
-    constexpr int kn = (k + NBUF - 1) % NBUF;  // holds tile t + NBUF - 1
-    if constexpr (kLanePages) {
-      make_tile(t + NBUF, dn, lpg_n);
-      issue(sets[kn]);
-    } else {
-      issue(sets[kn]);
-      make_tile(t + NBUF, dn, lpg_n);
-    }
-    compute(sets[k]);
-    sets[k].d = dn;
-#pragma unroll
-    for (int i = 0; i < NPG; ++i) sets[k].lpg[i] = lpg_n[i];
-    ++t;
-  };
-  int done = 0;
-  for (; done + NBUF <= ntiles; done += NBUF) static_for<NBUF>(step);
-  const int rest = ntiles - done;  // < NBUF tiles, already issued into sets[0 .. rest-1]
-  static_for<NBUF - 1>([&](auto jc) {
-    constexpr int j = decltype(jc)::value;
-    if (j < rest) compute(sets[j]);
-  });
-}
-
-template <int HD, int GQ, typename T, bool kLanePages, bool kPvMfma, int NBUF, int WAVES,
-          int kMinWgPerCu>
-__global__ __launch_bounds__(WAVES * 64, kMinWgPerCu) void split_partial_kernel(DecodeParams p) {
-  constexpr int kThreads = WAVES * 64;
-  extern __shared__ int32_t s_tiles[];  // [B + 1]
-  __shared__ int s_wave_tot[WAVES];
-
-  tile_prefix<kThreads>(p, s_tiles, s_wave_tot);  // ends with a barrier
-  zero_empty<HD, GQ, kThreads>(p, s_tiles);
-  const int B = p.batch;
-  if (blockIdx.x == 0 && blockIdx.y == 0) {
-    for (int i = threadIdx.x; i <= B; i += kThreads) p.ws_s[i] = s_tiles[i];
-  }
-
-  const int wave = rfl(threadIdx.x >> 6);
-  const int KH = p.heads_per_wg;
-  const int kh = wave % KH, sub = wave / KH;
-  const int kvh = blockIdx.x * KH + kh;
-  const int NT = rfl(s_tiles[B]);
-  const int R = min(p.num_ranges, NT);  // every range holds >= 1 tile
-  const int rr = blockIdx.y * p.subs + sub;
-  if (sub >= p.subs || kvh >= p.hkv || rr >= R) return;
-  const int lo = range_lo(rr, R, NT), hi = range_lo(rr + 1, R, NT);
-  run_range<HD, GQ, T, kLanePages, kPvMfma, NBUF>(p, s_tiles, kvh, rr, R, NT, lo, hi);
-}
-
-struct CombineParams {
-  const float *ws_o;
-  const float *ws_lse;
-  const int32_t *ws_s;
-  char *out;
-  int64_t o_sb, o_sh;  // bytes
-  int batch;
-  int hq;
-  int gq;
-  int num_ranges;
-  int chunk_blocks;  // blocks per (sequence, kv head) pair, a power of two
-};
-
-// Merge of two partial states (max, weight, accumulator) in the base-2 domain.
-__device__ __forceinline__ void lse_fold(float &M, float &W, float4 &A, float m2, float w2,
-                                         const float4 &a2) {
-  const float Mn = fmaxf(M, m2);
-  if (Mn == -INFINITY) return;
-  const float f1 = (M == -INFINITY) ? 0.f : fast_exp2(M - Mn);
-  const float f2 = (m2 == -INFINITY) ? 0.f : fast_exp2(m2 - Mn);
-  W = W * f1 + w2 * f2;
-  A.x = A.x * f1 + a2.x * f2;
-  A.y = A.y * f1 + a2.y * f2;
-  A.z = A.z * f1 + a2.z * f2;
-  A.w = A.w * f1 + a2.w * f2;
-  M = Mn;
-}
-
-// LSE combine: F = chunk_blocks blocks of kCombineThreads per (sequence b,
-// kv head) pair; block f takes CB = C / F of the pair's C float4 chunks of the
-// GQ x HD output and splits the pieces over G = kCombineThreads / CB groups.
-// Thread (g, c) folds pieces ra+g, ra+g+G, ... of chunk c, eight loads in
-// flight per step; the G groups are then merged by an LDS tree and the output
-// rounded once. The fold order depends on F only (a host choice), never on
-// timing. Pairs whose sequence lies inside one range (written by the partial
-// kernel) or is empty (zero-filled there) leave at once.
-constexpr int kCombineThreads = 256;
-
-template <int HD, int GQ, typename T>
-__global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(CombineParams p) {
-  using E = Elem<T>;
-  constexpr int C = GQ * HD / 4;  // float4 chunks per pair
-  static_assert(C <= kCombineThreads && kCombineThreads % C == 0, "chunks per pair");
-  constexpr int kUnroll = 8;
-  __shared__ float s_red[kCombineThreads * 6];
-  const int hkv = p.hq / GQ;
-  const int F = p.chunk_blocks;
-  const int CB = C / F;
-  const int groups = kCombineThreads / CB;
-  const int pair = blockIdx.x / F;
-  const int b = pair / hkv, kvh = pair % hkv;
-  const int g = threadIdx.x / CB;
-  const int c = (blockIdx.x % F) * CB + threadIdx.x % CB;
-  const int NT = p.ws_s[p.batch];
-  const int sb = p.ws_s[b], se = p.ws_s[b + 1];
-  // Prefix sums that do not describe tiles inside [0, NT) (a workspace the
-  // partial kernel did not fill) are skipped, so every index stays in range.
-  if (se <= sb || sb < 0 || se > NT) return;
-  const int R = min(p.num_ranges, NT);
-  const int ra = range_of(sb, R, NT), rb = range_of(se - 1, R, NT);
-  if (ra == rb) return;
-  const int slot_a = (range_lo(ra, R, NT) == sb) ? 0 : 1;
-  const int ns = p.num_ranges;
-  const int cc = c;
-  const int head = cc / (HD / 4);
-  float M = -INFINITY, W = 0.f;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int q0 = ra + g; q0 <= rb; q0 += kUnroll * groups) {
-    float l[kUnroll];
-    float4 ov[kUnroll];
-#pragma unroll
-    for (int i = 0; i < kUnroll; ++i) {
-      const int q = min(q0 + i * groups, rb);
-      const int64_t ps = ((int64_t)(kvh * ns + q) * 2 + (q == ra ? slot_a : 0)) * GQ + head;
-      l[i] = (q0 + i * groups <= rb) ? p.ws_lse[ps] : -INFINITY;
-      ov[i] = reinterpret_cast<const float4 *>(p.ws_o + ps * HD)[cc % (HD / 4)];
-    }
-#pragma unroll
-    for (int i = 0; i < kUnroll; ++i) lse_fold(M, W, acc, l[i], 1.f, ov[i]);
-  }
-  float *red = s_red + threadIdx.x * 6;
-  red[0] = M;
-  red[1] = W;
-  red[2] = acc.x;
-  red[3] = acc.y;
-  red[4] = acc.z;
-  red[5] = acc.w;
-  __syncthreads();
-#pragma unroll
-  for (int stride = groups / 2; stride >= 1; stride >>= 1) {  // groups is a power of two
-    if (g < stride) {
-      const float *o2 = s_red + (threadIdx.x + stride * CB) * 6;
-      lse_fold(M, W, acc, o2[0], o2[1], make_float4(o2[2], o2[3], o2[4], o2[5]));
-      red[0] = M;
-      red[1] = W;
-      red[2] = acc.x;
-      red[3] = acc.y;
-      red[4] = acc.z;
-      red[5] = acc.w;
-    }
-    __syncthreads();
-  }
-  if (g == 0) {
-    const float inv = W > 0.f ? 1.f / W : 0.f;
-    const uint32_t w0 =
-        (uint32_t)E::narrow(acc.x * inv) | ((uint32_t)E::narrow(acc.y * inv) << 16);
-    const uint32_t w1 =
-        (uint32_t)E::narrow(acc.z * inv) | ((uint32_t)E::narrow(acc.w * inv) << 16);
-    const int h = kvh * GQ + head;
-    *reinterpret_cast<uint2 *>(p.out + b * p.o_sb + h * p.o_sh + (cc % (HD / 4)) * 8) =
-        make_uint2(w0, w1);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Host side: argument checks, template selection, launch.
+int launch_partial_64(const DecodeParams &p, const Grid &g, int dtype, bool fp8, hipStream_t st);
+int launch_partial_128(const DecodeParams &p, const Grid &g, int dtype, bool fp8, hipStream_t st);
+int launch_partial_256(const DecodeParams &p, const Grid &g, int dtype, bool fp8, hipStream_t st);
+int launch_combine_64(const CombineParams &c, int dtype, hipStream_t st);
+int launch_combine_128(const CombineParams &c, int dtype, hipStream_t st);
+int launch_combine_256(const CombineParams &c, int dtype, hipStream_t st);
 
 static bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
@@ -895,11 +28,13 @@ static int ilog2_exact(int v) {
   return r;
 }
 
+static bool supported_hd(int hd) { return hd == 64 || hd == 128 || hd == 256; }
+
 struct SplitArgs {
   const void *q;
   int64_t q_sb, q_sh;
   const void *k, *v;
-  int64_t c_sp, c_st, c_sh;
+  int64_t c_sp, c_st, c_sh;  // cache strides in elements (bytes for fp8 caches)
   const int32_t *bt;
   int64_t bt_stride;
   const int32_t *seqlens;
@@ -910,6 +45,8 @@ struct SplitArgs {
   size_t ws_bytes;
   float scale;
   int batch, hq, hkv, hd, ps, btw, num_pages, dtype, num_splits;
+  bool fp8;  // caches hold OCP e4m3fn
+  const float *k_scale, *v_scale;
 };
 
 struct WsLayout {
@@ -931,10 +68,10 @@ static int check_split_args(const SplitArgs &a) {
     return MXFA_EINVAL;
   if (a.num_splits <= 0 || a.seqlen_add < 0) return MXFA_EINVAL;
   if (!(a.scale == a.scale) || a.scale == INFINITY || a.scale == -INFINITY) return MXFA_EINVAL;
-  if (a.hd != 64 && a.hd != 128) return MXFA_EUNSUPPORTED;
+  if (!supported_hd(a.hd)) return MXFA_EUNSUPPORTED;
   if (a.hq % a.hkv != 0) return MXFA_EUNSUPPORTED;
   const int gq = a.hq / a.hkv;
-  if (gq != 2 && gq != 4 && gq != 8) return MXFA_EUNSUPPORTED;
+  if (gq > kMaxGq) return MXFA_EUNSUPPORTED;
   if (a.dtype != MXFA_DTYPE_F16 && a.dtype != MXFA_DTYPE_BF16) return MXFA_EUNSUPPORTED;
   if (ilog2_exact(a.ps) < 0 || a.ps > 4096) return MXFA_EUNSUPPORTED;
   if (a.num_splits > 65535 || a.batch > kMaxBatch || a.hkv > 65535) return MXFA_EUNSUPPORTED;
@@ -943,51 +80,43 @@ static int check_split_args(const SplitArgs &a) {
   // Total tiles must fit int32: B * ceil(max_len / 16).
   if ((int64_t)a.batch * ((max_len + kTile - 1) / kTile) >= ((int64_t)1 << 31))
     return MXFA_EUNSUPPORTED;
-  // 16-byte fragments: pointers and every stride must keep 8-element alignment.
+  // 16-byte fragments: pointers and every byte stride must keep 16-byte
+  // alignment (8 elements of 16 bits, 16 fp8 elements).
+  const int64_t esz = a.fp8 ? 1 : 2;
   if (!aligned16(a.q) || !aligned16(a.k) || !aligned16(a.v)) return MXFA_EINVAL;
-  if ((a.q_sb | a.q_sh | a.c_sp | a.c_st | a.c_sh) & 7) return MXFA_EINVAL;
+  if ((a.q_sb | a.q_sh) & 7) return MXFA_EINVAL;
+  if (((a.c_sp | a.c_st | a.c_sh) * esz) & 15) return MXFA_EINVAL;
   if (a.q_sb < 0 || a.q_sh < 0 || a.c_sp < 0 || a.c_st < 0 || a.c_sh < 0 || a.bt_stride < 0)
     return MXFA_EINVAL;
   // Rows must not overlap: the per-tile descriptors cover whole rows.
   if ((a.ps > 1 && a.c_st < a.hd) || (gq > 1 && a.q_sh < a.hd)) return MXFA_EINVAL;
   // Byte offsets inside a tile and inside a q group are 32-bit.
-  if (((int64_t)(kTile - 1) * a.c_st + a.hd) * 2 >= ((int64_t)1 << 30))
+  if (((int64_t)(kTile - 1) * a.c_st + a.hd) * esz >= ((int64_t)1 << 30))
     return MXFA_EUNSUPPORTED;
-  if ((int64_t)(a.ps - 1) * a.c_st * 2 >= ((int64_t)1 << 32) || a.c_sh * 2 >= ((int64_t)1 << 32))
+  if ((int64_t)(a.ps - 1) * a.c_st * esz >= ((int64_t)1 << 32) ||
+      a.c_sh * esz >= ((int64_t)1 << 32))
     return MXFA_EUNSUPPORTED;
   if (((int64_t)(gq - 1) * a.q_sh + a.hd) * 2 >= ((int64_t)1 << 30)) return MXFA_EUNSUPPORTED;
   if (((uintptr_t)a.out & 7u) || ((a.o_sb | a.o_sh) & 3) || a.o_sb < 0 || a.o_sh < 0)
     return MXFA_EINVAL;
+  if (((uintptr_t)a.k_scale & 3u) || ((uintptr_t)a.v_scale & 3u)) return MXFA_EINVAL;
   if (!a.ws || !aligned16(a.ws)) return MXFA_EWORKSPACE;
   if (a.ws_bytes < ws_layout(a.batch, a.hq, a.hd, a.num_splits).bytes) return MXFA_EWORKSPACE;
   return MXFA_OK;
 }
 
-struct Grid {
-  int heads_per_wg, subs, gx, gy;
-};
-
-// Workgroups of `waves` waves: min(HKV, waves) kv heads x waves / that sub-ranges.
-static Grid grid_for(int hkv, int num_splits, int waves) {
-  Grid g;
-  g.heads_per_wg = hkv < waves ? hkv : waves;
-  g.subs = waves / g.heads_per_wg;
-  g.gx = (hkv + g.heads_per_wg - 1) / g.heads_per_wg;
-  g.gy = (num_splits + g.subs - 1) / g.subs;
-  return g;
-}
-
 static DecodeParams make_params(const SplitArgs &a, const Grid &g) {
   const WsLayout w = ws_layout(a.batch, a.hq, a.hd, a.num_splits);
+  const int64_t esz = a.fp8 ? 1 : 2;
   DecodeParams p;
   p.q = (const char *)a.q;
   p.q_sb = a.q_sb * 2;
   p.q_sh = a.q_sh * 2;
   p.k = (const char *)a.k;
   p.v = (const char *)a.v;
-  p.sp_bytes = a.c_sp * 2;
-  p.st_bytes = (uint32_t)(a.c_st * 2);
-  p.sh_bytes = (uint32_t)(a.c_sh * 2);
+  p.sp_bytes = a.c_sp * esz;
+  p.st_bytes = (uint32_t)(a.c_st * esz);
+  p.sh_bytes = (uint32_t)(a.c_sh * esz);
   p.bt = a.bt;
   p.bt_stride = a.bt_stride;
   p.seqlens = a.seqlens;
@@ -997,10 +126,13 @@ static DecodeParams make_params(const SplitArgs &a, const Grid &g) {
   p.ws_o = (float *)a.ws;
   p.ws_lse = (float *)a.ws + w.o_floats;
   p.ws_s = (int32_t *)((float *)a.ws + w.o_floats + w.lse_floats);
+  p.k_scale = a.fp8 ? a.k_scale : nullptr;
+  p.v_scale = a.fp8 ? a.v_scale : nullptr;
   p.scale_log2 = a.scale * kLog2e;
   p.seqlen_add = a.seqlen_add;
   p.batch = a.batch;
   p.hkv = a.hkv;
+  p.gq = a.hq / a.hkv;
   p.heads_per_wg = g.heads_per_wg;
   p.subs = g.subs;
   p.ps_log2 = ilog2_exact(a.ps);
@@ -1010,109 +142,30 @@ static DecodeParams make_params(const SplitArgs &a, const Grid &g) {
   return p;
 }
 
-// Waves per workgroup: one wave per kv head (KH = min(HKV, max) kv heads per
-// workgroup), at least 4 waves (S = 4 / KH sub-ranges when HKV < 4), at most
-// 8 at HD 64 and 4 at HD 128; one workgroup per CU. Measured on MI355X
-// (one call, config-2 lengths): at HD 128 eight-wave workgroups run as two
-// generations of four waves per CU (the second wave on each SIMD issues its
-// first loads only when the first finishes, since four waves already fill
-// the CU's vector-memory queue), which leaves a drain tail: four-wave
-// workgroups are 3% (GQ4) to 10% (GQ8) faster. At HD 64 all eight waves run
-// together; eight beat four by 2-3% at 8 kv heads, four beat two sub-ranges of
-// eight by 10% at 4 kv heads; two workgroups per CU lose 2-15% everywhere.
-template <int HD>
-constexpr int kMaxWaves = HD == 64 ? 8 : 4;
-constexpr int kMinWaves = 4;
-
-static int waves_for(int hd, int hkv) {
-  const int most = hd == 64 ? kMaxWaves<64> : kMaxWaves<128>;
-  const int kh = hkv < most ? hkv : most;
-  return kh >= kMinWaves ? kh : kMinWaves;
-}
-
-template <int HD>
-constexpr int kWgPerCu = 1;
-// Register sets of the tile pipeline: HD 64 tiles are half the bytes, so a
-// third set keeps as many bytes in flight per wave as HD 128 does with two.
-template <int HD>
-constexpr int kNbuf = HD == 64 ? 3 : 2;
-
-// PV on the matrix cores from this many query heads per kv head up. Measured
-// on MI355X (config-2 shape, one call): against DPP-broadcast FMAs on the VALU
-// the matrix cores are even at GQ 2 and faster at GQ 4 (2-3%) and GQ 8 (6% at
-// HD 128, 14% at HD 64), so every supported GQ uses them.
-constexpr int kPvMfmaMinGq = 2;
-
-template <int HD, int GQ, typename T, int WAVES>
-static int launch_w(const DecodeParams &p, const Grid &g, hipStream_t st) {
-  dim3 grid(g.gx, g.gy);
-  const size_t lds = (size_t)(p.batch + 1) * sizeof(int32_t);
-  constexpr bool kMfma = GQ >= kPvMfmaMinGq;
-  if (p.ps_log2 >= 4)
-    hipLaunchKernelGGL((split_partial_kernel<HD, GQ, T, false, kMfma, kNbuf<HD>, WAVES,
-                                             kWgPerCu<HD>>),
-                       grid, dim3(WAVES * 64), lds, st, p);
-  else
-    hipLaunchKernelGGL((split_partial_kernel<HD, GQ, T, true, kMfma, 2, WAVES, kWgPerCu<HD>>),
-                       grid, dim3(WAVES * 64), lds, st, p);
-  return hipGetLastError() == hipSuccess ? MXFA_OK : MXFA_ELAUNCH;
-}
-
-template <int HD, int GQ, typename T>
-static int launch_t(const DecodeParams &p, const Grid &g, hipStream_t st) {
-  if constexpr (kMaxWaves<HD> == 8) {
-    if (g.heads_per_wg * g.subs == 8) return launch_w<HD, GQ, T, 8>(p, g, st);
-  }
-  return launch_w<HD, GQ, T, 4>(p, g, st);
-}
-
-template <int HD, typename T>
-static int launch_gq(const DecodeParams &p, const Grid &g, int gq, hipStream_t st) {
-  switch (gq) {
-    case 2: return launch_t<HD, 2, T>(p, g, st);
-    case 4: return launch_t<HD, 4, T>(p, g, st);
-    case 8: return launch_t<HD, 8, T>(p, g, st);
-  }
-  return MXFA_EUNSUPPORTED;
-}
-
-// Blocks per pair: enough piece groups that a sequence of typical length
-// (num_splits / batch ranges, +1 for the range ends) folds its pieces in one
-// step of eight loads per thread; at most C / 16 (16 chunks per block).
-template <int HD, int GQ>
-static int combine_chunk_blocks(int batch, int num_splits) {
-  constexpr int C = GQ * HD / 4;
-  const int pieces = (num_splits + batch - 1) / batch + 1;
-  int f = 1;
-  while (f < C / 16 && (kCombineThreads * f / C) * 8 < pieces) f *= 2;
-  return f;
-}
-
-template <int HD, int GQ, typename T>
-static int launch_combine_t(CombineParams c, hipStream_t st) {
-  c.chunk_blocks = combine_chunk_blocks<HD, GQ>(c.batch, c.num_ranges);
-  dim3 grid(c.batch * (c.hq / GQ) * c.chunk_blocks);
-  hipLaunchKernelGGL((split_combine_kernel<HD, GQ, T>), grid, dim3(kCombineThreads), 0, st, c);
-  return hipGetLastError() == hipSuccess ? MXFA_OK : MXFA_ELAUNCH;
-}
-
-template <int HD, typename T>
-static int launch_combine_gq(const CombineParams &c, hipStream_t st) {
-  switch (c.gq) {
-    case 2: return launch_combine_t<HD, 2, T>(c, st);
-    case 4: return launch_combine_t<HD, 4, T>(c, st);
-    case 8: return launch_combine_t<HD, 8, T>(c, st);
-  }
-  return MXFA_EUNSUPPORTED;
-}
-
 static int launch_partial(const SplitArgs &a, hipStream_t st) {
   const Grid g = grid_for(a.hkv, a.num_splits, waves_for(a.hd, a.hkv));
   const DecodeParams p = make_params(a, g);
-  const int gq = a.hq / a.hkv;
-  if (a.dtype == MXFA_DTYPE_BF16)
-    return a.hd == 128 ? launch_gq<128, BF16>(p, g, gq, st) : launch_gq<64, BF16>(p, g, gq, st);
-  return a.hd == 128 ? launch_gq<128, F16>(p, g, gq, st) : launch_gq<64, F16>(p, g, gq, st);
+  switch (a.hd) {
+    case 64: return launch_partial_64(p, g, a.dtype, a.fp8, st);
+    case 128: return launch_partial_128(p, g, a.dtype, a.fp8, st);
+    default: return launch_partial_256(p, g, a.dtype, a.fp8, st);
+  }
+}
+
+// Heads per combine block: a typical crossing sequence has about
+// num_splits / batch + 1 pieces; enough piece groups G (a power of two) that
+// they fold in one step of eight loads, then as many heads as fit in the
+// block's kCombineThreads / G chunk threads (at most the next power of two
+// of HQ).
+static int combine_heads_per_block(int batch, int hq, int hd, int num_splits) {
+  const int ch = hd / 4;
+  const int pieces = (num_splits + batch - 1) / batch + 1;
+  int groups = 1;
+  while (groups * ch < kCombineThreads && groups * 8 < pieces) groups *= 2;
+  int h = kCombineThreads / (groups * ch);
+  if (h < 1) h = 1;
+  while (h > 1 && h / 2 >= hq) h /= 2;
+  return h;
 }
 
 static int launch_combine(void *ws, void *out, int64_t o_sb, int64_t o_sh, int batch, int hq,
@@ -1129,9 +182,12 @@ static int launch_combine(void *ws, void *out, int64_t o_sb, int64_t o_sh, int b
   c.hq = hq;
   c.gq = hq / hkv;
   c.num_ranges = ns;
-  if (dtype == MXFA_DTYPE_BF16)
-    return hd == 128 ? launch_combine_gq<128, BF16>(c, st) : launch_combine_gq<64, BF16>(c, st);
-  return hd == 128 ? launch_combine_gq<128, F16>(c, st) : launch_combine_gq<64, F16>(c, st);
+  c.heads_per_block = combine_heads_per_block(batch, hq, hd, ns);
+  switch (hd) {
+    case 64: return launch_combine_64(c, dtype, st);
+    case 128: return launch_combine_128(c, dtype, st);
+    default: return launch_combine_256(c, dtype, st);
+  }
 }
 
 static SplitArgs split_args(const void *q, int64_t q_stride_b, int64_t q_stride_h,
@@ -1170,6 +226,25 @@ static SplitArgs split_args(const void *q, int64_t q_stride_b, int64_t q_stride_
   a.num_pages = num_pages;
   a.dtype = dtype;
   a.num_splits = num_splits;
+  a.fp8 = false;
+  a.k_scale = nullptr;
+  a.v_scale = nullptr;
+  return a;
+}
+
+static int run_split(const SplitArgs &a, bool with_combine, hipStream_t st) {
+  int rc = check_split_args(a);
+  if (rc != MXFA_OK) return rc;
+  rc = launch_partial(a, st);
+  if (rc != MXFA_OK || !with_combine) return rc;
+  return launch_combine(a.ws, a.out, a.o_sb, a.o_sh, a.batch, a.hq, a.hkv, a.hd, a.dtype,
+                        a.num_splits, st);
+}
+
+static SplitArgs fp8_args(SplitArgs a, const float *k_scale, const float *v_scale) {
+  a.fp8 = true;
+  a.k_scale = k_scale;
+  a.v_scale = v_scale;
   return a;
 }
 
@@ -1203,8 +278,7 @@ int mxfa_split_heuristic(int batch, int q_heads, int kv_heads, int head_dim, int
   // each wave streams one (kv head, range). The kernel lowers the count to the
   // real tile total on the device.
   const Grid g = grid_for(kv_heads, 1, waves_for(head_dim, kv_heads));
-  const int64_t per_cu = head_dim == 64 ? kWgPerCu<64> : kWgPerCu<128>;
-  int64_t n = (int64_t)num_cus * per_cu * g.subs / g.gx;
+  int64_t n = (int64_t)num_cus * g.subs / g.gx;
   const int64_t cap = (int64_t)block_table_width * page_size;
   const int64_t cap_tiles = (int64_t)batch * ((cap + kTile - 1) / kTile);
   if (n > cap_tiles) n = cap_tiles;
@@ -1229,28 +303,31 @@ int mxfa_split_decode_workspace_size(int batch, int q_heads, int head_dim, int n
       const int32_t *seqlens, int seqlen_add, void *out, int64_t out_stride_b,              \
       int64_t out_stride_h, void *workspace, size_t workspace_bytes, float scale, int batch, \
       int q_heads, int kv_heads, int head_dim, int page_size, int block_table_width,        \
-      int num_pages, int dtype, int num_splits, void *stream
+      int num_pages, int dtype, int num_splits
 #define MXFA_SPLIT_ARGS                                                                      \
   q, q_stride_b, q_stride_h, k_cache, v_cache, cache_stride_page, cache_stride_token,       \
       cache_stride_head, block_table, bt_stride, seqlens, seqlen_add, out, out_stride_b,    \
       out_stride_h, workspace, workspace_bytes, scale, batch, q_heads, kv_heads, head_dim,  \
       page_size, block_table_width, num_pages, dtype, num_splits
 
-int mxfa_split_decode_launch(MXFA_SPLIT_PARAMS) {
-  const SplitArgs a = split_args(MXFA_SPLIT_ARGS);
-  int rc = check_split_args(a);
-  if (rc != MXFA_OK) return rc;
-  rc = launch_partial(a, (hipStream_t)stream);
-  if (rc != MXFA_OK) return rc;
-  return launch_combine(a.ws, a.out, a.o_sb, a.o_sh, a.batch, a.hq, a.hkv, a.hd, a.dtype,
-                        a.num_splits, (hipStream_t)stream);
+int mxfa_split_decode_launch(MXFA_SPLIT_PARAMS, void *stream) {
+  return run_split(split_args(MXFA_SPLIT_ARGS), true, (hipStream_t)stream);
 }
 
-int mxfa_split_decode_partial_launch(MXFA_SPLIT_PARAMS) {
-  const SplitArgs a = split_args(MXFA_SPLIT_ARGS);
-  const int rc = check_split_args(a);
-  if (rc != MXFA_OK) return rc;
-  return launch_partial(a, (hipStream_t)stream);
+int mxfa_split_decode_partial_launch(MXFA_SPLIT_PARAMS, void *stream) {
+  return run_split(split_args(MXFA_SPLIT_ARGS), false, (hipStream_t)stream);
+}
+
+int mxfa_split_decode_fp8_launch(MXFA_SPLIT_PARAMS, const float *k_scale, const float *v_scale,
+                                 void *stream) {
+  return run_split(fp8_args(split_args(MXFA_SPLIT_ARGS), k_scale, v_scale), true,
+                   (hipStream_t)stream);
+}
+
+int mxfa_split_decode_fp8_partial_launch(MXFA_SPLIT_PARAMS, const float *k_scale,
+                                         const float *v_scale, void *stream) {
+  return run_split(fp8_args(split_args(MXFA_SPLIT_ARGS), k_scale, v_scale), false,
+                   (hipStream_t)stream);
 }
 
 int mxfa_split_decode_combine_launch(void *workspace, size_t workspace_bytes, void *out,
@@ -1259,10 +336,8 @@ int mxfa_split_decode_combine_launch(void *workspace, size_t workspace_bytes, vo
                                      int num_splits, void *stream) {
   if (!workspace || !out) return MXFA_EINVAL;
   if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || num_splits <= 0) return MXFA_EINVAL;
-  if (head_dim != 64 && head_dim != 128) return MXFA_EUNSUPPORTED;
-  if (q_heads % kv_heads != 0) return MXFA_EUNSUPPORTED;
-  const int gq = q_heads / kv_heads;
-  if (gq != 2 && gq != 4 && gq != 8) return MXFA_EUNSUPPORTED;
+  if (!supported_hd(head_dim)) return MXFA_EUNSUPPORTED;
+  if (q_heads % kv_heads != 0 || q_heads / kv_heads > kMaxGq) return MXFA_EUNSUPPORTED;
   if (dtype != MXFA_DTYPE_F16 && dtype != MXFA_DTYPE_BF16) return MXFA_EUNSUPPORTED;
   if (batch > kMaxBatch || num_splits > 65535) return MXFA_EUNSUPPORTED;
   if (!aligned16(workspace) || ((uintptr_t)out & 7u) || ((out_stride_b | out_stride_h) & 3) ||

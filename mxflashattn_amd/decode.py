@@ -38,8 +38,10 @@ def _common_reason(q: torch.Tensor, kv_heads: int, head_dim: int) -> str | None:
     if head_dim not in native.SUPPORTED_HEAD_DIMS:
         return f"head_dim_{head_dim}_not_in_{native.SUPPORTED_HEAD_DIMS}"
     hq = q.shape[-2]
-    if kv_heads <= 0 or hq % kv_heads or hq // kv_heads not in native.SUPPORTED_GQA:
-        return f"gqa_ratio_{hq}/{kv_heads}_not_in_{native.SUPPORTED_GQA}"
+    # Any group of 1..16 query heads per kv head runs here (the reference's
+    # kernel stops at {2, 4, 8}; the API hands such calls down its chain).
+    if kv_heads <= 0 or hq % kv_heads or hq // kv_heads not in native.KERNEL_GQA:
+        return f"gqa_ratio_{hq}/{kv_heads}_not_in_1..16"
     return None
 
 

@@ -72,10 +72,15 @@ class DecoderModel:
     """Random-init weights of ``shape``; ``step`` runs one decode token per sequence."""
 
     def __init__(self, shape: DecoderShape, device: torch.device, dtype=torch.bfloat16,
-                 seed: int = 20261007) -> None:
+                 seed: int = 20261007, kv_cache_dtype: str = "auto") -> None:
         self.shape = shape
         self.device = device
         self.dtype = dtype
+        # vLLM's cache dtype string: "auto" (the model dtype) or "fp8" (e4m3fn
+        # with per-tensor scales, here 1.0 as a float32 device scalar per layer).
+        self.kv_cache_dtype = kv_cache_dtype
+        self.k_scale = torch.ones(1, device=device, dtype=torch.float32)
+        self.v_scale = torch.ones(1, device=device, dtype=torch.float32)
         g = torch.Generator(device=device)
         g.manual_seed(seed)
         s = shape
@@ -126,8 +131,11 @@ class DecoderModel:
     def attention(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                   kv_cache: torch.Tensor, meta: DecodeMetadata, out: torch.Tensor) -> None:
         """The two backend calls vLLM makes per layer: cache update, then decode."""
-        kv_cache_update(k, v, kv_cache, meta.slot_mapping)
-        forward_decode(q, kv_cache, meta, out, softmax_scale=self.scale)
+        kv_cache_update(k, v, kv_cache, meta.slot_mapping, self.kv_cache_dtype, self.k_scale,
+                        self.v_scale)
+        forward_decode(q, kv_cache, meta, out, softmax_scale=self.scale,
+                       kv_cache_dtype=self.kv_cache_dtype, k_scale=self.k_scale,
+                       v_scale=self.v_scale)
 
     def step(self, tokens: torch.Tensor, positions: torch.Tensor, kv_caches: list[torch.Tensor],
              meta: DecodeMetadata) -> torch.Tensor:
@@ -193,10 +201,13 @@ def build_state(model: DecoderModel, batch: int, prompt_lens: torch.Tensor, new_
     gd = torch.Generator(device=dev)
     gd.manual_seed(seed + 2)
     kv_caches = []
+    fp8 = model.kv_cache_dtype.startswith("fp8")
     for _ in range(s.layers):
         cache = torch.empty(2, total, page_size, s.kv_heads, s.head_dim, device=dev,
                             dtype=model.dtype)
         cache.normal_(generator=gd)
+        if fp8:  # N(0, 1) values are well inside e4m3fn's range
+            cache = cache.to(torch.float8_e4m3fn)
         kv_caches.append(cache)
     table = table.to(dev)
     seq_lens = prompt_lens.to(dev, torch.int32)  # lengths before the first decoded token
@@ -228,10 +239,11 @@ def advance(state: DecodeState) -> None:
 
 def run(batch: int = 128, new_tokens: int = 256, shape: DecoderShape = QWEN3_4B,
         median: int = 1024, sigma: float = 1.0, lo: int = 16, hi: int = 8192,
-        page_size: int = 16, device: torch.device | None = None, seed: int = 20261007) -> dict:
+        page_size: int = 16, device: torch.device | None = None, seed: int = 20261007,
+        kv_cache_dtype: str = "auto") -> dict:
     """Decode ``new_tokens`` tokens for ``batch`` sequences; timing and share."""
     device = device or torch.device("cuda", torch.cuda.current_device())
-    model = DecoderModel(shape, device, seed=seed)
+    model = DecoderModel(shape, device, seed=seed, kv_cache_dtype=kv_cache_dtype)
     prompt = lognormal_prompt_lengths(batch, median, sigma, lo, hi, seed)
     state = build_state(model, batch, prompt, new_tokens, page_size, seed)
     stream = torch.cuda.Stream(device)
@@ -292,7 +304,7 @@ def run(batch: int = 128, new_tokens: int = 256, shape: DecoderShape = QWEN3_4B,
     final_lens = state.meta.seq_lens.to(torch.int64)
     # K and V bytes the attention calls read per step, over all layers.
     kv_bytes_step = (int(final_lens.sum().item()) * shape.kv_heads * shape.head_dim * 2
-                     * model.embed.element_size() * shape.layers)
+                     * state.kv_caches[0].element_size() * shape.layers)
     finite = bool(torch.isfinite(logits.float()).all().item())
     del graph, attn_graph
     return {
@@ -302,6 +314,7 @@ def run(batch: int = 128, new_tokens: int = 256, shape: DecoderShape = QWEN3_4B,
         "attention_share": round(attn_ms / step_ms, 4),
         "attention_kv_gb_s": round(kv_bytes_step / (attn_ms * 1e-3) / 1e9, 1),
         "batch": batch,
+        "kv_cache_dtype": "fp8_e4m3" if kv_cache_dtype.startswith("fp8") else "bf16",
         "new_tokens": new_tokens,
         "timed_steps": steps,
         "layers": shape.layers,
@@ -321,12 +334,14 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--batch", type=int, default=128)
     ap.add_argument("--new-tokens", type=int, default=256)
     ap.add_argument("--layers", type=int, default=QWEN3_4B.layers)
+    ap.add_argument("--kv-cache-dtype", default="auto", choices=("auto", "fp8"))
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         print("decode_step needs a GPU", file=sys.stderr)
         return 2
     shape = DecoderShape(layers=args.layers)
-    print(json.dumps(run(args.batch, args.new_tokens, shape)))
+    print(json.dumps(run(args.batch, args.new_tokens, shape,
+                         kv_cache_dtype=args.kv_cache_dtype)))
     return 0
 
 

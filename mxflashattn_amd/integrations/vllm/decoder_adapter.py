@@ -15,7 +15,7 @@ from typing import Any
 
 import torch
 
-from ... import api
+from ... import api, native
 from ...dispatch import get_last_dispatch_info
 from .backend import record_event
 from .native_decode import reshape_and_cache_flash
@@ -220,13 +220,42 @@ def _decode_forward_graph(query: torch.Tensor, kv_cache: torch.Tensor, attn_meta
     return result.reshape(q.shape[0] * q.shape[1], -1), None
 
 
+def _fp8_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: Any,
+                output: torch.Tensor, softmax_scale: float, k_scale: Any,
+                v_scale: Any) -> torch.Tensor:
+    """One-token decode over an fp8 (e4m3fn) cache, straight on the HIP kernels
+    (the public API, like the reference's, takes 16-bit caches only)."""
+    if int(attn_metadata.max_query_len) != 1:
+        raise DecoderAdapterBlocked(
+            f"only_single_token_decode_supported:max_query_len={int(attn_metadata.max_query_len)}")
+    key_cache, value_cache = kv_cache.view(native.FP8_DTYPE).unbind(0)
+    n = int(attn_metadata.num_actual_tokens)
+    q = query[:n].reshape(n, 1, query.shape[1], query.shape[2])
+    target = output[:n].view(n, 1, query.shape[1], query.shape[2])
+    native.paged_decode_split(q, key_cache, value_cache,
+                              _int32_on(attn_metadata.block_table, query.device),
+                              _int32_on(attn_metadata.seq_lens.reshape(-1), query.device),
+                              softmax_scale, out=target, k_scale=k_scale, v_scale=v_scale)
+    record_event({"path": "mi355x_split_decode", "operation": "paged_decode_split",
+                  "fallback": "false", "kv_cache_dtype": "fp8_e4m3"})
+    return output
+
+
 def forward_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: Any,
-                   output: torch.Tensor, *, softmax_scale: float) -> torch.Tensor:
+                   output: torch.Tensor, *, softmax_scale: float, kv_cache_dtype: str = "auto",
+                   k_scale: Any = None, v_scale: Any = None) -> torch.Tensor:
     """The decode body of the backend's ``forward``: one-token paged decode into
     vLLM's output buffer, with the dispatch event the reference plugin records
     (integrations/vllm/vllm_plugin.py:297-299,399-431). Raises
     DecoderAdapterBlocked for calls outside the adapter contract (prefill,
-    cascade), which the backend hands to vLLM."""
+    cascade), which the backend hands to vLLM. kv_cache_dtype "fp8"/"fp8_e4m3"
+    (cache stored as e4m3fn or its uint8 codes) decodes with the layer's
+    per-tensor k_scale / v_scale; the reference has no fp8 path."""
+    if kv_cache_dtype in ("fp8", "fp8_e4m3"):
+        if output.dim() != 3 or not output.is_contiguous():
+            raise DecoderAdapterBlocked("fp8_decode_needs_contiguous_[tokens,heads,dim]_output")
+        return _fp8_decode(query, kv_cache, attn_metadata, output, softmax_scale, k_scale,
+                           v_scale)
     result, _ = decode_forward(query, kv_cache, attn_metadata, softmax_scale=softmax_scale,
                                causal=bool(attn_metadata.causal))
     info = get_last_dispatch_info()
@@ -244,8 +273,11 @@ def forward_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: A
 
 
 def kv_cache_update(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
-                    slot_mapping: torch.Tensor, kv_cache_dtype: str = "auto") -> None:
+                    slot_mapping: torch.Tensor, kv_cache_dtype: str = "auto",
+                    k_scale: Any = None, v_scale: Any = None) -> None:
     """The backend's ``do_kv_cache_update``: new K/V rows of [tokens, HKV, HD]
-    into the [2, blocks, PS, HKV, HD] cache at slot_mapping (vllm_plugin.py:507-511)."""
+    into the [2, blocks, PS, HKV, HD] cache at slot_mapping (vllm_plugin.py:507-511);
+    an fp8 cache stores them quantised with the layer's k_scale / v_scale."""
     key_cache, value_cache = kv_cache.unbind(0)
-    reshape_and_cache_flash(key, value, key_cache, value_cache, slot_mapping, kv_cache_dtype)
+    reshape_and_cache_flash(key, value, key_cache, value_cache, slot_mapping, kv_cache_dtype,
+                            k_scale, v_scale)

@@ -9,6 +9,10 @@ window, a dtype other than fp16/bf16 or different from the cache's, q_len > 1,
 head dim outside {64, 128}, GQA ratio outside {2, 4, 8}, or a page size that is
 not a power of two. The caller then runs the original implementation.
 
+MXFA_WIDE_CONTRACT=1 widens the guards to what the kernels take: head dim 256,
+1..16 query heads per kv head, and fp8 (e4m3fn) caches with per-tensor
+k_descale / v_descale (a scalar, or a tensor expanded from one).
+
 ``mx_kvcache_compat`` replaces ``_mx_kvcache_compat`` (:319-349): it drops
 vLLM-only keyword arguments, tries the native route, else the original vendor
 function, else the public API. ``reshape_and_cache_flash`` is the cache write
@@ -33,7 +37,21 @@ _VLLM_ONLY_KWARGS = ("s_aux", "return_softmax_lse", "scheduler_metadata", "fa_ve
                      "q_descale", "k_descale", "v_descale")
 
 
-def _guard(args: tuple, kwargs: dict) -> tuple[str | None, tuple]:
+def wide_contract() -> bool:
+    return os.getenv("MXFA_WIDE_CONTRACT", "0") == "1"
+
+
+def _per_tensor(scale: Any) -> bool:
+    """None, a float, or a float32 tensor holding one value (numel 1 or all
+    strides 0, as vLLM's layer scale expanded to [B, HKV])."""
+    if scale is None or isinstance(scale, (int, float)):
+        return True
+    return (isinstance(scale, torch.Tensor) and scale.dtype == torch.float32
+            and (scale.numel() == 1 or all(st == 0 for st in scale.stride())))
+
+
+def _guard(args: tuple, kwargs: dict, wide: bool = False,
+           descales: tuple = (None, None)) -> tuple[str | None, tuple]:
     """(reason, (q, k_cache, v_cache, block_table, seqlens)); reason None = take it."""
     q = args[0] if args else kwargs.get("q")
     if q is None or q.dim() not in (3, 4):
@@ -57,16 +75,21 @@ def _guard(args: tuple, kwargs: dict) -> tuple[str | None, tuple]:
     v_cache = kwargs.get("v_cache", args[2] if len(args) > 2 else None)
     if k_cache is None or v_cache is None:
         return "caches", ()
-    if q.dtype not in native.DTYPE_CODES or k_cache.dtype != q.dtype:
+    fp8 = wide and k_cache.dtype == native.FP8_DTYPE and v_cache.dtype == k_cache.dtype
+    if q.dtype not in native.DTYPE_CODES or (k_cache.dtype != q.dtype and not fp8):
         return "dtype", ()
+    if fp8 and not all(_per_tensor(d) for d in descales):
+        return "descale_not_per_tensor", ()
     if q.dim() == 4 and q.shape[1] != 1:
         return "query_length", ()
     if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
         return "cache_rank", ()
     hd, hq, hkv = q.shape[-1], q.shape[-2], k_cache.shape[2]
-    if hd not in native.SUPPORTED_HEAD_DIMS or k_cache.shape[3] != hd:
+    head_dims = native.KERNEL_HEAD_DIMS if wide else native.SUPPORTED_HEAD_DIMS
+    gqa = native.KERNEL_GQA if wide else native.SUPPORTED_GQA
+    if hd not in head_dims or k_cache.shape[3] != hd:
         return "head_dim", ()
-    if hkv <= 0 or hq % hkv or hq // hkv not in native.SUPPORTED_GQA:
+    if hkv <= 0 or hq % hkv or hq // hkv not in gqa:
         return "gqa_ratio", ()
     ps = k_cache.shape[1]
     if ps <= 0 or ps & (ps - 1) or ps > 4096:
@@ -76,11 +99,12 @@ def _guard(args: tuple, kwargs: dict) -> tuple[str | None, tuple]:
     return None, (q, k_cache, v_cache, bt, sl)
 
 
-def try_native_decode(args: tuple, kwargs: dict) -> torch.Tensor | None:
+def try_native_decode(args: tuple, kwargs: dict, k_descale: Any = None,
+                      v_descale: Any = None) -> torch.Tensor | None:
     """HIP decode of a vLLM flash_attn_with_kvcache call, or None to hand it back."""
     if os.getenv("MXFA_NATIVE_DECODE", "0") != "1":
         return None
-    reason, picked = _guard(args, kwargs)
+    reason, picked = _guard(args, kwargs, wide_contract(), (k_descale, v_descale))
     if reason is not None:
         record_event({"path": "native_decode", "fallback": "true",
                       "fallback_reason": f"guard:{reason}"})
@@ -98,8 +122,11 @@ def try_native_decode(args: tuple, kwargs: dict) -> torch.Tensor | None:
         if view is not None:
             out = view
     ns = native.default_num_splits(q4, k_cache, bt)
+    scales = {}
+    if k_cache.dtype == native.FP8_DTYPE:
+        scales = {"k_scale": k_descale, "v_scale": v_descale}
     result = native.paged_decode_split(q4, k_cache, v_cache, bt, sl, scale, out=out,
-                                       num_splits=ns)
+                                       num_splits=ns, **scales)
     if provided is not None and out is None:
         provided.copy_(result.reshape_as(provided))
         result = provided
@@ -114,11 +141,16 @@ def try_native_decode(args: tuple, kwargs: dict) -> torch.Tensor | None:
 
 def mx_kvcache_compat(*args, **kwargs):
     """Stand-in for vLLM's flash_attn_with_kvcache inside its attention forward."""
-    for name in _VLLM_ONLY_KWARGS:
-        kwargs.pop(name, None)
-    result = try_native_decode(args, kwargs)
+    popped = {name: kwargs.pop(name, None) for name in _VLLM_ONLY_KWARGS}
+    result = try_native_decode(args, kwargs, popped["k_descale"], popped["v_descale"])
     if result is not None:
         return result
+    k_cache = kwargs.get("k_cache", args[1] if len(args) > 1 else None)
+    if isinstance(k_cache, torch.Tensor) and k_cache.dtype == native.FP8_DTYPE:
+        # An fp8 cache is meaningless without its scales: give them back.
+        for name in ("q_descale", "k_descale", "v_descale"):
+            if popped[name] is not None:
+                kwargs[name] = popped[name]
     # Shapes the public API rejects must reach the original implementation
     # instead of raising inside vLLM.
     if official_kvcache is not None:
@@ -130,8 +162,21 @@ def reshape_and_cache_flash(key: torch.Tensor, value: torch.Tensor, key_cache: t
                             value_cache: torch.Tensor, slot_mapping: torch.Tensor,
                             kv_cache_dtype: str = "auto", k_scale: Any = None,
                             v_scale: Any = None) -> None:
-    """vLLM cache write (slot t -> page slot // PS, row slot % PS; slot < 0 skipped)."""
+    """vLLM cache write (slot t -> page slot // PS, row slot % PS; slot < 0 skipped).
+
+    kv_cache_dtype "fp8" / "fp8_e4m3": the caches hold e4m3fn (vLLM allocates
+    them as uint8) and each row is stored as e4m3fn(x / scale) with the layer's
+    per-tensor k_scale / v_scale."""
+    n = slot_mapping.shape[0]
+    if kv_cache_dtype in ("fp8", "fp8_e4m3"):
+        if key_cache.dtype == torch.uint8:
+            key_cache, value_cache = (key_cache.view(native.FP8_DTYPE),
+                                      value_cache.view(native.FP8_DTYPE))
+        if key_cache.dtype != native.FP8_DTYPE:
+            raise ValueError(f"kv_cache_dtype {kv_cache_dtype!r} needs uint8/e4m3fn caches")
+        native.reshape_and_cache(key[:n], value[:n], key_cache, value_cache, slot_mapping,
+                                 k_scale=k_scale, v_scale=v_scale)
+        return
     if kv_cache_dtype not in ("auto", None):
         raise NotImplementedError(f"kv_cache_dtype {kv_cache_dtype!r} is not supported")
-    n = slot_mapping.shape[0]
     native.reshape_and_cache(key[:n], value[:n], key_cache, value_cache, slot_mapping)

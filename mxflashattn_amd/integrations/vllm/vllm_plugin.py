@@ -73,9 +73,16 @@ class MXFlashAttnImpl(FlashAttentionImpl):
                                            output_block_scale)
         if output is None:
             raise ValueError("vLLM must provide an output buffer")
+        kv_dtype = getattr(self, "kv_cache_dtype", "auto") or "auto"
+        if kv_dtype.startswith("fp8") and not native_decode.wide_contract():
+            # fp8 caches are the vendor's unless the wider contract is on.
+            return super().forward(layer, query, key, value, kv_cache, attn_metadata, output,
+                                   output_scale, output_block_scale)
         try:
             return forward_decode(query, kv_cache, attn_metadata, output,
-                                  softmax_scale=self.scale)
+                                  softmax_scale=self.scale, kv_cache_dtype=kv_dtype,
+                                  k_scale=getattr(layer, "_k_scale", None),
+                                  v_scale=getattr(layer, "_v_scale", None))
         except DecoderAdapterBlocked as exc:
             record_event({"path": "vendor_prefill_or_blocked", "reason": str(exc)})
             if "single_token_decode" in str(exc):
@@ -84,7 +91,8 @@ class MXFlashAttnImpl(FlashAttentionImpl):
             raise
 
     def do_kv_cache_update(self, layer, key, value, kv_cache, slot_mapping):
-        kv_cache_update(key, value, kv_cache, slot_mapping, self.kv_cache_dtype)
+        kv_cache_update(key, value, kv_cache, slot_mapping, self.kv_cache_dtype,
+                        getattr(layer, "_k_scale", None), getattr(layer, "_v_scale", None))
 
 
 class MXFlashAttnBackend(FlashAttentionBackend):

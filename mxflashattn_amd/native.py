@@ -24,7 +24,7 @@ LIB_PATH = Path(
     os.environ.get("MXFLASHATTN_AMD_LIB")
     or Path(__file__).resolve().parent / "_lib" / "libmxfa_mi355x.so"
 )
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 MXFA_OK = 0
 MXFA_EUNSUPPORTED = -1
@@ -33,9 +33,17 @@ MXFA_EWORKSPACE = -3
 MXFA_ELAUNCH = -4
 
 DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
+# OCP e4m3fn, the fp8 format of gfx950 (MI300's e4m3fnuz is a different code).
+FP8_DTYPE = torch.float8_e4m3fn
 
+# The reference's decode contract (vllm_plugin.py:220-261 hands other shapes
+# back); the guards that mirror the reference use these.
 SUPPORTED_HEAD_DIMS = (64, 128)
 SUPPORTED_GQA = (2, 4, 8)
+# What the kernels take: head dims 64/128/256, 1..16 query heads per kv head,
+# 16-bit or fp8 caches.
+KERNEL_HEAD_DIMS = (64, 128, 256)
+KERNEL_GQA = tuple(range(1, 17))
 
 # Every entry point declared in include/mxfa_mi355x.h.
 EXPORTED_SYMBOLS = (
@@ -46,7 +54,10 @@ EXPORTED_SYMBOLS = (
     "mxfa_split_decode_launch",
     "mxfa_split_decode_partial_launch",
     "mxfa_split_decode_combine_launch",
+    "mxfa_split_decode_fp8_launch",
+    "mxfa_split_decode_fp8_partial_launch",
     "mxfa_reshape_and_cache_launch",
+    "mxfa_reshape_and_cache_fp8_launch",
     "mxfa_append_kv_launch",
 )
 
@@ -65,21 +76,18 @@ _p = ctypes.c_void_p
 _f = ctypes.c_float
 _sz = ctypes.c_size_t
 
+_SPLIT_ARGS = [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _p, _i64, _i64, _p,
+               _sz, _f, _i, _i, _i, _i, _i, _i, _i, _i, _i]
+
 _SIGNATURES = {
     "mxfa_abi_version": (_i, []),
     "mxfa_strerror": (ctypes.c_char_p, [_i]),
     "mxfa_split_heuristic": (_i, [_i, _i, _i, _i, _i, _i, _i, ctypes.POINTER(_i)]),
     "mxfa_split_decode_workspace_size": (_i, [_i, _i, _i, _i, ctypes.POINTER(_sz)]),
-    "mxfa_split_decode_launch": (
-        _i,
-        [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _p, _i64, _i64, _p, _sz,
-         _f, _i, _i, _i, _i, _i, _i, _i, _i, _i, _p],
-    ),
-    "mxfa_split_decode_partial_launch": (
-        _i,
-        [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _p, _i64, _i64, _p, _sz,
-         _f, _i, _i, _i, _i, _i, _i, _i, _i, _i, _p],
-    ),
+    "mxfa_split_decode_launch": (_i, _SPLIT_ARGS + [_p]),
+    "mxfa_split_decode_partial_launch": (_i, _SPLIT_ARGS + [_p]),
+    "mxfa_split_decode_fp8_launch": (_i, _SPLIT_ARGS + [_p, _p, _p]),
+    "mxfa_split_decode_fp8_partial_launch": (_i, _SPLIT_ARGS + [_p, _p, _p]),
     "mxfa_split_decode_combine_launch": (
         _i,
         [_p, _sz, _p, _i64, _i64, _i, _i, _i, _i, _i, _i, _p],
@@ -87,6 +95,10 @@ _SIGNATURES = {
     "mxfa_reshape_and_cache_launch": (
         _i,
         [_p, _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i, _i, _i, _i, _i, _i, _p],
+    ),
+    "mxfa_reshape_and_cache_fp8_launch": (
+        _i,
+        [_p, _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i, _i, _i, _i, _i, _i, _p, _p, _p],
     ),
     "mxfa_append_kv_launch": (
         _i,
@@ -254,12 +266,14 @@ def check_decode_shapes(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
         raise UnsupportedConfig("caches must be [pages, page_size, kv_heads, head_dim]")
     hq, hd = q.shape[-2], q.shape[-1]
     hkv = k_cache.shape[2]
-    if hd not in SUPPORTED_HEAD_DIMS or k_cache.shape[3] != hd:
-        raise UnsupportedConfig(f"head_dim {hd} not in {SUPPORTED_HEAD_DIMS}")
-    if hkv <= 0 or hq % hkv or hq // hkv not in SUPPORTED_GQA:
-        raise UnsupportedConfig(f"GQA ratio {hq}/{hkv} not in {SUPPORTED_GQA}")
-    if q.dtype not in DTYPE_CODES or k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
-        raise UnsupportedConfig("q and caches must share float16 or bfloat16")
+    if hd not in KERNEL_HEAD_DIMS or k_cache.shape[3] != hd:
+        raise UnsupportedConfig(f"head_dim {hd} not in {KERNEL_HEAD_DIMS}")
+    if hkv <= 0 or hq % hkv or hq // hkv not in KERNEL_GQA:
+        raise UnsupportedConfig(f"GQA ratio {hq}/{hkv} not in 1..16")
+    if q.dtype not in DTYPE_CODES:
+        raise UnsupportedConfig("q must be float16 or bfloat16")
+    if v_cache.dtype != k_cache.dtype or k_cache.dtype not in (q.dtype, FP8_DTYPE):
+        raise UnsupportedConfig("caches must share q's dtype or both be float8_e4m3fn")
     ps = k_cache.shape[1]
     if ps <= 0 or ps & (ps - 1) or ps > 4096:
         raise UnsupportedConfig(f"page size {ps} is not a power of two <= 4096")
@@ -277,6 +291,28 @@ def _launch_args(q, k_cache, v_cache, block_table, cache_seqlens, out, workspace
         float(softmax_scale), batch, hq, hkv, hd, ps, block_table.shape[1], pages,
         DTYPE_CODES[q.dtype], num_splits, _stream_handle(q.device),
     )
+
+
+_SCALARS: dict[tuple[int, float], torch.Tensor] = {}
+
+
+def _scale_ptr(scale, device: torch.device, name: str) -> int:
+    """Device address of an fp32 dequantisation scale: a one-element (or
+    broadcast, all strides 0) float32 GPU tensor, a Python float (kept in a
+    cached device scalar) or None (1.0)."""
+    if scale is None:
+        return 0
+    if isinstance(scale, torch.Tensor):
+        if scale.dtype != torch.float32 or scale.device != device:
+            raise ValueError(f"{name} must be a float32 tensor on {device}")
+        if scale.numel() != 1 and any(st != 0 for st in scale.stride()):
+            raise UnsupportedConfig(f"{name} must be one per-tensor scale")
+        return scale.data_ptr()
+    key = (device.index or 0, float(scale))
+    t = _SCALARS.get(key)
+    if t is None:
+        t = _SCALARS[key] = torch.tensor([float(scale)], dtype=torch.float32, device=device)
+    return t.data_ptr()
 
 
 def _prepare(q, k_cache, v_cache, block_table, cache_seqlens, out):
@@ -320,11 +356,15 @@ def paged_decode_split(
     out: torch.Tensor | None = None,
     num_splits: int | None = None,
     seqlen_add: int = 0,
+    k_scale: torch.Tensor | float | None = None,
+    v_scale: torch.Tensor | float | None = None,
 ) -> torch.Tensor:
     """Split-KV paged decode on the current stream; returns ``out`` shaped like q.
 
     q: [B, 1, HQ, HD] or [B, HQ, HD] (any strides with a contiguous last dim);
-    caches: [pages, PS, HKV, HD]; block_table: int32 [B, W]; cache_seqlens: int32 [B].
+    caches: [pages, PS, HKV, HD] of q's dtype, or float8_e4m3fn with the
+    per-tensor dequantisation scales k_scale / v_scale (float32 device scalars
+    for graph capture); block_table: int32 [B, W]; cache_seqlens: int32 [B].
     The attended length of sequence b is cache_seqlens[b] + seqlen_add.
     num_splits: balanced work ranges per kv head (default: split_heuristic).
     """
@@ -336,10 +376,15 @@ def paged_decode_split(
     stream = _stream_handle(q.device)
     ws_bytes = workspace_size(q.shape[0], q.shape[-2], q.shape[-1], num_splits)
     ws = WORKSPACE.get(q.device, stream, ws_bytes)
-    rc = lib.mxfa_split_decode_launch(*_launch_args(q, k_cache, v_cache, block_table,
-                                                    cache_seqlens, out, ws.data_ptr(), ws_bytes,
-                                                    softmax_scale, num_splits, seqlen_add))
-    _check(rc, "mxfa_split_decode_launch")
+    args = _launch_args(q, k_cache, v_cache, block_table, cache_seqlens, out, ws.data_ptr(),
+                        ws_bytes, softmax_scale, num_splits, seqlen_add)
+    if k_cache.dtype == FP8_DTYPE:
+        rc = lib.mxfa_split_decode_fp8_launch(*args[:-1], _scale_ptr(k_scale, q.device, "k_scale"),
+                                              _scale_ptr(v_scale, q.device, "v_scale"), args[-1])
+        _check(rc, "mxfa_split_decode_fp8_launch")
+    else:
+        rc = lib.mxfa_split_decode_launch(*args)
+        _check(rc, "mxfa_split_decode_launch")
     return out
 
 
@@ -354,6 +399,8 @@ def split_decode_partial(
     workspace: torch.Tensor,
     num_splits: int,
     seqlen_add: int = 0,
+    k_scale: torch.Tensor | float | None = None,
+    v_scale: torch.Tensor | float | None = None,
 ) -> None:
     """Partial stage only: sequences inside one work range land in ``out``, the
     pieces of the others in ``workspace``; ``split_decode_combine`` finishes."""
@@ -363,10 +410,16 @@ def split_decode_partial(
     if not workspace.is_contiguous():
         raise ValueError("workspace must be contiguous")
     nbytes = workspace.numel() * workspace.element_size()
-    rc = library().mxfa_split_decode_partial_launch(
-        *_launch_args(q, k_cache, v_cache, block_table, cache_seqlens, out, workspace.data_ptr(),
-                      nbytes, softmax_scale, num_splits, seqlen_add))
-    _check(rc, "mxfa_split_decode_partial_launch")
+    args = _launch_args(q, k_cache, v_cache, block_table, cache_seqlens, out,
+                        workspace.data_ptr(), nbytes, softmax_scale, num_splits, seqlen_add)
+    if k_cache.dtype == FP8_DTYPE:
+        rc = library().mxfa_split_decode_fp8_partial_launch(
+            *args[:-1], _scale_ptr(k_scale, q.device, "k_scale"),
+            _scale_ptr(v_scale, q.device, "v_scale"), args[-1])
+        _check(rc, "mxfa_split_decode_fp8_partial_launch")
+    else:
+        rc = library().mxfa_split_decode_partial_launch(*args)
+        _check(rc, "mxfa_split_decode_partial_launch")
 
 
 def split_decode_combine(workspace: torch.Tensor, out: torch.Tensor, kv_heads: int,
@@ -394,16 +447,24 @@ def reshape_and_cache(
     key_cache: torch.Tensor,
     value_cache: torch.Tensor,
     slot_mapping: torch.Tensor,
+    *,
+    k_scale: torch.Tensor | float | None = None,
+    v_scale: torch.Tensor | float | None = None,
 ) -> None:
-    """vLLM-format paged append: row t -> slot_mapping[t] (skipped when < 0)."""
+    """vLLM-format paged append: row t -> slot_mapping[t] (skipped when < 0).
+
+    float8_e4m3fn caches store e4m3fn_rne(saturate(x / scale)) with the
+    per-tensor k_scale / v_scale; 16-bit caches are a bit-exact copy."""
     if key.dim() != 3 or value.shape != key.shape:
         raise ValueError("key/value must be [num_tokens, kv_heads, head_dim]")
     if key_cache.dim() != 4 or value_cache.shape != key_cache.shape:
         raise ValueError("caches must be [pages, page_size, kv_heads, head_dim]")
     if key.shape[1:] != key_cache.shape[2:]:
         raise ValueError("key/value heads and head_dim must match the cache")
-    if key.dtype != key_cache.dtype or value.dtype != key.dtype or value_cache.dtype != key.dtype:
-        raise ValueError("key/value and caches must share a dtype")
+    fp8 = key_cache.dtype == FP8_DTYPE
+    if value.dtype != key.dtype or value_cache.dtype != key_cache.dtype or (
+            not fp8 and key.dtype != key_cache.dtype):
+        raise ValueError("key/value and caches must share a dtype (or the caches be fp8)")
     if key.stride() != value.stride() or key.stride(-1) != 1:
         key, value = key.contiguous(), value.contiguous()
     if value_cache.stride() != key_cache.stride() or key_cache.stride(-1) != 1:
@@ -417,13 +478,18 @@ def reshape_and_cache(
     if slots.numel() < n:
         raise ValueError("slot_mapping must have one entry per token")
     cs = key_cache.stride()
-    rc = library().mxfa_reshape_and_cache_launch(
-        key.data_ptr(), value.data_ptr(), key.stride(0), key.stride(1), key_cache.data_ptr(),
-        value_cache.data_ptr(), cs[0], cs[1], cs[2], slots.data_ptr(), n, key.shape[1],
-        key.shape[2], key_cache.shape[1], key_cache.shape[0], _dtype_code(key),
-        _stream_handle(key.device),
-    )
-    _check(rc, "mxfa_reshape_and_cache_launch")
+    common = (key.data_ptr(), value.data_ptr(), key.stride(0), key.stride(1),
+              key_cache.data_ptr(), value_cache.data_ptr(), cs[0], cs[1], cs[2], slots.data_ptr(),
+              n, key.shape[1], key.shape[2], key_cache.shape[1], key_cache.shape[0],
+              _dtype_code(key))
+    if fp8:
+        rc = library().mxfa_reshape_and_cache_fp8_launch(
+            *common, _scale_ptr(k_scale, key.device, "k_scale"),
+            _scale_ptr(v_scale, key.device, "v_scale"), _stream_handle(key.device))
+        _check(rc, "mxfa_reshape_and_cache_fp8_launch")
+    else:
+        rc = library().mxfa_reshape_and_cache_launch(*common, _stream_handle(key.device))
+        _check(rc, "mxfa_reshape_and_cache_launch")
 
 
 def append_kv(

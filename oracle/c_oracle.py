@@ -40,6 +40,14 @@ def library() -> ctypes.CDLL:
         lib.oracle_append_kv_u16.restype = i
         lib.oracle_reshape_and_cache_u16.argtypes = [p, p, p, p, p, i, i, i, i, i]
         lib.oracle_reshape_and_cache_u16.restype = i
+        sz = ctypes.c_size_t
+        lib.oracle_e4m3fn_decode.argtypes = [p, p, sz]
+        lib.oracle_e4m3fn_decode.restype = i
+        lib.oracle_e4m3fn_encode.argtypes = [p, p, sz]
+        lib.oracle_e4m3fn_encode.restype = i
+        f = ctypes.c_float
+        lib.oracle_reshape_and_cache_fp8.argtypes = [p, p, i, f, f, p, p, p, i, i, i, i, i]
+        lib.oracle_reshape_and_cache_fp8.restype = i
         _lib = lib
     return _lib
 
@@ -102,3 +110,49 @@ def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Ten
                                            hkv, d, kc.shape[1], kc.shape[0])
     as_t = lambda a: torch.from_numpy(a.view(np.int16)).view(k_cache.dtype)
     return as_t(kc), as_t(vc)
+
+
+def _u8(t: torch.Tensor) -> np.ndarray:
+    return np.ascontiguousarray(t.detach().cpu().contiguous().view(torch.uint8).numpy())
+
+
+def e4m3fn_decode(codes: torch.Tensor) -> torch.Tensor:
+    """fp8 e4m3fn tensor (or its uint8 codes) -> float32, exact; NaN codes -> NaN."""
+    raw = _u8(codes)
+    out = np.empty(raw.shape, dtype=np.float32)
+    library().oracle_e4m3fn_decode(_ptr(raw), _ptr(out), raw.size)
+    return torch.from_numpy(out)
+
+
+def e4m3fn_encode(x: torch.Tensor) -> torch.Tensor:
+    """float32 -> e4m3fn codes (uint8): saturating, round to nearest even."""
+    xs = np.ascontiguousarray(x.detach().cpu().float().numpy())
+    out = np.empty(xs.shape, dtype=np.uint8)
+    library().oracle_e4m3fn_encode(_ptr(xs), _ptr(out), xs.size)
+    return torch.from_numpy(out)
+
+
+def paged_decode_fp8_f64(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                         block_table: torch.Tensor, seqlens: torch.Tensor, scale: float,
+                         k_scale: float, v_scale: float) -> np.ndarray:
+    """fp64 attention over an fp8 cache dequantised as k_scale*K, v_scale*V:
+    the exact fp8 values go to the fp64 oracle with scale*k_scale, and the
+    output is multiplied by v_scale (both in fp64)."""
+    kf = e4m3fn_decode(k_cache)
+    vf = e4m3fn_decode(v_cache)
+    out = paged_decode_f64(q, kf, vf, block_table, seqlens, float(scale) * float(k_scale))
+    return out * float(v_scale)
+
+
+def reshape_and_cache_fp8(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                          v_cache: torch.Tensor, slots: torch.Tensor, k_scale: float,
+                          v_scale: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """Slot-mapping append into copies of fp8 caches; returns the new caches (uint8 codes)."""
+    kk, vv = _u16(key), _u16(value)
+    kc, vc = _u8(k_cache).copy(), _u8(v_cache).copy()
+    sm = np.ascontiguousarray(slots.detach().cpu().to(torch.int64).numpy())
+    t, hkv, d = kk.shape
+    library().oracle_reshape_and_cache_fp8(_ptr(kk), _ptr(vv), int(key.dtype == torch.bfloat16),
+                                           float(k_scale), float(v_scale), _ptr(kc), _ptr(vc),
+                                           _ptr(sm), t, hkv, d, kc.shape[1], kc.shape[0])
+    return torch.from_numpy(kc), torch.from_numpy(vc)

@@ -243,8 +243,12 @@ def fake_cuda(t):
     (32, 16, 64, torch.float16, None),
     (32, 4, 128, torch.bfloat16, None),
     (32, 8, 256, torch.bfloat16, "head_dim_256"),
-    (24, 8, 128, torch.bfloat16, "gqa_ratio_24/8"),
-    (32, 32, 128, torch.bfloat16, "gqa_ratio_32/32"),
+    # Any 1..16 query heads per kv head runs on the kernels (GQ 3, 1, 16).
+    (24, 8, 128, torch.bfloat16, None),
+    (32, 32, 128, torch.bfloat16, None),
+    (64, 4, 64, torch.float16, None),
+    (34, 2, 128, torch.bfloat16, "gqa_ratio_34/2"),
+    (64, 2, 128, torch.bfloat16, "gqa_ratio_64/2"),
     (32, 8, 128, torch.float32, "supports_only_float16_and_bfloat16"),
 ])
 def test_kvcache_route_qualification(hq, hkv, hd, dtype, reason):

@@ -44,7 +44,7 @@ def test_library_loads_and_reports_header_abi(lib):
 
 def test_every_header_function_is_exported_and_bound(lib):
     declared = header_functions()
-    assert len(declared) == len(set(declared)) == 9
+    assert len(declared) == len(set(declared)) == 12
     for name in declared:
         assert hasattr(lib, name), name
     assert set(declared) == set(native.EXPORTED_SYMBOLS) == set(native._SIGNATURES)
@@ -68,7 +68,7 @@ def test_strerror_is_distinct_per_code(lib):
 
 def heuristic_closed_form(b, hq, hkv, hd, ps, btw, cus):
     # One wave per (kv head, range): a workgroup has max(4, min(HKV, 8 at HD64,
-    # 4 at HD128)) waves = min(HKV, waves) kv heads x waves // that sub-ranges,
+    # 4 at HD128 and HD256)) waves = min(HKV, waves) kv heads x waves // that sub-ranges,
     # one workgroup per CU.
     waves = max(4, min(hkv, 8 if hd == 64 else 4))
     kh = min(hkv, waves)
@@ -91,6 +91,9 @@ def heuristic_closed_form(b, hq, hkv, hd, ps, btw, cus):
     (4, 8, 2, 64, 16, 128, 256),       # config 1: two sub-ranges of two kv heads
     (32, 32, 8, 64, 16, 512, 256),     # GQ4 HD64: eight waves
     (8, 96, 12, 128, 16, 64, 256),
+    (32, 64, 4, 256, 16, 512, 256),    # HD256 GQ16
+    (16, 48, 16, 256, 16, 128, 256),   # HD256 GQ3
+    (32, 32, 32, 128, 16, 512, 256),   # GQ1: 32 kv heads, 8 workgroups per range
 ])
 def test_split_heuristic_closed_form(args):
     assert native.split_heuristic(*args) == heuristic_closed_form(*args)
@@ -144,7 +147,7 @@ def decode_args(**over):
     (dict(q=None), -2), (dict(k=None), -2), (dict(bt=None), -2), (dict(seqlens=None), -2),
     (dict(out=None), -2), (dict(batch=0), -2), (dict(ns=0), -2), (dict(seqlen_add=-1), -2),
     (dict(scale=float("nan")), -2), (dict(scale=float("inf")), -2),
-    (dict(hd=96), -1), (dict(hd=256), -1), (dict(hq=24), -1), (dict(hq=48, hkv=16), -1),
+    (dict(hd=96), -1), (dict(hd=192), -1), (dict(hd=512), -1), (dict(hq=136), -1),
     (dict(hq=36), -1), (dict(dtype=2), -1), (dict(ps=12), -1), (dict(ps=8192), -1),
     (dict(ns=70000), -1), (dict(batch=20000), -1), (dict(btw=1 << 27, ps=16), -1),
     (dict(q=FAKE + 2), -2), (dict(k=FAKE + 8), -2), (dict(q_sh=100), -2), (dict(c_st=1028), -2),
@@ -155,6 +158,31 @@ def decode_args(**over):
 def test_decode_launch_rejects_before_launching(lib, over, code):
     assert lib.mxfa_split_decode_launch(*decode_args(**over)) == code
     assert lib.mxfa_split_decode_partial_launch(*decode_args(**over)) == code
+    fp8 = decode_args(**over)
+    assert lib.mxfa_split_decode_fp8_launch(*fp8[:-1], FAKE, FAKE, None) == code
+    assert lib.mxfa_split_decode_fp8_partial_launch(*fp8[:-1], None, None, None) == code
+
+
+@pytest.mark.parametrize("over,code", [
+    # fp8 caches: byte strides must stay multiples of 16 (16 e4m3fn elements).
+    (dict(c_st=8 * 128 + 8), -2), (dict(c_sh=136), -2), (dict(c_sp=16 * 8 * 128 + 8), -2),
+    (dict(c_st=64), -2), (dict(hd=192), -1), (dict(ws_bytes=1000), -3),
+])
+def test_fp8_decode_launch_rejects_before_launching(lib, over, code):
+    args = decode_args(**over)[:-1]
+    assert lib.mxfa_split_decode_fp8_launch(*args, FAKE, FAKE, None) == code
+    assert lib.mxfa_split_decode_fp8_partial_launch(*args, FAKE, FAKE, None) == code
+
+
+def test_fp8_decode_rejects_misaligned_scale_pointers(lib):
+    args = decode_args()[:-1]
+    assert lib.mxfa_split_decode_fp8_launch(*args, FAKE + 2, FAKE, None) == -2
+    assert lib.mxfa_split_decode_fp8_launch(*args, FAKE, FAKE + 1, None) == -2
+    # 16-bit strides that are fine for 16-bit caches (8 elements) are not for
+    # fp8 caches (8 bytes).
+    odd = decode_args(c_st=8 * 128 + 8, ws_bytes=1000)
+    assert lib.mxfa_split_decode_launch(*odd) == -3  # strides pass, workspace fails
+    assert lib.mxfa_split_decode_fp8_launch(*odd[:-1], FAKE, FAKE, None) == -2
 
 
 def test_combine_rejects_before_launching(lib):
@@ -192,6 +220,27 @@ def test_append_entry_points_reject_before_launching(lib):
     assert rc == -2  # misaligned cache
 
 
+def test_fp8_append_rejects_before_launching(lib):
+    f = lib.mxfa_reshape_and_cache_fp8_launch
+    ok = (FAKE, FAKE, 1024, 128, FAKE, FAKE, 16384, 1024, 128, FAKE, 4, 8, 128, 16, 100, 1,
+          FAKE, FAKE, None)
+
+    def call(**over):
+        names = ("key", "value", "s_t", "s_h", "kc", "vc", "c_sp", "c_st", "c_sh", "slots", "n",
+                 "hkv", "hd", "ps", "pages", "dtype", "ks", "vs", "stream")
+        a = dict(zip(names, ok))
+        a.update(over)
+        return f(*a.values())
+
+    assert call(slots=None) == -2
+    assert call(hd=120) == -1           # not a multiple of 16
+    assert call(dtype=5) == -1
+    assert call(c_st=1032) == -2        # byte stride not a multiple of 16
+    assert call(kc=FAKE + 8) == -2
+    assert call(ks=FAKE + 2) == -2
+    assert call(n=0, slots=None) == 0   # nothing to write
+
+
 def test_empty_appends_are_no_ops(lib):
     assert lib.mxfa_reshape_and_cache_launch(FAKE, FAKE, 1024, 128, FAKE, FAKE, 16384, 1024,
                                              128, None, 0, 8, 128, 16, 100, 1, None) == 0
@@ -216,8 +265,8 @@ def test_python_layer_refuses_host_tensors():
 
 
 @pytest.mark.parametrize("hq,hkv,hd,dtype,ps,match", [
-    (8, 2, 96, torch.float16, 16, "head_dim"), (6, 2, 64, torch.float16, 16, "GQA"),
-    (16, 1, 64, torch.float16, 16, "GQA"), (8, 2, 64, torch.float32, 16, "float16"),
+    (8, 2, 96, torch.float16, 16, "head_dim"), (6, 4, 64, torch.float16, 16, "GQA"),
+    (34, 2, 64, torch.float16, 16, "GQA"), (8, 2, 64, torch.float32, 16, "float16"),
     (8, 2, 64, torch.float16, 12, "page size"),
 ])
 def test_python_shape_contract(hq, hkv, hd, dtype, ps, match):
@@ -225,3 +274,25 @@ def test_python_shape_contract(hq, hkv, hd, dtype, ps, match):
     cache = torch.zeros(4, ps, hkv, hd, dtype=dtype)
     with pytest.raises(native.UnsupportedConfig, match=match):
         native.check_decode_shapes(q, cache, cache)
+
+
+@pytest.mark.parametrize("hq,hkv,hd,cache_dtype", [
+    (6, 2, 64, torch.float16), (16, 1, 128, torch.bfloat16), (16, 16, 256, torch.bfloat16),
+    (32, 8, 128, torch.float8_e4m3fn), (12, 4, 256, torch.float8_e4m3fn),
+])
+def test_python_shape_contract_wider_than_the_reference(hq, hkv, hd, cache_dtype):
+    """GQ 1..16, HD 256 and fp8 caches pass the kernel contract."""
+    q = torch.zeros(2, 1, hq, hd, dtype=torch.bfloat16 if cache_dtype != torch.float16
+                    else torch.float16)
+    cache = torch.zeros(4, 16, hkv, hd, dtype=cache_dtype)
+    native.check_decode_shapes(q, cache, cache)
+
+
+def test_python_shape_contract_rejects_mixed_and_fnuz_caches():
+    q = torch.zeros(2, 1, 8, 64, dtype=torch.bfloat16)
+    fp8 = torch.zeros(4, 16, 2, 64, dtype=torch.float8_e4m3fn)
+    with pytest.raises(native.UnsupportedConfig):
+        native.check_decode_shapes(q, fp8, torch.zeros(4, 16, 2, 64, dtype=torch.bfloat16))
+    fnuz = torch.zeros(4, 16, 2, 64, dtype=torch.float8_e4m3fnuz)
+    with pytest.raises(native.UnsupportedConfig):
+        native.check_decode_shapes(q, fnuz, fnuz)

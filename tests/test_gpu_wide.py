@@ -1,0 +1,228 @@
+"""GPU parity of the kernel contract beyond the reference's: 1..16 query heads
+per kv head, head dim 256, and fp8 (OCP e4m3fn) KV caches with per-tensor
+scales, through the C ABI.
+
+Oracles: the fp64 C oracle (oracle/decode_ref.c) on the same inputs; for fp8
+caches, on the exactly decoded e4m3fn values with scale*k_scale and the output
+times v_scale in fp64 (c_oracle.paged_decode_fp8_f64). Tolerances as for the
+16-bit path: max-abs <= 2e-3 (fp16), <= 1.6e-2 (bf16), with v_scale <= 1 so
+the outputs keep the magnitude of N(0, 1) rows. The fp8 append is bit-exact
+against oracle_reshape_and_cache_fp8.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from mxflashattn_amd import native
+from mxflashattn_amd.workloads import make_paged_batch
+from oracle import c_oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float16: 2e-3, torch.bfloat16: 1.6e-2}
+FP8 = torch.float8_e4m3fn
+
+
+def f64_expected(b) -> torch.Tensor:
+    out = c_oracle.paged_decode_f64(b.q.cpu(), b.k_cache.cpu(), b.v_cache.cpu(),
+                                    b.block_table.cpu(), b.cache_seqlens.cpu(), b.scale)
+    return torch.from_numpy(out).reshape(b.q.shape)
+
+
+def max_err(actual: torch.Tensor, expected: torch.Tensor) -> float:
+    return (actual.double().cpu() - expected.double().cpu()).abs().max().item()
+
+
+def decode(b, k_cache=None, v_cache=None, **kw) -> torch.Tensor:
+    out = native.paged_decode_split(b.q, b.k_cache if k_cache is None else k_cache,
+                                    b.v_cache if v_cache is None else v_cache, b.block_table,
+                                    b.cache_seqlens, b.scale, **kw)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("gq", [1, 3, 5, 6, 7, 12, 16])
+def test_group_sizes_and_head_dims(device, dtype, head_dim, gq):
+    lengths = torch.tensor([1, 17, 300, 0, 1000])
+    b = make_paged_batch(5, 2 * gq, 2, head_dim, dtype, lengths, seed=30 + gq).to(device)
+    expected = f64_expected(b)
+    for ns in (None, 1, 7, 64):
+        kw = {} if ns is None else dict(num_splits=ns)
+        got = decode(b, **kw)
+        assert torch.isfinite(got.float()).all()
+        assert max_err(got, expected) <= TOL[dtype], (ns, max_err(got, expected))
+        assert torch.equal(got[3].cpu(), torch.zeros_like(got[3].cpu()))  # empty sequence
+
+
+@pytest.mark.parametrize("page_size", [1, 4, 64])
+@pytest.mark.parametrize("gq", [2, 8, 16])
+def test_head_dim_256_page_sizes(device, page_size, gq):
+    lengths = torch.tensor([3, 129, 517])
+    b = make_paged_batch(3, 2 * gq, 2, 256, torch.bfloat16, lengths, page_size=page_size,
+                         seed=7).to(device)
+    expected = f64_expected(b)
+    assert max_err(decode(b), expected) <= TOL[torch.bfloat16]
+    assert max_err(decode(b, num_splits=12), expected) <= TOL[torch.bfloat16]
+
+
+def test_many_kv_heads_one_query_head_each(device):
+    # GQ 1 with 32 kv heads: 8 workgroups of 4 kv heads per range.
+    b = make_paged_batch(4, 32, 32, 128, torch.float16, torch.tensor([40, 700, 1, 2500]),
+                         seed=12).to(device)
+    assert max_err(decode(b), f64_expected(b)) <= TOL[torch.float16]
+
+
+def test_head_dim_256_config2_lengths(device):
+    # A Gemma-like decode layer: B = 32, 16 q / 8 kv heads of 256, L ~ U[1024, 8192].
+    b = make_paged_batch(32, 16, 8, 256, torch.bfloat16, (1024, 8192), seed=20261007).to(device)
+    assert max_err(decode(b), f64_expected(b)) <= TOL[torch.bfloat16]
+
+
+# ---------------------------------------------------------------------------
+# fp8 caches
+
+
+def fp8_caches(b, device):
+    return (b.k_cache.cpu().to(FP8).to(device), b.v_cache.cpu().to(FP8).to(device))
+
+
+def fp8_expected(b, k8, v8, k_scale, v_scale) -> torch.Tensor:
+    out = c_oracle.paged_decode_fp8_f64(b.q.cpu(), k8.cpu(), v8.cpu(), b.block_table.cpu(),
+                                        b.cache_seqlens.cpu(), b.scale, k_scale, v_scale)
+    return torch.from_numpy(out).reshape(b.q.shape)
+
+
+def scalar(x: float, device) -> torch.Tensor:
+    return torch.tensor([x], dtype=torch.float32, device=device)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("gq", [1, 2, 4, 8, 16])
+def test_fp8_cache_matches_oracle(device, dtype, head_dim, gq):
+    lengths = torch.tensor([1, 16, 33, 0, 700, 2000])
+    b = make_paged_batch(6, 2 * gq, 2, head_dim, dtype, lengths, seed=50 + gq).to(device)
+    k8, v8 = fp8_caches(b, device)
+    expected = fp8_expected(b, k8, v8, 2.0, 0.5)
+    ks, vs = scalar(2.0, device), scalar(0.5, device)
+    for ns in (None, 1, 5, 40):
+        kw = {} if ns is None else dict(num_splits=ns)
+        got = decode(b, k8, v8, k_scale=ks, v_scale=vs, **kw)
+        assert torch.isfinite(got.float()).all()
+        assert max_err(got, expected) <= TOL[dtype], (ns, max_err(got, expected))
+        assert torch.equal(got[3].cpu(), torch.zeros_like(got[3].cpu()))
+
+
+@pytest.mark.parametrize("page_size", [1, 8, 32])
+def test_fp8_small_and_large_pages(device, page_size):
+    b = make_paged_batch(3, 8, 2, 128, torch.bfloat16, torch.tensor([5, 200, 999]),
+                         page_size=page_size, seed=8).to(device)
+    k8, v8 = fp8_caches(b, device)
+    got = decode(b, k8, v8)  # no scales: 1.0
+    assert max_err(got, fp8_expected(b, k8, v8, 1.0, 1.0)) <= TOL[torch.bfloat16]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+def test_fp8_single_token_returns_every_code_exactly(device, dtype):
+    """One key: the output is v_scale * V row, and every finite e4m3fn value is
+    exact in fp16 and bf16, so the widening of V is checked code by code."""
+    codes = torch.arange(256, dtype=torch.uint8)
+    finite = codes[(codes & 0x7F) != 0x7F]  # 254 codes
+    hd = 128
+    rows = -(-finite.numel() // hd)
+    b = make_paged_batch(rows, 4, 2, hd, dtype, 1, seed=1)
+    v = torch.zeros(b.v_cache.shape, dtype=torch.uint8)
+    pattern = torch.cat([finite, finite[: rows * hd - finite.numel()]]).view(rows, hd)
+    for i in range(rows):
+        page = int(b.block_table[i, 0])
+        v[page, 0, :, :] = pattern[i]
+    b = b.to(device)
+    k8 = b.k_cache.cpu().to(FP8).to(device)
+    v8 = v.view(FP8).to(device)
+    got = decode(b, k8, v8).cpu()
+    want = c_oracle.e4m3fn_decode(pattern).to(dtype)
+    for i in range(rows):
+        for h in range(4):
+            assert torch.equal(got[i, 0, h], want[i]), (i, h)
+
+
+def test_fp8_scales_are_read_at_run_time_in_a_graph(device):
+    b = make_paged_batch(4, 16, 4, 128, torch.bfloat16, torch.tensor([10, 300, 77, 1200]),
+                         seed=21).to(device)
+    k8, v8 = fp8_caches(b, device)
+    ks, vs = scalar(1.0, device), scalar(1.0, device)
+    out = torch.empty_like(b.q)
+    stream = torch.cuda.Stream(device)
+    with torch.cuda.stream(stream):
+        decode(b, k8, v8, k_scale=ks, v_scale=vs, out=out)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        native.paged_decode_split(b.q, k8, v8, b.block_table, b.cache_seqlens, b.scale, out=out,
+                                  k_scale=ks, v_scale=vs)
+    for kx, vx in ((1.0, 1.0), (0.5, 0.25), (3.0, 1.0)):
+        ks.fill_(kx)
+        vs.fill_(vx)
+        with torch.cuda.stream(stream):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert max_err(out, fp8_expected(b, k8, v8, kx, vx)) <= TOL[torch.bfloat16], (kx, vx)
+        eager = decode(b, k8, v8, k_scale=ks, v_scale=vs)
+        assert torch.equal(out.cpu(), eager.cpu())
+
+
+def fp8_append_inputs(dtype, scale: float, seed: int):
+    """Rows mixing every regime of the conversion: N(0, 1), values beyond the
+    saturation point, e4m3fn subnormals, exact rounding ties and zeros."""
+    g = torch.Generator().manual_seed(seed)
+    t, hkv, hd = 40, 2, 128
+    x = torch.randn(t, hkv, hd, generator=g)
+    x[0] *= 1000.0                        # saturates to +-448
+    x[1] *= 1e-3                          # subnormal codes
+    grid = c_oracle.e4m3fn_decode(torch.arange(0, 126, dtype=torch.uint8)).double()
+    mids = ((grid[1:] + grid[:-1]) / 2).float()  # exact ties in fp32
+    x[2].view(-1)[: mids.numel()] = mids
+    x[3] = 0.0
+    x[4].view(-1)[::2] = -x[4].view(-1)[::2]
+    # Pre-scale so that x / scale hits the intended values (scale a power of two).
+    x = (x * scale).to(dtype)
+    return x
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("k_scale,v_scale", [(1.0, 1.0), (0.25, 4.0), (0.1, 3.0)])
+def test_fp8_reshape_and_cache_bit_exact(device, dtype, k_scale, v_scale):
+    key = fp8_append_inputs(dtype, k_scale, 3)
+    value = fp8_append_inputs(dtype, v_scale, 4)
+    pages, ps = 8, 16
+    k_cache = torch.randint(0, 256, (pages, ps, 2, 128), dtype=torch.uint8)
+    v_cache = torch.randint(0, 256, (pages, ps, 2, 128), dtype=torch.uint8)
+    slots = torch.randperm(pages * ps)[: key.shape[0]]
+    slots[5] = -1  # skipped
+    want_k, want_v = c_oracle.reshape_and_cache_fp8(key, value, k_cache, v_cache, slots,
+                                                    k_scale, v_scale)
+    kc, vc = k_cache.view(FP8).to(device), v_cache.view(FP8).to(device)
+    native.reshape_and_cache(key.to(device), value.to(device), kc, vc, slots.to(device),
+                             k_scale=scalar(k_scale, device), v_scale=scalar(v_scale, device))
+    torch.cuda.synchronize()
+    assert torch.equal(kc.cpu().view(torch.uint8), want_k)
+    assert torch.equal(vc.cpu().view(torch.uint8), want_v)
+
+
+def test_fp8_reshape_and_cache_keeps_nan_and_saturates_inf(device):
+    key = torch.zeros(2, 1, 16, dtype=torch.bfloat16)
+    key[0, 0, :4] = torch.tensor([float("nan"), float("inf"), -float("inf"), -0.0])
+    cache = torch.zeros(1, 16, 1, 16, dtype=torch.uint8).view(FP8).to(device)
+    vcache = cache.clone()
+    native.reshape_and_cache(key.to(device), key.to(device), cache, vcache,
+                             torch.tensor([0, 1], device=device))
+    torch.cuda.synchronize()
+    row = cache.cpu().view(torch.uint8)[0, 0, 0]
+    assert int(row[0]) & 0x7F == 0x7F  # NaN stays NaN
+    assert int(row[1]) == 0x7E and int(row[2]) == 0xFE  # +-448
+    assert int(row[3]) == 0x80  # -0

@@ -26,6 +26,14 @@ checks that a plausible mistake would fail:
   split_model
     - the LSE merge of any split of the keys, empty splits included, equals
       unsplit attention (the invariant behind csrc_native/m1_kernel.cpp:861-888)
+  c_oracle.e4m3fn_decode / e4m3fn_encode (fp8 caches; no reference counterpart)
+    - decode of all 256 codes equals torch's float8_e4m3fn -> float32
+    - encode equals torch's round-to-nearest-even conversion on in-range values,
+      exact midpoints (ties) included, and is the nearest finite code by brute
+      force; saturation to +-448 and NaN are fixed by hand-picked cases
+  c_oracle.reshape_and_cache_fp8 / paged_decode_fp8_f64
+    - the append equals torch index assignment of (x / scale).to(e4m3fn)
+    - fp8 decode equals the fp64 oracle on caches dequantised exactly
 """
 
 from __future__ import annotations
@@ -316,3 +324,85 @@ def test_split_model_matches_fp64_oracle():
     outs, lse = split_model.split_partials(b.q[0, 0, 0].double().numpy(), keys, vals, b.scale,
                                            64, 6)
     assert np.abs(split_model.lse_combine(outs, lse) - f64[0, 0]).max() < 1e-12
+
+
+FP8 = torch.float8_e4m3fn
+
+
+def test_e4m3fn_decode_matches_torch_for_every_code():
+    codes = torch.arange(256, dtype=torch.uint8)
+    mine = c_oracle.e4m3fn_decode(codes)
+    ref = codes.view(FP8).float()
+    assert torch.equal(torch.isnan(mine), torch.isnan(ref))
+    assert torch.isnan(mine).sum() == 2  # S.1111.111 only
+    ok = ~torch.isnan(ref)
+    assert torch.equal(mine[ok], ref[ok])
+    assert mine[0x7E] == 448.0 and mine[0x01] == 2.0 ** -9 and mine[0x08] == 2.0 ** -6
+
+
+def test_e4m3fn_encode_rounds_to_nearest_even_like_torch():
+    g = torch.Generator().manual_seed(0)
+    x = torch.cat([torch.randn(50000, generator=g) * s for s in (1e-3, 0.05, 1.0, 30.0, 150.0)])
+    x = x[x.abs() < 448]
+    assert torch.equal(c_oracle.e4m3fn_encode(x), x.to(FP8).view(torch.uint8))
+    # Exact midpoints between neighbouring codes: ties go to the even code.
+    grid = c_oracle.e4m3fn_decode(torch.arange(0, 127, dtype=torch.uint8)).double()
+    mids = ((grid[1:] + grid[:-1]) / 2).float()
+    mids = torch.cat([mids, -mids])
+    got = c_oracle.e4m3fn_encode(mids)
+    assert torch.equal(got, mids.to(FP8).view(torch.uint8))
+    assert ((got & 1) == 0).all()
+
+
+def test_e4m3fn_encode_is_the_nearest_code_by_brute_force():
+    finite = torch.arange(256, dtype=torch.uint8)
+    finite = finite[(finite & 0x7F) != 0x7F]
+    values = c_oracle.e4m3fn_decode(finite).double()
+    g = torch.Generator().manual_seed(1)
+    x = (torch.rand(4000, generator=g, dtype=torch.float64) * 2 - 1) * 440
+    x = torch.cat([x, x * 1e-3]).float()
+    got = c_oracle.e4m3fn_encode(x)
+    dist = (x.double()[:, None] - values[None, :]).abs()
+    best = dist.min(dim=1).values
+    mine = (x.double() - c_oracle.e4m3fn_decode(got).double()).abs()
+    assert torch.equal(mine, best)
+
+
+def test_e4m3fn_encode_saturates_and_keeps_nan():
+    x = torch.tensor([448.0, 449.0, 464.0, 500.0, 1e9, float("inf"), -float("inf"), -1e9,
+                      float("nan"), -0.0, 0.0, 2.0 ** -10, 2.0 ** -10 * 3])
+    got = c_oracle.e4m3fn_encode(x).tolist()
+    assert got[:8] == [0x7E, 0x7E, 0x7E, 0x7E, 0x7E, 0x7E, 0xFE, 0xFE]
+    assert got[8] & 0x7F == 0x7F
+    assert got[9:] == [0x80, 0x00, 0x00, 0x02]  # 2^-10 ties to 0; 1.5 * 2^-9 ties to 2
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fp8_append_oracle_is_scaled_index_assignment(dtype):
+    g = torch.Generator().manual_seed(2)
+    key = (torch.randn(12, 2, 64, generator=g) * 3).to(dtype)
+    value = (torch.randn(12, 2, 64, generator=g) * 3).to(dtype)
+    k_cache = torch.randint(0, 256, (5, 4, 2, 64), generator=g, dtype=torch.uint8)
+    v_cache = torch.randint(0, 256, (5, 4, 2, 64), generator=g, dtype=torch.uint8)
+    slots = torch.randperm(20, generator=g)[:12]
+    slots[3] = -1
+    ks, vs = 0.1, 0.75
+    got_k, got_v = c_oracle.reshape_and_cache_fp8(key, value, k_cache, v_cache, slots, ks, vs)
+    want_k, want_v = k_cache.clone(), v_cache.clone()
+    keep = slots >= 0
+    pg, off = slots[keep] // 4, slots[keep] % 4
+    want_k[pg, off] = (key[keep].float() / ks).clamp(-448, 448).to(FP8).view(torch.uint8)
+    want_v[pg, off] = (value[keep].float() / vs).clamp(-448, 448).to(FP8).view(torch.uint8)
+    assert torch.equal(got_k, want_k) and torch.equal(got_v, want_v)
+
+
+def test_fp8_decode_oracle_equals_fp64_oracle_on_dequantised_caches():
+    b = make_paged_batch(3, 8, 2, 64, torch.float32, torch.tensor([1, 50, 300]), seed=16)
+    k8, v8 = b.k_cache.to(FP8), b.v_cache.to(FP8)
+    got = c_oracle.paged_decode_fp8_f64(b.q, k8, v8, b.block_table, b.cache_seqlens, b.scale,
+                                        2.0, 0.5)
+    # Powers of two: the dequantised caches are exact in float32.
+    kf = c_oracle.e4m3fn_decode(k8) * 2.0
+    vf = c_oracle.e4m3fn_decode(v8) * 0.5
+    want = c_oracle.paged_decode_f64(b.q, kf, vf, b.block_table, b.cache_seqlens, b.scale)
+    assert np.abs(got - want).max() < 1e-12

@@ -148,6 +148,44 @@ def test_registration_reports_missing_vllm():
         assert result["reason"].startswith("vllm_v1_api_unavailable")
 
 
-def test_reshape_and_cache_flash_rejects_fp8_caches():
-    with pytest.raises(NotImplementedError, match="fp8"):
-        native_decode.reshape_and_cache_flash(None, None, None, None, torch.zeros(1), "fp8")
+def test_reshape_and_cache_flash_cache_dtypes():
+    # Other quantised formats are not supported.
+    with pytest.raises(NotImplementedError, match="fp8_e5m2"):
+        native_decode.reshape_and_cache_flash(None, None, None, None, torch.zeros(1), "fp8_e5m2")
+    # "fp8" needs e4m3fn caches (or their uint8 codes).
+    k = torch.zeros(2, 2, 64, dtype=torch.bfloat16)
+    cache = torch.zeros(4, 16, 2, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="uint8/e4m3fn"):
+        native_decode.reshape_and_cache_flash(k, k, cache, cache, torch.zeros(2), "fp8")
+    # uint8 caches are viewed as e4m3fn; host tensors are then refused.
+    codes = torch.zeros(4, 16, 2, 64, dtype=torch.uint8)
+    with pytest.raises(ValueError, match="GPU tensors"):
+        native_decode.reshape_and_cache_flash(k, k, codes, codes, torch.zeros(2), "fp8")
+
+
+def test_guard_wide_contract_opt_in(monkeypatch):
+    """The reference's guards by default; MXFA_WIDE_CONTRACT=1 widens them to
+    head dim 256, GQ 1..16 and fp8 caches with per-tensor descales."""
+    def call(hq, hkv, hd, cache_dtype=torch.bfloat16, descale=None):
+        q = torch.empty(4, 1, hq, hd, dtype=torch.bfloat16)
+        cache = torch.empty(10, 16, hkv, hd, dtype=cache_dtype)
+        kwargs = {"k_cache": cache, "v_cache": cache, "block_table": torch.zeros(4, 2),
+                  "cache_seqlens": torch.ones(4)}
+        wide = native_decode.wide_contract()
+        return native_decode._guard((q,), kwargs, wide, (descale, descale))[0]
+
+    monkeypatch.delenv("MXFA_WIDE_CONTRACT", raising=False)
+    assert call(16, 4, 256) == "head_dim"
+    assert call(24, 8, 128) == "gqa_ratio"
+    assert call(32, 8, 128, torch.float8_e4m3fn) == "dtype"
+    monkeypatch.setenv("MXFA_WIDE_CONTRACT", "1")
+    # Host tensors get as far as the device check: every shape guard passed.
+    assert call(16, 4, 256) == "device"
+    assert call(24, 8, 128) == "device"
+    assert call(8, 8, 64) == "device"
+    assert call(32, 8, 128, torch.float8_e4m3fn) == "device"
+    scalar = torch.ones(1, dtype=torch.float32).expand(4, 8)
+    assert call(32, 8, 128, torch.float8_e4m3fn, scalar) == "device"
+    assert call(32, 8, 128, torch.float8_e4m3fn, torch.ones(4, 8)) == "descale_not_per_tensor"
+    assert call(34, 2, 128) == "gqa_ratio"
+    assert call(32, 8, 96) == "head_dim"
