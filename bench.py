@@ -1,9 +1,10 @@
 #!/usr/bin/env python3
 """Decode-attention benchmark on one MI355X (BASELINE.json metric).
 
-One step = one split-KV paged decode call (a single fused kernel: split
-partials plus their LSE merge) over the whole synthetic batch of the named
-workload, inputs already resident in HBM. The KV pool is rotated across copies
+One step = one split-KV paged decode call (two kernels: the split partial
+kernel, then the LSE combine of the sequences that cross a work-range end)
+over the whole synthetic batch of the named workload, inputs already resident
+in HBM. The KV pool is rotated across copies
 totalling >= 1 GB so the 256 MB Infinity Cache cannot serve repeated reads.
 Prints ONE JSON line:
 
@@ -18,9 +19,12 @@ Prints ONE JSON line:
   cpu_baseline fp32 torch-CPU restatement of reference.attention_kvcache
                (oracle.reference_port) on the host cores, bounded sample
   cells        the six GQ x HD cells of config 2 and configs 1, 3, 4
+  wide         shapes beyond the reference's contract at config 2's batch and
+               lengths: fp8 (e4m3fn) caches, head dim 256, GQ 1 and 16
   decode_step  config 5: decode tok/s of a 36-layer random-init Qwen3-4B-shaped
                model whose attention runs through the vLLM backend path
-               (HIP-graph replayed steps), and attention's share of the step
+               (HIP-graph replayed steps), and attention's share of the step;
+               decode_step_fp8 is the same step with an fp8 KV cache
 """
 
 from __future__ import annotations
@@ -54,6 +58,8 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--no-cells", action="store_true", help="skip the per-cell table")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode-step", action="store_true", help="skip config 5")
+    ap.add_argument("--no-wide", action="store_true",
+                    help="skip the shapes beyond the reference's contract")
     ap.add_argument("--cpu-reps", type=int, default=15)
     return ap.parse_args()
 
@@ -221,18 +227,18 @@ def main() -> int:
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported on this build "
-              "(the decode path shards by sequence or kv head with no exchange; see DESIGN.md)",
-              file=sys.stderr)
+              "(decode attention shards by sequence or kv head with no exchange, so the "
+              "one-GPU figure is the per-GPU share)", file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
     from mxflashattn_amd import native
-    from mxflashattn_amd.workloads import CELLS, CONFIGS, DEFAULT_SEED
+    from mxflashattn_amd.workloads import CELLS, CONFIGS, DEFAULT_SEED, WIDE
 
     native.library()  # fail loudly when the HIP library is missing
     device = torch.device("cuda", 0)
-    spec = {**CONFIGS, **CELLS}[args.workload]
+    spec = {**CONFIGS, **CELLS, **WIDE}[args.workload]
     print(f"[bench] workload {args.workload}: steps={args.steps} warmup={args.warmup}",
           file=sys.stderr, flush=True)
     main_res = measure_workload(args.workload, spec, device, args.steps, args.warmup)
@@ -246,6 +252,12 @@ def main() -> int:
             cells[name] = measure_workload(name, cspec, device, 100, 10)
             print(f"[bench] {name}: {cells[name]}", file=sys.stderr, flush=True)
 
+    wide = {}
+    if not args.no_wide:
+        for name, wspec in WIDE.items():
+            wide[name] = measure_workload(name, wspec, device, 100, 10)
+            print(f"[bench] {name}: {wide[name]}", file=sys.stderr, flush=True)
+
     decode = None
     if not args.no_decode_step:
         from mxflashattn_amd.integrations.vllm import decode_step
@@ -257,6 +269,16 @@ def main() -> int:
             print(f"[bench] config5 decode step failed: {exc!r}", file=sys.stderr, flush=True)
             decode = {"error": repr(exc)}
         print(f"[bench] config5: {decode}", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+    decode_fp8 = None
+    if not args.no_decode_step and not args.no_wide:
+        print("[bench] config5 decode step, fp8 KV cache", file=sys.stderr, flush=True)
+        try:
+            decode_fp8 = decode_step.run(device=device, kv_cache_dtype="fp8")
+        except Exception as exc:
+            print(f"[bench] fp8 decode step failed: {exc!r}", file=sys.stderr, flush=True)
+            decode_fp8 = {"error": repr(exc)}
+        print(f"[bench] config5 fp8: {decode_fp8}", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
 
     cpu = None
@@ -303,7 +325,9 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
         "cells": cells,
+        "wide": wide,
         "decode_step": decode,
+        "decode_step_fp8": decode_fp8,
     }
     print(json.dumps(line))
     return 0

@@ -66,6 +66,15 @@ int mxfa_split_heuristic(int batch, int q_heads, int kv_heads, int head_dim, int
                          int block_table_width, int num_cus, int *num_splits);
 
 /*
+ * Split count for mxfa_split_decode_fp8_launch (same arguments as
+ * mxfa_split_heuristic). The launch shape follows the bytes of one head row,
+ * so an fp8 cache with head dim HD is sized like a 16-bit cache with HD/2.
+ * No reference counterpart (the reference has no fp8 cache).
+ */
+int mxfa_split_heuristic_fp8(int batch, int q_heads, int kv_heads, int head_dim, int page_size,
+                             int block_table_width, int num_cus, int *num_splits);
+
+/*
  * Bytes of caller-owned workspace the split launch needs. Replaces the
  * per-call at::empty of ows/mdws at csrc_native/m1_binding.cpp:94-96. Layout:
  * piece outputs fp32 [HKV, num_splits, 2, GQ, HD], piece base-2 LSEs fp32
@@ -151,7 +160,7 @@ int mxfa_split_decode_combine_launch(void *workspace, size_t workspace_bytes, vo
  * Uses the same workspace size and combine as the 16-bit launch.
  * No reference counterpart: the reference has no fp8 cache
  * (docs/support-matrix.md:27). For callers with an fp8 vLLM cache
- * (kv_cache_dtype "fp8"/"fp8_e4m3").
+ * (kv_cache_dtype "fp8"/"fp8_e4m3"); num_splits from mxfa_split_heuristic_fp8.
  */
 int mxfa_split_decode_fp8_launch(const void *q, int64_t q_stride_b, int64_t q_stride_h,
                                  const void *k_cache, const void *v_cache,

@@ -143,7 +143,7 @@ static DecodeParams make_params(const SplitArgs &a, const Grid &g) {
 }
 
 static int launch_partial(const SplitArgs &a, hipStream_t st) {
-  const Grid g = grid_for(a.hkv, a.num_splits, waves_for(a.hd, a.hkv));
+  const Grid g = grid_for(a.hkv, a.num_splits, waves_for(a.hd * (a.fp8 ? 1 : 2), a.hkv));
   const DecodeParams p = make_params(a, g);
   switch (a.hd) {
     case 64: return launch_partial_64(p, g, a.dtype, a.fp8, st);
@@ -248,6 +248,26 @@ static SplitArgs fp8_args(SplitArgs a, const float *k_scale, const float *v_scal
   return a;
 }
 
+static int split_heuristic(int batch, int q_heads, int kv_heads, int head_dim, int elem_bytes,
+                           int page_size, int block_table_width, int num_cus, int *num_splits) {
+  if (!num_splits) return MXFA_EINVAL;
+  if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || page_size <= 0 ||
+      block_table_width <= 0 || num_cus <= 0)
+    return MXFA_EINVAL;
+  // One range per wave: one workgroup (waves_for waves) fills every CU, and
+  // each wave streams one (kv head, range). The kernel lowers the count to the
+  // real tile total on the device.
+  const Grid g = grid_for(kv_heads, 1, waves_for(head_dim * elem_bytes, kv_heads));
+  int64_t n = (int64_t)num_cus * g.subs / g.gx;
+  const int64_t cap = (int64_t)block_table_width * page_size;
+  const int64_t cap_tiles = (int64_t)batch * ((cap + kTile - 1) / kTile);
+  if (n > cap_tiles) n = cap_tiles;
+  if (n < 1) n = 1;
+  if (n > 65535) n = 65535;
+  *num_splits = (int)n;
+  return MXFA_OK;
+}
+
 }  // namespace mxfa
 
 using namespace mxfa;
@@ -270,22 +290,14 @@ const char *mxfa_strerror(int code) {
 
 int mxfa_split_heuristic(int batch, int q_heads, int kv_heads, int head_dim, int page_size,
                          int block_table_width, int num_cus, int *num_splits) {
-  if (!num_splits) return MXFA_EINVAL;
-  if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || page_size <= 0 ||
-      block_table_width <= 0 || num_cus <= 0)
-    return MXFA_EINVAL;
-  // One range per wave: one workgroup (waves_for waves) fills every CU, and
-  // each wave streams one (kv head, range). The kernel lowers the count to the
-  // real tile total on the device.
-  const Grid g = grid_for(kv_heads, 1, waves_for(head_dim, kv_heads));
-  int64_t n = (int64_t)num_cus * g.subs / g.gx;
-  const int64_t cap = (int64_t)block_table_width * page_size;
-  const int64_t cap_tiles = (int64_t)batch * ((cap + kTile - 1) / kTile);
-  if (n > cap_tiles) n = cap_tiles;
-  if (n < 1) n = 1;
-  if (n > 65535) n = 65535;
-  *num_splits = (int)n;
-  return MXFA_OK;
+  return split_heuristic(batch, q_heads, kv_heads, head_dim, 2, page_size, block_table_width,
+                         num_cus, num_splits);
+}
+
+int mxfa_split_heuristic_fp8(int batch, int q_heads, int kv_heads, int head_dim, int page_size,
+                             int block_table_width, int num_cus, int *num_splits) {
+  return split_heuristic(batch, q_heads, kv_heads, head_dim, 1, page_size, block_table_width,
+                         num_cus, num_splits);
 }
 
 int mxfa_split_decode_workspace_size(int batch, int q_heads, int head_dim, int num_splits,

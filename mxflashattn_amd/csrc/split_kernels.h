@@ -869,22 +869,29 @@ __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(CombineP
 // ---------------------------------------------------------------------------
 // Launch shapes (host side, shared by the per-head-dim compilation units).
 
+// Launch shape by the bytes of one K (or V) head row, RB = HD * element size:
+// 64 (fp8 HD 64), 128 (16-bit HD 64, fp8 HD 128), 256 (16-bit HD 128, fp8
+// HD 256) or 512 (16-bit HD 256).
+template <int HD, bool kF8>
+constexpr int kRowBytes = HD * (kF8 ? 1 : 2);
+
 // Waves per workgroup: one wave per kv head (KH = min(HKV, max) kv heads per
 // workgroup), at least 4 waves (S = 4 / KH sub-ranges when HKV < 4), at most
-// 8 at HD 64 and 4 at HD 128 and 256; one workgroup per CU. Measured on MI355X
-// (one call, config-2 lengths): at HD 128 eight-wave workgroups run as two
-// generations of four waves per CU (the second wave on each SIMD issues its
-// first loads only when the first finishes, since four waves already fill
-// the CU's vector-memory queue), which leaves a drain tail: four-wave
-// workgroups are 3% (GQ4) to 10% (GQ8) faster. At HD 64 all eight waves run
-// together; eight beat four by 2-3% at 8 kv heads, four beat two sub-ranges of
-// eight by 10% at 4 kv heads; two workgroups per CU lose 2-15% everywhere.
-template <int HD>
-constexpr int kMaxWaves = HD == 64 ? 8 : 4;
+// 8 for rows of up to 128 bytes and 4 for longer rows; one workgroup per CU.
+// Measured on MI355X (one call, config-2 lengths): with 256-byte rows
+// eight-wave workgroups run as two generations of four waves per CU (the
+// second wave on each SIMD issues its first loads only when the first
+// finishes, since four waves already fill the CU's vector-memory queue), which
+// leaves a drain tail: four-wave workgroups are 3% (GQ4) to 10% (GQ8) faster.
+// With 128-byte rows all eight waves run together: eight beat four by 2-3%
+// (16-bit HD 64) and 15% (fp8 HD 128) at 8 kv heads; four beat two sub-ranges
+// of eight by 10% at 4 kv heads; two workgroups per CU lose 2-15% everywhere.
 constexpr int kMinWaves = 4;
+template <int HD, bool kF8>
+constexpr int kMaxWaves = kRowBytes<HD, kF8> <= 128 ? 8 : 4;
 
-inline int waves_for(int hd, int hkv) {
-  const int most = hd == 64 ? kMaxWaves<64> : kMaxWaves<128>;
+inline int waves_for(int row_bytes, int hkv) {
+  const int most = row_bytes <= 128 ? 8 : 4;
   const int kh = hkv < most ? hkv : most;
   return kh >= kMinWaves ? kh : kMinWaves;
 }
@@ -899,10 +906,11 @@ inline Grid grid_for(int hkv, int num_splits, int waves) {
   return g;
 }
 
-// Register sets of the tile pipeline: HD 64 tiles are half the bytes, so a
-// third set keeps as many bytes in flight per wave as HD 128 does with two.
-template <int HD>
-constexpr int kNbuf = HD == 64 ? 3 : 2;
+// Register sets of the tile pipeline: tiles of 128-byte rows are half the
+// bytes of 256-byte ones, so a third set keeps as many bytes in flight per
+// wave; 64-byte rows (fp8 HD 64) take a fourth.
+template <int HD, bool kF8>
+constexpr int kNbuf = kRowBytes<HD, kF8> <= 64 ? 4 : kRowBytes<HD, kF8> <= 128 ? 3 : 2;
 
 // Head rows of the MFMA layout for a group size (GQ <= 4 per row).
 inline int head_rows(int gq) { return gq <= 4 ? 1 : gq <= 8 ? 2 : 4; }
@@ -912,8 +920,8 @@ static int launch_partial_w(const DecodeParams &p, const Grid &g, hipStream_t st
   dim3 grid(g.gx, g.gy);
   const size_t lds = (size_t)(p.batch + 1) * sizeof(int32_t);
   if (p.ps_log2 >= 4)
-    hipLaunchKernelGGL((split_partial_kernel<HD, HR, T, kF8, false, kNbuf<HD>, WAVES>), grid,
-                       dim3(WAVES * 64), lds, st, p);
+    hipLaunchKernelGGL((split_partial_kernel<HD, HR, T, kF8, false, kNbuf<HD, kF8>, WAVES>),
+                       grid, dim3(WAVES * 64), lds, st, p);
   else
     hipLaunchKernelGGL((split_partial_kernel<HD, HR, T, kF8, true, 2, WAVES>), grid,
                        dim3(WAVES * 64), lds, st, p);
@@ -922,7 +930,7 @@ static int launch_partial_w(const DecodeParams &p, const Grid &g, hipStream_t st
 
 template <int HD, int HR, typename T, bool kF8>
 static int launch_partial_t(const DecodeParams &p, const Grid &g, hipStream_t st) {
-  if constexpr (kMaxWaves<HD> == 8) {
+  if constexpr (kMaxWaves<HD, kF8> == 8) {
     if (g.heads_per_wg * g.subs == 8) return launch_partial_w<HD, HR, T, kF8, 8>(p, g, st);
   }
   return launch_partial_w<HD, HR, T, kF8, 4>(p, g, st);

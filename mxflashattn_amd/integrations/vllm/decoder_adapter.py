@@ -252,8 +252,8 @@ def forward_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: A
     (cache stored as e4m3fn or its uint8 codes) decodes with the layer's
     per-tensor k_scale / v_scale; the reference has no fp8 path."""
     if kv_cache_dtype in ("fp8", "fp8_e4m3"):
-        if output.dim() != 3 or not output.is_contiguous():
-            raise DecoderAdapterBlocked("fp8_decode_needs_contiguous_[tokens,heads,dim]_output")
+        if not output.is_contiguous():
+            raise DecoderAdapterBlocked("fp8_decode_needs_a_contiguous_output")
         return _fp8_decode(query, kv_cache, attn_metadata, output, softmax_scale, k_scale,
                            v_scale)
     result, _ = decode_forward(query, kv_cache, attn_metadata, softmax_scale=softmax_scale,

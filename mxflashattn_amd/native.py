@@ -50,6 +50,7 @@ EXPORTED_SYMBOLS = (
     "mxfa_abi_version",
     "mxfa_strerror",
     "mxfa_split_heuristic",
+    "mxfa_split_heuristic_fp8",
     "mxfa_split_decode_workspace_size",
     "mxfa_split_decode_launch",
     "mxfa_split_decode_partial_launch",
@@ -83,6 +84,7 @@ _SIGNATURES = {
     "mxfa_abi_version": (_i, []),
     "mxfa_strerror": (ctypes.c_char_p, [_i]),
     "mxfa_split_heuristic": (_i, [_i, _i, _i, _i, _i, _i, _i, ctypes.POINTER(_i)]),
+    "mxfa_split_heuristic_fp8": (_i, [_i, _i, _i, _i, _i, _i, _i, ctypes.POINTER(_i)]),
     "mxfa_split_decode_workspace_size": (_i, [_i, _i, _i, _i, ctypes.POINTER(_sz)]),
     "mxfa_split_decode_launch": (_i, _SPLIT_ARGS + [_p]),
     "mxfa_split_decode_partial_launch": (_i, _SPLIT_ARGS + [_p]),
@@ -163,13 +165,14 @@ def _check(rc: int, what: str) -> None:
 
 @functools.lru_cache(maxsize=256)
 def split_heuristic(batch: int, q_heads: int, kv_heads: int, head_dim: int, page_size: int,
-                    block_table_width: int, num_cus: int) -> int:
+                    block_table_width: int, num_cus: int, fp8: bool = False) -> int:
     """Balanced ranges per kv head for a launch; integer-only, no device access."""
     ns = _i()
+    name = "mxfa_split_heuristic_fp8" if fp8 else "mxfa_split_heuristic"
     _check(
-        library().mxfa_split_heuristic(batch, q_heads, kv_heads, head_dim, page_size,
-                                       block_table_width, num_cus, ctypes.byref(ns)),
-        "mxfa_split_heuristic",
+        getattr(library(), name)(batch, q_heads, kv_heads, head_dim, page_size,
+                                 block_table_width, num_cus, ctypes.byref(ns)),
+        name,
     )
     return ns.value
 
@@ -342,7 +345,8 @@ def _prepare(q, k_cache, v_cache, block_table, cache_seqlens, out):
 
 def default_num_splits(q: torch.Tensor, k_cache: torch.Tensor, block_table: torch.Tensor) -> int:
     return split_heuristic(q.shape[0], q.shape[-2], k_cache.shape[2], q.shape[-1],
-                           k_cache.shape[1], block_table.shape[1], num_cus(q.device.index or 0))
+                           k_cache.shape[1], block_table.shape[1], num_cus(q.device.index or 0),
+                           k_cache.dtype == FP8_DTYPE)
 
 
 def paged_decode_split(

@@ -49,8 +49,10 @@ class PagedBatch:
         return int(self.cache_seqlens.sum().item())
 
     def kv_bytes(self) -> int:
-        """K and V bytes the call must read: sum_b 2 * L_b * HKV * HD * elem."""
-        return 2 * self.total_tokens() * self.kv_heads * self.head_dim * self.q.element_size()
+        """K and V bytes the call must read: sum_b 2 * L_b * HKV * HD * elem
+        (the cache's element: 2 bytes, or 1 for an fp8 cache)."""
+        return (2 * self.total_tokens() * self.kv_heads * self.head_dim
+                * self.k_cache.element_size())
 
     def algorithmic_bytes(self) -> int:
         """KV + q + out + used block-table entries + lengths."""
@@ -80,6 +82,7 @@ def make_paged_batch(
     peaky_scale: float = 8.0,
     seed: int = DEFAULT_SEED,
     device: torch.device | str = "cpu",
+    kv_dtype: torch.dtype | None = None,
 ) -> PagedBatch:
     """Build one synthetic decode batch.
 
@@ -87,7 +90,9 @@ def make_paged_batch(
     uniform integers, or one length for every sequence. The page pool holds
     ceil(pool_factor * pages needed) pages unless num_pages is given; every
     sequence gets distinct pages from a random permutation of the pool.
-    peaky_fraction of the K rows are multiplied by peaky_scale.
+    peaky_fraction of the K rows are multiplied by peaky_scale. kv_dtype
+    float8_e4m3fn stores the caches as fp8 (the same N(0, 1) draws, rounded to
+    nearest even; their dequantisation scales are 1).
     """
     device = torch.device(device)
     gen = torch.Generator(device=device)
@@ -124,6 +129,8 @@ def make_paged_batch(
         rows = k_cache.view(-1, head_dim)
         pick = torch.rand(rows.shape[0], generator=gen, device=device) < peaky_fraction
         rows[pick] = (rows[pick].float() * peaky_scale).to(dtype)
+    if kv_dtype is not None and kv_dtype != dtype:
+        k_cache, v_cache = k_cache.to(kv_dtype), v_cache.to(kv_dtype)
     return PagedBatch(
         q=q,
         k_cache=k_cache,
@@ -153,4 +160,22 @@ CELLS = {
     f"cell_gq{32 // hkv}_d{hd}": dict(batch=32, q_heads=32, kv_heads=hkv, head_dim=hd,
                                       dtype=torch.bfloat16, lengths=(1024, 8192))
     for hkv in (16, 8, 4) for hd in (128, 64)
+}
+
+
+# Shapes beyond the reference's contract (head dim 256, 1 or 16 query heads per
+# kv head, fp8 caches), at config 2's batch and lengths.
+WIDE = {
+    "wide_fp8_config2": dict(batch=32, q_heads=32, kv_heads=8, head_dim=128,
+                             dtype=torch.bfloat16, lengths=(1024, 8192),
+                             kv_dtype=torch.float8_e4m3fn),
+    "wide_fp8_gq8_d128": dict(batch=32, q_heads=32, kv_heads=4, head_dim=128,
+                              dtype=torch.bfloat16, lengths=(1024, 8192),
+                              kv_dtype=torch.float8_e4m3fn),
+    "wide_hd256_gq2": dict(batch=32, q_heads=16, kv_heads=8, head_dim=256,
+                           dtype=torch.bfloat16, lengths=(1024, 8192)),
+    "wide_gq1_d128": dict(batch=32, q_heads=32, kv_heads=32, head_dim=128,
+                          dtype=torch.bfloat16, lengths=(1024, 8192)),
+    "wide_gq16_d128": dict(batch=32, q_heads=64, kv_heads=4, head_dim=128,
+                           dtype=torch.bfloat16, lengths=(1024, 8192)),
 }

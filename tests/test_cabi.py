@@ -44,7 +44,7 @@ def test_library_loads_and_reports_header_abi(lib):
 
 def test_every_header_function_is_exported_and_bound(lib):
     declared = header_functions()
-    assert len(declared) == len(set(declared)) == 12
+    assert len(declared) == len(set(declared)) == 13
     for name in declared:
         assert hasattr(lib, name), name
     assert set(declared) == set(native.EXPORTED_SYMBOLS) == set(native._SIGNATURES)
@@ -66,11 +66,11 @@ def test_strerror_is_distinct_per_code(lib):
     assert lib.mxfa_strerror(-99).decode()
 
 
-def heuristic_closed_form(b, hq, hkv, hd, ps, btw, cus):
-    # One wave per (kv head, range): a workgroup has max(4, min(HKV, 8 at HD64,
-    # 4 at HD128 and HD256)) waves = min(HKV, waves) kv heads x waves // that sub-ranges,
-    # one workgroup per CU.
-    waves = max(4, min(hkv, 8 if hd == 64 else 4))
+def heuristic_closed_form(b, hq, hkv, hd, ps, btw, cus, elem_bytes=2):
+    # One wave per (kv head, range): a workgroup has max(4, min(HKV, 8 for head
+    # rows of <= 128 bytes, else 4)) waves = min(HKV, waves) kv heads x
+    # waves // that sub-ranges, one workgroup per CU.
+    waves = max(4, min(hkv, 8 if hd * elem_bytes <= 128 else 4))
     kh = min(hkv, waves)
     subs = waves // kh
     gx = -(-hkv // kh)
@@ -97,6 +97,8 @@ def heuristic_closed_form(b, hq, hkv, hd, ps, btw, cus):
 ])
 def test_split_heuristic_closed_form(args):
     assert native.split_heuristic(*args) == heuristic_closed_form(*args)
+    # fp8 caches: one-byte rows.
+    assert native.split_heuristic(*args, True) == heuristic_closed_form(*args, 1)
 
 
 def test_split_heuristic_known_values():
@@ -106,6 +108,10 @@ def test_split_heuristic_known_values():
     assert native.split_heuristic(32, 32, 16, 128, 16, 512, 256) == 64
     assert native.split_heuristic(4, 8, 2, 64, 16, 128, 256) == 512
     assert native.split_heuristic(1, 2, 1, 64, 16, 1, 256) == 1
+    # fp8 config 2: eight waves hold all 8 kv heads, one workgroup per range.
+    assert native.split_heuristic(32, 32, 8, 128, 16, 512, 256, True) == 256
+    assert native.split_heuristic(32, 32, 4, 128, 16, 512, 256, True) == 256
+    assert native.split_heuristic(32, 16, 8, 256, 16, 512, 256, True) == 128
 
 
 def test_split_heuristic_rejects_bad_sizes(lib):
@@ -113,7 +119,9 @@ def test_split_heuristic_rejects_bad_sizes(lib):
     for bad in [(0, 32, 8, 128, 16, 512, 256), (32, 32, 0, 128, 16, 512, 256),
                 (32, 32, 8, 128, 16, 0, 256), (32, 32, 8, 128, 16, 512, 0)]:
         assert lib.mxfa_split_heuristic(*bad, ctypes.byref(ns)) == native.MXFA_EINVAL
+        assert lib.mxfa_split_heuristic_fp8(*bad, ctypes.byref(ns)) == native.MXFA_EINVAL
     assert lib.mxfa_split_heuristic(32, 32, 8, 128, 16, 512, 256, None) == native.MXFA_EINVAL
+    assert lib.mxfa_split_heuristic_fp8(32, 32, 8, 128, 16, 512, 256, None) == native.MXFA_EINVAL
     assert ns.value == -7
 
 
