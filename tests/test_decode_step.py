@@ -93,3 +93,46 @@ def test_plugin_path_matches_oracle_attention_eager_and_graph(device):
         torch.cuda.synchronize()
         assert torch.equal(captured, eager)
         _ = torch.randn(1000, device=device).sum().item()  # unrelated eager work
+
+
+class OracleFp8AttentionModel(DecoderModel):
+    """The decoder with an fp8 cache: the cache write restated with torch's
+    round-to-nearest-even e4m3fn conversion after saturation (the append
+    kernel's semantics, pinned in tests/test_oracle.py), attention on the
+    exactly dequantised cache."""
+
+    def attention(self, layer, q, k, v, kv_cache, meta, out):
+        ps = kv_cache.shape[2]
+        slots = meta.slot_mapping
+        kv_cache[0, slots // ps, slots % ps] = (k.float() / self.k_scale).clamp(-448, 448).to(
+            torch.float8_e4m3fn)
+        kv_cache[1, slots // ps, slots % ps] = (v.float() / self.v_scale).clamp(-448, 448).to(
+            torch.float8_e4m3fn)
+        o = reference_port.attention_kvcache(
+            q.unsqueeze(1).float().cpu(), kv_cache[0].float().cpu() * self.k_scale.cpu(),
+            kv_cache[1].float().cpu() * self.v_scale.cpu(),
+            cache_seqlens=meta.seq_lens.cpu(), block_table=meta.block_table.cpu(),
+            softmax_scale=self.scale)
+        out.copy_(o.reshape(out.shape).to(out.device, out.dtype))
+
+
+@pytest.mark.gpu
+def test_plugin_path_with_fp8_cache_matches_oracle(device):
+    native_model = DecoderModel(TINY, device, seed=5, kv_cache_dtype="fp8")
+    ref_model = OracleFp8AttentionModel(TINY, device, seed=5, kv_cache_dtype="fp8")
+    for m in (native_model, ref_model):  # non-trivial per-tensor scales
+        m.k_scale.fill_(0.5)
+        m.v_scale.fill_(0.25)
+    prompt = torch.tensor([5, 40, 200, 17])
+    st = decode_step.build_state(native_model, 4, prompt, new_tokens=6, page_size=16)
+    assert st.kv_caches[0].dtype == torch.float8_e4m3fn
+    ref_caches = [c.clone() for c in st.kv_caches]
+    for _ in range(2):
+        logits = native_model.step(st.tokens, st.positions, st.kv_caches, st.meta)
+        expected = ref_model.step(st.tokens, st.positions, ref_caches, st.meta)
+        torch.cuda.synchronize()
+        assert (logits.float() - expected.float()).abs().max().item() <= 5e-2
+        # Layer 0's new rows depend on weights and tokens only: the quantising
+        # append is bit-exact there.
+        assert torch.equal(st.kv_caches[0].view(torch.uint8), ref_caches[0].view(torch.uint8))
+        decode_step.advance(st)
