@@ -1,5 +1,6 @@
-// Device helpers shared by the gfx950 kernels: element types, 16-byte row
-// fragments, wave64 DPP row reductions and fp32 -> fp16/bf16 rounding.
+// Device helpers shared by the gfx950 kernels: element types (exact widening
+// of 16-bit halves, fp32 -> fp16/bf16 rounding), the DPP row broadcast and
+// nontemporal loads.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -8,7 +9,6 @@
 namespace mxfa {
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-typedef __bf16 bf162_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -19,13 +19,9 @@ struct BF16 {};
 template <typename T>
 struct Elem;
 
-// fp16: dot2 on packed halves, widening by v_cvt_f32_f16, RNE narrowing.
+// fp16: widening by v_cvt_f32_f16, RNE narrowing.
 template <>
 struct Elem<F16> {
-  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a), __builtin_bit_cast(half2_t, b),
-                                  acc, false);
-  }
   static __device__ __forceinline__ float lo(uint32_t x) {
     return (float)__builtin_bit_cast(half2_t, x).x;
   }
@@ -37,13 +33,9 @@ struct Elem<F16> {
   }
 };
 
-// bf16: dot2 on packed bf16 pairs; widening is a 16-bit shift (exact); RNE narrowing.
+// bf16: widening is a 16-bit shift (exact); RNE narrowing.
 template <>
 struct Elem<BF16> {
-  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf162_t, a),
-                                           __builtin_bit_cast(bf162_t, b), acc, false);
-  }
   static __device__ __forceinline__ float lo(uint32_t x) { return __uint_as_float(x << 16); }
   static __device__ __forceinline__ float hi(uint32_t x) {
     return __uint_as_float(x & 0xffff0000u);
@@ -53,34 +45,8 @@ struct Elem<BF16> {
   }
 };
 
-// DPP controls (wave64, 16-lane rows).
-constexpr int kDppQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
-constexpr int kDppQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
-constexpr int kDppRowHalfMirror = 0x141;
-constexpr int kDppRowMirror = 0x140;
-constexpr int kDppRowNewBcast0 = 0x150;  // row_newbcast:n = 0x150 + n (lane n of each row)
-
-template <int Ctrl>
-__device__ __forceinline__ float dpp_f(float x) {
-  return __int_as_float(
-      __builtin_amdgcn_update_dpp(0, __float_as_int(x), Ctrl, 0xf, 0xf, false));
-}
-
-// Sum over groups of N consecutive lanes (N = 8 or 16); every lane of the group
-// receives the bit-identical total (each step adds a pair in commutative order).
-template <int N>
-__device__ __forceinline__ float group_sum(float x) {
-  static_assert(N == 8 || N == 16, "group must be 8 or 16 lanes");
-  x += dpp_f<kDppQuadXor1>(x);
-  x += dpp_f<kDppQuadXor2>(x);
-  x += dpp_f<kDppRowHalfMirror>(x);
-  if constexpr (N == 16) x += dpp_f<kDppRowMirror>(x);
-  return x;
-}
-
-__device__ __forceinline__ float xor_shfl(float x, int mask) {
-  return __shfl_xor(x, mask, 64);
-}
+// DPP control row_newbcast:n = 0x150 + n (lane n of each 16-lane row to the row).
+constexpr int kDppRowNewBcast0 = 0x150;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
