@@ -97,7 +97,7 @@ int mxfa_split_decode_workspace_size(int batch, int q_heads, int head_dim, int n
  * information plus explicit strides, seqlen_add and a sized workspace; the
  * per-split length c_len is gone because ranges are cut on the device.
  * Supported: HD in {64,128,256}, HQ/HKV in 1..16, PS a power of two in
- * [1, 4096], dtype F16/BF16 (q, caches and out share it), batch <= 16384,
+ * [1, 4096], dtype F16/BF16 (q, caches and out share it), batch <= 16000,
  * non-overlapping token rows (cache_stride_token >= HD when PS > 1) and query
  * heads (q_stride_h >= HD). The reference supports HD {64,128} and HQ/HKV
  * {2,4,8} only (integrations/vllm/vllm_plugin.py:220-261 hands the rest back).

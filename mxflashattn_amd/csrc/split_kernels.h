@@ -71,7 +71,9 @@ namespace mxfa {
 constexpr int kTile = 16;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleLog2 = 8.0f;
-constexpr int kMaxBatch = 16384;  // tile prefix sums live in LDS
+// Tile prefix sums live in LDS, (B + 1) int32 next to a few bytes of static
+// LDS: 16000 sequences keep a workgroup within 64 KB.
+constexpr int kMaxBatch = 16000;
 constexpr int kMaxGq = 16;        // query heads per kv head: the 16 MFMA columns
 constexpr uint32_t kSrdWord3 = 0x00020000u;  // raw 32-bit buffer, gfx9 family
 constexpr int kAuxStream = 2;                // nt: no temporal reuse expected

@@ -157,7 +157,7 @@ def decode_args(**over):
     (dict(scale=float("nan")), -2), (dict(scale=float("inf")), -2),
     (dict(hd=96), -1), (dict(hd=192), -1), (dict(hd=512), -1), (dict(hq=136), -1),
     (dict(hq=36), -1), (dict(dtype=2), -1), (dict(ps=12), -1), (dict(ps=8192), -1),
-    (dict(ns=70000), -1), (dict(batch=20000), -1), (dict(btw=1 << 27, ps=16), -1),
+    (dict(ns=70000), -1), (dict(batch=16001), -1), (dict(btw=1 << 27, ps=16), -1),
     (dict(q=FAKE + 2), -2), (dict(k=FAKE + 8), -2), (dict(q_sh=100), -2), (dict(c_st=1028), -2),
     (dict(o_sh=130), -2), (dict(out=FAKE + 2), -2),
     (dict(c_st=64), -2), (dict(q_sh=64), -2),  # overlapping rows

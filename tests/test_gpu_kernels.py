@@ -294,3 +294,37 @@ def test_graph_replays_match_eager(device):
         torch.cuda.synchronize()
         assert torch.equal(out, eager), i
         _ = (torch.randn(4096, device=device) * i).sum().item()
+
+
+def test_maximum_batch(device):
+    # 16000 sequences (the contract's maximum; the tile prefix sums fill 64 KB
+    # of LDS), short ragged lengths, empty ones included.
+    g = torch.Generator().manual_seed(17)
+    lengths = torch.randint(0, 40, (16000,), generator=g)
+    b = make_paged_batch(16000, 4, 2, 64, torch.float16, lengths, seed=17).to(device)
+    expected = torch.from_numpy(c_oracle.paged_decode_f64(
+        b.q.cpu(), b.k_cache.cpu(), b.v_cache.cpu(), b.block_table.cpu(), b.cache_seqlens.cpu(),
+        b.scale)).reshape(b.q.shape)
+    for ns in (None, 4096):
+        kw = {} if ns is None else dict(num_splits=ns)
+        assert max_err(run_native(b, **kw), expected) <= TOL[torch.float16]
+
+
+def test_most_splits_and_largest_page(device):
+    # 65535 ranges (the maximum; more than there are tiles, so R = NT) and
+    # 4096-token pages.
+    b = make_paged_batch(3, 8, 2, 128, torch.bfloat16, torch.tensor([5000, 1, 9000]),
+                         page_size=4096, seed=18).to(device)
+    expected = oracle_out(b)
+    assert max_err(run_native(b, num_splits=65535), expected) <= TOL[torch.bfloat16]
+    assert max_err(run_native(b), expected) <= TOL[torch.bfloat16]
+
+
+def test_long_context(device):
+    # One 131072-token sequence next to short ones.
+    b = make_paged_batch(3, 16, 2, 128, torch.bfloat16, torch.tensor([131072, 3, 700]),
+                         seed=19).to(device)
+    expected = torch.from_numpy(c_oracle.paged_decode_f64(
+        b.q.cpu(), b.k_cache.cpu(), b.v_cache.cpu(), b.block_table.cpu(), b.cache_seqlens.cpu(),
+        b.scale)).reshape(b.q.shape)
+    assert max_err(run_native(b), expected) <= TOL[torch.bfloat16]
