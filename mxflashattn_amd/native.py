@@ -177,6 +177,7 @@ def split_heuristic(batch: int, q_heads: int, kv_heads: int, head_dim: int, page
     return ns.value
 
 
+@functools.lru_cache(maxsize=256)
 def workspace_size(batch: int, q_heads: int, head_dim: int, num_splits: int) -> int:
     out = _sz()
     _check(library().mxfa_split_decode_workspace_size(batch, q_heads, head_dim, num_splits,
@@ -202,7 +203,7 @@ class _Workspace:
         self._lock = threading.Lock()
 
     def get(self, device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
-        key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+        key = (device.index if device.index is not None else _current_device(), stream)
         with self._lock:
             buf = self._buffers.get(key)
             if buf is None or buf.numel() < nbytes:
@@ -239,7 +240,15 @@ def _int32_contig(t: torch.Tensor, name: str) -> torch.Tensor:
     return t
 
 
+# The raw current-stream accessor skips the Stream object torch would build
+# (a few microseconds per call on the host).
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_current_device = getattr(torch._C, "_cuda_getDevice", None) or torch.cuda.current_device
+
+
 def _stream_handle(device: torch.device) -> int:
+    if _raw_stream is not None:
+        return _raw_stream(device.index if device.index is not None else _current_device())
     return torch.cuda.current_stream(device).cuda_stream
 
 
@@ -255,9 +264,10 @@ def _require_device(*tensors: torch.Tensor) -> torch.device:
     for t in tensors[1:]:
         if t.device != device:
             raise ValueError(f"all tensors must be on {device}, got one on {t.device}")
-    if (device.index or 0) != torch.cuda.current_device():
+    current = _current_device()
+    if (device.index or 0) != current:
         raise ValueError(f"tensors are on {device} but the current device is "
-                         f"cuda:{torch.cuda.current_device()}; call under torch.cuda.device")
+                         f"cuda:{current}; call under torch.cuda.device")
     return device
 
 
@@ -283,7 +293,7 @@ def check_decode_shapes(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
 
 
 def _launch_args(q, k_cache, v_cache, block_table, cache_seqlens, out, workspace, ws_bytes,
-                 softmax_scale, num_splits, seqlen_add):
+                 softmax_scale, num_splits, seqlen_add, stream=None):
     batch, hq, hd = q.shape[0], q.shape[-2], q.shape[-1]
     pages, ps, hkv = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
     qs, os_, cs = q.stride(), out.stride(), k_cache.stride()
@@ -292,7 +302,7 @@ def _launch_args(q, k_cache, v_cache, block_table, cache_seqlens, out, workspace
         block_table.data_ptr(), block_table.stride(0), cache_seqlens.data_ptr(), seqlen_add,
         out.data_ptr(), os_[0], os_[-2], workspace, ws_bytes,
         float(softmax_scale), batch, hq, hkv, hd, ps, block_table.shape[1], pages,
-        DTYPE_CODES[q.dtype], num_splits, _stream_handle(q.device),
+        DTYPE_CODES[q.dtype], num_splits, _stream_handle(q.device) if stream is None else stream,
     )
 
 
@@ -381,7 +391,7 @@ def paged_decode_split(
     ws_bytes = workspace_size(q.shape[0], q.shape[-2], q.shape[-1], num_splits)
     ws = WORKSPACE.get(q.device, stream, ws_bytes)
     args = _launch_args(q, k_cache, v_cache, block_table, cache_seqlens, out, ws.data_ptr(),
-                        ws_bytes, softmax_scale, num_splits, seqlen_add)
+                        ws_bytes, softmax_scale, num_splits, seqlen_add, stream)
     if k_cache.dtype == FP8_DTYPE:
         rc = lib.mxfa_split_decode_fp8_launch(*args[:-1], _scale_ptr(k_scale, q.device, "k_scale"),
                                               _scale_ptr(v_scale, q.device, "v_scale"), args[-1])
