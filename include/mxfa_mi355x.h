@@ -46,6 +46,7 @@ extern "C" {
 /* Element types. */
 #define MXFA_DTYPE_F16 0
 #define MXFA_DTYPE_BF16 1
+#define MXFA_DTYPE_FP8_E4M3 2 /* KV caches only (OCP e4m3fn) */
 
 /* ABI version of the loaded library (MXFA_ABI_VERSION). No reference counterpart. */
 int mxfa_abi_version(void);
@@ -112,6 +113,31 @@ int mxfa_split_decode_launch(const void *q, int64_t q_stride_b, int64_t q_stride
                              int q_heads, int kv_heads, int head_dim, int page_size,
                              int block_table_width, int num_pages, int dtype, int num_splits,
                              void *stream);
+
+/*
+ * Decode with q_len query tokens per sequence (1 <= q_len, q_len * HQ/HKV <=
+ * 16), for speculative decoding: q and out are [B, q_len, HQ, HD] with strides
+ * (stride_b, stride_t, stride_h, 1). Token t of sequence b sits at position
+ * L_b - q_len + t, L_b = seqlens[b] + seqlen_add; with causal != 0 it attends
+ * keys [0, L_b - q_len + t] (bottom-right aligned, as
+ * mxflashattn/reference.py:31-35), else all L_b keys; a token with no key gets
+ * zeros (the reference's nan_to_num). kv_dtype is dtype (16-bit caches) or
+ * MXFA_DTYPE_FP8_E4M3 with k_scale/v_scale as in mxfa_split_decode_fp8_launch.
+ * Workspace: mxfa_split_decode_workspace_size(batch, q_heads * q_len, ...).
+ * Partial and combine run as one call. Other arguments as
+ * mxfa_split_decode_launch. The reference's M1 takes q_len = 1 only
+ * (csrc_native/m1_binding.cpp:81-88); its API routes longer queries to the
+ * vendor, ATen or reference backends (mxflashattn/dispatch.py:89-170).
+ */
+int mxfa_split_decode_multi_launch(
+    const void *q, int64_t q_stride_b, int64_t q_stride_t, int64_t q_stride_h, int q_len,
+    int causal, const void *k_cache, const void *v_cache, int64_t cache_stride_page,
+    int64_t cache_stride_token, int64_t cache_stride_head, const int32_t *block_table,
+    int64_t bt_stride, const int32_t *seqlens, int seqlen_add, void *out, int64_t out_stride_b,
+    int64_t out_stride_t, int64_t out_stride_h, void *workspace, size_t workspace_bytes,
+    float scale, int batch, int q_heads, int kv_heads, int head_dim, int page_size,
+    int block_table_width, int num_pages, int dtype, int kv_dtype, const float *k_scale,
+    const float *v_scale, int num_splits, void *stream);
 
 /*
  * Partial stage alone: the first of the two launches of mxfa_split_decode_launch,

@@ -32,7 +32,7 @@ static bool supported_hd(int hd) { return hd == 64 || hd == 128 || hd == 256; }
 
 struct SplitArgs {
   const void *q;
-  int64_t q_sb, q_sh;
+  int64_t q_sb, q_st, q_sh;
   const void *k, *v;
   int64_t c_sp, c_st, c_sh;  // cache strides in elements (bytes for fp8 caches)
   const int32_t *bt;
@@ -40,13 +40,15 @@ struct SplitArgs {
   const int32_t *seqlens;
   int seqlen_add;
   void *out;
-  int64_t o_sb, o_sh;
+  int64_t o_sb, o_st, o_sh;
   void *ws;
   size_t ws_bytes;
   float scale;
   int batch, hq, hkv, hd, ps, btw, num_pages, dtype, num_splits;
   bool fp8;  // caches hold OCP e4m3fn
   const float *k_scale, *v_scale;
+  int ql;      // query tokens per sequence
+  int causal;  // bottom-right aligned causal mask
 };
 
 struct WsLayout {
@@ -71,7 +73,8 @@ static int check_split_args(const SplitArgs &a) {
   if (!supported_hd(a.hd)) return MXFA_EUNSUPPORTED;
   if (a.hq % a.hkv != 0) return MXFA_EUNSUPPORTED;
   const int gq = a.hq / a.hkv;
-  if (gq > kMaxGq) return MXFA_EUNSUPPORTED;
+  if (a.ql <= 0) return MXFA_EINVAL;
+  if (gq * a.ql > kMaxCols) return MXFA_EUNSUPPORTED;
   if (a.dtype != MXFA_DTYPE_F16 && a.dtype != MXFA_DTYPE_BF16) return MXFA_EUNSUPPORTED;
   if (ilog2_exact(a.ps) < 0 || a.ps > 4096) return MXFA_EUNSUPPORTED;
   if (a.num_splits > 65535 || a.batch > kMaxBatch || a.hkv > 65535) return MXFA_EUNSUPPORTED;
@@ -84,9 +87,10 @@ static int check_split_args(const SplitArgs &a) {
   // alignment (8 elements of 16 bits, 16 fp8 elements).
   const int64_t esz = a.fp8 ? 1 : 2;
   if (!aligned16(a.q) || !aligned16(a.k) || !aligned16(a.v)) return MXFA_EINVAL;
-  if ((a.q_sb | a.q_sh) & 7) return MXFA_EINVAL;
+  if ((a.q_sb | a.q_st | a.q_sh) & 7) return MXFA_EINVAL;
   if (((a.c_sp | a.c_st | a.c_sh) * esz) & 15) return MXFA_EINVAL;
-  if (a.q_sb < 0 || a.q_sh < 0 || a.c_sp < 0 || a.c_st < 0 || a.c_sh < 0 || a.bt_stride < 0)
+  if (a.q_sb < 0 || a.q_st < 0 || a.q_sh < 0 || a.c_sp < 0 || a.c_st < 0 || a.c_sh < 0 ||
+      a.bt_stride < 0)
     return MXFA_EINVAL;
   // Rows must not overlap: the per-tile descriptors cover whole rows.
   if ((a.ps > 1 && a.c_st < a.hd) || (gq > 1 && a.q_sh < a.hd)) return MXFA_EINVAL;
@@ -96,21 +100,30 @@ static int check_split_args(const SplitArgs &a) {
   if ((int64_t)(a.ps - 1) * a.c_st * esz >= ((int64_t)1 << 32) ||
       a.c_sh * esz >= ((int64_t)1 << 32))
     return MXFA_EUNSUPPORTED;
-  if (((int64_t)(gq - 1) * a.q_sh + a.hd) * 2 >= ((int64_t)1 << 30)) return MXFA_EUNSUPPORTED;
-  if (((uintptr_t)a.out & 7u) || ((a.o_sb | a.o_sh) & 3) || a.o_sb < 0 || a.o_sh < 0)
+  if (((int64_t)(a.ql - 1) * a.q_st + (int64_t)(gq - 1) * a.q_sh + a.hd) * 2 >=
+      ((int64_t)1 << 30))
+    return MXFA_EUNSUPPORTED;
+  if (((uintptr_t)a.out & 7u) || ((a.o_sb | a.o_st | a.o_sh) & 3) || a.o_sb < 0 ||
+      a.o_st < 0 || a.o_sh < 0)
+    return MXFA_EINVAL;
+  // Output rows of different (query token, head) pairs must not overlap.
+  if (a.ql > 1 && !((a.o_st >= (int64_t)a.hq * a.o_sh && a.o_sh >= a.hd) ||
+                    (a.o_sh >= (int64_t)a.ql * a.o_st && a.o_st >= a.hd)))
     return MXFA_EINVAL;
   if (((uintptr_t)a.k_scale & 3u) || ((uintptr_t)a.v_scale & 3u)) return MXFA_EINVAL;
   if (!a.ws || !aligned16(a.ws)) return MXFA_EWORKSPACE;
-  if (a.ws_bytes < ws_layout(a.batch, a.hq, a.hd, a.num_splits).bytes) return MXFA_EWORKSPACE;
+  if (a.ws_bytes < ws_layout(a.batch, a.hq * a.ql, a.hd, a.num_splits).bytes)
+    return MXFA_EWORKSPACE;
   return MXFA_OK;
 }
 
 static DecodeParams make_params(const SplitArgs &a, const Grid &g) {
-  const WsLayout w = ws_layout(a.batch, a.hq, a.hd, a.num_splits);
+  const WsLayout w = ws_layout(a.batch, a.hq * a.ql, a.hd, a.num_splits);
   const int64_t esz = a.fp8 ? 1 : 2;
   DecodeParams p;
   p.q = (const char *)a.q;
   p.q_sb = a.q_sb * 2;
+  p.q_st = a.q_st * 2;
   p.q_sh = a.q_sh * 2;
   p.k = (const char *)a.k;
   p.v = (const char *)a.v;
@@ -122,6 +135,7 @@ static DecodeParams make_params(const SplitArgs &a, const Grid &g) {
   p.seqlens = a.seqlens;
   p.out = (char *)a.out;
   p.o_sb = a.o_sb * 2;
+  p.o_st = a.o_st * 2;
   p.o_sh = a.o_sh * 2;
   p.ws_o = (float *)a.ws;
   p.ws_lse = (float *)a.ws + w.o_floats;
@@ -133,6 +147,8 @@ static DecodeParams make_params(const SplitArgs &a, const Grid &g) {
   p.batch = a.batch;
   p.hkv = a.hkv;
   p.gq = a.hq / a.hkv;
+  p.ql = a.ql;
+  p.causal = a.causal ? 1 : 0;
   p.heads_per_wg = g.heads_per_wg;
   p.subs = g.subs;
   p.ps_log2 = ilog2_exact(a.ps);
@@ -152,11 +168,11 @@ static int launch_partial(const SplitArgs &a, hipStream_t st) {
   }
 }
 
-// Heads per combine block: a typical crossing sequence has about
-// num_splits / batch + 1 pieces; enough piece groups G (a power of two) that
-// they fold in one step of eight loads, then as many heads as fit in the
-// block's kCombineThreads / G chunk threads (at most the next power of two
-// of HQ).
+// Rows (query token, head) per combine block: a typical crossing sequence has
+// about num_splits / batch + 1 pieces; enough piece groups G (a power of two)
+// that they fold in one step of eight loads, then as many rows as fit in the
+// block's kCombineThreads / G chunk threads (at most the next power of two of
+// the rows per sequence).
 static int combine_heads_per_block(int batch, int hq, int hd, int num_splits) {
   const int ch = hd / 4;
   const int pieces = (num_splits + batch - 1) / batch + 1;
@@ -168,21 +184,24 @@ static int combine_heads_per_block(int batch, int hq, int hd, int num_splits) {
   return h;
 }
 
-static int launch_combine(void *ws, void *out, int64_t o_sb, int64_t o_sh, int batch, int hq,
-                          int hkv, int hd, int dtype, int ns, hipStream_t st) {
-  const WsLayout w = ws_layout(batch, hq, hd, ns);
+static int launch_combine(void *ws, void *out, int64_t o_sb, int64_t o_st, int64_t o_sh,
+                          int batch, int hq, int hkv, int ql, int hd, int dtype, int ns,
+                          hipStream_t st) {
+  const WsLayout w = ws_layout(batch, hq * ql, hd, ns);
   CombineParams c;
   c.ws_o = (const float *)ws;
   c.ws_lse = (const float *)ws + w.o_floats;
   c.ws_s = (const int32_t *)((const float *)ws + w.o_floats + w.lse_floats);
   c.out = (char *)out;
   c.o_sb = o_sb * 2;
+  c.o_st = o_st * 2;
   c.o_sh = o_sh * 2;
   c.batch = batch;
   c.hq = hq;
   c.gq = hq / hkv;
+  c.ql = ql;
   c.num_ranges = ns;
-  c.heads_per_block = combine_heads_per_block(batch, hq, hd, ns);
+  c.heads_per_block = combine_heads_per_block(batch, hq * ql, hd, ns);
   switch (hd) {
     case 64: return launch_combine_64(c, dtype, st);
     case 128: return launch_combine_128(c, dtype, st);
@@ -201,6 +220,7 @@ static SplitArgs split_args(const void *q, int64_t q_stride_b, int64_t q_stride_
   SplitArgs a;
   a.q = q;
   a.q_sb = q_stride_b;
+  a.q_st = 0;
   a.q_sh = q_stride_h;
   a.k = k_cache;
   a.v = v_cache;
@@ -213,6 +233,7 @@ static SplitArgs split_args(const void *q, int64_t q_stride_b, int64_t q_stride_
   a.seqlen_add = seqlen_add;
   a.out = out;
   a.o_sb = out_stride_b;
+  a.o_st = 0;
   a.o_sh = out_stride_h;
   a.ws = workspace;
   a.ws_bytes = workspace_bytes;
@@ -229,6 +250,8 @@ static SplitArgs split_args(const void *q, int64_t q_stride_b, int64_t q_stride_
   a.fp8 = false;
   a.k_scale = nullptr;
   a.v_scale = nullptr;
+  a.ql = 1;
+  a.causal = 0;
   return a;
 }
 
@@ -237,8 +260,8 @@ static int run_split(const SplitArgs &a, bool with_combine, hipStream_t st) {
   if (rc != MXFA_OK) return rc;
   rc = launch_partial(a, st);
   if (rc != MXFA_OK || !with_combine) return rc;
-  return launch_combine(a.ws, a.out, a.o_sb, a.o_sh, a.batch, a.hq, a.hkv, a.hd, a.dtype,
-                        a.num_splits, st);
+  return launch_combine(a.ws, a.out, a.o_sb, a.o_st, a.o_sh, a.batch, a.hq, a.hkv, a.ql, a.hd,
+                        a.dtype, a.num_splits, st);
 }
 
 static SplitArgs fp8_args(SplitArgs a, const float *k_scale, const float *v_scale) {
@@ -349,7 +372,7 @@ int mxfa_split_decode_combine_launch(void *workspace, size_t workspace_bytes, vo
   if (!workspace || !out) return MXFA_EINVAL;
   if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || num_splits <= 0) return MXFA_EINVAL;
   if (!supported_hd(head_dim)) return MXFA_EUNSUPPORTED;
-  if (q_heads % kv_heads != 0 || q_heads / kv_heads > kMaxGq) return MXFA_EUNSUPPORTED;
+  if (q_heads % kv_heads != 0 || q_heads / kv_heads > kMaxCols) return MXFA_EUNSUPPORTED;
   if (dtype != MXFA_DTYPE_F16 && dtype != MXFA_DTYPE_BF16) return MXFA_EUNSUPPORTED;
   if (batch > kMaxBatch || num_splits > 65535) return MXFA_EUNSUPPORTED;
   if (!aligned16(workspace) || ((uintptr_t)out & 7u) || ((out_stride_b | out_stride_h) & 3) ||
@@ -357,8 +380,31 @@ int mxfa_split_decode_combine_launch(void *workspace, size_t workspace_bytes, vo
     return MXFA_EINVAL;
   if (workspace_bytes < ws_layout(batch, q_heads, head_dim, num_splits).bytes)
     return MXFA_EWORKSPACE;
-  return launch_combine(workspace, out, out_stride_b, out_stride_h, batch, q_heads, kv_heads,
-                        head_dim, dtype, num_splits, (hipStream_t)stream);
+  return launch_combine(workspace, out, out_stride_b, 0, out_stride_h, batch, q_heads, kv_heads,
+                        1, head_dim, dtype, num_splits, (hipStream_t)stream);
+}
+
+int mxfa_split_decode_multi_launch(
+    const void *q, int64_t q_stride_b, int64_t q_stride_t, int64_t q_stride_h, int q_len,
+    int causal, const void *k_cache, const void *v_cache, int64_t cache_stride_page,
+    int64_t cache_stride_token, int64_t cache_stride_head, const int32_t *block_table,
+    int64_t bt_stride, const int32_t *seqlens, int seqlen_add, void *out, int64_t out_stride_b,
+    int64_t out_stride_t, int64_t out_stride_h, void *workspace, size_t workspace_bytes,
+    float scale, int batch, int q_heads, int kv_heads, int head_dim, int page_size,
+    int block_table_width, int num_pages, int dtype, int kv_dtype, const float *k_scale,
+    const float *v_scale, int num_splits, void *stream) {
+  SplitArgs a = split_args(q, q_stride_b, q_stride_h, k_cache, v_cache, cache_stride_page,
+                           cache_stride_token, cache_stride_head, block_table, bt_stride,
+                           seqlens, seqlen_add, out, out_stride_b, out_stride_h, workspace,
+                           workspace_bytes, scale, batch, q_heads, kv_heads, head_dim, page_size,
+                           block_table_width, num_pages, dtype, num_splits);
+  if (kv_dtype == MXFA_DTYPE_FP8_E4M3) a = fp8_args(a, k_scale, v_scale);
+  else if (kv_dtype != dtype) return MXFA_EUNSUPPORTED;
+  a.q_st = q_stride_t;
+  a.o_st = out_stride_t;
+  a.ql = q_len;
+  a.causal = causal;
+  return run_split(a, true, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -19,9 +19,10 @@
 //          valid rows, so rows past the sequence end and the padding tile past
 //          the range end read as zeros and cost no memory traffic. K and V
 //          carry the nontemporal hint (read once per call).
-//   QK     on the matrix cores: S^T[16 tokens x 16 heads] = K[16 x HD].Q^T[HD x 16]
-//          (v_mfma_f32_16x16x32, HD/32 steps; query heads >= GQ are zero
-//          columns). 16-bit caches: lane l holds K bytes [64c + 16(l/16), +16)
+//   QK     on the matrix cores: S^T[16 tokens x 16 columns] = K[16 x HD].Q^T[HD x 16]
+//          (v_mfma_f32_16x16x32, HD/32 steps). Column c = t*GQ + g is query
+//          token t (of QL new tokens per sequence) and query head g of the
+//          group; columns >= GQ*QL are zero. 16-bit caches: lane l holds K bytes [64c + 16(l/16), +16)
 //          of token l%16 for step c. fp8 caches: lane l loads K bytes
 //          [64m + 16(l/16), +16) (16 elements) and widens them exactly to the
 //          element type for steps 2m and 2m+1; q is read in the same order.
@@ -45,9 +46,13 @@
 // across the XCDs' separate L2s): sequences that cross a range end fold their
 // pieces with base-2 LSE weights.
 //
-// Workspace (fp32 unless noted), R = num_splits: ws_o [HKV, R, 2, GQ, HD] piece
-// outputs (slot 0 = first piece of a range, slot 1 = last piece when it
-// differs), ws_lse [HKV, R, 2, GQ], ws_s int32 [B + 1] tile prefix sums.
+// Several query tokens per sequence (QL, decode with draft tokens): token t
+// sits at position L - QL + t and, with the causal mask, sees keys
+// [0, L - QL + t] (the bottom-right alignment of the reference's mask).
+//
+// Workspace (fp32 unless noted), R = num_splits, C = GQ*QL: ws_o [HKV, R, 2, C, HD]
+// piece outputs (slot 0 = first piece of a range, slot 1 = last piece when it
+// differs), ws_lse [HKV, R, 2, C], ws_s int32 [B + 1] tile prefix sums.
 //
 // Reference counterpart: paged_decode_v3 split mode and split_combine
 // (csrc_native/m1_kernel.cpp:553-888) with the split count of
@@ -74,7 +79,7 @@ constexpr float kRescaleLog2 = 8.0f;
 // Tile prefix sums live in LDS, (B + 1) int32 next to a few bytes of static
 // LDS: 16000 sequences keep a workgroup within 64 KB.
 constexpr int kMaxBatch = 16000;
-constexpr int kMaxGq = 16;        // query heads per kv head: the 16 MFMA columns
+constexpr int kMaxCols = 16;      // query tokens x heads per kv head: the 16 MFMA columns
 constexpr uint32_t kSrdWord3 = 0x00020000u;  // raw 32-bit buffer, gfx9 family
 constexpr int kAuxStream = 2;                // nt: no temporal reuse expected
 constexpr int kOffOut = 0x40000000;          // a lane offset no descriptor covers
@@ -88,7 +93,7 @@ constexpr int kRangeStart = 16;  // first tile of the range
 
 struct DecodeParams {
   const char *q;
-  int64_t q_sb, q_sh;  // bytes
+  int64_t q_sb, q_st, q_sh;  // bytes (batch, query token, head)
   const char *k;
   const char *v;
   int64_t sp_bytes;   // page stride
@@ -98,7 +103,7 @@ struct DecodeParams {
   int64_t bt_stride;
   const int32_t *seqlens;
   char *out;
-  int64_t o_sb, o_sh;  // bytes
+  int64_t o_sb, o_st, o_sh;  // bytes
   float *ws_o;
   float *ws_lse;
   int32_t *ws_s;
@@ -109,6 +114,8 @@ struct DecodeParams {
   int batch;
   int hkv;
   int gq;
+  int ql;      // query tokens per sequence
+  int causal;  // mask keys after each query token's position
   int heads_per_wg;
   int subs;
   int ps_log2;
@@ -126,10 +133,11 @@ struct CombineParams {
   const float *ws_lse;
   const int32_t *ws_s;
   char *out;
-  int64_t o_sb, o_sh;  // bytes
+  int64_t o_sb, o_st, o_sh;  // bytes
   int batch;
   int hq;
   int gq;
+  int ql;
   int num_ranges;
   int heads_per_block;  // a power of two; heads_per_block * HD / 4 <= kCombineThreads
 };
@@ -375,8 +383,11 @@ __device__ __forceinline__ void zero_empty(const DecodeParams &p, const int32_t 
   for (int b = blockIdx.y; b < p.batch; b += gridDim.y) {
     if (s[b + 1] != s[b]) continue;
     char *row = p.out + b * p.o_sb + (int64_t)kv0 * p.gq * p.o_sh;
-    for (int i = threadIdx.x; i < nh * F; i += kThreads)
-      *reinterpret_cast<uint2 *>(row + (i / F) * p.o_sh + (i % F) * 8) = make_uint2(0u, 0u);
+    for (int i = threadIdx.x; i < p.ql * nh * F; i += kThreads) {
+      const int t = i / (nh * F), j = i % (nh * F);
+      *reinterpret_cast<uint2 *>(row + t * p.o_st + (j / F) * p.o_sh + (j % F) * 8) =
+          make_uint2(0u, 0u);
+    }
   }
 }
 
@@ -417,6 +428,7 @@ struct Tile {
   int b;      // sequence
   int tok0;   // first token of the tile within the sequence
   int valid;  // tokens of the tile that exist (0: padding past the range end)
+  int rem;    // keys from the tile start to the sequence end (0: padding)
   int flags;
   int pg;  // page id (block-table entry), page-uniform tiles only
 };
@@ -437,6 +449,7 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   constexpr int NPG = kLanePages ? 1 + U : 1;
   const int B = p.batch;
   const int gq = p.gq;
+  const int nc = gq * p.ql;  // used columns
 
   const int lane = threadIdx.x & 63;
   const int row = lane >> 4;  // DPP row
@@ -459,8 +472,13 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   int v_off[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) v_off[u] = (4 * row + u) * (int)st + col * VB;
-  const int q_off = col < gq ? col * (int)p.q_sh + row * (kF8 ? 32 : 16) : kOffOut;
-  const int q_bytes = (gq - 1) * (int)p.q_sh + HD * 2;
+  // Column col = query token ct, group head cg; the causal mask hides the
+  // last c_hide keys of the sequence from it.
+  const int ct = col / gq, cg = col - (col / gq) * gq;
+  const int c_hide = p.causal ? p.ql - 1 - ct : 0;
+  const int q_off =
+      col < nc ? ct * (int)p.q_st + cg * (int)p.q_sh + row * (kF8 ? 32 : 16) : kOffOut;
+  const int q_bytes = (p.ql - 1) * (int)p.q_st + (gq - 1) * (int)p.q_sh + HD * 2;
   auto q_step = [](int cc) { return kF8 ? (cc >> 1) * 128 + (cc & 1) * 16 : cc * 64; };
 
   // Sequence holding tile lo: largest b with s[b] <= lo (then s[b+1] > lo).
@@ -485,6 +503,7 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
       d.b = pb;
       d.tok0 = 0;
       d.valid = 0;
+      d.rem = 0;
       d.flags = 0;
       d.pg = 0;
 #pragma unroll
@@ -502,7 +521,8 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
     }
     d.b = pb;
     d.tok0 = (t - p_start) * kTile;
-    d.valid = min(kTile, p_len - d.tok0);
+    d.rem = p_len - d.tok0;
+    d.valid = min(kTile, d.rem);
     const bool seq_start = d.tok0 == 0, seq_end = d.tok0 + kTile >= p_len;
     d.flags = ((t == lo || seq_start) ? kFirst : 0) | ((t == hi - 1 || seq_end) ? kLast : 0) |
               (seq_start ? kSeqStart : 0) | (seq_end ? kSeqEnd : 0) | (t == lo ? kRangeStart : 0);
@@ -593,19 +613,22 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
     const int b = d.b;
     const bool whole = piece_from_start && (d.flags & kSeqEnd);
     const int slot = piece_first_in_range ? 0 : 1;
-    const int64_t pbase = ((int64_t)(kvh * ns + rr) * 2 + slot) * gq;
+    const int64_t pbase = ((int64_t)(kvh * ns + rr) * 2 + slot) * nc;
     static_for<4>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
-      const int hh = 4 * row + i;  // head of accumulator element i in this lane
+      const int hh = 4 * row + i;  // column of accumulator element i in this lane
       const float Dh = head_of_row<HR, i>(dt, row);
       const float Mh = head_of_row<HR, i>(m, row);
-      if (hh >= gq) return;
+      if (hh >= nc) return;
       const float inv = Dh > 0.f ? v_scale / Dh : 0.f;
       float v[VD];
 #pragma unroll
       for (int j = 0; j < VD; ++j) v[j] = oacc[j][i];
       if (whole) {
-        store_row<VD, E>(p.out + b * p.o_sb + (kvh * gq + hh) * p.o_sh + col * (VD * 2), v, inv);
+        const int ht = hh / gq, hg = hh - (hh / gq) * gq;
+        store_row<VD, E>(p.out + b * p.o_sb + ht * p.o_st + (kvh * gq + hg) * p.o_sh +
+                             col * (VD * 2),
+                         v, inv);
       } else {
         float4 *dst = reinterpret_cast<float4 *>(p.ws_o + (pbase + hh) * HD + col * VD);
 #pragma unroll
@@ -647,7 +670,7 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
     bool need = false;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const bool valid = (col < gq) & (4 * row + i < d.valid);
+      const bool valid = (col < nc) & (4 * row + i < d.rem - c_hide);
       x[i] = valid ? (acc0[i] + acc1[i]) * c : -INFINITY;
       need |= x[i] > m + kRescaleLog2;
     }
@@ -803,9 +826,10 @@ __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(CombineP
   const int H = p.heads_per_block;
   const int CB = H * CH;
   const int groups = kCombineThreads / CB;
-  const int nblk = (p.hq + H - 1) / H;
+  const int nv = p.hq * p.ql;  // (query token, head) rows per sequence
+  const int nblk = (nv + H - 1) / H;
   const int b = blockIdx.x / nblk;
-  const int h = (blockIdx.x % nblk) * H + (threadIdx.x % CB) / CH;
+  const int vh = (blockIdx.x % nblk) * H + (threadIdx.x % CB) / CH;
   const int cc = threadIdx.x % CH;
   const int g = threadIdx.x / CB;
   const int NT = p.ws_s[p.batch];
@@ -818,8 +842,10 @@ __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(CombineP
   if (ra == rb) return;
   const int slot_a = (range_lo(ra, R, NT) == sb) ? 0 : 1;
   const int ns = p.num_ranges;
-  const bool live = h < p.hq;  // the last block of a sequence may run past HQ
-  const int kvh = live ? h / p.gq : 0, hh = live ? h % p.gq : 0;
+  const bool live = vh < nv;  // the last block of a sequence may run past the rows
+  const int t = live ? vh / p.hq : 0, h = live ? vh - t * p.hq : 0;
+  const int kvh = h / p.gq, hh = t * p.gq + (h - kvh * p.gq);  // piece column
+  const int nc = p.gq * p.ql;
   float M = -INFINITY, W = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   if (live) {
@@ -829,7 +855,7 @@ __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(CombineP
 #pragma unroll
       for (int i = 0; i < kUnroll; ++i) {
         const int q = min(q0 + i * groups, rb);
-        const int64_t ps = ((int64_t)(kvh * ns + q) * 2 + (q == ra ? slot_a : 0)) * p.gq + hh;
+        const int64_t ps = ((int64_t)(kvh * ns + q) * 2 + (q == ra ? slot_a : 0)) * nc + hh;
         l[i] = (q0 + i * groups <= rb) ? p.ws_lse[ps] : -INFINITY;
         ov[i] = reinterpret_cast<const float4 *>(p.ws_o + ps * HD)[cc];
       }
@@ -864,7 +890,8 @@ __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(CombineP
         (uint32_t)E::narrow(acc.x * inv) | ((uint32_t)E::narrow(acc.y * inv) << 16);
     const uint32_t w1 =
         (uint32_t)E::narrow(acc.z * inv) | ((uint32_t)E::narrow(acc.w * inv) << 16);
-    *reinterpret_cast<uint2 *>(p.out + b * p.o_sb + h * p.o_sh + cc * 8) = make_uint2(w0, w1);
+    *reinterpret_cast<uint2 *>(p.out + b * p.o_sb + t * p.o_st + h * p.o_sh + cc * 8) =
+        make_uint2(w0, w1);
   }
 }
 
@@ -914,8 +941,8 @@ inline Grid grid_for(int hkv, int num_splits, int waves) {
 template <int HD, bool kF8>
 constexpr int kNbuf = kRowBytes<HD, kF8> <= 64 ? 4 : kRowBytes<HD, kF8> <= 128 ? 3 : 2;
 
-// Head rows of the MFMA layout for a group size (GQ <= 4 per row).
-inline int head_rows(int gq) { return gq <= 4 ? 1 : gq <= 8 ? 2 : 4; }
+// Rows of the MFMA layout that hold used columns (4 columns per row).
+inline int head_rows(int cols) { return cols <= 4 ? 1 : cols <= 8 ? 2 : 4; }
 
 template <int HD, int HR, typename T, bool kF8, int WAVES>
 static int launch_partial_w(const DecodeParams &p, const Grid &g, hipStream_t st) {
@@ -940,7 +967,7 @@ static int launch_partial_t(const DecodeParams &p, const Grid &g, hipStream_t st
 
 template <int HD, typename T, bool kF8>
 static int launch_partial_hr(const DecodeParams &p, const Grid &g, hipStream_t st) {
-  switch (head_rows(p.gq)) {
+  switch (head_rows(p.gq * p.ql)) {
     case 1: return launch_partial_t<HD, 1, T, kF8>(p, g, st);
     case 2: return launch_partial_t<HD, 2, T, kF8>(p, g, st);
     default: return launch_partial_t<HD, 4, T, kF8>(p, g, st);
@@ -961,7 +988,8 @@ int launch_partial_hd(const DecodeParams &p, const Grid &g, int dtype, bool fp8,
 
 template <int HD>
 int launch_combine_hd(const CombineParams &c, int dtype, hipStream_t st) {
-  const int nblk = (c.hq + c.heads_per_block - 1) / c.heads_per_block;
+  // One block per (sequence, heads_per_block rows of (query token, head)).
+  const int nblk = (c.hq * c.ql + c.heads_per_block - 1) / c.heads_per_block;
   dim3 grid(c.batch * nblk);
   if (dtype == MXFA_DTYPE_BF16)
     hipLaunchKernelGGL((split_combine_kernel<HD, BF16>), grid, dim3(kCombineThreads), 0, st, c);

@@ -6,11 +6,14 @@ the dispatch chain continues), otherwise ``run`` launches it. Checks here read
 only shapes, dtypes and devices, never device data, so a qualifying call does
 not synchronise the stream.
 
-  flash_attn_with_kvcache  paged or dense cache, q_len 1, optional k/v append
-                           (append kernel, then decode over seqlens + S_new,
-                           then cache_seqlens += S_new on the device).
-  flash_attn_func          q_len 1: k/v [B, S, HKV, D] is a dense cache of S
-                           tokens per sequence.
+  flash_attn_with_kvcache  paged or dense cache, q_len QL with QL * GQ <= 16
+                           (one token, or a few draft tokens at the end of
+                           each sequence with the reference's bottom-right
+                           causal mask), optional k/v append (append kernel,
+                           then decode over seqlens + S_new, then
+                           cache_seqlens += S_new on the device).
+  flash_attn_func          q_len QL with QL * GQ <= 16: k/v [B, S, HKV, D] is a
+                           dense cache of S tokens per sequence.
   flash_attn_varlen_func   every sequence has at most one query token: packed
                            k/v are a cache of one-token pages whose block table
                            row b is cu_seqlens_k[b] + arange(max_seqlen_k).
@@ -28,6 +31,14 @@ from . import native
 from .dispatch import DecodeRoute
 
 _ACCEL = {"cuda"}
+
+
+def _query_length_reason(q: torch.Tensor, kv_heads: int) -> str | None:
+    """q is [B, QL, HQ, D]: QL query tokens x GQ heads fill the kernel's columns."""
+    ql, gq = q.shape[1], q.shape[-2] // kv_heads
+    if ql < 1 or ql * gq > native.KERNEL_COLUMNS:
+        return f"query_length_{ql}_times_gqa_{gq}_exceeds_{native.KERNEL_COLUMNS}"
+    return None
 
 
 def _common_reason(q: torch.Tensor, kv_heads: int, head_dim: int) -> str | None:
@@ -69,11 +80,10 @@ def _dense_table(batch: int, pages_per_seq: int, device: torch.device) -> torch.
 
 def route_kvcache(q, k_cache, v_cache, k, v, cache_seqlens, block_table, scale,
                   causal) -> DecodeRoute:
-    reason = _common_reason(q, k_cache.shape[2], q.shape[-1])
+    reason = _common_reason(q, k_cache.shape[2], q.shape[-1]) or _query_length_reason(
+        q, k_cache.shape[2])
     if reason is not None:
         return DecodeRoute(reason)
-    if q.shape[1] != 1:
-        return DecodeRoute(f"query_length_{q.shape[1]}_is_not_single_token_decode")
     if k_cache.stride(-1) != 1 or v_cache.stride() != k_cache.stride():
         return DecodeRoute("cache_layout_not_supported")
     if block_table is None:
@@ -96,7 +106,8 @@ def route_kvcache(q, k_cache, v_cache, k, v, cache_seqlens, block_table, scale,
         new = 0 if k is None else k.shape[1]
         if new:
             native.append_kv(k, v, kc, vc, table, cache_seqlens)
-        out = native.paged_decode_split(q, kc, vc, table, cache_seqlens, scale, seqlen_add=new)
+        out = native.paged_decode_split(q, kc, vc, table, cache_seqlens, scale, seqlen_add=new,
+                                        causal=causal)
         if new:
             cache_seqlens.add_(new)
         return out
@@ -105,11 +116,9 @@ def route_kvcache(q, k_cache, v_cache, k, v, cache_seqlens, block_table, scale,
 
 
 def route_dense(q, k, v, scale, causal) -> DecodeRoute:
-    reason = _common_reason(q, k.shape[2], q.shape[-1])
+    reason = _common_reason(q, k.shape[2], q.shape[-1]) or _query_length_reason(q, k.shape[2])
     if reason is not None:
         return DecodeRoute(reason)
-    if q.shape[1] != 1:
-        return DecodeRoute(f"query_length_{q.shape[1]}_is_not_single_token_decode")
     kc, vc = _dense_as_pages(k), _dense_as_pages(v)
     if kc is None or vc is None or kc.stride(-1) != 1 or vc.stride() != kc.stride():
         return DecodeRoute("dense_kv_not_viewable_as_pages")
@@ -118,7 +127,7 @@ def route_dense(q, k, v, scale, causal) -> DecodeRoute:
         batch = q.shape[0]
         table = _dense_table(batch, kc.shape[0] // batch, q.device)
         lengths = torch.full((batch,), k.shape[1], dtype=torch.int32, device=q.device)
-        return native.paged_decode_split(q, kc, vc, table, lengths, scale)
+        return native.paged_decode_split(q, kc, vc, table, lengths, scale, causal=causal)
 
     return DecodeRoute(None, run)
 

@@ -33,6 +33,7 @@ MXFA_EWORKSPACE = -3
 MXFA_ELAUNCH = -4
 
 DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
+DTYPE_FP8_E4M3 = 2
 # OCP e4m3fn, the fp8 format of gfx950 (MI300's e4m3fnuz is a different code).
 FP8_DTYPE = torch.float8_e4m3fn
 
@@ -41,9 +42,11 @@ FP8_DTYPE = torch.float8_e4m3fn
 SUPPORTED_HEAD_DIMS = (64, 128)
 SUPPORTED_GQA = (2, 4, 8)
 # What the kernels take: head dims 64/128/256, 1..16 query heads per kv head,
-# 16-bit or fp8 caches.
+# 16-bit or fp8 caches; query tokens per sequence x query heads per kv head
+# <= 16 (the MFMA columns).
 KERNEL_HEAD_DIMS = (64, 128, 256)
 KERNEL_GQA = tuple(range(1, 17))
+KERNEL_COLUMNS = 16
 
 # Every entry point declared in include/mxfa_mi355x.h.
 EXPORTED_SYMBOLS = (
@@ -57,6 +60,7 @@ EXPORTED_SYMBOLS = (
     "mxfa_split_decode_combine_launch",
     "mxfa_split_decode_fp8_launch",
     "mxfa_split_decode_fp8_partial_launch",
+    "mxfa_split_decode_multi_launch",
     "mxfa_reshape_and_cache_launch",
     "mxfa_reshape_and_cache_fp8_launch",
     "mxfa_append_kv_launch",
@@ -90,6 +94,11 @@ _SIGNATURES = {
     "mxfa_split_decode_partial_launch": (_i, _SPLIT_ARGS + [_p]),
     "mxfa_split_decode_fp8_launch": (_i, _SPLIT_ARGS + [_p, _p, _p]),
     "mxfa_split_decode_fp8_partial_launch": (_i, _SPLIT_ARGS + [_p, _p, _p]),
+    "mxfa_split_decode_multi_launch": (
+        _i,
+        [_p, _i64, _i64, _i64, _i, _i, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _p, _i64,
+         _i64, _i64, _p, _sz, _f, _i, _i, _i, _i, _i, _i, _i, _i, _i, _p, _p, _i, _p],
+    ),
     "mxfa_split_decode_combine_launch": (
         _i,
         [_p, _sz, _p, _i64, _i64, _i, _i, _i, _i, _i, _i, _p],
@@ -273,8 +282,8 @@ def _require_device(*tensors: torch.Tensor) -> torch.device:
 
 def check_decode_shapes(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
     """Raise UnsupportedConfig when the kernel contract does not cover the call."""
-    if q.dim() not in (3, 4) or (q.dim() == 4 and q.shape[1] != 1):
-        raise UnsupportedConfig(f"q must be [B,1,HQ,HD] or [B,HQ,HD], got {tuple(q.shape)}")
+    if q.dim() not in (3, 4) or (q.dim() == 4 and q.shape[1] < 1):
+        raise UnsupportedConfig(f"q must be [B,QL,HQ,HD] or [B,HQ,HD], got {tuple(q.shape)}")
     if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
         raise UnsupportedConfig("caches must be [pages, page_size, kv_heads, head_dim]")
     hq, hd = q.shape[-2], q.shape[-1]
@@ -283,6 +292,9 @@ def check_decode_shapes(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
         raise UnsupportedConfig(f"head_dim {hd} not in {KERNEL_HEAD_DIMS}")
     if hkv <= 0 or hq % hkv or hq // hkv not in KERNEL_GQA:
         raise UnsupportedConfig(f"GQA ratio {hq}/{hkv} not in 1..16")
+    ql = q.shape[1] if q.dim() == 4 else 1
+    if ql * (hq // hkv) > KERNEL_COLUMNS:
+        raise UnsupportedConfig(f"{ql} query tokens x GQA {hq // hkv} exceeds {KERNEL_COLUMNS}")
     if q.dtype not in DTYPE_CODES:
         raise UnsupportedConfig("q must be float16 or bfloat16")
     if v_cache.dtype != k_cache.dtype or k_cache.dtype not in (q.dtype, FP8_DTYPE):
@@ -332,7 +344,8 @@ def _prepare(q, k_cache, v_cache, block_table, cache_seqlens, out):
     check_decode_shapes(q, k_cache, v_cache)
     batch = q.shape[0]
     hd = q.shape[-1]
-    if q.stride(-1) != 1 or (q.shape[-2] > 1 and q.stride(-2) < hd):
+    if q.stride(-1) != 1 or (q.shape[-2] > 1 and q.stride(-2) < hd) or (
+            q.dim() == 4 and q.shape[1] > 1 and q.stride(1) % 8):
         q = q.contiguous()
     if k_cache.stride(-1) != 1 or v_cache.stride() != k_cache.stride():
         raise UnsupportedConfig("k_cache and v_cache must share strides with a contiguous last dim")
@@ -351,6 +364,23 @@ def _prepare(q, k_cache, v_cache, block_table, cache_seqlens, out):
         raise ValueError("out must match q's shape and dtype with a contiguous last dim")
     _require_device(q, out)
     return q, block_table, cache_seqlens, out
+
+
+def _launch_multi(q, k_cache, v_cache, block_table, cache_seqlens, out, workspace, ws_bytes,
+                  softmax_scale, num_splits, seqlen_add, stream, causal, k_scale, v_scale):
+    batch, ql, hq, hd = q.shape
+    pages, ps, hkv = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
+    qs, os_, cs = q.stride(), out.stride(), k_cache.stride()
+    fp8 = k_cache.dtype == FP8_DTYPE
+    rc = library().mxfa_split_decode_multi_launch(
+        q.data_ptr(), qs[0], qs[1], qs[2], ql, int(bool(causal)), k_cache.data_ptr(),
+        v_cache.data_ptr(), cs[0], cs[1], cs[2], block_table.data_ptr(), block_table.stride(0),
+        cache_seqlens.data_ptr(), seqlen_add, out.data_ptr(), os_[0], os_[1], os_[2], workspace,
+        ws_bytes, float(softmax_scale), batch, hq, hkv, hd, ps, block_table.shape[1], pages,
+        DTYPE_CODES[q.dtype], DTYPE_FP8_E4M3 if fp8 else DTYPE_CODES[q.dtype],
+        _scale_ptr(k_scale, q.device, "k_scale") if fp8 else 0,
+        _scale_ptr(v_scale, q.device, "v_scale") if fp8 else 0, num_splits, stream)
+    _check(rc, "mxfa_split_decode_multi_launch")
 
 
 def default_num_splits(q: torch.Tensor, k_cache: torch.Tensor, block_table: torch.Tensor) -> int:
@@ -372,10 +402,13 @@ def paged_decode_split(
     seqlen_add: int = 0,
     k_scale: torch.Tensor | float | None = None,
     v_scale: torch.Tensor | float | None = None,
+    causal: bool = False,
 ) -> torch.Tensor:
     """Split-KV paged decode on the current stream; returns ``out`` shaped like q.
 
-    q: [B, 1, HQ, HD] or [B, HQ, HD] (any strides with a contiguous last dim);
+    q: [B, QL, HQ, HD] or [B, HQ, HD] (any strides with a contiguous last dim);
+    QL > 1 query tokens sit at the last QL positions of each sequence, and
+    ``causal`` masks the keys after each one (QL * HQ/HKV <= 16);
     caches: [pages, PS, HKV, HD] of q's dtype, or float8_e4m3fn with the
     per-tensor dequantisation scales k_scale / v_scale (float32 device scalars
     for graph capture); block_table: int32 [B, W]; cache_seqlens: int32 [B].
@@ -388,8 +421,14 @@ def paged_decode_split(
     if num_splits is None:
         num_splits = default_num_splits(q, k_cache, block_table)
     stream = _stream_handle(q.device)
-    ws_bytes = workspace_size(q.shape[0], q.shape[-2], q.shape[-1], num_splits)
+    ql = q.shape[1] if q.dim() == 4 else 1
+    ws_bytes = workspace_size(q.shape[0], q.shape[-2] * ql, q.shape[-1], num_splits)
     ws = WORKSPACE.get(q.device, stream, ws_bytes)
+    if ql > 1:
+        _launch_multi(q, k_cache, v_cache, block_table, cache_seqlens, out, ws.data_ptr(),
+                      ws_bytes, softmax_scale, num_splits, seqlen_add, stream, causal, k_scale,
+                      v_scale)
+        return out
     args = _launch_args(q, k_cache, v_cache, block_table, cache_seqlens, out, ws.data_ptr(),
                         ws_bytes, softmax_scale, num_splits, seqlen_add, stream)
     if k_cache.dtype == FP8_DTYPE:

@@ -262,10 +262,22 @@ def test_kvcache_route_qualification(hq, hkv, hd, dtype, reason):
 
 
 def test_kvcache_route_declines_prefill_and_odd_pages():
-    q = fake_cuda(torch.empty(4, 2, 32, 128, dtype=torch.bfloat16))
     cache = fake_cuda(torch.empty(10, 16, 8, 128, dtype=torch.bfloat16))
+    # A few draft tokens per sequence fit the 16 kernel columns (QL x GQ <= 16);
+    # longer queries (prefill) are declined.
+    for ql in (2, 4):
+        q = fake_cuda(torch.empty(4, ql, 32, 128, dtype=torch.bfloat16))
+        route = decode.route_kvcache(q, cache, cache, None, None, None, torch.empty(4, 2), 0.1,
+                                     True)
+        assert route.reason is None and route.run is not None
+    q = fake_cuda(torch.empty(4, 5, 32, 128, dtype=torch.bfloat16))
     assert decode.route_kvcache(q, cache, cache, None, None, None, torch.empty(4, 2), 0.1,
-                                False).reason.startswith("query_length_2")
+                                False).reason.startswith("query_length_5_times_gqa_4")
+    q = fake_cuda(torch.empty(4, 2, 32, 128, dtype=torch.bfloat16))
+    q16 = fake_cuda(torch.empty(4, 2, 32, 128, dtype=torch.bfloat16))
+    cache2 = fake_cuda(torch.empty(10, 16, 2, 128, dtype=torch.bfloat16))  # GQ 16
+    assert decode.route_kvcache(q16, cache2, cache2, None, None, None, torch.empty(4, 2), 0.1,
+                                False).reason.startswith("query_length_2_times_gqa_16")
     q1 = fake_cuda(torch.empty(4, 1, 32, 128, dtype=torch.bfloat16))
     odd = fake_cuda(torch.empty(10, 12, 8, 128, dtype=torch.bfloat16))
     assert decode.route_kvcache(q1, odd, odd, None, None, None, torch.empty(4, 2), 0.1,

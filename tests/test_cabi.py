@@ -44,7 +44,7 @@ def test_library_loads_and_reports_header_abi(lib):
 
 def test_every_header_function_is_exported_and_bound(lib):
     declared = header_functions()
-    assert len(declared) == len(set(declared)) == 13
+    assert len(declared) == len(set(declared)) == 14
     for name in declared:
         assert hasattr(lib, name), name
     assert set(declared) == set(native.EXPORTED_SYMBOLS) == set(native._SIGNATURES)
@@ -191,6 +191,34 @@ def test_fp8_decode_rejects_misaligned_scale_pointers(lib):
     odd = decode_args(c_st=8 * 128 + 8, ws_bytes=1000)
     assert lib.mxfa_split_decode_launch(*odd) == -3  # strides pass, workspace fails
     assert lib.mxfa_split_decode_fp8_launch(*odd[:-1], FAKE, FAKE, None) == -2
+
+
+def multi_args(**over):
+    """A well-formed argument tuple for mxfa_split_decode_multi_launch (QL = 2)."""
+    a = dict(q=FAKE, q_sb=2 * 32 * 128, q_st=32 * 128, q_sh=128, ql=2, causal=1, k=FAKE, v=FAKE,
+             c_sp=16 * 8 * 128, c_st=8 * 128, c_sh=128, bt=FAKE, bt_stride=64, seqlens=FAKE,
+             seqlen_add=0, out=FAKE, o_sb=2 * 32 * 128, o_st=32 * 128, o_sh=128, ws=FAKE,
+             ws_bytes=1 << 30, scale=0.088, batch=32, hq=32, hkv=8, hd=128, ps=16, btw=64,
+             pages=4096, dtype=1, kv_dtype=1, ks=None, vs=None, ns=32, stream=None)
+    a.update(over)
+    return tuple(a.values())
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(ql=0), -2), (dict(ql=5), -1), (dict(ql=2, hkv=2), -1),   # QL x GQ > 16
+    (dict(q_st=100), -2), (dict(o_st=130), -2),
+    (dict(o_st=128, o_sh=128), -2),                                 # token rows overlap heads
+    (dict(kv_dtype=0), -1), (dict(kv_dtype=2, ks=FAKE + 1), -2),
+    (dict(ws_bytes=native.workspace_size(32, 32, 128, 32)), -3),     # sized for QL = 1
+    (dict(hd=96), -1), (dict(q=None), -2),
+])
+def test_multi_launch_rejects_before_launching(lib, over, code):
+    assert lib.mxfa_split_decode_multi_launch(*multi_args(**over)) == code
+
+
+def test_multi_launch_workspace_is_per_query_token(lib):
+    need = native.workspace_size(32, 64, 128, 32)  # q_heads x q_len rows
+    assert lib.mxfa_split_decode_multi_launch(*multi_args(ws_bytes=need - 1)) == -3
 
 
 def test_combine_rejects_before_launching(lib):

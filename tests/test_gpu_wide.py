@@ -226,3 +226,96 @@ def test_fp8_reshape_and_cache_keeps_nan_and_saturates_inf(device):
     assert int(row[0]) & 0x7F == 0x7F  # NaN stays NaN
     assert int(row[1]) == 0x7E and int(row[2]) == 0xFE  # +-448
     assert int(row[3]) == 0x80  # -0
+
+
+# ---------------------------------------------------------------------------
+# Several query tokens per sequence (decode with draft tokens)
+
+
+def port_expected(b, causal: bool) -> torch.Tensor:
+    """fp32 restatement of reference.attention_kvcache (bottom-right causal mask)."""
+    from oracle import reference_port
+
+    cpu = b.to("cpu")
+    out = torch.zeros(cpu.q.shape, dtype=torch.float32)
+    for i in range(cpu.batch):  # the reference raises on an empty sequence; zeros here
+        if int(cpu.cache_seqlens[i]) == 0:
+            continue
+        out[i:i + 1] = reference_port.attention_kvcache(
+            cpu.q[i:i + 1].float(), cpu.k_cache.float(), cpu.v_cache.float(),
+            cache_seqlens=cpu.cache_seqlens[i:i + 1].clone(), block_table=cpu.block_table[i:i + 1],
+            softmax_scale=cpu.scale, causal=causal).float()
+    return out
+
+
+def with_query_tokens(b, ql: int, seed: int):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(b.batch, ql, b.q_heads, b.head_dim, generator=g).to(b.q.dtype)
+    b.q = q.to(b.q.device)
+    return b
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("ql,gq", [(2, 1), (2, 4), (3, 4), (4, 4), (2, 8), (8, 2), (16, 1)])
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "full"])
+def test_query_tokens_match_reference(device, dtype, head_dim, ql, gq, causal):
+    # Lengths shorter than QL leave the first tokens without keys (zeros).
+    lengths = torch.tensor([1, 2, 17, 300, 0, 1000])
+    b = make_paged_batch(6, 2 * gq, 2, head_dim, dtype, lengths, seed=60 + ql).to(device)
+    b = with_query_tokens(b, ql, 61)
+    expected = port_expected(b, causal)
+    for ns in (None, 1, 9, 64):
+        kw = {} if ns is None else dict(num_splits=ns)
+        got = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table,
+                                        b.cache_seqlens, b.scale, causal=causal, **kw)
+        torch.cuda.synchronize()
+        assert got.shape == b.q.shape
+        assert torch.isfinite(got.float()).all()
+        assert max_err(got, expected) <= TOL[dtype], (ns, max_err(got, expected))
+        assert torch.equal(got[4].cpu(), torch.zeros_like(got[4].cpu()))
+
+
+def test_query_tokens_fp8_and_head_dim_256(device):
+    b = make_paged_batch(4, 8, 2, 256, torch.bfloat16, torch.tensor([3, 64, 500, 1200]),
+                         seed=70).to(device)
+    b = with_query_tokens(b, 3, 71)
+    assert max_err(native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table,
+                                             b.cache_seqlens, b.scale, causal=True),
+                   port_expected(b, True)) <= TOL[torch.bfloat16]
+    k8, v8 = fp8_caches(b, device)
+    b8 = type(b)(b.q, k8.cpu().float().to(torch.bfloat16).to(device),
+                 v8.cpu().float().to(torch.bfloat16).to(device), b.block_table, b.cache_seqlens,
+                 b.scale)  # the exactly dequantised caches, scales 1
+    got = native.paged_decode_split(b.q, k8, v8, b.block_table, b.cache_seqlens, b.scale,
+                                    causal=True)
+    torch.cuda.synchronize()
+    assert max_err(got, port_expected(b8, True)) <= TOL[torch.bfloat16]
+
+
+def test_query_tokens_through_the_api_with_append(device):
+    """flash_attn_with_kvcache with two new tokens per sequence: append, then
+    causal decode of both, then lengths advanced; against the reference port."""
+    import mxflashattn_amd as mx
+    from oracle import reference_port
+
+    b = make_paged_batch(3, 16, 4, 128, torch.bfloat16, torch.tensor([5, 90, 400]),
+                         block_table_width=40, seed=80)
+    g = torch.Generator().manual_seed(81)
+    q = torch.randn(3, 2, 16, 128, generator=g).to(torch.bfloat16)
+    k_new = torch.randn(3, 2, 4, 128, generator=g).to(torch.bfloat16)
+    v_new = torch.randn(3, 2, 4, 128, generator=g).to(torch.bfloat16)
+    kc, vc, sl = b.k_cache.clone(), b.v_cache.clone(), b.cache_seqlens.clone()
+    expected = reference_port.attention_kvcache(
+        q.float(), kc.float(), vc.float(), cache_seqlens=sl, block_table=b.block_table,
+        k=k_new.float(), v=v_new.float(), softmax_scale=b.scale, causal=True).float()
+    gpu = b.to(device)
+    lens = gpu.cache_seqlens.clone()
+    out = mx.flash_attn_with_kvcache(q.to(device), gpu.k_cache, gpu.v_cache, k=k_new.to(device),
+                                     v=v_new.to(device), cache_seqlens=lens,
+                                     block_table=gpu.block_table, softmax_scale=b.scale,
+                                     causal=True)
+    torch.cuda.synchronize()
+    assert mx.get_last_dispatch_info().backend == mx.BACKEND_MI355X
+    assert max_err(out, expected) <= TOL[torch.bfloat16]
+    assert lens.cpu().tolist() == (b.cache_seqlens + 2).tolist()
