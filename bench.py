@@ -20,7 +20,8 @@ Prints ONE JSON line:
                (oracle.reference_port) on the host cores, bounded sample
   cells        the six GQ x HD cells of config 2 and configs 1, 3, 4
   wide         shapes beyond the reference's contract at config 2's batch and
-               lengths: fp8 (e4m3fn) caches, head dim 256, GQ 1 and 16
+               lengths: fp8 (e4m3fn) caches, head dim 256, GQ 1 and 16, and
+               4 query tokens per sequence (causal draft-token verification)
   decode_step  config 5: decode tok/s of a 36-layer random-init Qwen3-4B-shaped
                model whose attention runs through the vLLM backend path
                (HIP-graph replayed steps), and attention's share of the step;
@@ -68,7 +69,7 @@ def build_pools(spec: dict, device: torch.device):
     """One batch plus extra copies of its caches so the rotation covers >= 1 GB."""
     from mxflashattn_amd.workloads import make_paged_batch
 
-    base = make_paged_batch(**spec, device=device)
+    base = make_paged_batch(**{k: v for k, v in spec.items() if k != "causal"}, device=device)
     cache_bytes = 2 * base.k_cache.numel() * base.k_cache.element_size()
     copies = max(2, math.ceil(ROTATE_BYTES / max(1, cache_bytes)))
     pools = [(base.k_cache, base.v_cache)]
@@ -140,9 +141,11 @@ def measure_workload(name: str, spec: dict, device, steps: int, warmup: int) -> 
     out = torch.empty_like(base.q)
     ns = native.default_num_splits(base.q, base.k_cache, base.block_table)
 
+    causal = bool(spec.get("causal", False))
+
     def call(kc, vc):
         native.paged_decode_split(base.q, kc, vc, base.block_table, base.cache_seqlens,
-                                  base.scale, out=out, num_splits=ns)
+                                  base.scale, out=out, num_splits=ns, causal=causal)
 
     us_eager, us_eager_mean = time_calls(call, pools, steps, warmup, stream)
     side = torch.cuda.Stream(device)
@@ -156,7 +159,7 @@ def measure_workload(name: str, spec: dict, device, steps: int, warmup: int) -> 
         native.split_decode_partial(base.q, kc, vc, base.block_table, base.cache_seqlens,
                                     base.scale, out, ws, ns)
 
-    us_partial = time_graph(partial, pools, steps, warmup, side)
+    us_partial = time_graph(partial, pools, steps, warmup, side) if base.q.shape[1] == 1 else None
     kv = base.kv_bytes()
     alg = base.algorithmic_bytes()
     gbs = kv / (us_graph * 1e-6) / 1e9
@@ -170,8 +173,8 @@ def measure_workload(name: str, spec: dict, device, steps: int, warmup: int) -> 
         "kv_bytes": kv,
         "algorithmic_bytes": alg,
         "alg_gb_s": round(alg / (us_graph * 1e-6) / 1e9, 1),
-        "partial_kernel_us": round(us_partial, 3),
-        "partial_kernel_gb_s": round(alg / (us_partial * 1e-6) / 1e9, 1),
+        "partial_kernel_us": round(us_partial, 3) if us_partial else None,
+        "partial_kernel_gb_s": round(alg / (us_partial * 1e-6) / 1e9, 1) if us_partial else None,
         "num_splits": ns,
         "rotation_copies": len(pools),
     }

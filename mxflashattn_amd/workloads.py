@@ -83,6 +83,7 @@ def make_paged_batch(
     seed: int = DEFAULT_SEED,
     device: torch.device | str = "cpu",
     kv_dtype: torch.dtype | None = None,
+    q_len: int = 1,
 ) -> PagedBatch:
     """Build one synthetic decode batch.
 
@@ -92,7 +93,8 @@ def make_paged_batch(
     sequence gets distinct pages from a random permutation of the pool.
     peaky_fraction of the K rows are multiplied by peaky_scale. kv_dtype
     float8_e4m3fn stores the caches as fp8 (the same N(0, 1) draws, rounded to
-    nearest even; their dequantisation scales are 1).
+    nearest even; their dequantisation scales are 1). q_len > 1 gives every
+    sequence that many query tokens (the last q_len positions of its length).
     """
     device = torch.device(device)
     gen = torch.Generator(device=device)
@@ -122,7 +124,7 @@ def make_paged_batch(
     def randn(*shape: int) -> torch.Tensor:
         return torch.randn(*shape, generator=gen, device=device, dtype=torch.float32).to(dtype)
 
-    q = randn(batch, 1, q_heads, head_dim)
+    q = randn(batch, q_len, q_heads, head_dim)
     k_cache = randn(num_pages, page_size, kv_heads, head_dim)
     v_cache = randn(num_pages, page_size, kv_heads, head_dim)
     if peaky_fraction > 0:
@@ -178,4 +180,8 @@ WIDE = {
                           dtype=torch.bfloat16, lengths=(1024, 8192)),
     "wide_gq16_d128": dict(batch=32, q_heads=64, kv_heads=4, head_dim=128,
                            dtype=torch.bfloat16, lengths=(1024, 8192)),
+    # Config 2 verifying 4 tokens per sequence (3 draft tokens), causal: the
+    # same KV bytes as one token.
+    "wide_q4_config2": dict(batch=32, q_heads=32, kv_heads=8, head_dim=128,
+                            dtype=torch.bfloat16, lengths=(1024, 8192), q_len=4, causal=True),
 }
