@@ -10,8 +10,10 @@ head dim outside {64, 128}, GQA ratio outside {2, 4, 8}, or a page size that is
 not a power of two. The caller then runs the original implementation.
 
 MXFA_WIDE_CONTRACT=1 widens the guards to what the kernels take: head dim 256,
-1..16 query heads per kv head, and fp8 (e4m3fn) caches with per-tensor
-k_descale / v_descale (a scalar, or a tensor expanded from one).
+1..16 query heads per kv head, fp8 (e4m3fn) caches with per-tensor
+k_descale / v_descale (a scalar, or a tensor expanded from one), and q of
+[B, QL, HQ, D] with QL x GQ <= 16 (draft-token verification, with the call's
+causal flag).
 
 ``mx_kvcache_compat`` replaces ``_mx_kvcache_compat`` (:319-349): it drops
 vLLM-only keyword arguments, tries the native route, else the original vendor
@@ -80,7 +82,7 @@ def _guard(args: tuple, kwargs: dict, wide: bool = False,
         return "dtype", ()
     if fp8 and not all(_per_tensor(d) for d in descales):
         return "descale_not_per_tensor", ()
-    if q.dim() == 4 and q.shape[1] != 1:
+    if q.dim() == 4 and q.shape[1] != 1 and not wide:
         return "query_length", ()
     if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
         return "cache_rank", ()
@@ -91,6 +93,8 @@ def _guard(args: tuple, kwargs: dict, wide: bool = False,
         return "head_dim", ()
     if hkv <= 0 or hq % hkv or hq // hkv not in gqa:
         return "gqa_ratio", ()
+    if q.dim() == 4 and q.shape[1] * (hq // hkv) > native.KERNEL_COLUMNS:
+        return "query_length", ()
     ps = k_cache.shape[1]
     if ps <= 0 or ps & (ps - 1) or ps > 4096:
         return "page_size", ()
@@ -126,7 +130,8 @@ def try_native_decode(args: tuple, kwargs: dict, k_descale: Any = None,
     if k_cache.dtype == native.FP8_DTYPE:
         scales = {"k_scale": k_descale, "v_scale": v_descale}
     result = native.paged_decode_split(q4, k_cache, v_cache, bt, sl, scale, out=out,
-                                       num_splits=ns, **scales)
+                                       num_splits=ns, causal=bool(kwargs.get("causal", False)),
+                                       **scales)
     if provided is not None and out is None:
         provided.copy_(result.reshape_as(provided))
         result = provided

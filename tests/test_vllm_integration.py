@@ -189,3 +189,15 @@ def test_guard_wide_contract_opt_in(monkeypatch):
     assert call(32, 8, 128, torch.float8_e4m3fn, torch.ones(4, 8)) == "descale_not_per_tensor"
     assert call(34, 2, 128) == "gqa_ratio"
     assert call(32, 8, 96) == "head_dim"
+
+    def call_ql(ql, hq, hkv):
+        q = torch.empty(4, ql, hq, 128, dtype=torch.bfloat16)
+        cache = torch.empty(10, 16, hkv, 128, dtype=torch.bfloat16)
+        kwargs = {"k_cache": cache, "v_cache": cache, "block_table": torch.zeros(4, 2),
+                  "cache_seqlens": torch.ones(4), "causal": True}
+        return native_decode._guard((q,), kwargs, native_decode.wide_contract())[0]
+
+    assert call_ql(4, 32, 8) == "device"       # 4 tokens x GQ 4 = 16 columns
+    assert call_ql(5, 32, 8) == "query_length"
+    monkeypatch.delenv("MXFA_WIDE_CONTRACT")
+    assert call_ql(2, 32, 8) == "query_length"  # the reference's guard
