@@ -433,10 +433,10 @@ struct Tile {
   int pg;  // page id (block-table entry), page-uniform tiles only
 };
 
-// One wave: the tiles [lo, hi) of kv head kvh, range rr of R. HR = head rows
-// (GQ <= 4 HR), T = element type of q, out and the MFMA operands, kF8 = e4m3fn
-// caches. Accumulator lane (r, c) holds heads 4r..4r+3, dims c*VD + jb in
-// block jb.
+// One wave: the tiles [lo, hi) of kv head kvh, range rr of R. HR = DPP rows
+// holding used columns (GQ*QL <= 4 HR), T = element type of q, out and the MFMA
+// operands, kF8 = e4m3fn caches. Accumulator lane (r, c) holds columns
+// 4r..4r+3, dims c*VD + jb in block jb.
 template <int HD, int HR, typename T, bool kF8, bool kLanePages, int NBUF>
 __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *s_tiles, int kvh,
                                           int rr, int R, int NT, int lo, int hi) {
@@ -453,7 +453,7 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
 
   const int lane = threadIdx.x & 63;
   const int row = lane >> 4;  // DPP row
-  const int col = lane & 15;  // head (score layout) / V column
+  const int col = lane & 15;  // column (score layout) / V column
   const int ps_mask = (1 << p.ps_log2) - 1;
   const uint32_t st = p.st_bytes;
   const uint64_t head_off = (uint64_t)kvh * p.sh_bytes;
@@ -466,7 +466,7 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   const int ns = p.num_ranges;  // workspace stride
 
   // Lane offsets inside a tile: K in the MFMA A layout, V row-contiguous, q as
-  // the MFMA B operand (columns >= GQ read nothing). For fp8 caches step
+  // the MFMA B operand (columns >= GQ*QL read nothing). For fp8 caches step
   // 2m + s of lane row r covers dims 64m + 16r + 8s .. +7; q follows it.
   const int k_off = col * (int)st + row * 16;
   int v_off[U];
@@ -594,8 +594,8 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   };
 
   // Running state of the current piece.
-  float m = -INFINITY;  // reference max (base 2) of head `col`, same in every row
-  float dsum = 0.f;     // partial denominator of head `col` over this row's tokens
+  float m = -INFINITY;  // reference max (base 2) of column `col`, same in every row
+  float dsum = 0.f;     // partial denominator of column `col` over this row's tokens
   f32x4 oacc[VD];       // PV accumulators
   uint4 qf[NCH];
   auto clear_acc = [&]() {
@@ -689,7 +689,7 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
       });
       m = mn;
     }
-    // m = -inf: this head has seen no valid token, its scores here are -inf too.
+    // m = -inf: this column has seen no valid token, its scores here are -inf too.
     const float mr = m == -INFINITY ? 0.f : m;
     float pr[4];
 #pragma unroll
