@@ -319,3 +319,25 @@ def test_query_tokens_through_the_api_with_append(device):
     assert mx.get_last_dispatch_info().backend == mx.BACKEND_MI355X
     assert max_err(out, expected) <= TOL[torch.bfloat16]
     assert lens.cpu().tolist() == (b.cache_seqlens + 2).tolist()
+
+
+@pytest.mark.parametrize("sq,sk", [(1, 70), (3, 70), (4, 4), (4, 2)])
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "full"])
+def test_dense_query_tokens_through_flash_attn_func(device, sq, sk, causal):
+    """flash_attn_func with a few query tokens runs on the HIP kernels (dense
+    k/v viewed as pages) and matches the reference's batched attention,
+    bottom-right causal mask included (sq > sk leaves the first rows empty)."""
+    import mxflashattn_amd as mx
+    from oracle import reference_port
+
+    g = torch.Generator().manual_seed(90 + sq)
+    q = torch.randn(3, sq, 8, 64, generator=g).to(torch.float16)
+    k = torch.randn(3, sk, 2, 64, generator=g).to(torch.float16)
+    v = torch.randn(3, sk, 2, 64, generator=g).to(torch.float16)
+    expected = reference_port.attention_batched(q.float(), k.float(), v.float(),
+                                                softmax_scale=0.125, causal=causal).float()
+    out = mx.flash_attn_func(q.to(device), k.to(device), v.to(device), softmax_scale=0.125,
+                             causal=causal)
+    torch.cuda.synchronize()
+    assert mx.get_last_dispatch_info().backend == mx.BACKEND_MI355X
+    assert max_err(out, expected) <= TOL[torch.float16]
