@@ -1,0 +1,87 @@
+"""A seeded random sweep over the whole kernel contract against the oracles.
+
+Each case draws a shape (batch, kv heads, GQ, head dim, page size, lengths
+including 0 and lengths shorter than the query tokens), a query token count
+with QL x GQ <= 16, causal or not, fp16/bf16, an fp8 cache or not, strided q
+and out, a head-major or token-major cache, and a split count, then compares
+the HIP result with the reference port (fp32; exactly dequantised caches for
+fp8) at the north-star tolerances. Seeds are fixed: every run checks the same
+cases.
+"""
+
+from __future__ import annotations
+
+import random
+
+import pytest
+import torch
+
+from mxflashattn_amd import native
+from mxflashattn_amd.workloads import make_paged_batch
+from oracle import reference_port
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float16: 2e-3, torch.bfloat16: 1.6e-2}
+FP8 = torch.float8_e4m3fn
+
+
+def draw(seed: int) -> dict:
+    r = random.Random(seed)
+    hkv = r.choice([1, 2, 3, 4, 8])
+    gq = r.choice([1, 2, 3, 4, 5, 8, 16])
+    ql = r.choice([q for q in (1, 1, 1, 2, 3, 4, 8) if q * gq <= 16])
+    batch = r.randint(1, 9)
+    ps = r.choice([1, 2, 8, 16, 16, 16, 64, 256])
+    lengths = [r.choice([0, 1, 2, r.randint(3, 40), r.randint(40, 700), r.randint(700, 3000)])
+               for _ in range(batch)]
+    return dict(hkv=hkv, gq=gq, ql=ql, batch=batch, ps=ps, lengths=lengths,
+                hd=r.choice([64, 128, 256]), dtype=r.choice([torch.float16, torch.bfloat16]),
+                fp8=r.random() < 0.3, causal=r.random() < 0.6, strided=r.random() < 0.4,
+                head_major=r.random() < 0.25, ns=r.choice([None, None, 1, 3, 17, 300]))
+
+
+def expected(q, kc, vc, bt, sl, scale, causal) -> torch.Tensor:
+    out = torch.zeros(q.shape, dtype=torch.float32)
+    for i in range(q.shape[0]):
+        if int(sl[i]) == 0:  # the reference raises on an empty sequence; the kernel gives 0
+            continue
+        out[i:i + 1] = reference_port.attention_kvcache(
+            q[i:i + 1].float(), kc.float(), vc.float(), cache_seqlens=sl[i:i + 1].clone(),
+            block_table=bt[i:i + 1], softmax_scale=scale, causal=causal).float()
+    return out
+
+
+@pytest.mark.parametrize("seed", range(150))
+def test_random_contract_sweep(device, seed):
+    c = draw(seed)
+    hq = c["hkv"] * c["gq"]
+    b = make_paged_batch(c["batch"], hq, c["hkv"], c["hd"], c["dtype"],
+                         torch.tensor(c["lengths"]), page_size=c["ps"], seed=1000 + seed,
+                         q_len=c["ql"])
+    kc, vc = b.k_cache, b.v_cache
+    if c["fp8"]:
+        kc, vc = kc.to(FP8), vc.to(FP8)
+    ref = expected(b.q, kc, vc, b.block_table, b.cache_seqlens, b.scale, c["causal"])
+    kd, vd = kc.to(device), vc.to(device)
+    if c["head_major"]:  # [pages, HKV, PS, HD] storage viewed as [pages, PS, HKV, HD]
+        kd = kd.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+        vd = vd.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+    q = b.q.to(device)
+    out = None
+    if c["strided"]:  # q and out as slices of wider buffers
+        wide = torch.randn(c["batch"], c["ql"], hq + 3, c["hd"], device=device).to(c["dtype"])
+        wide[:, :, 2:2 + hq] = q
+        q = wide[:, :, 2:2 + hq]
+        obuf = torch.zeros(c["batch"], c["ql"], hq + 5, c["hd"], device=device, dtype=c["dtype"])
+        out = obuf[:, :, 1:1 + hq]
+    kw = {} if c["ns"] is None else dict(num_splits=c["ns"])
+    got = native.paged_decode_split(q, kd, vd, b.block_table.to(device),
+                                    b.cache_seqlens.to(device), b.scale, out=out,
+                                    causal=c["causal"], **kw)
+    torch.cuda.synchronize()
+    err = (got.float().cpu() - ref).abs().max().item()
+    assert err <= TOL[c["dtype"]], (c, err)
+    if out is not None:  # nothing written outside the slice
+        assert torch.equal(obuf[:, :, :1].cpu(), torch.zeros_like(obuf[:, :, :1].cpu()))
+        assert torch.equal(obuf[:, :, 1 + hq:].cpu(), torch.zeros_like(obuf[:, :, 1 + hq:].cpu()))
