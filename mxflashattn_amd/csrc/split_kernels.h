@@ -316,6 +316,11 @@ __device__ __forceinline__ void static_for(F &&f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
+// Lane c of each 16-lane row takes the value of lane c ^ 8 (row_ror:8).
+__device__ __forceinline__ uint32_t row_swap8(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x128, 0xf, 0xf, false);
+}
+
 template <int H>
 __device__ __forceinline__ float row_bcast(float x) {
   return __int_as_float(
@@ -445,8 +450,13 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   constexpr int NKL = kF8 ? HD / 64 : NCH;   // 16-byte K loads per lane and tile
   constexpr int VD = HD / 16;                // V elements per lane
   constexpr int VB = kF8 ? VD : 2 * VD;      // V bytes per lane and token
-  constexpr int U = 4;                       // V loads per tile (token 4r+u in DPP row r)
+  constexpr int U = 4;                       // V tokens per lane (token 4r+u in DPP row r)
   constexpr int NPG = kLanePages ? 1 + U : 1;
+  // 8-byte V slots (128-byte rows): lanes c and c^8 of a row load 16 bytes
+  // (slots 2(c&7), 2(c&7)+1) of two tokens each and swap halves, so a tile
+  // takes two 16-byte loads per lane instead of four 8-byte ones. Lane c then
+  // holds slot 2(c&7) + (c>>3).
+  constexpr bool kShareV = VB == 8 && !kLanePages;
   const int B = p.batch;
   const int gq = p.gq;
   const int nc = gq * p.ql;  // used columns
@@ -547,7 +557,8 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
 
   struct Set {
     uint4 k[NKL];
-    Frag<VB> v[U];
+    Frag<VB> v[kShareV ? 1 : U];  // kShareV: unused
+    uint4 vr[kShareV ? 2 : 1];    // kShareV: tokens 4r+2h, 4r+2h+1, 16 bytes each
     uint4 q[NCH];
     int lpg[NPG];
     Tile d;
@@ -570,8 +581,15 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
       const __amdgpu_buffer_rsrc_t rv = make_srd(p.v + tile_off, bytes);
 #pragma unroll
       for (int cc = 0; cc < NKL; ++cc) s.k[cc] = buf_load16<kAuxStream>(rk, k_off + cc * 64);
+      if constexpr (kShareV) {
+        const int t0 = 4 * row + 2 * (col >> 3);
+        const int vo = (col & 7) * 16;
+        s.vr[0] = buf_load16<kAuxStream>(rv, t0 * (int)st + vo);
+        s.vr[1] = buf_load16<kAuxStream>(rv, (t0 + 1) * (int)st + vo);
+      } else {
 #pragma unroll
-      for (int u = 0; u < U; ++u) s.v[u].template load_buf<kAuxStream>(rv, v_off[u]);
+        for (int u = 0; u < U; ++u) s.v[u].template load_buf<kAuxStream>(rv, v_off[u]);
+      }
     } else {
       // Lane pages: every lane addresses its own page; positions past the
       // sequence end were clamped to its last token (their scores are masked).
@@ -607,6 +625,8 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   for (int cc = 0; cc < NCH; ++cc) qf[cc] = make_uint4(0u, 0u, 0u, 0u);
   bool piece_from_start = false;
   bool piece_first_in_range = false;
+  // V slot of this lane: the VD dims it holds (and writes) start at vslot*VD.
+  const int vslot = kShareV ? 2 * (col & 7) + (col >> 3) : col;
 
   auto finalize = [&](const Tile &d) {
     const float dt = rows_sum(dsum);  // lane (any row, h): denominator of head h
@@ -627,10 +647,10 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
       if (whole) {
         const int ht = hh / gq, hg = hh - (hh / gq) * gq;
         store_row<VD, E>(p.out + b * p.o_sb + ht * p.o_st + (kvh * gq + hg) * p.o_sh +
-                             col * (VD * 2),
+                             vslot * (VD * 2),
                          v, inv);
       } else {
-        float4 *dst = reinterpret_cast<float4 *>(p.ws_o + (pbase + hh) * HD + col * VD);
+        float4 *dst = reinterpret_cast<float4 *>(p.ws_o + (pbase + hh) * HD + vslot * VD);
 #pragma unroll
         for (int j = 0; j < VD / 4; ++j)
           dst[j] = make_float4(v[4 * j] * inv, v[4 * j + 1] * inv, v[4 * j + 2] * inv,
@@ -703,17 +723,39 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
             (PvMfma<T>::widen(ph[2]) + PvMfma<T>::widen(ph[3]));
     const uint2 a = make_uint2((uint32_t)ph[0] | ((uint32_t)ph[1] << 16),
                                (uint32_t)ph[2] | ((uint32_t)ph[3] << 16));
-    // V words of the four tokens as element pairs (fp8: widened here, once).
+    // The lane's V bytes of its four tokens (kShareV: halves swapped with lane
+    // c^8 first), then as element pairs (fp8: widened here, once).
+    constexpr int VW = VB / 4;  // words per token
+    uint32_t vt[U][VW];
+    if constexpr (kShareV) {
+      const bool hi = col >= 8;
+      const uint4 a = s.vr[0], bq = s.vr[1];
+      const uint32_t r0 = row_swap8(hi ? a.x : a.z), r1 = row_swap8(hi ? a.y : a.w);
+      const uint32_t r2 = row_swap8(hi ? bq.x : bq.z), r3 = row_swap8(hi ? bq.y : bq.w);
+      vt[0][0] = hi ? r0 : a.x;
+      vt[0][1] = hi ? r1 : a.y;
+      vt[1][0] = hi ? r2 : bq.x;
+      vt[1][1] = hi ? r3 : bq.y;
+      vt[2][0] = hi ? a.z : r0;
+      vt[2][1] = hi ? a.w : r1;
+      vt[3][0] = hi ? bq.z : r2;
+      vt[3][1] = hi ? bq.w : r3;
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int w = 0; w < VW; ++w) vt[u][w] = s.v[u].w[w];
+    }
     uint32_t vw[U][VD / 2];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
 #pragma unroll
       for (int wi = 0; wi < VD / 2; ++wi) {
         if constexpr (kF8)
-          vw[u][wi] = (wi & 1) ? Fp8Widen<T>::template pair<true>(s.v[u].w[wi >> 1])
-                               : Fp8Widen<T>::template pair<false>(s.v[u].w[wi >> 1]);
+          vw[u][wi] = (wi & 1) ? Fp8Widen<T>::template pair<true>(vt[u][wi >> 1])
+                               : Fp8Widen<T>::template pair<false>(vt[u][wi >> 1]);
         else
-          vw[u][wi] = s.v[u].w[wi];
+          vw[u][wi] = vt[u][wi];
       }
     }
 #pragma unroll
