@@ -201,3 +201,23 @@ def test_guard_wide_contract_opt_in(monkeypatch):
     assert call_ql(5, 32, 8) == "query_length"
     monkeypatch.delenv("MXFA_WIDE_CONTRACT")
     assert call_ql(2, 32, 8) == "query_length"  # the reference's guard
+
+
+def test_vllm_compat_release_gate(tmp_path):
+    """Mirrors tests/test_vllm_compat.py of the reference, plus local labels and the report."""
+    from mxflashattn_amd.integrations.vllm import compat
+
+    result = compat.classify_vllm("0.17.0")
+    assert result.supported and result.status == "supported"
+    assert compat.classify_vllm("0.17.1+rocm700").status == "supported"
+    result = compat.classify_vllm("0.30.0")
+    assert not result.supported and result.status == "probe_required"
+    assert compat.classify_vllm(None).status == "not_installed"
+    assert compat.classify_vllm("future-build").status == "unknown"
+    assert compat.classify_vllm("7").status == "unknown"
+    assert compat.classify_vllm("0.40.0").status == "unsupported"
+    assert compat.classify_vllm("0.16.2").status == "unsupported"
+    out = tmp_path / "r" / "vllm.json"
+    report = compat.main(["--output", str(out)])
+    assert json.loads(out.read_text()) == report
+    assert report["status"] == compat.classify_vllm(compat.detect_vllm_version()).status
