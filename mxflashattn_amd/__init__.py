@@ -17,11 +17,15 @@ from .dispatch import (
     get_last_dispatch_info,
 )
 from .native import append_kv, paged_decode_split, reshape_and_cache
+from .policy import AdaptiveDispatchPolicy, DispatchDecision, DispatchPolicyConfig, WorkloadShape
 
 __all__ = [
+    "AdaptiveDispatchPolicy",
     "BACKEND_MI355X",
     "BackendUnavailableError",
+    "DispatchDecision",
     "DispatchInfo",
+    "DispatchPolicyConfig",
     "ErrorSummary",
     "append_kv",
     "flash_attn_func",
@@ -31,6 +35,7 @@ __all__ = [
     "paged_decode_split",
     "reshape_and_cache",
     "summarize_error",
+    "WorkloadShape",
 ]
 
 __version__ = "0.1.0"

@@ -221,3 +221,47 @@ def test_vllm_compat_release_gate(tmp_path):
     report = compat.main(["--output", str(out)])
     assert json.loads(out.read_text()) == report
     assert report["status"] == compat.classify_vllm(compat.detect_vllm_version()).status
+
+
+def _start_worker(tmp_path, env_extra, code, shadow=None):
+    import os
+    import pathlib
+    import subprocess
+    import sys
+
+    root = pathlib.Path(__file__).resolve().parents[1]
+    hook = root / "mxflashattn_amd" / "integrations" / "vllm" / "autoregister"
+    env = {k: v for k, v in os.environ.items()
+           if k not in ("MXFLASHATTN_AUTOREGISTER", "MXFLASHATTN_REGISTRATION_ERROR_LOG")}
+    env["PYTHONPATH"] = os.pathsep.join([str(hook)] + ([str(shadow)] if shadow else []) +
+                                        [str(root)])
+    env.update(env_extra)
+    return subprocess.run([sys.executable, "-c", code], env=env, cwd=tmp_path,
+                          capture_output=True, text=True, timeout=120)
+
+
+def test_autoregister_hook_runs_only_when_asked(tmp_path):
+    """The sitecustomize hook (reference sitecustomize.py:8-17) in a fresh process."""
+    probe = ("import sys; print('mxflashattn_amd.integrations.vllm.backend' in sys.modules, "
+             "sys.modules['sitecustomize'].__file__)")
+    off = _start_worker(tmp_path, {}, probe)
+    assert off.returncode == 0, off.stderr
+    assert off.stdout.split()[0] == "False" and "autoregister" in off.stdout
+    on = _start_worker(tmp_path, {"MXFLASHATTN_AUTOREGISTER": "1"}, probe)
+    assert on.returncode == 0, on.stderr
+    assert on.stdout.split()[0] == "True"
+
+
+def test_autoregister_hook_logs_failures_and_lets_the_worker_start(tmp_path):
+    log = tmp_path / "reg.log"
+    # A package that fails to import, ahead of the real one on the path, stands
+    # for any failure inside registration.
+    shadow = tmp_path / "shadow"
+    (shadow / "mxflashattn_amd").mkdir(parents=True)
+    (shadow / "mxflashattn_amd" / "__init__.py").write_text("raise RuntimeError('boom')\n")
+    run = _start_worker(tmp_path, {"MXFLASHATTN_AUTOREGISTER": "1",
+                                   "MXFLASHATTN_REGISTRATION_ERROR_LOG": str(log)},
+                        "print('worker up')", shadow=shadow)
+    assert run.returncode == 0, run.stderr
+    assert run.stdout.strip() == "worker up"
+    assert log.read_text() == "RuntimeError: boom\n"
