@@ -12,6 +12,8 @@ Prints ONE JSON line:
                calls replayed from a HIP graph (no host launch overhead)
   us_per_call_eager  the same calls launched one by one from Python, median of
                per-call HIP events
+  us_per_call_warm   graph replays on one KV pool, never rotated (cache-warm
+               where the working set fits the Infinity Cache; not `value`)
   roofline     the dominant kernel, split_partial_kernel, alone: algorithmic
                bytes (KV + q + out + used block-table entries + lengths) / its
                average duration (HIP events around graph replays of
@@ -150,6 +152,10 @@ def measure_workload(name: str, spec: dict, device, steps: int, warmup: int) -> 
     us_eager, us_eager_mean = time_calls(call, pools, steps, warmup, stream)
     side = torch.cuda.Stream(device)
     us_graph = time_graph(call, pools, steps, warmup, side)
+    # Warm: the same graph replays on one pool that is never rotated, so a
+    # working set under the 256 MB Infinity Cache is partly served from it.
+    # Reported beside the rotated figure of record, never as `value`.
+    us_warm = time_graph(call, pools[:1], steps, 0, side)
 
     # The dominant kernel alone: partial-only launches, same inputs and stream.
     ws = torch.empty(native.workspace_size(base.batch, base.q_heads, base.head_dim, ns),
@@ -170,6 +176,8 @@ def measure_workload(name: str, spec: dict, device, steps: int, warmup: int) -> 
         "kv_gb_s": round(gbs, 1),
         "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
         "kv_gb_s_eager": round(kv / (us_eager * 1e-6) / 1e9, 1),
+        "us_per_call_warm": round(us_warm, 3),
+        "kv_gb_s_warm": round(kv / (us_warm * 1e-6) / 1e9, 1),
         "kv_bytes": kv,
         "algorithmic_bytes": alg,
         "alg_gb_s": round(alg / (us_graph * 1e-6) / 1e9, 1),
@@ -313,6 +321,8 @@ def main() -> int:
         "us_per_call": main_res["us_per_call"],
         "us_per_call_eager": main_res["us_per_call_eager"],
         "kv_gb_s_eager": main_res["kv_gb_s_eager"],
+        "us_per_call_warm": main_res["us_per_call_warm"],
+        "kv_gb_s_warm": main_res["kv_gb_s_warm"],
         "pct_hbm_peak": main_res["pct_hbm_peak"],
         "num_splits": main_res["num_splits"],
         "roofline": {

@@ -6,9 +6,13 @@ write-back and swaps only the attention calls. With
 MXFLASHATTN_GRAPH_OFFICIAL_SPLIT=1 the implementation's module-level
 ``flash_attn_with_kvcache`` is replaced by ``native_decode.mx_kvcache_compat``
 for the duration of the forward call (restored in ``finally``); an "invalid
-argument" failure is retried once with the untouched functions. Otherwise the
-forward runs ``decode_forward`` (public API) and falls back to vLLM for prefill.
-The KV-cache update uses the HIP append kernel (``reshape_and_cache_flash``).
+argument" failure is retried once with the untouched functions. The reference
+also swaps ``flash_attn_varlen_func`` there; prefill is not on this path, so it
+stays vLLM's. Encoder layers (``attn_type`` "encoder" / "encoder_only", which
+the reference sends to its dense API and on to the vendor kernel) run vLLM's
+own forward. Otherwise the forward runs ``decode_forward`` (public API) and
+falls back to vLLM for prefill. The KV-cache update uses the HIP append kernel
+(``reshape_and_cache_flash``).
 Classes live at module scope because vLLM resolves the backend by import path
 in its worker processes.
 """
@@ -31,6 +35,7 @@ def _forward_official_split(impl, layer, query, key, value, kv_cache, metadata, 
                             output_scale, output_block_scale):
     fn = FlashAttentionImpl.forward
     glb = fn.__globals__
+    had_kv = "flash_attn_with_kvcache" in glb
     old_kv = glb.get("flash_attn_with_kvcache")
     native_decode.official_kvcache = old_kv
     glb["flash_attn_with_kvcache"] = native_decode.mx_kvcache_compat
@@ -51,7 +56,10 @@ def _forward_official_split(impl, layer, query, key, value, kv_cache, metadata, 
                      "operation": "official_split_invalid_argument_fallback",
                      "fallback": "true", "fallback_reason": "official_split_invalid_argument"}
     finally:
-        glb["flash_attn_with_kvcache"] = old_kv
+        if had_kv:
+            glb["flash_attn_with_kvcache"] = old_kv
+        else:
+            glb.pop("flash_attn_with_kvcache", None)
         native_decode.official_kvcache = None
     record_event(event)
     return result
@@ -73,6 +81,12 @@ class MXFlashAttnImpl(FlashAttentionImpl):
                                            output_block_scale)
         if output is None:
             raise ValueError("vLLM must provide an output buffer")
+        # vLLM's AttentionType values compare equal to these strings.
+        if getattr(self, "attn_type", "decoder") in ("encoder", "encoder_only"):
+            result = super().forward(layer, query, key, value, kv_cache, attn_metadata, output,
+                                     output_scale, output_block_scale)
+            record_event({"path": "vendor_direct", "operation": "encoder", "fallback": "false"})
+            return result
         kv_dtype = getattr(self, "kv_cache_dtype", "auto") or "auto"
         if kv_dtype.startswith("fp8") and not native_decode.wide_contract():
             # fp8 caches are the vendor's unless the wider contract is on.
