@@ -296,6 +296,35 @@ def test_graph_replays_match_eager(device):
         _ = (torch.randn(4096, device=device) * i).sum().item()
 
 
+def test_concurrent_streams_use_separate_workspaces(device):
+    # Two streams (default priority) launch decode calls of different shapes
+    # with no synchronisation between them, so their kernels may overlap on
+    # the GPU; each stream has its own workspace, so every output equals the
+    # single-stream result bitwise.
+    g = torch.Generator().manual_seed(83)
+    a = make_paged_batch(12, 32, 8, 128, torch.bfloat16,
+                         torch.randint(1000, 4000, (12,), generator=g), seed=83).to(device)
+    c = make_paged_batch(20, 16, 4, 64, torch.float16,
+                         torch.randint(500, 3000, (20,), generator=g), seed=84).to(device)
+    ref_a, ref_c = run_native(a), run_native(c)
+    sa, sc = torch.cuda.Stream(device), torch.cuda.Stream(device)
+    outs_a = [torch.full_like(a.q, float("nan")) for _ in range(6)]
+    outs_c = [torch.full_like(c.q, float("nan")) for _ in range(6)]
+    torch.cuda.synchronize()
+    for oa, oc in zip(outs_a, outs_c):
+        with torch.cuda.stream(sa):
+            native.paged_decode_split(a.q, a.k_cache, a.v_cache, a.block_table, a.cache_seqlens,
+                                      a.scale, out=oa)
+        with torch.cuda.stream(sc):
+            native.paged_decode_split(c.q, c.k_cache, c.v_cache, c.block_table, c.cache_seqlens,
+                                      c.scale, out=oc)
+    torch.cuda.synchronize()
+    for i, (oa, oc) in enumerate(zip(outs_a, outs_c)):
+        assert torch.equal(oa, ref_a), i
+        assert torch.equal(oc, ref_c), i
+    assert max_err(ref_a, oracle_out(a)) <= TOL[torch.bfloat16]
+
+
 def test_maximum_batch(device):
     # 16000 sequences (the contract's maximum; the tile prefix sums fill 64 KB
     # of LDS), short ragged lengths, empty ones included.
