@@ -18,14 +18,17 @@
 //          its page (head offset folded in) and whose size covers exactly the
 //          valid rows, so rows past the sequence end and the padding tile past
 //          the range end read as zeros and cost no memory traffic. K and V
-//          carry the nontemporal hint (read once per call).
+//          carry the nontemporal hint (read once per call). With 128-byte
+//          head rows, lanes c and c^8 of a DPP row load 16 V bytes of two
+//          tokens each and swap halves (one DPP move per word).
 //   QK     on the matrix cores: S^T[16 tokens x 16 columns] = K[16 x HD].Q^T[HD x 16]
 //          (v_mfma_f32_16x16x32, HD/32 steps). Column c = t*GQ + g is query
 //          token t (of QL new tokens per sequence) and query head g of the
-//          group; columns >= GQ*QL are zero. 16-bit caches: lane l holds K bytes [64c + 16(l/16), +16)
-//          of token l%16 for step c. fp8 caches: lane l loads K bytes
-//          [64m + 16(l/16), +16) (16 elements) and widens them exactly to the
-//          element type for steps 2m and 2m+1; q is read in the same order.
+//          group; columns >= GQ*QL are zero. 16-bit caches: lane l holds K
+//          bytes [64c + 16(l/16), +16) of token l%16 for step c. fp8 caches:
+//          lane l loads K bytes [64m + 16(l/16), +16) (16 elements) and widens
+//          them exactly to the element type for steps 2m and 2m+1; q is read
+//          in the same order.
 //          Result: lane (r = l/16, h = l%16) holds tokens 4r+i, i = 0..3, head h.
 //   softmax base 2; the reference max m of each head is shared by the wave and
 //          only moves (wave-uniform branch) when a score passes it by
@@ -321,6 +324,7 @@ __device__ __forceinline__ uint32_t row_swap8(uint32_t x) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x128, 0xf, 0xf, false);
 }
 
+// Every lane takes the value of lane H of its own 16-lane row (row_newbcast:H).
 template <int H>
 __device__ __forceinline__ float row_bcast(float x) {
   return __int_as_float(
