@@ -52,6 +52,22 @@ def _per_tensor(scale: Any) -> bool:
             and (scale.numel() == 1 or all(st == 0 for st in scale.stride())))
 
 
+def _no_window(window: Any, causal: bool, ql: int) -> bool:
+    """True when window_size masks nothing for this call. FlashAttention's
+    (left, right): -1 is unbounded. Any left bound >= 0 hides keys (0 keeps
+    only the query's own position); a right bound matters only when a query
+    token could see keys after it (several tokens, not causal). The
+    reference's guard rejects positive sizes only (vllm_plugin.py:236-247)."""
+    if window is None:
+        return True
+    try:
+        left, right = (window, -1) if not isinstance(window, (tuple, list)) else window
+        left, right = int(left), int(right)
+    except (TypeError, ValueError):
+        return False
+    return left < 0 and (right < 0 or causal or ql == 1)
+
+
 def _guard(args: tuple, kwargs: dict, wide: bool = False,
            descales: tuple = (None, None)) -> tuple[str | None, tuple]:
     """(reason, (q, k_cache, v_cache, block_table, seqlens)); reason None = take it."""
@@ -64,15 +80,14 @@ def _guard(args: tuple, kwargs: dict, wide: bool = False,
         return "block_table_or_seqlens", ()
     if kwargs.get("alibi_slopes") is not None:
         return "alibi", ()
-    window = kwargs.get("window_size")
-    if window is not None:
-        # (-1, -1) or -1 means no sliding window; a positive size needs masking.
-        try:
-            values = window if isinstance(window, (tuple, list)) else (window,)
-            if any(int(x) > 0 for x in values):
-                return "window", ()
-        except (TypeError, ValueError):
-            return "window", ()
+    if not _no_window(kwargs.get("window_size"), bool(kwargs.get("causal", False)),
+                      q.shape[1] if q.dim() == 4 else 1):
+        return "window", ()
+    try:
+        if float(kwargs.get("softcap") or 0.0) != 0.0:
+            return "softcap", ()
+    except (TypeError, ValueError):
+        return "softcap", ()
     k_cache = kwargs.get("k_cache", args[1] if len(args) > 1 else None)
     v_cache = kwargs.get("v_cache", args[2] if len(args) > 2 else None)
     if k_cache is None or v_cache is None:
@@ -145,21 +160,45 @@ def try_native_decode(args: tuple, kwargs: dict, k_descale: Any = None,
 
 
 def mx_kvcache_compat(*args, **kwargs):
-    """Stand-in for vLLM's flash_attn_with_kvcache inside its attention forward."""
+    """Stand-in for vLLM's flash_attn_with_kvcache inside its attention forward.
+
+    The kernel computes plain softmax attention, so a call with attention sinks
+    (``s_aux``) or one that asks for the log-sum-exp is never taken. A call
+    that is not taken goes back to vLLM's own function with every keyword vLLM
+    passed. The reference (vllm_plugin.py:335-339) strips the vLLM-only
+    keywords for every call, because its vendor wheel does not accept them;
+    vLLM's function on ROCm does, and stripping ``s_aux`` there would drop the
+    sinks silently. Only the fallback to this package's public API, which has
+    no such parameters, goes without them."""
+    given = {name: kwargs[name] for name in _VLLM_ONLY_KWARGS if name in kwargs}
     popped = {name: kwargs.pop(name, None) for name in _VLLM_ONLY_KWARGS}
-    result = try_native_decode(args, kwargs, popped["k_descale"], popped["v_descale"])
-    if result is not None:
-        return result
+    declined = None
+    if popped["s_aux"] is not None:
+        declined = "attention_sinks"
+    elif popped["return_softmax_lse"]:
+        declined = "softmax_lse"
+    if declined is None:
+        result = try_native_decode(args, kwargs, popped["k_descale"], popped["v_descale"])
+        if result is not None:
+            return result
+    elif os.getenv("MXFA_NATIVE_DECODE", "0") == "1":
+        record_event({"path": "native_decode", "fallback": "true",
+                      "fallback_reason": f"guard:{declined}"})
+    # Shapes the public API rejects must reach the original implementation
+    # instead of raising inside vLLM.
+    if official_kvcache is not None:
+        return official_kvcache(*args, **kwargs, **given)
+    if popped["s_aux"] is not None:
+        raise NotImplementedError("attention sinks (s_aux) are not supported by the "
+                                  "MXFlashAttn API; call vLLM's flash_attn_with_kvcache")
+    if popped["return_softmax_lse"]:
+        kwargs["return_softmax_lse"] = True  # the API raises its own error for it
     k_cache = kwargs.get("k_cache", args[1] if len(args) > 1 else None)
     if isinstance(k_cache, torch.Tensor) and k_cache.dtype == native.FP8_DTYPE:
         # An fp8 cache is meaningless without its scales: give them back.
         for name in ("q_descale", "k_descale", "v_descale"):
             if popped[name] is not None:
                 kwargs[name] = popped[name]
-    # Shapes the public API rejects must reach the original implementation
-    # instead of raising inside vLLM.
-    if official_kvcache is not None:
-        return official_kvcache(*args, **kwargs)
     return api.flash_attn_with_kvcache(*args, **kwargs)
 
 

@@ -10,8 +10,10 @@ argument" failure is retried once with the untouched functions. The reference
 also swaps ``flash_attn_varlen_func`` there; prefill is not on this path, so it
 stays vLLM's. Encoder layers (``attn_type`` "encoder" / "encoder_only", which
 the reference sends to its dense API and on to the vendor kernel) run vLLM's
-own forward. Otherwise the forward runs ``decode_forward`` (public API) and
-falls back to vLLM for prefill. The KV-cache update uses the HIP append kernel
+own forward, and so do layers with a sliding window, ALiBi slopes,
+logit soft-capping or attention sinks, which the reference's forward sends to
+its decoder regardless. Otherwise the forward runs ``decode_forward`` (public
+API) and falls back to vLLM for prefill. The KV-cache update uses the HIP append kernel
 (``reshape_and_cache_flash``).
 Classes live at module scope because vLLM resolves the backend by import path
 in its worker processes.
@@ -65,6 +67,21 @@ def _forward_official_split(impl, layer, query, key, value, kv_cache, metadata, 
     return result
 
 
+def _layer_option(impl) -> str | None:
+    """An option of the layer that the decode kernel does not compute (vLLM's
+    FlashAttentionImpl applies them in its own forward), or None."""
+    if getattr(impl, "alibi_slopes", None) is not None:
+        return "alibi"
+    window = getattr(impl, "sliding_window", None)
+    if window is not None and not native_decode._no_window(window, True, 1):
+        return "window"
+    if getattr(impl, "logits_soft_cap", None):
+        return "softcap"
+    if getattr(impl, "sinks", None) is not None:
+        return "attention_sinks"
+    return None
+
+
 class MXFlashAttnImpl(FlashAttentionImpl):
     def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None,
                 output_scale=None, output_block_scale=None):
@@ -86,6 +103,14 @@ class MXFlashAttnImpl(FlashAttentionImpl):
             result = super().forward(layer, query, key, value, kv_cache, attn_metadata, output,
                                      output_scale, output_block_scale)
             record_event({"path": "vendor_direct", "operation": "encoder", "fallback": "false"})
+            return result
+        option = _layer_option(self)
+        if option is not None:
+            # Sliding windows, ALiBi, soft-capping and sinks: vLLM's forward.
+            result = super().forward(layer, query, key, value, kv_cache, attn_metadata, output,
+                                     output_scale, output_block_scale)
+            record_event({"path": "vendor_direct", "operation": "layer_option",
+                          "fallback": "true", "fallback_reason": option})
             return result
         kv_dtype = getattr(self, "kv_cache_dtype", "auto") or "auto"
         if kv_dtype.startswith("fp8") and not native_decode.wide_contract():

@@ -51,15 +51,51 @@ def test_official_kvcache_compat_falls_back_to_vendor_for_unsupported_shapes(
     assert calls == [(args, kwargs)]
 
 
-def test_compat_drops_vllm_only_keywords(monkeypatch):
+def test_compat_hands_calls_back_to_vllm_unchanged(monkeypatch):
+    # The reference strips vLLM-only keywords (vllm_plugin.py:335-339) for its
+    # vendor wheel; vLLM's own function takes them, so a declined call goes
+    # back exactly as vLLM made it.
     seen = {}
     monkeypatch.setattr(native_decode, "official_kvcache",
                         lambda *a, **k: seen.update(k) or "vendor")
     kwargs = kv_kwargs()
     kwargs.update(s_aux=None, scheduler_metadata=None, fa_version=3, q_descale=None,
                   k_descale=None, v_descale=None, return_softmax_lse=False)
+    expected = dict(kwargs)
     assert native_decode.mx_kvcache_compat(torch.empty(1, 1, 16, 128), **kwargs) == "vendor"
-    assert set(seen) == {"k_cache", "v_cache", "block_table", "cache_seqlens"}
+    assert seen.keys() == expected.keys()
+    assert all(seen[k] is expected[k] for k in expected)
+
+
+@pytest.mark.parametrize("extra,reason", [
+    (dict(s_aux=torch.zeros(16)), "attention_sinks"),
+    (dict(return_softmax_lse=True), "softmax_lse"),
+])
+def test_compat_never_takes_sinks_or_lse_requests(monkeypatch, extra, reason):
+    """The kernel has no sinks and returns no LSE: such calls reach vLLM with
+    those keywords intact (the reference drops them and computes without)."""
+    monkeypatch.setenv("MXFA_NATIVE_DECODE", "1")
+    seen = {}
+    monkeypatch.setattr(native_decode, "official_kvcache",
+                        lambda *a, **k: seen.update(k) or "vendor")
+    monkeypatch.setattr(native_decode, "try_native_decode",
+                        lambda *a, **k: pytest.fail("must not reach the kernel"))
+    backend.clear_dispatch_events(truncate_log=False)
+    kwargs = kv_kwargs()
+    kwargs.update(extra)
+    assert native_decode.mx_kvcache_compat(q_of(), **kwargs) == "vendor"
+    for k, v in extra.items():
+        assert seen[k] is v
+    assert backend.get_dispatch_events() == [
+        {"path": "native_decode", "fallback": "true", "fallback_reason": f"guard:{reason}"}]
+
+
+def test_compat_without_vllm_function_refuses_what_the_api_cannot_do(monkeypatch):
+    monkeypatch.setattr(native_decode, "official_kvcache", None)
+    with pytest.raises(NotImplementedError, match="s_aux"):
+        native_decode.mx_kvcache_compat(q_of(), s_aux=torch.zeros(16), **kv_kwargs())
+    with pytest.raises(NotImplementedError, match="return_softmax_lse"):
+        native_decode.mx_kvcache_compat(q_of(), return_softmax_lse=True, **kv_kwargs())
 
 
 def q_of(q_heads=16, head_dim=128, dtype=torch.float16, rank=4):
@@ -88,6 +124,11 @@ def test_native_guard_hands_back_unsupported_calls(case, reason):
 @pytest.mark.parametrize("extra,reason", [
     (dict(alibi_slopes=torch.zeros(16)), "alibi"),
     (dict(window_size=(128, 0)), "window"),
+    (dict(window_size=(0, 0)), "window"),     # keeps only the query's own key
+    (dict(window_size=(0, -1)), "window"),
+    (dict(window_size=5), "window"),
+    (dict(window_size="wide"), "window"),
+    (dict(softcap=30.0), "softcap"),
     (dict(block_table=None), "block_table_or_seqlens"),
     (dict(cache_seqlens=torch.ones(3, dtype=torch.int32)), "block_table_or_seqlens"),
 ])
@@ -95,6 +136,22 @@ def test_native_guard_option_checks(extra, reason):
     kwargs = kv_kwargs()
     kwargs.update(extra)
     assert native_decode._guard((q_of(),), kwargs)[0] == reason
+
+
+def test_native_guard_window_right_bound_matters_only_for_later_keys(monkeypatch):
+    # One query token, or causal masking, sees no key after itself: a right
+    # bound of 0 masks nothing there. Several non-causal tokens would.
+    monkeypatch.setenv("MXFA_WIDE_CONTRACT", "1")
+    for window, causal, ql, reason in (((-1, 0), False, 1, "device"),
+                                       ((-1, 0), True, 3, "device"),
+                                       ((-1, 0), False, 3, "window"),
+                                       ((-1, -1), False, 3, "device"),
+                                       (-1, False, 3, "device")):
+        kwargs = kv_kwargs()
+        kwargs.update(window_size=window, causal=causal, softcap=0.0)
+        q = torch.empty(1, ql, 16, 128, dtype=torch.float16)
+        wide = native_decode.wide_contract()
+        assert native_decode._guard((q,), kwargs, wide)[0] == reason, (window, causal, ql)
 
 
 def test_native_guard_accepts_no_window_and_rank3_queries():

@@ -153,6 +153,37 @@ def test_pure_split_encoders_and_default_fp8_go_to_vllm(plugin, monkeypatch):
     assert _forward(mod, mod.MXFlashAttnImpl(kv_cache_dtype="fp8")) == "vendor_kvcache"
 
 
+@pytest.mark.parametrize("attr,value,reason", [
+    ("alibi_slopes", torch.zeros(8), "alibi"),
+    ("sliding_window", (127, 0), "window"),
+    ("sliding_window", (0, 0), "window"),
+    ("logits_soft_cap", 30.0, "softcap"),
+    ("sinks", torch.zeros(8), "attention_sinks"),
+])
+def test_layer_options_the_kernel_lacks_run_vllms_forward(plugin, monkeypatch, attr, value,
+                                                          reason):
+    # The reference's forward decodes such layers without them.
+    mod, _ = plugin
+    monkeypatch.setattr(mod, "forward_decode",
+                        lambda *a, **k: pytest.fail("must not reach the decode adapter"))
+    impl = mod.MXFlashAttnImpl()
+    impl.sliding_window, impl.logits_soft_cap = (-1, -1), 0.0   # vLLM's defaults
+    setattr(impl, attr, value)
+    assert _forward(mod, impl) == "vendor_kvcache"
+    assert backend.get_dispatch_events() == [
+        {"path": "vendor_direct", "operation": "layer_option", "fallback": "true",
+         "fallback_reason": reason}]
+
+
+def test_layer_defaults_reach_the_adapter(plugin, monkeypatch):
+    mod, _ = plugin
+    monkeypatch.setattr(mod, "forward_decode", lambda *a, **k: "decoded")
+    impl = mod.MXFlashAttnImpl()
+    impl.alibi_slopes, impl.sliding_window, impl.logits_soft_cap, impl.sinks = (
+        None, (-1, -1), 0.0, None)
+    assert _forward(mod, impl) == "decoded"
+
+
 def test_decode_goes_through_the_adapter_with_layer_scales(plugin, monkeypatch):
     mod, _ = plugin
     seen = []
