@@ -105,8 +105,11 @@ class MXFlashAttnImpl(FlashAttentionImpl):
             record_event({"path": "vendor_direct", "operation": "encoder", "fallback": "false"})
             return result
         option = _layer_option(self)
+        if option is None and (output_scale is not None or output_block_scale is not None):
+            option = "output_quantization"  # vLLM's forward decides (it raises for it)
         if option is not None:
-            # Sliding windows, ALiBi, soft-capping and sinks: vLLM's forward.
+            # Sliding windows, ALiBi, soft-capping, sinks, a quantised output:
+            # vLLM's forward.
             result = super().forward(layer, query, key, value, kv_cache, attn_metadata, output,
                                      output_scale, output_block_scale)
             record_event({"path": "vendor_direct", "operation": "layer_option",

@@ -175,6 +175,16 @@ def test_layer_options_the_kernel_lacks_run_vllms_forward(plugin, monkeypatch, a
          "fallback_reason": reason}]
 
 
+def test_quantised_output_goes_to_vllm(plugin, monkeypatch):
+    mod, _ = plugin
+    monkeypatch.setattr(mod, "forward_decode",
+                        lambda *a, **k: pytest.fail("must not reach the decode adapter"))
+    impl = mod.MXFlashAttnImpl()
+    assert impl.forward(None, "q", "k", "v", "kv", "meta", "out", output_scale="s") == \
+        "vendor_kvcache"
+    assert backend.get_dispatch_events()[-1]["fallback_reason"] == "output_quantization"
+
+
 def test_layer_defaults_reach_the_adapter(plugin, monkeypatch):
     mod, _ = plugin
     monkeypatch.setattr(mod, "forward_decode", lambda *a, **k: "decoded")
