@@ -113,6 +113,13 @@ def fast_layout(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: Any)
     )
 
 
+def _no_cascade(attn_metadata: Any) -> None:
+    # Cascade attention splits a shared prefix out of every request's pages:
+    # decoding the per-request pages alone would miss it.
+    if bool(getattr(attn_metadata, "use_cascade", False)):
+        raise DecoderAdapterBlocked("cascade_attention_not_supported_by_adapter")
+
+
 def _int32_on(t: torch.Tensor, device: torch.device) -> torch.Tensor:
     # Convert only when needed: an unconditional .to() costs a dispatch per layer.
     if t.device == device and t.dtype == torch.int32:
@@ -128,6 +135,7 @@ def decode_forward(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: A
     omitted and seq_lens describes the populated cache.
     """
     if os.getenv("MXFLASHATTN_GRAPH_DECODE", "0") == "1":
+        _no_cascade(attn_metadata)
         has_padded_decode = (
             attn_metadata.seq_lens.ndim == 1
             and attn_metadata.block_table.ndim == 2
@@ -146,6 +154,7 @@ def decode_forward(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: A
         return _decode_forward_graph(query, kv_cache, attn_metadata,
                                      softmax_scale=softmax_scale, causal=causal)
     if _transparent_enabled():
+        _no_cascade(attn_metadata)
         if int(attn_metadata.max_query_len) != 1:
             raise DecoderAdapterBlocked(
                 f"only_single_token_decode_supported:max_query_len={int(attn_metadata.max_query_len)}"
@@ -164,8 +173,7 @@ def decode_forward(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: A
               else fast_layout(query, kv_cache, attn_metadata))
     if not bool(attn_metadata.causal) and causal:
         raise DecoderAdapterBlocked("metadata_causal_flag_is_false")
-    if bool(attn_metadata.use_cascade):
-        raise DecoderAdapterBlocked("cascade_attention_not_supported_by_adapter")
+    _no_cascade(attn_metadata)
     if layout.max_query_len != 1:
         raise DecoderAdapterBlocked(
             f"only_single_token_decode_supported:max_query_len={layout.max_query_len}"
@@ -225,6 +233,7 @@ def _fp8_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: Any,
                 v_scale: Any) -> torch.Tensor:
     """One-token decode over an fp8 (e4m3fn) cache, straight on the HIP kernels
     (the public API, like the reference's, takes 16-bit caches only)."""
+    _no_cascade(attn_metadata)
     if int(attn_metadata.max_query_len) != 1:
         raise DecoderAdapterBlocked(
             f"only_single_token_decode_supported:max_query_len={int(attn_metadata.max_query_len)}")

@@ -91,6 +91,23 @@ def test_cascade_and_fp8_are_blocked():
         decode_forward(q, cache.float(), metadata, softmax_scale=0.125)
 
 
+@pytest.mark.parametrize("mode", ["MXFLASHATTN_GRAPH_DECODE", "MXFLASHATTN_TRANSPARENT"])
+def test_cascade_is_blocked_on_every_path(monkeypatch, mode):
+    # A cascade call's pages hold only each request's suffix: decoding them
+    # alone would miss the shared prefix.
+    monkeypatch.setenv(mode, "1")
+    monkeypatch.setattr(decoder_adapter, "flash_attn_with_kvcache",
+                        lambda *a, **k: pytest.fail("cascade must not be decoded"))
+    q, cache, metadata = make_case()
+    metadata.use_cascade = True
+    with pytest.raises(DecoderAdapterBlocked, match="cascade"):
+        decode_forward(q, cache, metadata, softmax_scale=0.125)
+    with pytest.raises(DecoderAdapterBlocked, match="cascade"):
+        decoder_adapter.forward_decode(q, cache.view(torch.uint8), metadata,
+                                       torch.empty(2, 256, dtype=q.dtype),
+                                       softmax_scale=0.125, kv_cache_dtype="fp8")
+
+
 def test_transparent_path_flattens_capture_seq_lens(monkeypatch):
     monkeypatch.setenv("MXFLASHATTN_TRANSPARENT", "1")
     monkeypatch.setenv("MXFLASHATTN_ALLOW_FALLBACK", "1")
