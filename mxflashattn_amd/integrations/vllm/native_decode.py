@@ -35,6 +35,11 @@ from .backend import record_event
 # compat wrapper hands unsupported calls back to.
 official_kvcache: Callable[..., Any] | None = None
 
+# vLLM kv_cache_dtype values whose caches the HIP kernels hold: the model's
+# own 16-bit type ("auto" or named), and OCP e4m3fn with per-tensor scales.
+SIXTEEN_BIT_KV_DTYPES = ("auto", None, "bfloat16", "float16", "half")
+FP8_KV_DTYPES = ("fp8", "fp8_e4m3")
+
 _VLLM_ONLY_KWARGS = ("s_aux", "return_softmax_lse", "scheduler_metadata", "fa_version",
                      "q_descale", "k_descale", "v_descale")
 
@@ -221,6 +226,6 @@ def reshape_and_cache_flash(key: torch.Tensor, value: torch.Tensor, key_cache: t
         native.reshape_and_cache(key[:n], value[:n], key_cache, value_cache, slot_mapping,
                                  k_scale=k_scale, v_scale=v_scale)
         return
-    if kv_cache_dtype not in ("auto", None):
+    if kv_cache_dtype not in SIXTEEN_BIT_KV_DTYPES:
         raise NotImplementedError(f"kv_cache_dtype {kv_cache_dtype!r} is not supported")
     native.reshape_and_cache(key[:n], value[:n], key_cache, value_cache, slot_mapping)

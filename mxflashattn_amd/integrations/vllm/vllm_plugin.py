@@ -82,6 +82,14 @@ def _layer_option(impl) -> str | None:
     return None
 
 
+def _decodes_here(kv_dtype: str) -> bool:
+    """Whether decode over this cache format runs on the HIP kernels: 16-bit
+    caches always, e4m3fn caches under the wider contract."""
+    if kv_dtype in native_decode.SIXTEEN_BIT_KV_DTYPES:
+        return True
+    return kv_dtype in native_decode.FP8_KV_DTYPES and native_decode.wide_contract()
+
+
 class MXFlashAttnImpl(FlashAttentionImpl):
     def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None,
                 output_scale=None, output_block_scale=None):
@@ -116,8 +124,9 @@ class MXFlashAttnImpl(FlashAttentionImpl):
                           "fallback": "true", "fallback_reason": option})
             return result
         kv_dtype = getattr(self, "kv_cache_dtype", "auto") or "auto"
-        if kv_dtype.startswith("fp8") and not native_decode.wide_contract():
-            # fp8 caches are the vendor's unless the wider contract is on.
+        if not _decodes_here(kv_dtype):
+            # fp8 caches are vLLM's unless the wider contract is on; e5m2 and
+            # other formats always are.
             return super().forward(layer, query, key, value, kv_cache, attn_metadata, output,
                                    output_scale, output_block_scale)
         try:
@@ -133,7 +142,10 @@ class MXFlashAttnImpl(FlashAttentionImpl):
             raise
 
     def do_kv_cache_update(self, layer, key, value, kv_cache, slot_mapping):
-        kv_cache_update(key, value, kv_cache, slot_mapping, self.kv_cache_dtype,
+        kv_dtype = getattr(self, "kv_cache_dtype", "auto") or "auto"
+        if kv_dtype not in native_decode.SIXTEEN_BIT_KV_DTYPES + native_decode.FP8_KV_DTYPES:
+            return super().do_kv_cache_update(layer, key, value, kv_cache, slot_mapping)
+        kv_cache_update(key, value, kv_cache, slot_mapping, kv_dtype,
                         getattr(layer, "_k_scale", None), getattr(layer, "_v_scale", None))
 
 

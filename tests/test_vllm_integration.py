@@ -209,6 +209,13 @@ def test_reshape_and_cache_flash_cache_dtypes():
     # Other quantised formats are not supported.
     with pytest.raises(NotImplementedError, match="fp8_e5m2"):
         native_decode.reshape_and_cache_flash(None, None, None, None, torch.zeros(1), "fp8_e5m2")
+    # Named 16-bit cache types are the plain copy (host tensors: refused at the device check).
+    k16 = torch.zeros(2, 2, 64, dtype=torch.bfloat16)
+    c16 = torch.zeros(4, 16, 2, 64, dtype=torch.bfloat16)
+    for name in ("bfloat16", "float16", "half"):
+        with pytest.raises(ValueError, match="GPU tensors"):
+            native_decode.reshape_and_cache_flash(k16, k16, c16, c16,
+                                                  torch.zeros(2, dtype=torch.int64), name)
     # "fp8" needs e4m3fn caches (or their uint8 codes).
     k = torch.zeros(2, 2, 64, dtype=torch.bfloat16)
     cache = torch.zeros(4, 16, 2, 64, dtype=torch.bfloat16)

@@ -33,6 +33,9 @@ class FlashAttentionImpl:
                 output_scale=None, output_block_scale=None):
         return flash_attn_with_kvcache(query, kv_cache)
 
+    def do_kv_cache_update(self, layer, key, value, kv_cache, slot_mapping):
+        return "vendor_cache_update"
+
 class FlashAttentionBackend:
     pass
 '''
@@ -232,6 +235,29 @@ def test_blocked_decode_hands_prefill_back_and_raises_otherwise(plugin, monkeypa
          "reason": "only_single_token_decode_supported:max_query_len=7"},
         {"path": "vendor_prefill_or_blocked",
          "reason": "cascade_attention_not_supported_by_adapter"}]
+
+
+@pytest.mark.parametrize("kv_dtype", ["fp8_e5m2", "fp8_inc", "fp8_ds_mla"])
+def test_cache_formats_the_kernels_lack_stay_with_vllm(plugin, monkeypatch, kv_dtype):
+    mod, _ = plugin
+    monkeypatch.setenv("MXFA_WIDE_CONTRACT", "1")
+    monkeypatch.setattr(mod, "forward_decode", lambda *a, **k: pytest.fail("decode adapter"))
+    monkeypatch.setattr(mod, "kv_cache_update", lambda *a: pytest.fail("HIP cache update"))
+    impl = mod.MXFlashAttnImpl(kv_cache_dtype=kv_dtype)
+    assert _forward(mod, impl) == "vendor_kvcache"
+    assert impl.do_kv_cache_update(None, "k", "v", "cache", "slots") == "vendor_cache_update"
+
+
+def test_named_sixteen_bit_caches_run_here(plugin, monkeypatch):
+    mod, _ = plugin
+    seen = []
+    monkeypatch.setattr(mod, "forward_decode", lambda *a, **k: seen.append(k) or "decoded")
+    monkeypatch.setattr(mod, "kv_cache_update", lambda *a: seen.append(a))
+    for kv_dtype in ("auto", "bfloat16", "float16", "half"):
+        impl = mod.MXFlashAttnImpl(kv_cache_dtype=kv_dtype)
+        assert _forward(mod, impl) == "decoded"
+        impl.do_kv_cache_update(types.SimpleNamespace(), "k", "v", "cache", "slots")
+    assert len(seen) == 8
 
 
 def test_kv_cache_update_passes_the_cache_dtype_and_layer_scales(plugin, monkeypatch):
