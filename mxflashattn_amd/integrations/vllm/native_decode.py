@@ -133,9 +133,23 @@ def try_native_decode(args: tuple, kwargs: dict, k_descale: Any = None,
         record_event({"path": "native_decode", "fallback": "true",
                       "fallback_reason": f"guard:{reason}"})
         return None
+    try:
+        return _native_decode(picked, kwargs, k_descale, v_descale)
+    except native.NativeLibraryError:
+        raise  # a missing or stale build is a deployment error, not a shape to hand back
+    except Exception as exc:  # as vllm_plugin.py:314-317: never take the model down
+        record_event({"path": "native_decode", "fallback": "true",
+                      "fallback_reason": repr(exc)})
+        return None
+
+
+def _native_decode(picked: tuple, kwargs: dict, k_descale: Any,
+                   v_descale: Any) -> torch.Tensor:
     q, k_cache, v_cache, bt, sl = picked
     hq, hd = q.shape[-2], q.shape[-1]
-    scale = kwargs.get("softmax_scale") or hd ** -0.5
+    # An explicit 0.0 is a scale (uniform weights), not "use the default".
+    scale = kwargs.get("softmax_scale")
+    scale = hd ** -0.5 if scale is None else float(scale)
     # vLLM passes q as [T, HQ, D] or [B, 1, HQ, D], possibly a strided slice of
     # the fused QKV buffer: the kernel takes the strides as they are.
     q4 = q.reshape(q.shape[0], 1, hq, hd) if q.dim() == 3 else q

@@ -329,3 +329,44 @@ def test_autoregister_hook_logs_failures_and_lets_the_worker_start(tmp_path):
     assert run.returncode == 0, run.stderr
     assert run.stdout.strip() == "worker up"
     assert log.read_text() == "RuntimeError: boom\n"
+
+
+def _picked_guard(monkeypatch):
+    # Host tensors stop at the device check; pretend every guard passed.
+    monkeypatch.setattr(native_decode, "_guard",
+                        lambda args, kwargs, *a: (None, (args[0], kwargs["k_cache"],
+                                                         kwargs["v_cache"],
+                                                         kwargs["block_table"],
+                                                         kwargs["cache_seqlens"])))
+    monkeypatch.setenv("MXFA_NATIVE_DECODE", "1")
+    monkeypatch.setattr(native_decode.native, "default_num_splits", lambda *a: 4)
+
+
+def test_native_decode_keeps_an_explicit_zero_scale(monkeypatch):
+    _picked_guard(monkeypatch)
+    seen = []
+    monkeypatch.setattr(native_decode.native, "paged_decode_split",
+                        lambda q, k, v, bt, sl, scale, **kw: seen.append(scale) or q)
+    native_decode.try_native_decode((q_of(),), dict(kv_kwargs(), softmax_scale=0.0))
+    native_decode.try_native_decode((q_of(),), kv_kwargs())
+    assert seen == [0.0, 128 ** -0.5]
+
+
+def test_native_decode_errors_hand_back_but_a_missing_build_raises(monkeypatch):
+    _picked_guard(monkeypatch)
+    backend.clear_dispatch_events(truncate_log=False)
+
+    def unsupported(*a, **k):
+        raise native_decode.native.UnsupportedConfig("page stride")
+
+    monkeypatch.setattr(native_decode.native, "paged_decode_split", unsupported)
+    assert native_decode.try_native_decode((q_of(),), kv_kwargs()) is None
+    event = backend.get_dispatch_events()[-1]
+    assert event["fallback"] == "true" and "page stride" in event["fallback_reason"]
+
+    def missing(*a, **k):
+        raise native_decode.native.NativeLibraryError("native library not built")
+
+    monkeypatch.setattr(native_decode.native, "paged_decode_split", missing)
+    with pytest.raises(native_decode.native.NativeLibraryError):
+        native_decode.try_native_decode((q_of(),), kv_kwargs())
