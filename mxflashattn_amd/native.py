@@ -2,8 +2,8 @@
 
 This module is the thin host layer between torch tensors and the C entry
 points: it checks shapes, passes raw device pointers and element strides, keeps
-a per-(device, stream) workspace so steady-state calls allocate nothing, and launches on the caller's current HIP stream without
-synchronising.
+a per-(device, stream) workspace so steady-state calls allocate nothing, and
+launches on the caller's current HIP stream without synchronising.
 
 Reference counterpart: the pybind module ``mxmmain`` (``csrc_native/m1_binding.cpp``),
 ``paged_decode_split`` at ``csrc_native/m1_binding.cpp:78-115``.
