@@ -19,7 +19,8 @@ Prints ONE JSON line:
                average duration (HIP events around graph replays of
                partial-only launches, on the launch stream), against 8 TB/s
   cpu_baseline fp32 torch-CPU restatement of reference.attention_kvcache
-               (oracle.reference_port) on the host cores, bounded sample
+               (oracle.reference_port) on the host cores, bounded sample of the
+               workload, plus config 1 (the reference's CPU-runnable case)
   cells        the six GQ x HD cells of config 2 and configs 1, 3, 4
   wide         shapes beyond the reference's contract at config 2's batch and
                lengths: fp8 (e4m3fn) caches, head dim 256, GQ 1 and 16, and
@@ -191,19 +192,12 @@ def measure_workload(name: str, spec: dict, device, steps: int, warmup: int) -> 
     return res
 
 
-def cpu_baseline(spec: dict, reps: int) -> dict:
-    """Time the fp32 CPU restatement on the same batch (CPU tensors)."""
+def _time_port(spec: dict, reps: int) -> tuple[float, object]:
+    """Median seconds per call of the fp32 CPU restatement on one batch."""
     from mxflashattn_amd.workloads import make_paged_batch
     from oracle import reference_port
 
-    # The host cores this process may use; a GPU box's share is capped by
-    # OMP_NUM_THREADS whatever os.cpu_count() reports.
-    cores = len(os.sched_getaffinity(0))
-    cap = os.environ.get("OMP_NUM_THREADS", "")
-    if cap.isdigit() and int(cap) > 0:
-        cores = min(cores, int(cap))
-    torch.set_num_threads(max(1, cores))
-    b = make_paged_batch(**spec, device="cpu")
+    b = make_paged_batch(**{k: v for k, v in spec.items() if k != "causal"}, device="cpu")
     times = []
     for i in range(reps + 1):
         t0 = time.perf_counter()
@@ -212,15 +206,36 @@ def cpu_baseline(spec: dict, reps: int) -> dict:
                                          block_table=b.block_table, softmax_scale=b.scale)
         if i:
             times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
+    return statistics.median(times), b
+
+
+def cpu_baseline(name: str, spec: dict, reps: int) -> dict:
+    """Time the fp32 CPU restatement on the same batch (CPU tensors), and on
+    config 1, the reference's CPU-runnable case."""
+    from mxflashattn_amd.workloads import CONFIGS
+
+    # The host cores this process may use; a GPU box's share is capped by
+    # OMP_NUM_THREADS whatever os.cpu_count() reports.
+    cores = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    if cap.isdigit() and int(cap) > 0:
+        cores = min(cores, int(cap))
+    torch.set_num_threads(max(1, cores))
+    med, b = _time_port(spec, reps)
+    med1, b1 = _time_port(CONFIGS["config1_cpu_ref"], 50)
     return {
         "value": round(b.kv_bytes() / med / 1e9, 3),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"{MAIN_WORKLOAD} full batch (B={b.batch}, {b.total_tokens()} tokens), "
+        "sample": (f"{name} full batch (B={b.batch}, {b.total_tokens()} tokens), "
                    f"median of {reps} calls after 1 warmup; {med * 1e3:.1f} ms per call"),
         "ms_per_call": round(med * 1e3, 2),
+        "config1_cpu_ref": {
+            "ms_per_call": round(med1 * 1e3, 3),
+            "kv_gb_s": round(b1.kv_bytes() / med1 / 1e9, 3),
+            "sample": f"B={b1.batch}, {b1.total_tokens()} tokens, median of 50 calls",
+        },
     }
 
 
@@ -295,7 +310,7 @@ def main() -> int:
     cpu = None
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
-        cpu = cpu_baseline(spec, args.cpu_reps)
+        cpu = cpu_baseline(args.workload, spec, args.cpu_reps)
 
     achieved = main_res["partial_kernel_gb_s"]
     line = {
