@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define MXFA_ABI_VERSION 3
+#define MXFA_ABI_VERSION 4
 
 /* Return codes. */
 #define MXFA_OK 0
@@ -121,7 +121,12 @@ int mxfa_split_decode_launch(const void *q, int64_t q_stride_b, int64_t q_stride
  * L_b - q_len + t, L_b = seqlens[b] + seqlen_add; with causal != 0 it attends
  * keys [0, L_b - q_len + t] (bottom-right aligned, as
  * mxflashattn/reference.py:31-35), else all L_b keys; a token with no key gets
- * zeros (the reference's nan_to_num). kv_dtype is dtype (16-bit caches) or
+ * zeros (the reference's nan_to_num). window_left >= 0 is a sliding window:
+ * the token at position i also drops keys before i - window_left
+ * (FlashAttention's window_size (window_left, 0) with causal, (window_left,
+ * -1) without); -1 means none. The
+ * reference has no window: its guards hand such calls to the vendor
+ * (integrations/vllm/vllm_plugin.py:236-247). kv_dtype is dtype (16-bit caches) or
  * MXFA_DTYPE_FP8_E4M3 with k_scale/v_scale as in mxfa_split_decode_fp8_launch.
  * Workspace: mxfa_split_decode_workspace_size(batch, q_heads * q_len, ...).
  * Partial and combine run as one call. Other arguments as
@@ -131,8 +136,9 @@ int mxfa_split_decode_launch(const void *q, int64_t q_stride_b, int64_t q_stride
  */
 int mxfa_split_decode_multi_launch(
     const void *q, int64_t q_stride_b, int64_t q_stride_t, int64_t q_stride_h, int q_len,
-    int causal, const void *k_cache, const void *v_cache, int64_t cache_stride_page,
-    int64_t cache_stride_token, int64_t cache_stride_head, const int32_t *block_table,
+    int causal, int window_left, const void *k_cache, const void *v_cache,
+    int64_t cache_stride_page, int64_t cache_stride_token, int64_t cache_stride_head,
+    const int32_t *block_table,
     int64_t bt_stride, const int32_t *seqlens, int seqlen_add, void *out, int64_t out_stride_b,
     int64_t out_stride_t, int64_t out_stride_h, void *workspace, size_t workspace_bytes,
     float scale, int batch, int q_heads, int kv_heads, int head_dim, int page_size,

@@ -49,6 +49,7 @@ struct SplitArgs {
   const float *k_scale, *v_scale;
   int ql;      // query tokens per sequence
   int causal;  // bottom-right aligned causal mask
+  int window_left;  // sliding window (keys >= position - window_left), -1: none
 };
 
 struct WsLayout {
@@ -73,7 +74,8 @@ static int check_split_args(const SplitArgs &a) {
   if (!supported_hd(a.hd)) return MXFA_EUNSUPPORTED;
   if (a.hq % a.hkv != 0) return MXFA_EUNSUPPORTED;
   const int gq = a.hq / a.hkv;
-  if (a.ql <= 0) return MXFA_EINVAL;
+  if (a.ql <= 0 || a.window_left < -1) return MXFA_EINVAL;
+  if (a.window_left > (1 << 30)) return MXFA_EUNSUPPORTED;
   if (gq * a.ql > kMaxCols) return MXFA_EUNSUPPORTED;
   if (a.dtype != MXFA_DTYPE_F16 && a.dtype != MXFA_DTYPE_BF16) return MXFA_EUNSUPPORTED;
   if (ilog2_exact(a.ps) < 0 || a.ps > 4096) return MXFA_EUNSUPPORTED;
@@ -149,6 +151,7 @@ static DecodeParams make_params(const SplitArgs &a, const Grid &g) {
   p.gq = a.hq / a.hkv;
   p.ql = a.ql;
   p.causal = a.causal ? 1 : 0;
+  p.window_left = a.window_left;
   p.heads_per_wg = g.heads_per_wg;
   p.subs = g.subs;
   p.ps_log2 = ilog2_exact(a.ps);
@@ -252,6 +255,7 @@ static SplitArgs split_args(const void *q, int64_t q_stride_b, int64_t q_stride_
   a.v_scale = nullptr;
   a.ql = 1;
   a.causal = 0;
+  a.window_left = -1;
   return a;
 }
 
@@ -386,7 +390,8 @@ int mxfa_split_decode_combine_launch(void *workspace, size_t workspace_bytes, vo
 
 int mxfa_split_decode_multi_launch(
     const void *q, int64_t q_stride_b, int64_t q_stride_t, int64_t q_stride_h, int q_len,
-    int causal, const void *k_cache, const void *v_cache, int64_t cache_stride_page,
+    int causal, int window_left, const void *k_cache, const void *v_cache,
+    int64_t cache_stride_page,
     int64_t cache_stride_token, int64_t cache_stride_head, const int32_t *block_table,
     int64_t bt_stride, const int32_t *seqlens, int seqlen_add, void *out, int64_t out_stride_b,
     int64_t out_stride_t, int64_t out_stride_h, void *workspace, size_t workspace_bytes,
@@ -404,6 +409,7 @@ int mxfa_split_decode_multi_launch(
   a.o_st = out_stride_t;
   a.ql = q_len;
   a.causal = causal;
+  a.window_left = window_left;
   return run_split(a, true, (hipStream_t)stream);
 }
 

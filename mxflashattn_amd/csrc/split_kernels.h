@@ -119,6 +119,7 @@ struct DecodeParams {
   int gq;
   int ql;      // query tokens per sequence
   int causal;  // mask keys after each query token's position
+  int window_left;  // sliding window: token at position i sees keys >= i - window_left (-1: none)
   int heads_per_wg;
   int subs;
   int ps_log2;
@@ -159,6 +160,20 @@ __device__ __forceinline__ int seq_len_of(const int32_t *seqlens, int b, int add
   int L = as_const(seqlens)[b] + add;
   L = L < 0 ? 0 : L;
   return L > max_len ? max_len : L;
+}
+
+// First tile of a sequence of L keys that any of its QL query tokens sees: the
+// earliest token (position L - QL) sees keys >= L - QL - window_left. Tiles are
+// aligned to the sequence start; with no window this is tile 0.
+__device__ __forceinline__ int first_tile_of(int L, int ql, int window_left) {
+  if (window_left < 0) return 0;
+  const int first_key = L - ql - window_left;
+  return first_key > 0 ? first_key / kTile : 0;
+}
+
+// Tiles of a sequence of L keys inside the window (L > 0: at least one).
+__device__ __forceinline__ int tiles_of(int L, int ql, int window_left) {
+  return (L + kTile - 1) / kTile - first_tile_of(L, ql, window_left);
 }
 
 // First tile of range r out of R over NT tiles, and the range holding tile t.
@@ -355,7 +370,8 @@ __device__ __forceinline__ void tile_prefix(const DecodeParams &p, int32_t *s, i
   int local = 0;
   for (int i = 0; i < per; ++i) {
     const int b = b0 + i;
-    if (b < B) local += (seq_len_of(p.seqlens, b, p.seqlen_add, p.max_len) + kTile - 1) / kTile;
+    if (b < B) local += tiles_of(seq_len_of(p.seqlens, b, p.seqlen_add, p.max_len), p.ql,
+                                 p.window_left);
   }
   // Inclusive scan of `local` across the workgroup.
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -374,7 +390,7 @@ __device__ __forceinline__ void tile_prefix(const DecodeParams &p, int32_t *s, i
     const int b = b0 + i;
     if (b < B) {
       s[b] = run;
-      run += (seq_len_of(p.seqlens, b, p.seqlen_add, p.max_len) + kTile - 1) / kTile;
+      run += tiles_of(seq_len_of(p.seqlens, b, p.seqlen_add, p.max_len), p.ql, p.window_left);
     }
   }
   if (threadIdx.x == kThreads - 1) s[B] = base + x;
@@ -487,9 +503,12 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
 #pragma unroll
   for (int u = 0; u < U; ++u) v_off[u] = (4 * row + u) * (int)st + col * VB;
   // Column col = query token ct, group head cg; the causal mask hides the
-  // last c_hide keys of the sequence from it.
+  // last c_hide keys of the sequence from it, and the window all keys more
+  // than c_reach from the sequence end. Key k of a sequence of L keys is seen
+  // when c_hide < L - k <= c_reach.
   const int ct = col / gq, cg = col - (col / gq) * gq;
   const int c_hide = p.causal ? p.ql - 1 - ct : 0;
+  const int c_reach = p.window_left >= 0 ? p.ql - ct + p.window_left : 0x3fffffff;
   const int q_off =
       col < nc ? ct * (int)p.q_st + cg * (int)p.q_sh + row * (kF8 ? 32 : 16) : kOffOut;
   const int q_bytes = (p.ql - 1) * (int)p.q_st + (gq - 1) * (int)p.q_sh + HD * 2;
@@ -510,6 +529,7 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   int p_start = rfl(s_tiles[pb]);
   int p_end = rfl(s_tiles[pb + 1]);
   int p_len = seq_len_of(p.seqlens, pb, p.seqlen_add, p.max_len);
+  int p_first = first_tile_of(p_len, p.ql, p.window_left);  // tile of the sequence at p_start
   ConstI32 p_bt = as_const(p.bt + (int64_t)pb * p.bt_stride);
 
   auto make_tile = [&](int t, Tile &d, int (&lpg)[NPG]) {
@@ -531,13 +551,14 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
         p_end = rfl(s_tiles[pb + 1]);
       } while (t >= p_end);
       p_len = seq_len_of(p.seqlens, pb, p.seqlen_add, p.max_len);
+      p_first = first_tile_of(p_len, p.ql, p.window_left);
       p_bt = as_const(p.bt + (int64_t)pb * p.bt_stride);
     }
     d.b = pb;
-    d.tok0 = (t - p_start) * kTile;
+    d.tok0 = (t - p_start + p_first) * kTile;
     d.rem = p_len - d.tok0;
     d.valid = min(kTile, d.rem);
-    const bool seq_start = d.tok0 == 0, seq_end = d.tok0 + kTile >= p_len;
+    const bool seq_start = t == p_start, seq_end = d.tok0 + kTile >= p_len;
     d.flags = ((t == lo || seq_start) ? kFirst : 0) | ((t == hi - 1 || seq_end) ? kLast : 0) |
               (seq_start ? kSeqStart : 0) | (seq_end ? kSeqEnd : 0) | (t == lo ? kRangeStart : 0);
     if constexpr (kLanePages) {
@@ -694,7 +715,8 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
     bool need = false;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const bool valid = (col < nc) & (4 * row + i < d.rem - c_hide);
+      const int r = 4 * row + i;
+      const bool valid = (col < nc) & (r < d.rem - c_hide) & (r >= d.rem - c_reach);
       x[i] = valid ? (acc0[i] + acc1[i]) * c : -INFINITY;
       need |= x[i] > m + kRescaleLog2;
     }

@@ -24,7 +24,7 @@ LIB_PATH = Path(
     os.environ.get("MXFLASHATTN_AMD_LIB")
     or Path(__file__).resolve().parent / "_lib" / "libmxfa_mi355x.so"
 )
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 MXFA_OK = 0
 MXFA_EUNSUPPORTED = -1
@@ -96,7 +96,7 @@ _SIGNATURES = {
     "mxfa_split_decode_fp8_partial_launch": (_i, _SPLIT_ARGS + [_p, _p, _p]),
     "mxfa_split_decode_multi_launch": (
         _i,
-        [_p, _i64, _i64, _i64, _i, _i, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _p, _i64,
+        [_p, _i64, _i64, _i64, _i, _i, _i, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _p, _i64,
          _i64, _i64, _p, _sz, _f, _i, _i, _i, _i, _i, _i, _i, _i, _i, _p, _p, _i, _p],
     ),
     "mxfa_split_decode_combine_launch": (
@@ -367,13 +367,17 @@ def _prepare(q, k_cache, v_cache, block_table, cache_seqlens, out):
 
 
 def _launch_multi(q, k_cache, v_cache, block_table, cache_seqlens, out, workspace, ws_bytes,
-                  softmax_scale, num_splits, seqlen_add, stream, causal, k_scale, v_scale):
+                  softmax_scale, num_splits, seqlen_add, stream, causal, k_scale, v_scale,
+                  window_left):
+    if q.dim() == 3:
+        q, out = q.unsqueeze(1), out.unsqueeze(1)
     batch, ql, hq, hd = q.shape
     pages, ps, hkv = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
     qs, os_, cs = q.stride(), out.stride(), k_cache.stride()
     fp8 = k_cache.dtype == FP8_DTYPE
     rc = library().mxfa_split_decode_multi_launch(
-        q.data_ptr(), qs[0], qs[1], qs[2], ql, int(bool(causal)), k_cache.data_ptr(),
+        q.data_ptr(), qs[0], qs[1], qs[2], ql, int(bool(causal)), int(window_left),
+        k_cache.data_ptr(),
         v_cache.data_ptr(), cs[0], cs[1], cs[2], block_table.data_ptr(), block_table.stride(0),
         cache_seqlens.data_ptr(), seqlen_add, out.data_ptr(), os_[0], os_[1], os_[2], workspace,
         ws_bytes, float(softmax_scale), batch, hq, hkv, hd, ps, block_table.shape[1], pages,
@@ -403,6 +407,7 @@ def paged_decode_split(
     k_scale: torch.Tensor | float | None = None,
     v_scale: torch.Tensor | float | None = None,
     causal: bool = False,
+    window_left: int = -1,
 ) -> torch.Tensor:
     """Split-KV paged decode on the current stream; returns ``out`` shaped like q.
 
@@ -413,8 +418,13 @@ def paged_decode_split(
     per-tensor dequantisation scales k_scale / v_scale (float32 device scalars
     for graph capture); block_table: int32 [B, W]; cache_seqlens: int32 [B].
     The attended length of sequence b is cache_seqlens[b] + seqlen_add.
+    window_left >= 0: sliding window, the token at position i sees keys
+    >= i - window_left (FlashAttention's window_size (window_left, 0) with
+    causal, (window_left, -1) without).
     num_splits: balanced work ranges per kv head (default: split_heuristic).
     """
+    if int(window_left) < -1:
+        raise ValueError(f"window_left must be >= -1, got {window_left}")
     q, block_table, cache_seqlens, out = _prepare(q, k_cache, v_cache, block_table,
                                                   cache_seqlens, out)
     lib = library()
@@ -424,10 +434,10 @@ def paged_decode_split(
     ql = q.shape[1] if q.dim() == 4 else 1
     ws_bytes = workspace_size(q.shape[0], q.shape[-2] * ql, q.shape[-1], num_splits)
     ws = WORKSPACE.get(q.device, stream, ws_bytes)
-    if ql > 1:
+    if ql > 1 or window_left >= 0:
         _launch_multi(q, k_cache, v_cache, block_table, cache_seqlens, out, ws.data_ptr(),
                       ws_bytes, softmax_scale, num_splits, seqlen_add, stream, causal, k_scale,
-                      v_scale)
+                      v_scale, window_left)
         return out
     args = _launch_args(q, k_cache, v_cache, block_table, cache_seqlens, out, ws.data_ptr(),
                         ws_bytes, softmax_scale, num_splits, seqlen_add, stream)

@@ -13,6 +13,12 @@ Semantics follow the reference function by function:
                                          cache_seqlens[b] + t (paged: page
                                          block_table[b, pos // PS], row pos % PS),
                                          gather, attention, then cache_seqlens += S_new.
+
+window_left (attention_single, attention_kvcache) has no reference
+counterpart: the reference rejects sliding windows (validation.py:56-76). With
+window_left >= 0 the query at key position p also drops keys before
+p - window_left, on top of the causal mask. It is pinned by identities against
+the unwindowed port (tests/test_oracle.py), not by the reference.
 """
 
 from __future__ import annotations
@@ -23,7 +29,8 @@ import torch
 
 
 def attention_single(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
-                     softmax_scale: float | None = None, causal: bool = False) -> torch.Tensor:
+                     softmax_scale: float | None = None, causal: bool = False,
+                     window_left: int = -1) -> torch.Tensor:
     """q [Lq, HQ, D], k/v [Lk, HKV, D] -> [Lq, HQ, D] in q.dtype (reference.py:8-40)."""
     if q.shape[0] == 0:
         return q.clone()
@@ -38,11 +45,13 @@ def attention_single(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     kf = k.float().permute(1, 0, 2).repeat_interleave(group, dim=0)
     vf = v.float().permute(1, 0, 2).repeat_interleave(group, dim=0)
     scores = torch.bmm(qf, kf.transpose(1, 2).contiguous()) * scale
-    if causal:
-        # query i sits at key position i + (Lk - Lq); it may not see later keys.
-        qpos = torch.arange(lq).unsqueeze(1) + (lk - lq)
-        kpos = torch.arange(lk).unsqueeze(0)
+    # query i sits at key position i + (Lk - Lq).
+    qpos = torch.arange(lq).unsqueeze(1) + (lk - lq)
+    kpos = torch.arange(lk).unsqueeze(0)
+    if causal:  # it may not see later keys
         scores = scores.masked_fill((kpos > qpos).unsqueeze(0), float("-inf"))
+    if window_left >= 0:  # nor keys more than window_left before it
+        scores = scores.masked_fill((kpos < qpos - window_left).unsqueeze(0), float("-inf"))
     probs = torch.nan_to_num(torch.softmax(scores, dim=-1), nan=0.0, posinf=0.0, neginf=0.0)
     return torch.bmm(probs, vf).permute(1, 0, 2).to(q.dtype)
 
@@ -81,7 +90,8 @@ def gather_pages(cache: torch.Tensor, pages: list[int], length: int) -> torch.Te
 def attention_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, *,
                       cache_seqlens: torch.Tensor, block_table: torch.Tensor | None,
                       k: torch.Tensor | None = None, v: torch.Tensor | None = None,
-                      softmax_scale: float | None = None, causal: bool = False) -> torch.Tensor:
+                      softmax_scale: float | None = None, causal: bool = False,
+                      window_left: int = -1) -> torch.Tensor:
     """Decode/append against a dense or paged cache (reference.py:88-139).
 
     Mutates the caches (append) and cache_seqlens (+= S_new) like the reference.
@@ -106,7 +116,8 @@ def attention_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
                 v_cache[row[page], off] = v[b, t]
             kb = gather_pages(k_cache, row, total)
             vb = gather_pages(v_cache, row, total)
-        outs.append(attention_single(q[b], kb, vb, softmax_scale=softmax_scale, causal=causal))
+        outs.append(attention_single(q[b], kb, vb, softmax_scale=softmax_scale, causal=causal,
+                                     window_left=window_left))
     if k is not None:
         cache_seqlens.add_(s_new)
     return torch.stack(outs) if outs else q.clone()

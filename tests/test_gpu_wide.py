@@ -232,8 +232,9 @@ def test_fp8_reshape_and_cache_keeps_nan_and_saturates_inf(device):
 # Several query tokens per sequence (decode with draft tokens)
 
 
-def port_expected(b, causal: bool) -> torch.Tensor:
-    """fp32 restatement of reference.attention_kvcache (bottom-right causal mask)."""
+def port_expected(b, causal: bool, window_left: int = -1) -> torch.Tensor:
+    """fp32 restatement of reference.attention_kvcache (bottom-right causal mask;
+    window_left >= 0 adds the sliding window of the port, pinned in test_oracle)."""
     from oracle import reference_port
 
     cpu = b.to("cpu")
@@ -244,7 +245,7 @@ def port_expected(b, causal: bool) -> torch.Tensor:
         out[i:i + 1] = reference_port.attention_kvcache(
             cpu.q[i:i + 1].float(), cpu.k_cache.float(), cpu.v_cache.float(),
             cache_seqlens=cpu.cache_seqlens[i:i + 1].clone(), block_table=cpu.block_table[i:i + 1],
-            softmax_scale=cpu.scale, causal=causal).float()
+            softmax_scale=cpu.scale, causal=causal, window_left=window_left).float()
     return out
 
 
@@ -341,3 +342,81 @@ def test_dense_query_tokens_through_flash_attn_func(device, sq, sk, causal):
     torch.cuda.synchronize()
     assert mx.get_last_dispatch_info().backend == mx.BACKEND_MI355X
     assert max_err(out, expected) <= TOL[torch.float16]
+
+
+# ---------------------------------------------------------------------------
+# Sliding window (window_left): keys before position - window_left are dropped;
+# each sequence's tiles start at the first tile the window reaches.
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("window", [0, 16, 17, 100, 5000])
+@pytest.mark.parametrize("ql,gq,causal", [(1, 4, False), (2, 4, True), (3, 4, True),
+                                          (4, 4, False), (2, 8, True)])
+def test_window_matches_reference(device, dtype, head_dim, window, ql, gq, causal):
+    lengths = torch.tensor([1, 2, 17, 300, 0, 1000, 33])
+    b = make_paged_batch(7, 2 * gq, 2, head_dim, dtype, lengths, seed=80 + window).to(device)
+    b = with_query_tokens(b, ql, 81)
+    if ql == 1:
+        b.q = b.q[:, 0]  # [B, HQ, HD]: the one-token form takes the window too
+    expected = port_expected(b if ql > 1 else with_query_tokens_view(b), causal, window)
+    for ns in (None, 1, 9, 64):
+        kw = {} if ns is None else dict(num_splits=ns)
+        got = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table,
+                                        b.cache_seqlens, b.scale, causal=causal,
+                                        window_left=window, **kw)
+        torch.cuda.synchronize()
+        got = got if ql > 1 else got.unsqueeze(1)
+        assert torch.isfinite(got.float()).all()
+        assert max_err(got, expected) <= TOL[dtype], (ns, max_err(got, expected))
+        assert torch.equal(got[4].cpu(), torch.zeros_like(got[4].cpu()))
+
+
+def with_query_tokens_view(b):
+    """The same batch with q as [B, 1, HQ, HD] (for the reference port)."""
+    return type(b)(b.q.unsqueeze(1), b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
+                   b.scale)
+
+
+@pytest.mark.parametrize("page_size", [1, 4, 64])
+@pytest.mark.parametrize("window", [0, 5, 40])
+def test_window_with_small_and_large_pages(device, page_size, window):
+    b = make_paged_batch(5, 8, 2, 128, torch.bfloat16, torch.tensor([1, 9, 64, 130, 700]),
+                         seed=85, page_size=page_size).to(device)
+    b = with_query_tokens(b, 2, 86)
+    got = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
+                                    b.scale, causal=True, window_left=window)
+    torch.cuda.synchronize()
+    assert max_err(got, port_expected(b, True, window)) <= TOL[torch.bfloat16]
+
+
+@pytest.mark.parametrize("window", [0, 31, 200])
+def test_window_fp8_and_head_dim_256(device, window):
+    b = make_paged_batch(4, 8, 2, 256, torch.bfloat16, torch.tensor([3, 64, 500, 1200]),
+                         seed=87).to(device)
+    b = with_query_tokens(b, 2, 88)
+    got = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
+                                    b.scale, causal=True, window_left=window)
+    torch.cuda.synchronize()
+    assert max_err(got, port_expected(b, True, window)) <= TOL[torch.bfloat16]
+    k8, v8 = fp8_caches(b, device)
+    b8 = type(b)(b.q, k8.cpu().float().to(torch.bfloat16).to(device),
+                 v8.cpu().float().to(torch.bfloat16).to(device), b.block_table, b.cache_seqlens,
+                 b.scale)  # the exactly dequantised caches, scales 1
+    got = native.paged_decode_split(b.q, k8, v8, b.block_table, b.cache_seqlens, b.scale,
+                                    causal=True, window_left=window)
+    torch.cuda.synchronize()
+    assert max_err(got, port_expected(b8, True, window)) <= TOL[torch.bfloat16]
+
+
+def test_window_on_a_long_sequence(device):
+    # 120,000 keys with a 128-key window: only the last tiles are read, and
+    # the result matches the port's masked attention over all the keys.
+    n, window = 120_000, 128
+    b = make_paged_batch(2, 16, 2, 128, torch.bfloat16, torch.tensor([n, 5000]),
+                         seed=89).to(device)
+    got = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
+                                    b.scale, window_left=window)
+    torch.cuda.synchronize()
+    assert max_err(got, port_expected(b, False, window)) <= TOL[torch.bfloat16]

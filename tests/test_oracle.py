@@ -406,3 +406,77 @@ def test_fp8_decode_oracle_equals_fp64_oracle_on_dequantised_caches():
     vf = c_oracle.e4m3fn_decode(v8) * 0.5
     want = c_oracle.paged_decode_f64(b.q, kf, vf, b.block_table, b.cache_seqlens, b.scale)
     assert np.abs(got - want).max() < 1e-12
+
+
+# Sliding window (window_left): an extension with no reference counterpart,
+# pinned by identities against the unwindowed port and by library attention.
+
+@pytest.mark.parametrize("window", [0, 1, 15, 16, 17, 64, 299, 1000])
+def test_window_equals_attention_over_the_last_keys(window):
+    # One query token at position L-1 sees keys [L-1-window, L-1]: the same as
+    # unwindowed attention over those keys alone, computed by slicing.
+    lengths = torch.tensor([1, 5, 16, 17, 100, 300])
+    b = make_paged_batch(6, 8, 2, 64, torch.float32, lengths, seed=41)
+    got = reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache,
+                                           cache_seqlens=b.cache_seqlens.clone(),
+                                           block_table=b.block_table, window_left=window)
+    for i, n in enumerate(lengths.tolist()):
+        row = b.block_table[i].tolist()
+        keep = min(n, window + 1)
+        kb = gather_dense(b.k_cache, row, n)[n - keep:]
+        vb = gather_dense(b.v_cache, row, n)[n - keep:]
+        want = reference_port.attention_single(b.q[i], kb, vb, softmax_scale=b.scale)
+        torch.testing.assert_close(got[i], want, atol=2e-6, rtol=1e-6)
+
+
+@pytest.mark.parametrize("window", [0, 3, 20])
+def test_window_rows_of_several_tokens_are_single_token_windows(window):
+    # Causal token t of QL sits at position L-QL+t: its output is one-token
+    # windowed decode over the cache cut at that position.
+    ql, lengths = 3, torch.tensor([3, 9, 40])
+    b = make_paged_batch(3, 8, 4, 64, torch.float32, lengths, seed=42, q_len=ql)
+    got = reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache,
+                                           cache_seqlens=b.cache_seqlens.clone(),
+                                           block_table=b.block_table, causal=True,
+                                           window_left=window)
+    for i, n in enumerate(lengths.tolist()):
+        for t in range(ql):
+            cut = torch.tensor([n - ql + t + 1])
+            one = reference_port.attention_kvcache(
+                b.q[i:i + 1, t:t + 1], b.k_cache, b.v_cache, cache_seqlens=cut,
+                block_table=b.block_table[i:i + 1], window_left=window)
+            torch.testing.assert_close(got[i, t], one[0, 0])
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_window_matches_library_attention_with_a_built_mask(causal):
+    ql, window, n = 4, 6, 30
+    b = make_paged_batch(1, 4, 2, 64, torch.float64, torch.tensor([n]), seed=43, q_len=ql)
+    got = reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache,
+                                           cache_seqlens=b.cache_seqlens.clone(),
+                                           block_table=b.block_table, causal=causal,
+                                           window_left=window)
+    row = b.block_table[0].tolist()
+    keys, values = gather_dense(b.k_cache, row, n), gather_dense(b.v_cache, row, n)
+    allowed = torch.zeros(ql, n, dtype=torch.bool)
+    for t in range(ql):
+        pos = n - ql + t
+        for j in range(n):
+            allowed[t, j] = j >= pos - window and (j <= pos or not causal)
+    for h in range(4):
+        qh = b.q[0, :, h].unsqueeze(0).unsqueeze(0)
+        kh = keys[:, h // 2].unsqueeze(0).unsqueeze(0)
+        vh = values[:, h // 2].unsqueeze(0).unsqueeze(0)
+        want = F.scaled_dot_product_attention(qh, kh, vh, attn_mask=allowed, scale=b.scale)
+        # The port computes in fp32 (as reference.py does); a wrong mask would
+        # differ by O(0.1).
+        torch.testing.assert_close(got[0, :, h], want[0, 0], atol=2e-6, rtol=1e-5)
+
+
+def test_window_covering_the_sequence_changes_nothing():
+    b = make_paged_batch(3, 8, 2, 64, torch.float32, torch.tensor([1, 50, 128]), seed=44,
+                         q_len=2)
+    args = dict(cache_seqlens=b.cache_seqlens, block_table=b.block_table, causal=True)
+    plain = reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache, **args)
+    wide = reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache, window_left=127, **args)
+    assert torch.equal(plain, wide)
