@@ -228,43 +228,55 @@ def _decode_forward_graph(query: torch.Tensor, kv_cache: torch.Tensor, attn_meta
     return result.reshape(q.shape[0] * q.shape[1], -1), None
 
 
-def _fp8_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: Any,
-                output: torch.Tensor, softmax_scale: float, k_scale: Any,
-                v_scale: Any) -> torch.Tensor:
-    """One-token decode over an fp8 (e4m3fn) cache, straight on the HIP kernels
-    (the public API, like the reference's, takes 16-bit caches only)."""
+def _native_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: Any,
+                   output: torch.Tensor, softmax_scale: float, k_scale: Any, v_scale: Any,
+                   fp8: bool, window_left: int) -> torch.Tensor:
+    """One-token decode straight on the HIP kernels, for what the public API
+    (like the reference's) does not take: an fp8 (e4m3fn) cache and/or a
+    sliding window."""
     _no_cascade(attn_metadata)
     if int(attn_metadata.max_query_len) != 1:
         raise DecoderAdapterBlocked(
             f"only_single_token_decode_supported:max_query_len={int(attn_metadata.max_query_len)}")
-    key_cache, value_cache = kv_cache.view(native.FP8_DTYPE).unbind(0)
+    if not output.is_contiguous():
+        raise DecoderAdapterBlocked("native_decode_needs_a_contiguous_output")
+    caches = kv_cache.view(native.FP8_DTYPE) if fp8 else kv_cache
+    key_cache, value_cache = caches.unbind(0)
     n = int(attn_metadata.num_actual_tokens)
     q = query[:n].reshape(n, 1, query.shape[1], query.shape[2])
     target = output[:n].view(n, 1, query.shape[1], query.shape[2])
+    scales = dict(k_scale=k_scale, v_scale=v_scale) if fp8 else {}
     native.paged_decode_split(q, key_cache, value_cache,
                               _int32_on(attn_metadata.block_table, query.device),
                               _int32_on(attn_metadata.seq_lens.reshape(-1), query.device),
-                              softmax_scale, out=target, k_scale=k_scale, v_scale=v_scale)
-    record_event({"path": "mi355x_split_decode", "operation": "paged_decode_split",
-                  "fallback": "false", "kv_cache_dtype": "fp8_e4m3"})
+                              softmax_scale, out=target, window_left=window_left, **scales)
+    event = {"path": "mi355x_split_decode", "operation": "paged_decode_split",
+             "fallback": "false"}
+    if fp8:
+        event["kv_cache_dtype"] = "fp8_e4m3"
+    if window_left >= 0:
+        event["window_left"] = str(window_left)
+    record_event(event)
     return output
 
 
 def forward_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: Any,
                    output: torch.Tensor, *, softmax_scale: float, kv_cache_dtype: str = "auto",
-                   k_scale: Any = None, v_scale: Any = None) -> torch.Tensor:
+                   k_scale: Any = None, v_scale: Any = None,
+                   window_left: int = -1) -> torch.Tensor:
     """The decode body of the backend's ``forward``: one-token paged decode into
     vLLM's output buffer, with the dispatch event the reference plugin records
     (integrations/vllm/vllm_plugin.py:297-299,399-431). Raises
     DecoderAdapterBlocked for calls outside the adapter contract (prefill,
     cascade), which the backend hands to vLLM. kv_cache_dtype "fp8"/"fp8_e4m3"
     (cache stored as e4m3fn or its uint8 codes) decodes with the layer's
-    per-tensor k_scale / v_scale; the reference has no fp8 path."""
-    if kv_cache_dtype in ("fp8", "fp8_e4m3"):
-        if not output.is_contiguous():
-            raise DecoderAdapterBlocked("fp8_decode_needs_a_contiguous_output")
-        return _fp8_decode(query, kv_cache, attn_metadata, output, softmax_scale, k_scale,
-                           v_scale)
+    per-tensor k_scale / v_scale, and window_left >= 0 with the layer's
+    sliding window (the query at position i sees keys >= i - window_left);
+    the reference has neither."""
+    fp8 = kv_cache_dtype in ("fp8", "fp8_e4m3")
+    if fp8 or window_left >= 0:
+        return _native_decode(query, kv_cache, attn_metadata, output, softmax_scale, k_scale,
+                              v_scale, fp8, window_left)
     result, _ = decode_forward(query, kv_cache, attn_metadata, softmax_scale=softmax_scale,
                                causal=bool(attn_metadata.causal))
     info = get_last_dispatch_info()

@@ -73,9 +73,27 @@ def _no_window(window: Any, causal: bool, ql: int) -> bool:
     return left < 0 and (right < 0 or causal or ql == 1)
 
 
+def window_for_kernel(window: Any, causal: bool, ql: int) -> tuple[int, bool] | None:
+    """FlashAttention's window_size as the kernel's (window_left, causal), or
+    None when the kernel cannot express it. -1 is unbounded on either side; a
+    right bound of 0 is the causal mask; a positive right bound matters only
+    for several non-causal query tokens, which the kernel has no bound for."""
+    if window is None:
+        return -1, causal
+    try:
+        left, right = (window, -1) if not isinstance(window, (tuple, list)) else window
+        left, right = int(left), int(right)
+    except (TypeError, ValueError):
+        return None
+    if right > 0 and not causal and ql > 1:
+        return None
+    return (left if left >= 0 else -1), causal or (right == 0 and ql > 1)
+
+
 def _guard(args: tuple, kwargs: dict, wide: bool = False,
            descales: tuple = (None, None)) -> tuple[str | None, tuple]:
-    """(reason, (q, k_cache, v_cache, block_table, seqlens)); reason None = take it."""
+    """(reason, (q, k_cache, v_cache, block_table, seqlens, window_left, causal));
+    reason None = take it. Sliding windows are taken under the wider contract."""
     q = args[0] if args else kwargs.get("q")
     if q is None or q.dim() not in (3, 4):
         return "query_rank", ()
@@ -85,9 +103,18 @@ def _guard(args: tuple, kwargs: dict, wide: bool = False,
         return "block_table_or_seqlens", ()
     if kwargs.get("alibi_slopes") is not None:
         return "alibi", ()
-    if not _no_window(kwargs.get("window_size"), bool(kwargs.get("causal", False)),
-                      q.shape[1] if q.dim() == 4 else 1):
+    ql = q.shape[1] if q.dim() == 4 else 1
+    causal = bool(kwargs.get("causal", False))
+    window = kwargs.get("window_size")
+    if wide:
+        mapped = window_for_kernel(window, causal, ql)
+        if mapped is None:
+            return "window", ()
+        window_left, causal = mapped
+    elif not _no_window(window, causal, ql):
         return "window", ()
+    else:
+        window_left = -1
     try:
         if float(kwargs.get("softcap") or 0.0) != 0.0:
             return "softcap", ()
@@ -120,7 +147,7 @@ def _guard(args: tuple, kwargs: dict, wide: bool = False,
         return "page_size", ()
     if q.device.type != "cuda":
         return "device", ()
-    return None, (q, k_cache, v_cache, bt, sl)
+    return None, (q, k_cache, v_cache, bt, sl, window_left, causal)
 
 
 def try_native_decode(args: tuple, kwargs: dict, k_descale: Any = None,
@@ -145,7 +172,7 @@ def try_native_decode(args: tuple, kwargs: dict, k_descale: Any = None,
 
 def _native_decode(picked: tuple, kwargs: dict, k_descale: Any,
                    v_descale: Any) -> torch.Tensor:
-    q, k_cache, v_cache, bt, sl = picked
+    q, k_cache, v_cache, bt, sl, window_left, causal = picked
     hq, hd = q.shape[-2], q.shape[-1]
     # An explicit 0.0 is a scale (uniform weights), not "use the default".
     scale = kwargs.get("softmax_scale")
@@ -164,7 +191,7 @@ def _native_decode(picked: tuple, kwargs: dict, k_descale: Any,
     if k_cache.dtype == native.FP8_DTYPE:
         scales = {"k_scale": k_descale, "v_scale": v_descale}
     result = native.paged_decode_split(q4, k_cache, v_cache, bt, sl, scale, out=out,
-                                       num_splits=ns, causal=bool(kwargs.get("causal", False)),
+                                       num_splits=ns, causal=causal, window_left=window_left,
                                        **scales)
     if provided is not None and out is None:
         provided.copy_(result.reshape_as(provided))

@@ -10,9 +10,10 @@ argument" failure is retried once with the untouched functions. The reference
 also swaps ``flash_attn_varlen_func`` there; prefill is not on this path, so it
 stays vLLM's. Encoder layers (``attn_type`` "encoder" / "encoder_only", which
 the reference sends to its dense API and on to the vendor kernel) run vLLM's
-own forward, and so do layers with a sliding window, ALiBi slopes,
-logit soft-capping or attention sinks, which the reference's forward sends to
-its decoder regardless. Otherwise the forward runs ``decode_forward`` (public
+own forward, and so do layers with ALiBi slopes, logit soft-capping or
+attention sinks, and sliding-window layers unless the wider contract is on
+(then the kernel applies the window); the reference's forward sends all of
+them to its decoder regardless. Otherwise the forward runs ``decode_forward`` (public
 API) and falls back to vLLM for prefill. The KV-cache update uses the HIP append kernel
 (``reshape_and_cache_flash``).
 Classes live at module scope because vLLM resolves the backend by import path
@@ -67,13 +68,22 @@ def _forward_official_split(impl, layer, query, key, value, kv_cache, metadata, 
     return result
 
 
+def _layer_window(impl) -> int:
+    """The layer's sliding window as the kernel's window_left (-1: none);
+    vLLM stores it as FlashAttention's (window - 1, 0)."""
+    mapped = native_decode.window_for_kernel(getattr(impl, "sliding_window", None), True, 1)
+    return -1 if mapped is None else mapped[0]
+
+
 def _layer_option(impl) -> str | None:
     """An option of the layer that the decode kernel does not compute (vLLM's
-    FlashAttentionImpl applies them in its own forward), or None."""
+    FlashAttentionImpl applies them in its own forward), or None. Sliding
+    windows are computed under the wider contract."""
     if getattr(impl, "alibi_slopes", None) is not None:
         return "alibi"
     window = getattr(impl, "sliding_window", None)
-    if window is not None and not native_decode._no_window(window, True, 1):
+    if (window is not None and not native_decode._no_window(window, True, 1)
+            and not native_decode.wide_contract()):
         return "window"
     if getattr(impl, "logits_soft_cap", None):
         return "softcap"
@@ -133,7 +143,8 @@ class MXFlashAttnImpl(FlashAttentionImpl):
             return forward_decode(query, kv_cache, attn_metadata, output,
                                   softmax_scale=self.scale, kv_cache_dtype=kv_dtype,
                                   k_scale=getattr(layer, "_k_scale", None),
-                                  v_scale=getattr(layer, "_v_scale", None))
+                                  v_scale=getattr(layer, "_v_scale", None),
+                                  window_left=_layer_window(self))
         except DecoderAdapterBlocked as exc:
             record_event({"path": "vendor_prefill_or_blocked", "reason": str(exc)})
             if "single_token_decode" in str(exc):

@@ -24,6 +24,7 @@ class PagedBatch:
     block_table: torch.Tensor   # int32 [B, W]
     cache_seqlens: torch.Tensor  # int32 [B]
     scale: float
+    window_left: int = -1       # sliding window of the decode call (-1: none)
 
     @property
     def batch(self) -> int:
@@ -48,22 +49,38 @@ class PagedBatch:
     def total_tokens(self) -> int:
         return int(self.cache_seqlens.sum().item())
 
+    def attended_tokens(self) -> torch.Tensor:
+        """Keys per sequence that some query token sees: L_b, or with a
+        sliding window min(L_b, window_left + QL) (the QL tokens' windows
+        together)."""
+        lens = self.cache_seqlens.to(torch.int64).cpu()
+        if self.window_left < 0:
+            return lens
+        return torch.clamp(lens, max=self.window_left + self.q.shape[1])
+
+    def total_tokens(self) -> int:
+        return int(self.cache_seqlens.sum().item())
+
     def kv_bytes(self) -> int:
-        """K and V bytes the call must read: sum_b 2 * L_b * HKV * HD * elem
-        (the cache's element: 2 bytes, or 1 for an fp8 cache)."""
-        return (2 * self.total_tokens() * self.kv_heads * self.head_dim
+        """K and V bytes the call must read: sum_b 2 * A_b * HKV * HD * elem,
+        A_b the attended keys (L_b without a window), elem the cache's
+        element (2 bytes, or 1 for an fp8 cache)."""
+        return (2 * int(self.attended_tokens().sum()) * self.kv_heads * self.head_dim
                 * self.k_cache.element_size())
 
     def algorithmic_bytes(self) -> int:
         """KV + q + out + used block-table entries + lengths."""
         ps = self.page_size
-        pages = int(((self.cache_seqlens + ps - 1) // ps).sum().item())
+        lens = self.cache_seqlens.to(torch.int64).cpu()
+        first = ((lens - self.attended_tokens()) // ps)
+        pages = int(((lens + ps - 1) // ps - first).sum().item())
         qo = 2 * self.q.numel() * self.q.element_size()
         return self.kv_bytes() + qo + 4 * pages + 4 * self.batch
 
     def to(self, device: torch.device | str) -> "PagedBatch":
         return PagedBatch(self.q.to(device), self.k_cache.to(device), self.v_cache.to(device),
-                          self.block_table.to(device), self.cache_seqlens.to(device), self.scale)
+                          self.block_table.to(device), self.cache_seqlens.to(device), self.scale,
+                          self.window_left)
 
 
 def make_paged_batch(
@@ -84,6 +101,7 @@ def make_paged_batch(
     device: torch.device | str = "cpu",
     kv_dtype: torch.dtype | None = None,
     q_len: int = 1,
+    window_left: int = -1,
 ) -> PagedBatch:
     """Build one synthetic decode batch.
 
@@ -95,6 +113,8 @@ def make_paged_batch(
     float8_e4m3fn stores the caches as fp8 (the same N(0, 1) draws, rounded to
     nearest even; their dequantisation scales are 1). q_len > 1 gives every
     sequence that many query tokens (the last q_len positions of its length).
+    window_left is recorded for the decode call (a sliding window) and changes
+    the bytes the call must read, not the data.
     """
     device = torch.device(device)
     gen = torch.Generator(device=device)
@@ -140,6 +160,7 @@ def make_paged_batch(
         block_table=table.to(device),
         cache_seqlens=lens.to(torch.int32).to(device),
         scale=head_dim ** -0.5,
+        window_left=window_left,
     )
 
 
@@ -184,4 +205,10 @@ WIDE = {
     # same KV bytes as one token.
     "wide_q4_config2": dict(batch=32, q_heads=32, kv_heads=8, head_dim=128,
                             dtype=torch.bfloat16, lengths=(1024, 8192), q_len=4, causal=True),
+    # Config 2 with a 1024-key sliding window (the local layers of models that
+    # alternate local and global attention): each sequence reads its last
+    # 1024 keys, 1/4.5 of the full call's bytes.
+    "wide_window1024_config2": dict(batch=32, q_heads=32, kv_heads=8, head_dim=128,
+                                    dtype=torch.bfloat16, lengths=(1024, 8192),
+                                    window_left=1023),
 }

@@ -136,3 +136,48 @@ def test_plugin_path_with_fp8_cache_matches_oracle(device):
         # append is bit-exact there.
         assert torch.equal(st.kv_caches[0].view(torch.uint8), ref_caches[0].view(torch.uint8))
         decode_step.advance(st)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kv_dtype", ["auto", "fp8"])
+def test_adapter_window_decode_matches_oracle(device, kv_dtype):
+    """forward_decode with a layer's sliding window (the backend under the
+    wider contract), on a vLLM-layout cache [2, blocks, PS, HKV, HD], against
+    the port's windowed attention; fp8 caches on their exactly decoded values."""
+    from types import SimpleNamespace
+
+    from mxflashattn_amd.integrations.vllm import decoder_adapter
+
+    g = torch.Generator().manual_seed(31)
+    hq, hkv, hd, ps = 8, 2, 128, 16
+    lengths = torch.tensor([1, 40, 300, 1000], dtype=torch.int32)
+    need = [(int(n) + ps - 1) // ps for n in lengths]
+    blocks = sum(need) + 3
+    perm = torch.randperm(blocks, generator=g).to(torch.int32)
+    table = torch.zeros(4, max(need), dtype=torch.int32)
+    at = 0
+    for b, n in enumerate(need):
+        table[b, :n] = perm[at:at + n]
+        at += n
+    cache = torch.randn(2, blocks, ps, hkv, hd, generator=g).to(torch.bfloat16)
+    if kv_dtype == "fp8":
+        codes = cache.float().to(torch.float8_e4m3fn)
+        ref_cache, dev_cache = codes.float().to(torch.bfloat16), codes.view(torch.uint8)
+    else:
+        ref_cache, dev_cache = cache, cache
+    q = torch.randn(4, hq, hd, generator=g).to(torch.bfloat16)
+    meta = SimpleNamespace(num_actual_tokens=4, max_query_len=1, use_cascade=False, causal=True,
+                           seq_lens=lengths.to(device), block_table=table.to(device))
+    one = torch.ones(1, dtype=torch.float32, device=device)
+    scale = hd ** -0.5
+    for window in (0, 17, 100, 5000):
+        out = torch.full((4, hq * hd), float("nan"), dtype=torch.bfloat16, device=device)
+        decoder_adapter.forward_decode(q.to(device), dev_cache.to(device), meta, out,
+                                       softmax_scale=scale, kv_cache_dtype=kv_dtype,
+                                       k_scale=one, v_scale=one, window_left=window)
+        torch.cuda.synchronize()
+        want = reference_port.attention_kvcache(
+            q.unsqueeze(1), ref_cache[0], ref_cache[1], cache_seqlens=lengths.clone(),
+            block_table=table, softmax_scale=scale, window_left=window)
+        err = (out.float().cpu() - want.reshape(4, -1).float()).abs().max().item()
+        assert err <= 1.6e-2, (window, err)

@@ -138,20 +138,42 @@ def test_native_guard_option_checks(extra, reason):
     assert native_decode._guard((q_of(),), kwargs)[0] == reason
 
 
+def _guard_reason(window, causal, ql):
+    kwargs = kv_kwargs()
+    kwargs.update(window_size=window, causal=causal, softcap=0.0)
+    q = torch.empty(1, ql, 16, 128, dtype=torch.float16)
+    return native_decode._guard((q,), kwargs, native_decode.wide_contract())[0]
+
+
 def test_native_guard_window_right_bound_matters_only_for_later_keys(monkeypatch):
+    # The reference's contract: any window that masks something is handed back.
     # One query token, or causal masking, sees no key after itself: a right
     # bound of 0 masks nothing there. Several non-causal tokens would.
-    monkeypatch.setenv("MXFA_WIDE_CONTRACT", "1")
+    monkeypatch.delenv("MXFA_WIDE_CONTRACT", raising=False)
     for window, causal, ql, reason in (((-1, 0), False, 1, "device"),
-                                       ((-1, 0), True, 3, "device"),
+                                       ((-1, 0), True, 3, "query_length"),
                                        ((-1, 0), False, 3, "window"),
-                                       ((-1, -1), False, 3, "device"),
-                                       (-1, False, 3, "device")):
-        kwargs = kv_kwargs()
-        kwargs.update(window_size=window, causal=causal, softcap=0.0)
-        q = torch.empty(1, ql, 16, 128, dtype=torch.float16)
-        wide = native_decode.wide_contract()
-        assert native_decode._guard((q,), kwargs, wide)[0] == reason, (window, causal, ql)
+                                       ((-1, -1), False, 1, "device"),
+                                       (-1, False, 1, "device"),
+                                       ((127, 0), True, 1, "window")):
+        assert _guard_reason(window, causal, ql) == reason, (window, causal, ql)
+
+
+def test_wide_guard_takes_sliding_windows(monkeypatch):
+    monkeypatch.setenv("MXFA_WIDE_CONTRACT", "1")
+    for window, causal, ql, reason in (((127, 0), True, 1, "device"),
+                                       ((0, 0), False, 1, "device"),
+                                       ((5, -1), False, 3, "device"),
+                                       ((-1, 0), False, 3, "device"),   # right 0 = causal
+                                       ((-1, 2), False, 3, "window"),   # no kernel bound
+                                       ((4, 2), True, 3, "device"),
+                                       ("wide", True, 1, "window")):
+        assert _guard_reason(window, causal, ql) == reason, (window, causal, ql)
+    assert native_decode.window_for_kernel((127, 0), False, 1) == (127, False)
+    assert native_decode.window_for_kernel((-1, 0), False, 3) == (-1, True)
+    assert native_decode.window_for_kernel((7, 0), False, 2) == (7, True)
+    assert native_decode.window_for_kernel(None, True, 2) == (-1, True)
+    assert native_decode.window_for_kernel((3, 5), False, 2) is None
 
 
 def test_native_guard_accepts_no_window_and_rank3_queries():
@@ -337,7 +359,7 @@ def _picked_guard(monkeypatch):
                         lambda args, kwargs, *a: (None, (args[0], kwargs["k_cache"],
                                                          kwargs["v_cache"],
                                                          kwargs["block_table"],
-                                                         kwargs["cache_seqlens"])))
+                                                         kwargs["cache_seqlens"], -1, False)))
     monkeypatch.setenv("MXFA_NATIVE_DECODE", "1")
     monkeypatch.setattr(native_decode.native, "default_num_splits", lambda *a: 4)
 

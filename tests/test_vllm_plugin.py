@@ -188,6 +188,17 @@ def test_quantised_output_goes_to_vllm(plugin, monkeypatch):
     assert backend.get_dispatch_events()[-1]["fallback_reason"] == "output_quantization"
 
 
+def test_sliding_window_layers_decode_here_under_the_wider_contract(plugin, monkeypatch):
+    mod, _ = plugin
+    seen = []
+    monkeypatch.setattr(mod, "forward_decode", lambda *a, **k: seen.append(k) or "decoded")
+    monkeypatch.setenv("MXFA_WIDE_CONTRACT", "1")
+    impl = mod.MXFlashAttnImpl()
+    impl.sliding_window, impl.logits_soft_cap = (1023, 0), 0.0  # vLLM's form of a 1024 window
+    assert _forward(mod, impl) == "decoded"
+    assert seen[0]["window_left"] == 1023
+
+
 def test_layer_defaults_reach_the_adapter(plugin, monkeypatch):
     mod, _ = plugin
     monkeypatch.setattr(mod, "forward_decode", lambda *a, **k: "decoded")
@@ -211,8 +222,10 @@ def test_decode_goes_through_the_adapter_with_layer_scales(plugin, monkeypatch):
     monkeypatch.setenv("MXFA_WIDE_CONTRACT", "1")
     assert _forward(mod, mod.MXFlashAttnImpl(kv_cache_dtype="fp8"), layer=layer) == "decoded"
     assert seen == [
-        dict(softmax_scale=0.125, kv_cache_dtype="auto", k_scale="ks", v_scale="vs"),
-        dict(softmax_scale=0.125, kv_cache_dtype="fp8", k_scale="ks", v_scale="vs")]
+        dict(softmax_scale=0.125, kv_cache_dtype="auto", k_scale="ks", v_scale="vs",
+             window_left=-1),
+        dict(softmax_scale=0.125, kv_cache_dtype="fp8", k_scale="ks", v_scale="vs",
+             window_left=-1)]
     with pytest.raises(ValueError, match="output buffer"):
         _forward(mod, output=None)
 

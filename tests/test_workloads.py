@@ -64,3 +64,18 @@ def test_bench_refuses_more_than_one_gpu():
     assert proc.returncode == 2
     assert "measures one GPU" in proc.stderr
     assert proc.stdout == ""
+
+
+def test_window_changes_the_bytes_a_call_reads():
+    lengths = torch.tensor([5, 100, 2000])
+    plain = make_paged_batch(3, 8, 2, 64, torch.float16, lengths, seed=3)
+    win = make_paged_batch(3, 8, 2, 64, torch.float16, lengths, seed=3, window_left=99)
+    assert torch.equal(plain.k_cache, win.k_cache)  # same data
+    assert plain.kv_bytes() == 2 * 2105 * 2 * 64 * 2
+    assert win.attended_tokens().tolist() == [5, 100, 100]
+    assert win.kv_bytes() == 2 * 205 * 2 * 64 * 2
+    # Pages overlapping the window: 1 + 7 + pages 118..124 (keys 1900..1999).
+    assert win.algorithmic_bytes() - win.kv_bytes() == 2 * win.q.numel() * 2 + 4 * (1 + 7 + 7) + 12
+    two = make_paged_batch(3, 8, 2, 64, torch.float16, lengths, seed=3, window_left=99, q_len=2)
+    assert two.attended_tokens().tolist() == [5, 100, 101]
+    assert win.to("cpu").window_left == 99
