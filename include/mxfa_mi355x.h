@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define MXFA_ABI_VERSION 4
+#define MXFA_ABI_VERSION 5
 
 /* Return codes. */
 #define MXFA_OK 0
@@ -124,9 +124,13 @@ int mxfa_split_decode_launch(const void *q, int64_t q_stride_b, int64_t q_stride
  * zeros (the reference's nan_to_num). window_left >= 0 is a sliding window:
  * the token at position i also drops keys before i - window_left
  * (FlashAttention's window_size (window_left, 0) with causal, (window_left,
- * -1) without); -1 means none. The
- * reference has no window: its guards hand such calls to the vendor
- * (integrations/vllm/vllm_plugin.py:236-247). kv_dtype is dtype (16-bit caches) or
+ * -1) without); -1 means none. sinks, if not null, holds one fp32 logit per
+ * query head (HQ values, 4-byte aligned, on the scale of the scaled scores):
+ * each output row becomes sum_j e^(s_j) v_j / (sum_j e^(s_j) + e^(sinks[h])),
+ * a softmax with one extra zero-valued column (the "s_aux" of vLLM's
+ * FlashAttention). The reference has neither: its guards hand windows to the
+ * vendor (integrations/vllm/vllm_plugin.py:236-247) and drop s_aux
+ * (:335-339). kv_dtype is dtype (16-bit caches) or
  * MXFA_DTYPE_FP8_E4M3 with k_scale/v_scale as in mxfa_split_decode_fp8_launch.
  * Workspace: mxfa_split_decode_workspace_size(batch, q_heads * q_len, ...).
  * Partial and combine run as one call. Other arguments as
@@ -136,8 +140,8 @@ int mxfa_split_decode_launch(const void *q, int64_t q_stride_b, int64_t q_stride
  */
 int mxfa_split_decode_multi_launch(
     const void *q, int64_t q_stride_b, int64_t q_stride_t, int64_t q_stride_h, int q_len,
-    int causal, int window_left, const void *k_cache, const void *v_cache,
-    int64_t cache_stride_page, int64_t cache_stride_token, int64_t cache_stride_head,
+    int causal, int window_left, const float *sinks, const void *k_cache,
+    const void *v_cache, int64_t cache_stride_page, int64_t cache_stride_token, int64_t cache_stride_head,
     const int32_t *block_table,
     int64_t bt_stride, const int32_t *seqlens, int seqlen_add, void *out, int64_t out_stride_b,
     int64_t out_stride_t, int64_t out_stride_h, void *workspace, size_t workspace_bytes,

@@ -50,6 +50,7 @@ struct SplitArgs {
   int ql;      // query tokens per sequence
   int causal;  // bottom-right aligned causal mask
   int window_left;  // sliding window (keys >= position - window_left), -1: none
+  const float *sinks;  // per query head softmax sink logits, nullptr: none
 };
 
 struct WsLayout {
@@ -112,7 +113,8 @@ static int check_split_args(const SplitArgs &a) {
   if (a.ql > 1 && !((a.o_st >= (int64_t)a.hq * a.o_sh && a.o_sh >= a.hd) ||
                     (a.o_sh >= (int64_t)a.ql * a.o_st && a.o_st >= a.hd)))
     return MXFA_EINVAL;
-  if (((uintptr_t)a.k_scale & 3u) || ((uintptr_t)a.v_scale & 3u)) return MXFA_EINVAL;
+  if (((uintptr_t)a.k_scale & 3u) || ((uintptr_t)a.v_scale & 3u) || ((uintptr_t)a.sinks & 3u))
+    return MXFA_EINVAL;
   if (!a.ws || !aligned16(a.ws)) return MXFA_EWORKSPACE;
   if (a.ws_bytes < ws_layout(a.batch, a.hq * a.ql, a.hd, a.num_splits).bytes)
     return MXFA_EWORKSPACE;
@@ -152,6 +154,7 @@ static DecodeParams make_params(const SplitArgs &a, const Grid &g) {
   p.ql = a.ql;
   p.causal = a.causal ? 1 : 0;
   p.window_left = a.window_left;
+  p.sinks = a.sinks;
   p.heads_per_wg = g.heads_per_wg;
   p.subs = g.subs;
   p.ps_log2 = ilog2_exact(a.ps);
@@ -187,7 +190,8 @@ static int combine_heads_per_block(int batch, int hq, int hd, int num_splits) {
   return h;
 }
 
-static int launch_combine(void *ws, void *out, int64_t o_sb, int64_t o_st, int64_t o_sh,
+static int launch_combine(void *ws, void *out, const float *sinks, int64_t o_sb, int64_t o_st,
+                          int64_t o_sh,
                           int batch, int hq, int hkv, int ql, int hd, int dtype, int ns,
                           hipStream_t st) {
   const WsLayout w = ws_layout(batch, hq * ql, hd, ns);
@@ -205,6 +209,7 @@ static int launch_combine(void *ws, void *out, int64_t o_sb, int64_t o_st, int64
   c.ql = ql;
   c.num_ranges = ns;
   c.heads_per_block = combine_heads_per_block(batch, hq * ql, hd, ns);
+  c.sinks = sinks;
   switch (hd) {
     case 64: return launch_combine_64(c, dtype, st);
     case 128: return launch_combine_128(c, dtype, st);
@@ -256,6 +261,7 @@ static SplitArgs split_args(const void *q, int64_t q_stride_b, int64_t q_stride_
   a.ql = 1;
   a.causal = 0;
   a.window_left = -1;
+  a.sinks = nullptr;
   return a;
 }
 
@@ -264,8 +270,8 @@ static int run_split(const SplitArgs &a, bool with_combine, hipStream_t st) {
   if (rc != MXFA_OK) return rc;
   rc = launch_partial(a, st);
   if (rc != MXFA_OK || !with_combine) return rc;
-  return launch_combine(a.ws, a.out, a.o_sb, a.o_st, a.o_sh, a.batch, a.hq, a.hkv, a.ql, a.hd,
-                        a.dtype, a.num_splits, st);
+  return launch_combine(a.ws, a.out, a.sinks, a.o_sb, a.o_st, a.o_sh, a.batch, a.hq, a.hkv,
+                        a.ql, a.hd, a.dtype, a.num_splits, st);
 }
 
 static SplitArgs fp8_args(SplitArgs a, const float *k_scale, const float *v_scale) {
@@ -384,13 +390,14 @@ int mxfa_split_decode_combine_launch(void *workspace, size_t workspace_bytes, vo
     return MXFA_EINVAL;
   if (workspace_bytes < ws_layout(batch, q_heads, head_dim, num_splits).bytes)
     return MXFA_EWORKSPACE;
-  return launch_combine(workspace, out, out_stride_b, 0, out_stride_h, batch, q_heads, kv_heads,
+  return launch_combine(workspace, out, nullptr, out_stride_b, 0, out_stride_h, batch, q_heads,
+                        kv_heads,
                         1, head_dim, dtype, num_splits, (hipStream_t)stream);
 }
 
 int mxfa_split_decode_multi_launch(
     const void *q, int64_t q_stride_b, int64_t q_stride_t, int64_t q_stride_h, int q_len,
-    int causal, int window_left, const void *k_cache, const void *v_cache,
+    int causal, int window_left, const float *sinks, const void *k_cache, const void *v_cache,
     int64_t cache_stride_page,
     int64_t cache_stride_token, int64_t cache_stride_head, const int32_t *block_table,
     int64_t bt_stride, const int32_t *seqlens, int seqlen_add, void *out, int64_t out_stride_b,
@@ -410,6 +417,7 @@ int mxfa_split_decode_multi_launch(
   a.ql = q_len;
   a.causal = causal;
   a.window_left = window_left;
+  a.sinks = sinks;
   return run_split(a, true, (hipStream_t)stream);
 }
 

@@ -112,6 +112,7 @@ struct DecodeParams {
   int32_t *ws_s;
   const float *k_scale;  // fp8 caches: dequantisation scales (nullptr: 1)
   const float *v_scale;
+  const float *sinks;    // per query head logit added once to each denominator (nullptr: none)
   float scale_log2;
   int seqlen_add;
   int batch;
@@ -144,6 +145,7 @@ struct CombineParams {
   int ql;
   int num_ranges;
   int heads_per_block;  // a power of two; heads_per_block * HD / 4 <= kCombineThreads
+  const float *sinks;   // as DecodeParams::sinks
 };
 
 // Block tables and lengths are read-only for the whole call; reading them
@@ -665,12 +667,17 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
       const float Dh = head_of_row<HR, i>(dt, row);
       const float Mh = head_of_row<HR, i>(m, row);
       if (hh >= nc) return;
-      const float inv = Dh > 0.f ? v_scale / Dh : 0.f;
+      const int ht = hh / gq, hg = hh - (hh / gq) * gq;
+      // A sink joins the denominator once per (sequence, head): here for a
+      // sequence whole in the range, in the combine for a split one. With no
+      // key seen (Mh = -inf) the term is +inf and the output 0.
+      float Dw = Dh;
+      if (whole && p.sinks) Dw += fast_exp2(p.sinks[kvh * gq + hg] * kLog2e - Mh);
+      const float inv = Dw > 0.f ? v_scale / Dw : 0.f;
       float v[VD];
 #pragma unroll
       for (int j = 0; j < VD; ++j) v[j] = oacc[j][i];
       if (whole) {
-        const int ht = hh / gq, hg = hh - (hh / gq) * gq;
         store_row<VD, E>(p.out + b * p.o_sb + ht * p.o_st + (kvh * gq + hg) * p.o_sh +
                              vslot * (VD * 2),
                          v, inv);
@@ -953,6 +960,7 @@ __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(CombineP
     __syncthreads();
   }
   if (g == 0 && live) {
+    if (p.sinks) W += fast_exp2(p.sinks[h] * kLog2e - M);  // M = -inf: W = inf, out 0
     const float inv = W > 0.f ? 1.f / W : 0.f;
     const uint32_t w0 =
         (uint32_t)E::narrow(acc.x * inv) | ((uint32_t)E::narrow(acc.y * inv) << 16);

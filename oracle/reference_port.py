@@ -19,6 +19,11 @@ counterpart: the reference rejects sliding windows (validation.py:56-76). With
 window_left >= 0 the query at key position p also drops keys before
 p - window_left, on top of the causal mask. It is pinned by identities against
 the unwindowed port (tests/test_oracle.py), not by the reference.
+
+sinks (float32 [HQ], same scale as the scaled scores) is vLLM's s_aux: one
+extra softmax column per head with a zero value row; the reference drops it
+(integrations/vllm/vllm_plugin.py:335-339). Pinned against library attention
+over one appended key whose score is the sink (tests/test_oracle.py).
 """
 
 from __future__ import annotations
@@ -30,7 +35,8 @@ import torch
 
 def attention_single(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
                      softmax_scale: float | None = None, causal: bool = False,
-                     window_left: int = -1) -> torch.Tensor:
+                     window_left: int = -1,
+                     sinks: torch.Tensor | None = None) -> torch.Tensor:
     """q [Lq, HQ, D], k/v [Lk, HKV, D] -> [Lq, HQ, D] in q.dtype (reference.py:8-40)."""
     if q.shape[0] == 0:
         return q.clone()
@@ -52,7 +58,12 @@ def attention_single(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
         scores = scores.masked_fill((kpos > qpos).unsqueeze(0), float("-inf"))
     if window_left >= 0:  # nor keys more than window_left before it
         scores = scores.masked_fill((kpos < qpos - window_left).unsqueeze(0), float("-inf"))
-    probs = torch.nan_to_num(torch.softmax(scores, dim=-1), nan=0.0, posinf=0.0, neginf=0.0)
+    if sinks is not None:  # one more column per head, dropped after the softmax
+        sink = sinks.float().view(hq, 1, 1).expand(hq, lq, 1)
+        probs = torch.softmax(torch.cat([scores, sink], dim=-1), dim=-1)[..., :lk]
+    else:
+        probs = torch.softmax(scores, dim=-1)
+    probs = torch.nan_to_num(probs, nan=0.0, posinf=0.0, neginf=0.0)
     return torch.bmm(probs, vf).permute(1, 0, 2).to(q.dtype)
 
 
@@ -91,7 +102,8 @@ def attention_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
                       cache_seqlens: torch.Tensor, block_table: torch.Tensor | None,
                       k: torch.Tensor | None = None, v: torch.Tensor | None = None,
                       softmax_scale: float | None = None, causal: bool = False,
-                      window_left: int = -1) -> torch.Tensor:
+                      window_left: int = -1,
+                      sinks: torch.Tensor | None = None) -> torch.Tensor:
     """Decode/append against a dense or paged cache (reference.py:88-139).
 
     Mutates the caches (append) and cache_seqlens (+= S_new) like the reference.
@@ -117,7 +129,7 @@ def attention_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
             kb = gather_pages(k_cache, row, total)
             vb = gather_pages(v_cache, row, total)
         outs.append(attention_single(q[b], kb, vb, softmax_scale=softmax_scale, causal=causal,
-                                     window_left=window_left))
+                                     window_left=window_left, sinks=sinks))
     if k is not None:
         cache_seqlens.add_(s_new)
     return torch.stack(outs) if outs else q.clone()

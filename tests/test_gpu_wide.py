@@ -232,7 +232,7 @@ def test_fp8_reshape_and_cache_keeps_nan_and_saturates_inf(device):
 # Several query tokens per sequence (decode with draft tokens)
 
 
-def port_expected(b, causal: bool, window_left: int = -1) -> torch.Tensor:
+def port_expected(b, causal: bool, window_left: int = -1, sinks=None) -> torch.Tensor:
     """fp32 restatement of reference.attention_kvcache (bottom-right causal mask;
     window_left >= 0 adds the sliding window of the port, pinned in test_oracle)."""
     from oracle import reference_port
@@ -245,7 +245,8 @@ def port_expected(b, causal: bool, window_left: int = -1) -> torch.Tensor:
         out[i:i + 1] = reference_port.attention_kvcache(
             cpu.q[i:i + 1].float(), cpu.k_cache.float(), cpu.v_cache.float(),
             cache_seqlens=cpu.cache_seqlens[i:i + 1].clone(), block_table=cpu.block_table[i:i + 1],
-            softmax_scale=cpu.scale, causal=causal, window_left=window_left).float()
+            softmax_scale=cpu.scale, causal=causal, window_left=window_left,
+            sinks=None if sinks is None else sinks.cpu()).float()
     return out
 
 
@@ -420,3 +421,65 @@ def test_window_on_a_long_sequence(device):
                                     b.scale, window_left=window)
     torch.cuda.synchronize()
     assert max_err(got, port_expected(b, False, window)) <= TOL[torch.bfloat16]
+
+
+# ---------------------------------------------------------------------------
+# Attention sinks (vLLM's s_aux): one logit per query head in every softmax
+# denominator, added in the partial kernel for sequences whole in a range and
+# in the combine for split ones.
+
+
+def sink_values(hq: int, device) -> torch.Tensor:
+    vals = torch.linspace(-2.0, 3.0, hq)
+    vals[0] = float("-inf")     # a head without a sink
+    vals[-1] = 20.0             # a sink that outweighs every key
+    return vals.to(torch.float32).to(device)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("ql,gq,causal,window", [(1, 4, False, -1), (1, 8, False, 31),
+                                                 (2, 4, True, -1), (3, 4, True, 50),
+                                                 (4, 2, False, -1)])
+def test_sinks_match_reference(device, dtype, head_dim, ql, gq, causal, window):
+    lengths = torch.tensor([1, 2, 17, 300, 0, 1000, 33])
+    b = make_paged_batch(7, 2 * gq, 2, head_dim, dtype, lengths, seed=90 + ql).to(device)
+    b = with_query_tokens(b, ql, 91)
+    sinks = sink_values(2 * gq, device)
+    expected = port_expected(b, causal, window, sinks)
+    for ns in (None, 1, 9, 64):
+        kw = {} if ns is None else dict(num_splits=ns)
+        got = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table,
+                                        b.cache_seqlens, b.scale, causal=causal,
+                                        window_left=window, sinks=sinks, **kw)
+        torch.cuda.synchronize()
+        assert torch.isfinite(got.float()).all()
+        assert max_err(got, expected) <= TOL[dtype], (ns, max_err(got, expected))
+        assert torch.equal(got[4].cpu(), torch.zeros_like(got[4].cpu()))
+
+
+def test_sinks_with_fp8_caches_and_head_dim_256(device):
+    b = make_paged_batch(4, 8, 2, 256, torch.bfloat16, torch.tensor([3, 64, 500, 1200]),
+                         seed=92).to(device)
+    sinks = sink_values(8, device)
+    got = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
+                                    b.scale, sinks=sinks)
+    torch.cuda.synchronize()
+    assert max_err(got, port_expected(b, False, -1, sinks)) <= TOL[torch.bfloat16]
+    k8, v8 = fp8_caches(b, device)
+    b8 = type(b)(b.q, k8.cpu().float().to(torch.bfloat16).to(device),
+                 v8.cpu().float().to(torch.bfloat16).to(device), b.block_table, b.cache_seqlens,
+                 b.scale)
+    got = native.paged_decode_split(b.q, k8, v8, b.block_table, b.cache_seqlens, b.scale,
+                                    sinks=sinks)
+    torch.cuda.synchronize()
+    assert max_err(got, port_expected(b8, False, -1, sinks)) <= TOL[torch.bfloat16]
+
+
+def test_sinks_are_checked_on_the_host(device):
+    b = make_paged_batch(2, 8, 2, 64, torch.bfloat16, torch.tensor([5, 9]), seed=93).to(device)
+    for bad in (torch.zeros(7, device=device), torch.zeros(8, device=device).half(),
+                torch.zeros(8), torch.zeros(16, device=device)[::2]):
+        with pytest.raises(ValueError, match="sinks"):
+            native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table,
+                                      b.cache_seqlens, b.scale, sinks=bad)

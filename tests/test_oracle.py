@@ -480,3 +480,45 @@ def test_window_covering_the_sequence_changes_nothing():
     plain = reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache, **args)
     wide = reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache, window_left=127, **args)
     assert torch.equal(plain, wide)
+
+
+# Attention sinks (vLLM's s_aux): an extension with no reference counterpart.
+
+def test_sinks_of_minus_infinity_change_nothing():
+    b = make_paged_batch(3, 8, 2, 64, torch.float32, torch.tensor([1, 50, 300]), seed=51,
+                         q_len=2)
+    args = dict(cache_seqlens=b.cache_seqlens, block_table=b.block_table, causal=True)
+    plain = reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache, **args)
+    sunk = reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache,
+                                            sinks=torch.full((8,), float("-inf")), **args)
+    torch.testing.assert_close(plain, sunk, atol=1e-7, rtol=1e-6)
+
+
+def test_sinks_match_library_attention_over_one_appended_key():
+    # For one query token, a key k* with q.k* * scale = sink and a zero value
+    # row makes library attention equal to attention with that sink.
+    hq, hkv, hd, n = 8, 2, 64, 77
+    b = make_paged_batch(1, hq, hkv, hd, torch.float64, torch.tensor([n]), seed=52)
+    sinks = torch.linspace(-3.0, 4.0, hq, dtype=torch.float64)
+    got = reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache,
+                                           cache_seqlens=b.cache_seqlens.clone(),
+                                           block_table=b.block_table, sinks=sinks)
+    row = b.block_table[0].tolist()
+    keys, values = gather_dense(b.k_cache, row, n), gather_dense(b.v_cache, row, n)
+    for h in range(hq):
+        qh = b.q[0, 0, h]
+        kstar = qh * sinks[h] / (b.scale * qh.dot(qh))
+        kh = torch.cat([keys[:, h // (hq // hkv)], kstar[None]])[None, None]
+        vh = torch.cat([values[:, h // (hq // hkv)], torch.zeros(1, hd, dtype=torch.float64)])
+        want = F.scaled_dot_product_attention(qh.view(1, 1, 1, -1), kh, vh[None, None],
+                                              scale=b.scale).view(-1)
+        torch.testing.assert_close(got[0, 0, h], want, atol=2e-6, rtol=1e-5)
+
+
+def test_a_dominant_sink_silences_the_output():
+    b = make_paged_batch(2, 4, 2, 64, torch.float32, torch.tensor([5, 40]), seed=53)
+    out = reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache,
+                                           cache_seqlens=b.cache_seqlens.clone(),
+                                           block_table=b.block_table,
+                                           sinks=torch.full((4,), 1.0e4))
+    assert torch.equal(out, torch.zeros_like(out))
