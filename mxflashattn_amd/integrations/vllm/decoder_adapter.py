@@ -230,10 +230,10 @@ def _decode_forward_graph(query: torch.Tensor, kv_cache: torch.Tensor, attn_meta
 
 def _native_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: Any,
                    output: torch.Tensor, softmax_scale: float, k_scale: Any, v_scale: Any,
-                   fp8: bool, window_left: int) -> torch.Tensor:
+                   fp8: bool, window_left: int, sinks: Any = None) -> torch.Tensor:
     """One-token decode straight on the HIP kernels, for what the public API
-    (like the reference's) does not take: an fp8 (e4m3fn) cache and/or a
-    sliding window."""
+    (like the reference's) does not take: an fp8 (e4m3fn) cache, a sliding
+    window, attention sinks."""
     _no_cascade(attn_metadata)
     if int(attn_metadata.max_query_len) != 1:
         raise DecoderAdapterBlocked(
@@ -249,13 +249,16 @@ def _native_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: A
     native.paged_decode_split(q, key_cache, value_cache,
                               _int32_on(attn_metadata.block_table, query.device),
                               _int32_on(attn_metadata.seq_lens.reshape(-1), query.device),
-                              softmax_scale, out=target, window_left=window_left, **scales)
+                              softmax_scale, out=target, window_left=window_left,
+                              sinks=sinks, **scales)
     event = {"path": "mi355x_split_decode", "operation": "paged_decode_split",
              "fallback": "false"}
     if fp8:
         event["kv_cache_dtype"] = "fp8_e4m3"
     if window_left >= 0:
         event["window_left"] = str(window_left)
+    if sinks is not None:
+        event["sinks"] = "true"
     record_event(event)
     return output
 
@@ -263,20 +266,21 @@ def _native_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: A
 def forward_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: Any,
                    output: torch.Tensor, *, softmax_scale: float, kv_cache_dtype: str = "auto",
                    k_scale: Any = None, v_scale: Any = None,
-                   window_left: int = -1) -> torch.Tensor:
+                   window_left: int = -1, sinks: Any = None) -> torch.Tensor:
     """The decode body of the backend's ``forward``: one-token paged decode into
     vLLM's output buffer, with the dispatch event the reference plugin records
     (integrations/vllm/vllm_plugin.py:297-299,399-431). Raises
     DecoderAdapterBlocked for calls outside the adapter contract (prefill,
     cascade), which the backend hands to vLLM. kv_cache_dtype "fp8"/"fp8_e4m3"
     (cache stored as e4m3fn or its uint8 codes) decodes with the layer's
-    per-tensor k_scale / v_scale, and window_left >= 0 with the layer's
-    sliding window (the query at position i sees keys >= i - window_left);
-    the reference has neither."""
+    per-tensor k_scale / v_scale, window_left >= 0 with the layer's sliding
+    window (the query at position i sees keys >= i - window_left), and sinks
+    (float32 [HQ]) with the layer's attention sinks; the reference has none
+    of these."""
     fp8 = kv_cache_dtype in ("fp8", "fp8_e4m3")
-    if fp8 or window_left >= 0:
+    if fp8 or window_left >= 0 or sinks is not None:
         return _native_decode(query, kv_cache, attn_metadata, output, softmax_scale, k_scale,
-                              v_scale, fp8, window_left)
+                              v_scale, fp8, window_left, sinks)
     result, _ = decode_forward(query, kv_cache, attn_metadata, softmax_scale=softmax_scale,
                                causal=bool(attn_metadata.causal))
     info = get_last_dispatch_info()

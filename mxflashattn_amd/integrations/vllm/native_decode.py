@@ -151,7 +151,7 @@ def _guard(args: tuple, kwargs: dict, wide: bool = False,
 
 
 def try_native_decode(args: tuple, kwargs: dict, k_descale: Any = None,
-                      v_descale: Any = None) -> torch.Tensor | None:
+                      v_descale: Any = None, sinks: Any = None) -> torch.Tensor | None:
     """HIP decode of a vLLM flash_attn_with_kvcache call, or None to hand it back."""
     if os.getenv("MXFA_NATIVE_DECODE", "0") != "1":
         return None
@@ -161,7 +161,7 @@ def try_native_decode(args: tuple, kwargs: dict, k_descale: Any = None,
                       "fallback_reason": f"guard:{reason}"})
         return None
     try:
-        return _native_decode(picked, kwargs, k_descale, v_descale)
+        return _native_decode(picked, kwargs, k_descale, v_descale, sinks)
     except native.NativeLibraryError:
         raise  # a missing or stale build is a deployment error, not a shape to hand back
     except Exception as exc:  # as vllm_plugin.py:314-317: never take the model down
@@ -170,8 +170,8 @@ def try_native_decode(args: tuple, kwargs: dict, k_descale: Any = None,
         return None
 
 
-def _native_decode(picked: tuple, kwargs: dict, k_descale: Any,
-                   v_descale: Any) -> torch.Tensor:
+def _native_decode(picked: tuple, kwargs: dict, k_descale: Any, v_descale: Any,
+                   sinks: Any = None) -> torch.Tensor:
     q, k_cache, v_cache, bt, sl, window_left, causal = picked
     hq, hd = q.shape[-2], q.shape[-1]
     # An explicit 0.0 is a scale (uniform weights), not "use the default".
@@ -192,7 +192,7 @@ def _native_decode(picked: tuple, kwargs: dict, k_descale: Any,
         scales = {"k_scale": k_descale, "v_scale": v_descale}
     result = native.paged_decode_split(q4, k_cache, v_cache, bt, sl, scale, out=out,
                                        num_splits=ns, causal=causal, window_left=window_left,
-                                       **scales)
+                                       sinks=sinks, **scales)
     if provided is not None and out is None:
         provided.copy_(result.reshape_as(provided))
         result = provided
@@ -205,11 +205,21 @@ def _native_decode(picked: tuple, kwargs: dict, k_descale: Any,
     return result
 
 
+def _sinks_for_kernel(s_aux: Any, q: Any) -> torch.Tensor | None:
+    """vLLM's s_aux as the kernel's sinks (float32 [HQ] on q's GPU), or None."""
+    if not (isinstance(s_aux, torch.Tensor) and isinstance(q, torch.Tensor)):
+        return None
+    if s_aux.dim() != 1 or s_aux.shape[0] != q.shape[-2] or s_aux.device != q.device:
+        return None
+    return s_aux.to(torch.float32).contiguous()
+
+
 def mx_kvcache_compat(*args, **kwargs):
     """Stand-in for vLLM's flash_attn_with_kvcache inside its attention forward.
 
-    The kernel computes plain softmax attention, so a call with attention sinks
-    (``s_aux``) or one that asks for the log-sum-exp is never taken. A call
+    A call that asks for the log-sum-exp is never taken, nor one with attention
+    sinks (``s_aux``) unless the wider contract is on (then they are the
+    kernel's per-head sinks). A call
     that is not taken goes back to vLLM's own function with every keyword vLLM
     passed. The reference (vllm_plugin.py:335-339) strips the vLLM-only
     keywords for every call, because its vendor wheel does not accept them;
@@ -218,13 +228,17 @@ def mx_kvcache_compat(*args, **kwargs):
     no such parameters, goes without them."""
     given = {name: kwargs[name] for name in _VLLM_ONLY_KWARGS if name in kwargs}
     popped = {name: kwargs.pop(name, None) for name in _VLLM_ONLY_KWARGS}
-    declined = None
-    if popped["s_aux"] is not None:
-        declined = "attention_sinks"
-    elif popped["return_softmax_lse"]:
+    declined, sinks = None, None
+    if popped["return_softmax_lse"]:
         declined = "softmax_lse"
+    elif popped["s_aux"] is not None:
+        q = args[0] if args else kwargs.get("q")
+        sinks = _sinks_for_kernel(popped["s_aux"], q) if wide_contract() else None
+        if sinks is None:
+            declined = "attention_sinks"
     if declined is None:
-        result = try_native_decode(args, kwargs, popped["k_descale"], popped["v_descale"])
+        result = try_native_decode(args, kwargs, popped["k_descale"], popped["v_descale"],
+                                   sinks=sinks)
         if result is not None:
             return result
     elif os.getenv("MXFA_NATIVE_DECODE", "0") == "1":

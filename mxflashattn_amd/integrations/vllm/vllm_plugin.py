@@ -10,10 +10,10 @@ argument" failure is retried once with the untouched functions. The reference
 also swaps ``flash_attn_varlen_func`` there; prefill is not on this path, so it
 stays vLLM's. Encoder layers (``attn_type`` "encoder" / "encoder_only", which
 the reference sends to its dense API and on to the vendor kernel) run vLLM's
-own forward, and so do layers with ALiBi slopes, logit soft-capping or
-attention sinks, and sliding-window layers unless the wider contract is on
-(then the kernel applies the window); the reference's forward sends all of
-them to its decoder regardless. Otherwise the forward runs ``decode_forward`` (public
+own forward, and so do layers with ALiBi slopes or logit soft-capping, and
+sliding-window or attention-sink layers unless the wider contract is on (then
+the kernel applies the window and the sinks); the reference's forward sends
+all of them to its decoder regardless. Otherwise the forward runs ``decode_forward`` (public
 API) and falls back to vLLM for prefill. The KV-cache update uses the HIP append kernel
 (``reshape_and_cache_flash``).
 Classes live at module scope because vLLM resolves the backend by import path
@@ -75,10 +75,17 @@ def _layer_window(impl) -> int:
     return -1 if mapped is None else mapped[0]
 
 
+def _layer_sinks(impl, query):
+    """The layer's attention sinks (vLLM keeps them per query head) as the
+    kernel's float32 [HQ], or None."""
+    sinks = getattr(impl, "sinks", None)
+    return None if sinks is None else native_decode._sinks_for_kernel(sinks, query)
+
+
 def _layer_option(impl) -> str | None:
     """An option of the layer that the decode kernel does not compute (vLLM's
     FlashAttentionImpl applies them in its own forward), or None. Sliding
-    windows are computed under the wider contract."""
+    windows and attention sinks are computed under the wider contract."""
     if getattr(impl, "alibi_slopes", None) is not None:
         return "alibi"
     window = getattr(impl, "sliding_window", None)
@@ -87,7 +94,7 @@ def _layer_option(impl) -> str | None:
         return "window"
     if getattr(impl, "logits_soft_cap", None):
         return "softcap"
-    if getattr(impl, "sinks", None) is not None:
+    if getattr(impl, "sinks", None) is not None and not native_decode.wide_contract():
         return "attention_sinks"
     return None
 
@@ -144,7 +151,8 @@ class MXFlashAttnImpl(FlashAttentionImpl):
                                   softmax_scale=self.scale, kv_cache_dtype=kv_dtype,
                                   k_scale=getattr(layer, "_k_scale", None),
                                   v_scale=getattr(layer, "_v_scale", None),
-                                  window_left=_layer_window(self))
+                                  window_left=_layer_window(self),
+                                  sinks=_layer_sinks(self, query))
         except DecoderAdapterBlocked as exc:
             record_event({"path": "vendor_prefill_or_blocked", "reason": str(exc)})
             if "single_token_decode" in str(exc):

@@ -90,6 +90,22 @@ def test_compat_never_takes_sinks_or_lse_requests(monkeypatch, extra, reason):
         {"path": "native_decode", "fallback": "true", "fallback_reason": f"guard:{reason}"}]
 
 
+def test_wide_compat_takes_sinks_of_one_logit_per_query_head(monkeypatch):
+    monkeypatch.setenv("MXFA_NATIVE_DECODE", "1")
+    monkeypatch.setenv("MXFA_WIDE_CONTRACT", "1")
+    seen = []
+    monkeypatch.setattr(native_decode, "official_kvcache", lambda *a, **k: "vendor")
+    monkeypatch.setattr(native_decode, "try_native_decode",
+                        lambda args, kwargs, kd, vd, sinks=None: seen.append(sinks) or "native")
+    good = torch.linspace(-1, 1, 16, dtype=torch.bfloat16)
+    assert native_decode.mx_kvcache_compat(q_of(), s_aux=good, **kv_kwargs()) == "native"
+    assert seen[0].dtype == torch.float32 and torch.equal(seen[0], good.float())
+    # Not one value per query head: handed back with s_aux intact.
+    assert native_decode.mx_kvcache_compat(q_of(), s_aux=torch.zeros(8), **kv_kwargs()) == \
+        "vendor"
+    assert len(seen) == 1
+
+
 def test_compat_without_vllm_function_refuses_what_the_api_cannot_do(monkeypatch):
     monkeypatch.setattr(native_decode, "official_kvcache", None)
     with pytest.raises(NotImplementedError, match="s_aux"):
