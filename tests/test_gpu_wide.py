@@ -483,3 +483,37 @@ def test_sinks_are_checked_on_the_host(device):
         with pytest.raises(ValueError, match="sinks"):
             native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table,
                                       b.cache_seqlens, b.scale, sinks=bad)
+
+
+def test_graph_replays_of_the_general_entry_point_match_eager(device):
+    # Several query tokens, a sliding window, sinks and an fp8 cache: the
+    # general entry point captured in a HIP graph (workspace from an eager call
+    # on the capture stream first), replayed with eager work in between.
+    b = make_paged_batch(5, 16, 4, 128, torch.bfloat16, torch.tensor([700, 3, 1500, 64, 0]),
+                         seed=95).to(device)
+    b = with_query_tokens(b, 2, 96)
+    k8, v8 = fp8_caches(b, device)
+    sinks = sink_values(16, device)
+    one = torch.ones(1, dtype=torch.float32, device=device)
+    stream = torch.cuda.Stream(device)
+    out = torch.empty_like(b.q)
+
+    def call():
+        native.paged_decode_split(b.q, k8, v8, b.block_table, b.cache_seqlens, b.scale,
+                                  out=out, causal=True, window_left=300, sinks=sinks,
+                                  k_scale=one, v_scale=one)
+
+    with torch.cuda.stream(stream):
+        call()
+        eager = out.clone()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        call()
+    for i in range(4):
+        out.fill_(float("nan"))
+        with torch.cuda.stream(stream):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), i
+        _ = (torch.randn(4096, device=device) * i).sum().item()
