@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define MXFA_ABI_VERSION 5
+#define MXFA_ABI_VERSION 6
 
 /* Return codes. */
 #define MXFA_OK 0
@@ -128,9 +128,11 @@ int mxfa_split_decode_launch(const void *q, int64_t q_stride_b, int64_t q_stride
  * query head (HQ values, 4-byte aligned, on the scale of the scaled scores):
  * each output row becomes sum_j e^(s_j) v_j / (sum_j e^(s_j) + e^(sinks[h])),
  * a softmax with one extra zero-valued column (the "s_aux" of vLLM's
- * FlashAttention). The reference has neither: its guards hand windows to the
- * vendor (integrations/vllm/vllm_plugin.py:236-247) and drop s_aux
- * (:335-339). kv_dtype is dtype (16-bit caches) or
+ * FlashAttention). softcap > 0 caps every scaled score s to softcap *
+ * tanh(s / softcap) before the mask and softmax (FlashAttention's softcap); 0
+ * means none. The reference has none of these: its guards hand windows to the
+ * vendor (integrations/vllm/vllm_plugin.py:236-247), drop s_aux (:335-339)
+ * and its API rejects softcap (mxflashattn/validation.py:56-76). kv_dtype is dtype (16-bit caches) or
  * MXFA_DTYPE_FP8_E4M3 with k_scale/v_scale as in mxfa_split_decode_fp8_launch.
  * Workspace: mxfa_split_decode_workspace_size(batch, q_heads * q_len, ...).
  * Partial and combine run as one call. Other arguments as
@@ -140,9 +142,9 @@ int mxfa_split_decode_launch(const void *q, int64_t q_stride_b, int64_t q_stride
  */
 int mxfa_split_decode_multi_launch(
     const void *q, int64_t q_stride_b, int64_t q_stride_t, int64_t q_stride_h, int q_len,
-    int causal, int window_left, const float *sinks, const void *k_cache,
-    const void *v_cache, int64_t cache_stride_page, int64_t cache_stride_token, int64_t cache_stride_head,
-    const int32_t *block_table,
+    int causal, int window_left, const float *sinks, float softcap, const void *k_cache,
+    const void *v_cache, int64_t cache_stride_page, int64_t cache_stride_token,
+    int64_t cache_stride_head, const int32_t *block_table,
     int64_t bt_stride, const int32_t *seqlens, int seqlen_add, void *out, int64_t out_stride_b,
     int64_t out_stride_t, int64_t out_stride_h, void *workspace, size_t workspace_bytes,
     float scale, int batch, int q_heads, int kv_heads, int head_dim, int page_size,

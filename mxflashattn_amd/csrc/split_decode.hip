@@ -51,6 +51,7 @@ struct SplitArgs {
   int causal;  // bottom-right aligned causal mask
   int window_left;  // sliding window (keys >= position - window_left), -1: none
   const float *sinks;  // per query head softmax sink logits, nullptr: none
+  float softcap;       // logit soft-capping (0: none)
 };
 
 struct WsLayout {
@@ -76,6 +77,7 @@ static int check_split_args(const SplitArgs &a) {
   if (a.hq % a.hkv != 0) return MXFA_EUNSUPPORTED;
   const int gq = a.hq / a.hkv;
   if (a.ql <= 0 || a.window_left < -1) return MXFA_EINVAL;
+  if (!(a.softcap >= 0.f) || a.softcap == INFINITY) return MXFA_EINVAL;
   if (a.window_left > (1 << 30)) return MXFA_EUNSUPPORTED;
   if (gq * a.ql > kMaxCols) return MXFA_EUNSUPPORTED;
   if (a.dtype != MXFA_DTYPE_F16 && a.dtype != MXFA_DTYPE_BF16) return MXFA_EUNSUPPORTED;
@@ -155,6 +157,7 @@ static DecodeParams make_params(const SplitArgs &a, const Grid &g) {
   p.causal = a.causal ? 1 : 0;
   p.window_left = a.window_left;
   p.sinks = a.sinks;
+  p.softcap = a.softcap;
   p.heads_per_wg = g.heads_per_wg;
   p.subs = g.subs;
   p.ps_log2 = ilog2_exact(a.ps);
@@ -262,6 +265,7 @@ static SplitArgs split_args(const void *q, int64_t q_stride_b, int64_t q_stride_
   a.causal = 0;
   a.window_left = -1;
   a.sinks = nullptr;
+  a.softcap = 0.f;
   return a;
 }
 
@@ -397,8 +401,8 @@ int mxfa_split_decode_combine_launch(void *workspace, size_t workspace_bytes, vo
 
 int mxfa_split_decode_multi_launch(
     const void *q, int64_t q_stride_b, int64_t q_stride_t, int64_t q_stride_h, int q_len,
-    int causal, int window_left, const float *sinks, const void *k_cache, const void *v_cache,
-    int64_t cache_stride_page,
+    int causal, int window_left, const float *sinks, float softcap, const void *k_cache,
+    const void *v_cache, int64_t cache_stride_page,
     int64_t cache_stride_token, int64_t cache_stride_head, const int32_t *block_table,
     int64_t bt_stride, const int32_t *seqlens, int seqlen_add, void *out, int64_t out_stride_b,
     int64_t out_stride_t, int64_t out_stride_h, void *workspace, size_t workspace_bytes,
@@ -418,6 +422,7 @@ int mxfa_split_decode_multi_launch(
   a.causal = causal;
   a.window_left = window_left;
   a.sinks = sinks;
+  a.softcap = softcap;
   return run_split(a, true, (hipStream_t)stream);
 }
 

@@ -114,6 +114,7 @@ struct DecodeParams {
   const float *v_scale;
   const float *sinks;    // per query head logit added once to each denominator (nullptr: none)
   float scale_log2;
+  float softcap;         // logit soft-capping: s -> softcap * tanh(s / softcap) (0: none)
   int seqlen_add;
   int batch;
   int hkv;
@@ -341,6 +342,12 @@ __device__ __forceinline__ uint32_t row_swap8(uint32_t x) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x128, 0xf, 0xf, false);
 }
 
+// tanh(y) = 1 - 2 / (e^(2y) + 1) from the hardware exp2 and reciprocal; exact
+// saturation to +-1 for large |y|, absolute error ~1e-7 near 0.
+__device__ __forceinline__ float tanh_exp2(float y) {
+  return 1.f - 2.f * __builtin_amdgcn_rcpf(fast_exp2(2.f * kLog2e * y) + 1.f);
+}
+
 // Every lane takes the value of lane H of its own 16-lane row (row_newbcast:H).
 template <int H>
 __device__ __forceinline__ float row_bcast(float x) {
@@ -496,6 +503,12 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
     if (p.v_scale) v_scale = ((ConstF32)p.v_scale)[0];
   }
   const int ns = p.num_ranges;  // workspace stride
+  // Soft-capping of the scaled score s = acc * scale * k_scale: the base-2
+  // score becomes cap_out * tanh(acc * cap_in) (no division by the scale, so
+  // scale 0 stays 0).
+  const bool capped = p.softcap > 0.f;
+  const float cap_in = capped ? c / (kLog2e * p.softcap) : 0.f;
+  const float cap_out = p.softcap * kLog2e;
 
   // Lane offsets inside a tile: K in the MFMA A layout, V row-contiguous, q as
   // the MFMA B operand (columns >= GQ*QL read nothing). For fp8 caches step
@@ -721,10 +734,16 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
     float x[4];
     bool need = false;
 #pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = (acc0[i] + acc1[i]) * c;
+    if (capped) {  // wave-uniform
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[i] = cap_out * tanh_exp2((acc0[i] + acc1[i]) * cap_in);
+    }
+#pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * row + i;
       const bool valid = (col < nc) & (r < d.rem - c_hide) & (r >= d.rem - c_reach);
-      x[i] = valid ? (acc0[i] + acc1[i]) * c : -INFINITY;
+      x[i] = valid ? x[i] : -INFINITY;
       need |= x[i] > m + kRescaleLog2;
     }
     if (__builtin_amdgcn_ballot_w64(need) != 0) {

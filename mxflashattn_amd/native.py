@@ -24,7 +24,7 @@ LIB_PATH = Path(
     os.environ.get("MXFLASHATTN_AMD_LIB")
     or Path(__file__).resolve().parent / "_lib" / "libmxfa_mi355x.so"
 )
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 MXFA_OK = 0
 MXFA_EUNSUPPORTED = -1
@@ -96,8 +96,8 @@ _SIGNATURES = {
     "mxfa_split_decode_fp8_partial_launch": (_i, _SPLIT_ARGS + [_p, _p, _p]),
     "mxfa_split_decode_multi_launch": (
         _i,
-        [_p, _i64, _i64, _i64, _i, _i, _i, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _p,
-         _i64,
+        [_p, _i64, _i64, _i64, _i, _i, _i, _p, _f, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i,
+         _p, _i64,
          _i64, _i64, _p, _sz, _f, _i, _i, _i, _i, _i, _i, _i, _i, _i, _p, _p, _i, _p],
     ),
     "mxfa_split_decode_combine_launch": (
@@ -369,7 +369,7 @@ def _prepare(q, k_cache, v_cache, block_table, cache_seqlens, out):
 
 def _launch_multi(q, k_cache, v_cache, block_table, cache_seqlens, out, workspace, ws_bytes,
                   softmax_scale, num_splits, seqlen_add, stream, causal, k_scale, v_scale,
-                  window_left, sinks):
+                  window_left, sinks, softcap):
     if q.dim() == 3:
         q, out = q.unsqueeze(1), out.unsqueeze(1)
     batch, ql, hq, hd = q.shape
@@ -378,7 +378,7 @@ def _launch_multi(q, k_cache, v_cache, block_table, cache_seqlens, out, workspac
     fp8 = k_cache.dtype == FP8_DTYPE
     rc = library().mxfa_split_decode_multi_launch(
         q.data_ptr(), qs[0], qs[1], qs[2], ql, int(bool(causal)), int(window_left),
-        _sinks_ptr(sinks, q), k_cache.data_ptr(),
+        _sinks_ptr(sinks, q), float(softcap), k_cache.data_ptr(),
         v_cache.data_ptr(), cs[0], cs[1], cs[2], block_table.data_ptr(), block_table.stride(0),
         cache_seqlens.data_ptr(), seqlen_add, out.data_ptr(), os_[0], os_[1], os_[2], workspace,
         ws_bytes, float(softmax_scale), batch, hq, hkv, hd, ps, block_table.shape[1], pages,
@@ -422,6 +422,7 @@ def paged_decode_split(
     causal: bool = False,
     window_left: int = -1,
     sinks: torch.Tensor | None = None,
+    softcap: float = 0.0,
 ) -> torch.Tensor:
     """Split-KV paged decode on the current stream; returns ``out`` shaped like q.
 
@@ -437,10 +438,13 @@ def paged_decode_split(
     causal, (window_left, -1) without).
     sinks: float32 [HQ] per-head logits on the scale of the scaled scores,
     each added once to its row's softmax denominator (vLLM's s_aux).
+    softcap > 0: every scaled score s becomes softcap * tanh(s / softcap).
     num_splits: balanced work ranges per kv head (default: split_heuristic).
     """
     if int(window_left) < -1:
         raise ValueError(f"window_left must be >= -1, got {window_left}")
+    if not (0.0 <= float(softcap) < float("inf")):
+        raise ValueError(f"softcap must be finite and >= 0, got {softcap}")
     q, block_table, cache_seqlens, out = _prepare(q, k_cache, v_cache, block_table,
                                                   cache_seqlens, out)
     lib = library()
@@ -450,10 +454,10 @@ def paged_decode_split(
     ql = q.shape[1] if q.dim() == 4 else 1
     ws_bytes = workspace_size(q.shape[0], q.shape[-2] * ql, q.shape[-1], num_splits)
     ws = WORKSPACE.get(q.device, stream, ws_bytes)
-    if ql > 1 or window_left >= 0 or sinks is not None:
+    if ql > 1 or window_left >= 0 or sinks is not None or softcap > 0:
         _launch_multi(q, k_cache, v_cache, block_table, cache_seqlens, out, ws.data_ptr(),
                       ws_bytes, softmax_scale, num_splits, seqlen_add, stream, causal, k_scale,
-                      v_scale, window_left, sinks)
+                      v_scale, window_left, sinks, softcap)
         return out
     args = _launch_args(q, k_cache, v_cache, block_table, cache_seqlens, out, ws.data_ptr(),
                         ws_bytes, softmax_scale, num_splits, seqlen_add, stream)

@@ -24,6 +24,11 @@ sinks (float32 [HQ], same scale as the scaled scores) is vLLM's s_aux: one
 extra softmax column per head with a zero value row; the reference drops it
 (integrations/vllm/vllm_plugin.py:335-339). Pinned against library attention
 over one appended key whose score is the sink (tests/test_oracle.py).
+
+softcap > 0 caps every scaled score s to softcap * tanh(s / softcap) before the
+masks (FlashAttention's softcap); the reference rejects it
+(validation.py:56-76). Pinned by its limits: a tiny cap gives uniform weights
+(the mean of the visible V rows), a huge one no change.
 """
 
 from __future__ import annotations
@@ -35,8 +40,8 @@ import torch
 
 def attention_single(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
                      softmax_scale: float | None = None, causal: bool = False,
-                     window_left: int = -1,
-                     sinks: torch.Tensor | None = None) -> torch.Tensor:
+                     window_left: int = -1, sinks: torch.Tensor | None = None,
+                     softcap: float = 0.0) -> torch.Tensor:
     """q [Lq, HQ, D], k/v [Lk, HKV, D] -> [Lq, HQ, D] in q.dtype (reference.py:8-40)."""
     if q.shape[0] == 0:
         return q.clone()
@@ -51,6 +56,8 @@ def attention_single(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     kf = k.float().permute(1, 0, 2).repeat_interleave(group, dim=0)
     vf = v.float().permute(1, 0, 2).repeat_interleave(group, dim=0)
     scores = torch.bmm(qf, kf.transpose(1, 2).contiguous()) * scale
+    if softcap > 0:
+        scores = softcap * torch.tanh(scores / softcap)
     # query i sits at key position i + (Lk - Lq).
     qpos = torch.arange(lq).unsqueeze(1) + (lk - lq)
     kpos = torch.arange(lk).unsqueeze(0)
@@ -102,8 +109,8 @@ def attention_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
                       cache_seqlens: torch.Tensor, block_table: torch.Tensor | None,
                       k: torch.Tensor | None = None, v: torch.Tensor | None = None,
                       softmax_scale: float | None = None, causal: bool = False,
-                      window_left: int = -1,
-                      sinks: torch.Tensor | None = None) -> torch.Tensor:
+                      window_left: int = -1, sinks: torch.Tensor | None = None,
+                      softcap: float = 0.0) -> torch.Tensor:
     """Decode/append against a dense or paged cache (reference.py:88-139).
 
     Mutates the caches (append) and cache_seqlens (+= S_new) like the reference.
@@ -129,7 +136,8 @@ def attention_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
             kb = gather_pages(k_cache, row, total)
             vb = gather_pages(v_cache, row, total)
         outs.append(attention_single(q[b], kb, vb, softmax_scale=softmax_scale, causal=causal,
-                                     window_left=window_left, sinks=sinks))
+                                     window_left=window_left, sinks=sinks,
+                                     softcap=softcap))
     if k is not None:
         cache_seqlens.add_(s_new)
     return torch.stack(outs) if outs else q.clone()

@@ -232,7 +232,8 @@ def test_fp8_reshape_and_cache_keeps_nan_and_saturates_inf(device):
 # Several query tokens per sequence (decode with draft tokens)
 
 
-def port_expected(b, causal: bool, window_left: int = -1, sinks=None) -> torch.Tensor:
+def port_expected(b, causal: bool, window_left: int = -1, sinks=None,
+                  softcap: float = 0.0) -> torch.Tensor:
     """fp32 restatement of reference.attention_kvcache (bottom-right causal mask;
     window_left >= 0 adds the sliding window of the port, pinned in test_oracle)."""
     from oracle import reference_port
@@ -246,7 +247,7 @@ def port_expected(b, causal: bool, window_left: int = -1, sinks=None) -> torch.T
             cpu.q[i:i + 1].float(), cpu.k_cache.float(), cpu.v_cache.float(),
             cache_seqlens=cpu.cache_seqlens[i:i + 1].clone(), block_table=cpu.block_table[i:i + 1],
             softmax_scale=cpu.scale, causal=causal, window_left=window_left,
-            sinks=None if sinks is None else sinks.cpu()).float()
+            sinks=None if sinks is None else sinks.cpu(), softcap=softcap).float()
     return out
 
 
@@ -517,3 +518,47 @@ def test_graph_replays_of_the_general_entry_point_match_eager(device):
         torch.cuda.synchronize()
         assert torch.equal(out, eager), i
         _ = (torch.randn(4096, device=device) * i).sum().item()
+
+
+# ---------------------------------------------------------------------------
+# Logit soft-capping: s -> cap * tanh(s / cap) on the scaled scores.
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("cap", [0.5, 5.0, 30.0])
+@pytest.mark.parametrize("ql,gq,causal,window,with_sinks", [(1, 4, False, -1, False),
+                                                            (2, 4, True, 40, True),
+                                                            (2, 8, False, -1, False)])
+def test_softcap_matches_reference(device, dtype, head_dim, cap, ql, gq, causal, window,
+                                   with_sinks):
+    lengths = torch.tensor([1, 17, 300, 0, 1000])
+    b = make_paged_batch(5, 2 * gq, 2, head_dim, dtype, lengths, seed=97).to(device)
+    b = with_query_tokens(b, ql, 98)
+    b.q = (b.q.float() * 3).to(dtype)  # scores of a few units, where the cap bites
+    sinks = sink_values(2 * gq, device) if with_sinks else None
+    expected = port_expected(b, causal, window, sinks, cap)
+    for ns in (None, 1, 9):
+        kw = {} if ns is None else dict(num_splits=ns)
+        got = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table,
+                                        b.cache_seqlens, b.scale, causal=causal,
+                                        window_left=window, sinks=sinks, softcap=cap, **kw)
+        torch.cuda.synchronize()
+        assert torch.isfinite(got.float()).all()
+        assert max_err(got, expected) <= TOL[dtype], (ns, max_err(got, expected))
+
+
+def test_softcap_with_fp8_caches(device):
+    b = make_paged_batch(4, 8, 2, 128, torch.bfloat16, torch.tensor([3, 64, 500, 1200]),
+                         seed=99).to(device)
+    k8, v8 = fp8_caches(b, device)
+    b8 = type(b)(b.q, k8.cpu().float().to(torch.bfloat16).to(device),
+                 v8.cpu().float().to(torch.bfloat16).to(device), b.block_table, b.cache_seqlens,
+                 b.scale)
+    two = torch.full((1,), 2.0, dtype=torch.float32, device=device)
+    got = native.paged_decode_split(b.q, k8, v8, b.block_table, b.cache_seqlens, b.scale,
+                                    softcap=4.0, k_scale=two)
+    torch.cuda.synchronize()
+    # k_scale 2 doubles every score before the cap: the port on 2 * K.
+    b8.k_cache = (b8.k_cache.float() * 2).to(torch.bfloat16)
+    assert max_err(got, port_expected(b8, False, -1, None, 4.0)) <= TOL[torch.bfloat16]

@@ -522,3 +522,42 @@ def test_a_dominant_sink_silences_the_output():
                                            block_table=b.block_table,
                                            sinks=torch.full((4,), 1.0e4))
     assert torch.equal(out, torch.zeros_like(out))
+
+
+# Logit soft-capping: an extension with no reference counterpart.
+
+def test_a_tiny_softcap_gives_uniform_weights():
+    lengths = torch.tensor([3, 40])
+    b = make_paged_batch(2, 4, 2, 64, torch.float32, lengths, seed=61)
+    out = reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache,
+                                           cache_seqlens=b.cache_seqlens.clone(),
+                                           block_table=b.block_table, softcap=1e-6)
+    for i, n in enumerate(lengths.tolist()):
+        mean = gather_dense(b.v_cache, b.block_table[i].tolist(), n).mean(0)  # [HKV, D]
+        torch.testing.assert_close(out[i, 0], mean.repeat_interleave(2, 0), atol=1e-5,
+                                   rtol=1e-5)
+
+
+def test_a_huge_softcap_changes_nothing():
+    b = make_paged_batch(2, 8, 2, 64, torch.float32, torch.tensor([30, 500]), seed=62)
+    args = dict(cache_seqlens=b.cache_seqlens, block_table=b.block_table)
+    plain = reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache, **args)
+    capped = reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache, softcap=1e7, **args)
+    torch.testing.assert_close(plain, capped, atol=1e-6, rtol=1e-5)
+
+
+def test_softcap_on_two_keys_by_hand():
+    # q = e0, k_j = a_j e0: scaled scores s_j = a_j * scale; capped weights
+    # exp(cap * tanh(s_j / cap)) computed here by hand.
+    cap, scale, a = 2.0, 0.5, (3.0, -1.0)
+    q = torch.zeros(1, 1, 8)
+    q[0, 0, 0] = 1.0
+    k = torch.zeros(2, 1, 8)
+    v = torch.zeros(2, 1, 8)
+    for j, aj in enumerate(a):
+        k[j, 0, 0] = aj
+        v[j, 0, j + 1] = 1.0
+    w = [math.exp(cap * math.tanh(aj * scale / cap)) for aj in a]
+    out = reference_port.attention_single(q, k, v, softmax_scale=scale, softcap=cap)
+    assert out[0, 0, 1].item() == pytest.approx(w[0] / sum(w), abs=1e-6)
+    assert out[0, 0, 2].item() == pytest.approx(w[1] / sum(w), abs=1e-6)
