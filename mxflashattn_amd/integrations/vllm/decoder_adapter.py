@@ -230,10 +230,11 @@ def _decode_forward_graph(query: torch.Tensor, kv_cache: torch.Tensor, attn_meta
 
 def _native_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: Any,
                    output: torch.Tensor, softmax_scale: float, k_scale: Any, v_scale: Any,
-                   fp8: bool, window_left: int, sinks: Any = None) -> torch.Tensor:
+                   fp8: bool, window_left: int, sinks: Any = None,
+                   softcap: float = 0.0) -> torch.Tensor:
     """One-token decode straight on the HIP kernels, for what the public API
     (like the reference's) does not take: an fp8 (e4m3fn) cache, a sliding
-    window, attention sinks."""
+    window, attention sinks, logit soft-capping."""
     _no_cascade(attn_metadata)
     if int(attn_metadata.max_query_len) != 1:
         raise DecoderAdapterBlocked(
@@ -250,7 +251,7 @@ def _native_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: A
                               _int32_on(attn_metadata.block_table, query.device),
                               _int32_on(attn_metadata.seq_lens.reshape(-1), query.device),
                               softmax_scale, out=target, window_left=window_left,
-                              sinks=sinks, **scales)
+                              sinks=sinks, softcap=softcap, **scales)
     event = {"path": "mi355x_split_decode", "operation": "paged_decode_split",
              "fallback": "false"}
     if fp8:
@@ -259,6 +260,8 @@ def _native_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: A
         event["window_left"] = str(window_left)
     if sinks is not None:
         event["sinks"] = "true"
+    if softcap > 0:
+        event["softcap"] = str(softcap)
     record_event(event)
     return output
 
@@ -266,7 +269,8 @@ def _native_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: A
 def forward_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: Any,
                    output: torch.Tensor, *, softmax_scale: float, kv_cache_dtype: str = "auto",
                    k_scale: Any = None, v_scale: Any = None,
-                   window_left: int = -1, sinks: Any = None) -> torch.Tensor:
+                   window_left: int = -1, sinks: Any = None,
+                   softcap: float = 0.0) -> torch.Tensor:
     """The decode body of the backend's ``forward``: one-token paged decode into
     vLLM's output buffer, with the dispatch event the reference plugin records
     (integrations/vllm/vllm_plugin.py:297-299,399-431). Raises
@@ -275,12 +279,12 @@ def forward_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: A
     (cache stored as e4m3fn or its uint8 codes) decodes with the layer's
     per-tensor k_scale / v_scale, window_left >= 0 with the layer's sliding
     window (the query at position i sees keys >= i - window_left), and sinks
-    (float32 [HQ]) with the layer's attention sinks; the reference has none
-    of these."""
+    (float32 [HQ]) with the layer's attention sinks, softcap > 0 with its logit
+    soft-capping; the reference has none of these."""
     fp8 = kv_cache_dtype in ("fp8", "fp8_e4m3")
-    if fp8 or window_left >= 0 or sinks is not None:
+    if fp8 or window_left >= 0 or sinks is not None or softcap > 0:
         return _native_decode(query, kv_cache, attn_metadata, output, softmax_scale, k_scale,
-                              v_scale, fp8, window_left, sinks)
+                              v_scale, fp8, window_left, sinks, softcap)
     result, _ = decode_forward(query, kv_cache, attn_metadata, softmax_scale=softmax_scale,
                                causal=bool(attn_metadata.causal))
     info = get_last_dispatch_info()

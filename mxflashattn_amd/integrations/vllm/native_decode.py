@@ -92,8 +92,9 @@ def window_for_kernel(window: Any, causal: bool, ql: int) -> tuple[int, bool] | 
 
 def _guard(args: tuple, kwargs: dict, wide: bool = False,
            descales: tuple = (None, None)) -> tuple[str | None, tuple]:
-    """(reason, (q, k_cache, v_cache, block_table, seqlens, window_left, causal));
-    reason None = take it. Sliding windows are taken under the wider contract."""
+    """(reason, (q, k_cache, v_cache, block_table, seqlens, window_left, causal,
+    softcap)); reason None = take it. Sliding windows and soft-capping are taken
+    under the wider contract."""
     q = args[0] if args else kwargs.get("q")
     if q is None or q.dim() not in (3, 4):
         return "query_rank", ()
@@ -116,9 +117,10 @@ def _guard(args: tuple, kwargs: dict, wide: bool = False,
     else:
         window_left = -1
     try:
-        if float(kwargs.get("softcap") or 0.0) != 0.0:
-            return "softcap", ()
+        softcap = float(kwargs.get("softcap") or 0.0)
     except (TypeError, ValueError):
+        return "softcap", ()
+    if softcap != 0.0 and not (wide and 0.0 < softcap < float("inf")):
         return "softcap", ()
     k_cache = kwargs.get("k_cache", args[1] if len(args) > 1 else None)
     v_cache = kwargs.get("v_cache", args[2] if len(args) > 2 else None)
@@ -147,7 +149,7 @@ def _guard(args: tuple, kwargs: dict, wide: bool = False,
         return "page_size", ()
     if q.device.type != "cuda":
         return "device", ()
-    return None, (q, k_cache, v_cache, bt, sl, window_left, causal)
+    return None, (q, k_cache, v_cache, bt, sl, window_left, causal, softcap)
 
 
 def try_native_decode(args: tuple, kwargs: dict, k_descale: Any = None,
@@ -172,7 +174,7 @@ def try_native_decode(args: tuple, kwargs: dict, k_descale: Any = None,
 
 def _native_decode(picked: tuple, kwargs: dict, k_descale: Any, v_descale: Any,
                    sinks: Any = None) -> torch.Tensor:
-    q, k_cache, v_cache, bt, sl, window_left, causal = picked
+    q, k_cache, v_cache, bt, sl, window_left, causal, softcap = picked
     hq, hd = q.shape[-2], q.shape[-1]
     # An explicit 0.0 is a scale (uniform weights), not "use the default".
     scale = kwargs.get("softmax_scale")
@@ -192,7 +194,7 @@ def _native_decode(picked: tuple, kwargs: dict, k_descale: Any, v_descale: Any,
         scales = {"k_scale": k_descale, "v_scale": v_descale}
     result = native.paged_decode_split(q4, k_cache, v_cache, bt, sl, scale, out=out,
                                        num_splits=ns, causal=causal, window_left=window_left,
-                                       sinks=sinks, **scales)
+                                       sinks=sinks, softcap=softcap, **scales)
     if provided is not None and out is None:
         provided.copy_(result.reshape_as(provided))
         result = provided

@@ -10,10 +10,10 @@ argument" failure is retried once with the untouched functions. The reference
 also swaps ``flash_attn_varlen_func`` there; prefill is not on this path, so it
 stays vLLM's. Encoder layers (``attn_type`` "encoder" / "encoder_only", which
 the reference sends to its dense API and on to the vendor kernel) run vLLM's
-own forward, and so do layers with ALiBi slopes or logit soft-capping, and
-sliding-window or attention-sink layers unless the wider contract is on (then
-the kernel applies the window and the sinks); the reference's forward sends
-all of them to its decoder regardless. Otherwise the forward runs ``decode_forward`` (public
+own forward, and so do layers with ALiBi slopes, and sliding-window,
+attention-sink or soft-capped layers unless the wider contract is on (then the
+kernel applies the window, the sinks and the cap); the reference's forward
+sends all of them to its decoder regardless. Otherwise the forward runs ``decode_forward`` (public
 API) and falls back to vLLM for prefill. The KV-cache update uses the HIP append kernel
 (``reshape_and_cache_flash``).
 Classes live at module scope because vLLM resolves the backend by import path
@@ -85,14 +85,15 @@ def _layer_sinks(impl, query):
 def _layer_option(impl) -> str | None:
     """An option of the layer that the decode kernel does not compute (vLLM's
     FlashAttentionImpl applies them in its own forward), or None. Sliding
-    windows and attention sinks are computed under the wider contract."""
+    windows, attention sinks and soft-capping are computed under the wider
+    contract."""
     if getattr(impl, "alibi_slopes", None) is not None:
         return "alibi"
     window = getattr(impl, "sliding_window", None)
     if (window is not None and not native_decode._no_window(window, True, 1)
             and not native_decode.wide_contract()):
         return "window"
-    if getattr(impl, "logits_soft_cap", None):
+    if getattr(impl, "logits_soft_cap", None) and not native_decode.wide_contract():
         return "softcap"
     if getattr(impl, "sinks", None) is not None and not native_decode.wide_contract():
         return "attention_sinks"
@@ -152,7 +153,8 @@ class MXFlashAttnImpl(FlashAttentionImpl):
                                   k_scale=getattr(layer, "_k_scale", None),
                                   v_scale=getattr(layer, "_v_scale", None),
                                   window_left=_layer_window(self),
-                                  sinks=_layer_sinks(self, query))
+                                  sinks=_layer_sinks(self, query),
+                                  softcap=float(getattr(self, "logits_soft_cap", 0.0) or 0.0))
         except DecoderAdapterBlocked as exc:
             record_event({"path": "vendor_prefill_or_blocked", "reason": str(exc)})
             if "single_token_decode" in str(exc):

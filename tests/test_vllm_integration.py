@@ -175,6 +175,18 @@ def test_native_guard_window_right_bound_matters_only_for_later_keys(monkeypatch
         assert _guard_reason(window, causal, ql) == reason, (window, causal, ql)
 
 
+def test_wide_guard_takes_soft_capping(monkeypatch):
+    monkeypatch.delenv("MXFA_WIDE_CONTRACT", raising=False)
+    kwargs = dict(kv_kwargs(), softcap=30.0)
+    assert native_decode._guard((q_of(),), kwargs)[0] == "softcap"
+    monkeypatch.setenv("MXFA_WIDE_CONTRACT", "1")
+    reason, picked = native_decode._guard((q_of(),), kwargs, True)
+    assert reason == "device"   # every other guard passed on host tensors
+    for bad in (-1.0, float("inf"), "x"):
+        assert native_decode._guard((q_of(),), dict(kv_kwargs(), softcap=bad), True)[0] == \
+            "softcap"
+
+
 def test_wide_guard_takes_sliding_windows(monkeypatch):
     monkeypatch.setenv("MXFA_WIDE_CONTRACT", "1")
     for window, causal, ql, reason in (((127, 0), True, 1, "device"),
@@ -375,7 +387,8 @@ def _picked_guard(monkeypatch):
                         lambda args, kwargs, *a: (None, (args[0], kwargs["k_cache"],
                                                          kwargs["v_cache"],
                                                          kwargs["block_table"],
-                                                         kwargs["cache_seqlens"], -1, False)))
+                                                         kwargs["cache_seqlens"], -1, False,
+                                                         0.0)))
     monkeypatch.setenv("MXFA_NATIVE_DECODE", "1")
     monkeypatch.setattr(native_decode.native, "default_num_splits", lambda *a: 4)
 

@@ -210,8 +210,20 @@ def test_sink_layers_decode_here_under_the_wider_contract(plugin, monkeypatch):
     query = torch.zeros(4, 8, 64)
     assert impl.forward(None, query, None, None, "kv", "meta", "out") == "decoded"
     assert seen[0]["window_left"] == 127
+    assert seen[0]["softcap"] == 0.0
     assert seen[0]["sinks"].dtype == torch.float32
     assert torch.equal(seen[0]["sinks"], impl.sinks.float())
+
+
+def test_soft_capped_layers_decode_here_under_the_wider_contract(plugin, monkeypatch):
+    mod, _ = plugin
+    seen = []
+    monkeypatch.setattr(mod, "forward_decode", lambda *a, **k: seen.append(k) or "decoded")
+    monkeypatch.setenv("MXFA_WIDE_CONTRACT", "1")
+    impl = mod.MXFlashAttnImpl()
+    impl.sliding_window, impl.logits_soft_cap = (-1, -1), 50.0
+    assert _forward(mod, impl) == "decoded"
+    assert seen[0]["softcap"] == 50.0
 
 
 def test_layer_defaults_reach_the_adapter(plugin, monkeypatch):
@@ -238,9 +250,9 @@ def test_decode_goes_through_the_adapter_with_layer_scales(plugin, monkeypatch):
     assert _forward(mod, mod.MXFlashAttnImpl(kv_cache_dtype="fp8"), layer=layer) == "decoded"
     assert seen == [
         dict(softmax_scale=0.125, kv_cache_dtype="auto", k_scale="ks", v_scale="vs",
-             window_left=-1, sinks=None),
+             window_left=-1, sinks=None, softcap=0.0),
         dict(softmax_scale=0.125, kv_cache_dtype="fp8", k_scale="ks", v_scale="vs",
-             window_left=-1, sinks=None)]
+             window_left=-1, sinks=None, softcap=0.0)]
     with pytest.raises(ValueError, match="output buffer"):
         _forward(mod, output=None)
 
