@@ -471,7 +471,7 @@ struct Tile {
 // holding used columns (GQ*QL <= 4 HR), T = element type of q, out and the MFMA
 // operands, kF8 = e4m3fn caches. Accumulator lane (r, c) holds columns
 // 4r..4r+3, dims c*VD + jb in block jb.
-template <int HD, int HR, typename T, bool kF8, bool kLanePages, int NBUF>
+template <int HD, int HR, typename T, bool kF8, bool kLanePages, int NBUF, bool kExtras>
 __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *s_tiles, int kvh,
                                           int rr, int R, int NT, int lo, int hi) {
   using E = Elem<T>;
@@ -503,10 +503,11 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
     if (p.v_scale) v_scale = ((ConstF32)p.v_scale)[0];
   }
   const int ns = p.num_ranges;  // workspace stride
-  // Soft-capping of the scaled score s = acc * scale * k_scale: the base-2
-  // score becomes cap_out * tanh(acc * cap_in) (no division by the scale, so
-  // scale 0 stays 0).
-  const bool capped = p.softcap > 0.f;
+  // kExtras: a sliding window, soft-capping and/or sinks are on (the loop
+  // without them carries no trace of any). Soft-capping of the scaled score s = acc * scale *
+  // k_scale: the base-2 score becomes cap_out * tanh(acc * cap_in) (no
+  // division by the scale, so scale 0 stays 0).
+  const bool capped = kExtras && p.softcap > 0.f;
   const float cap_in = capped ? c / (kLog2e * p.softcap) : 0.f;
   const float cap_out = p.softcap * kLog2e;
 
@@ -685,7 +686,9 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
       // sequence whole in the range, in the combine for a split one. With no
       // key seen (Mh = -inf) the term is +inf and the output 0.
       float Dw = Dh;
-      if (whole && p.sinks) Dw += fast_exp2(p.sinks[kvh * gq + hg] * kLog2e - Mh);
+      if constexpr (kExtras) {
+        if (whole && p.sinks) Dw += fast_exp2(p.sinks[kvh * gq + hg] * kLog2e - Mh);
+      }
       const float inv = Dw > 0.f ? v_scale / Dw : 0.f;
       float v[VD];
 #pragma unroll
@@ -735,14 +738,17 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
     bool need = false;
 #pragma unroll
     for (int i = 0; i < 4; ++i) x[i] = (acc0[i] + acc1[i]) * c;
-    if (capped) {  // wave-uniform
+    if constexpr (kExtras) {
+      if (capped) {  // wave-uniform
 #pragma unroll
-      for (int i = 0; i < 4; ++i) x[i] = cap_out * tanh_exp2((acc0[i] + acc1[i]) * cap_in);
+        for (int i = 0; i < 4; ++i) x[i] = cap_out * tanh_exp2((acc0[i] + acc1[i]) * cap_in);
+      }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * row + i;
-      const bool valid = (col < nc) & (r < d.rem - c_hide) & (r >= d.rem - c_reach);
+      bool valid = (col < nc) & (r < d.rem - c_hide);
+      if constexpr (kExtras) valid &= r >= d.rem - c_reach;
       x[i] = valid ? x[i] : -INFINITY;
       need |= x[i] > m + kRescaleLog2;
     }
@@ -861,7 +867,10 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   });
 }
 
-template <int HD, int HR, typename T, bool kF8, bool kLanePages, int NBUF, int WAVES>
+// kExtras: the call has a sliding window, soft-capping or sinks (the host picks
+// the instantiation; without them the kernel is the plain one).
+template <int HD, int HR, typename T, bool kF8, bool kLanePages, int NBUF, int WAVES,
+          bool kExtras>
 __global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(DecodeParams p) {
   constexpr int kThreads = WAVES * 64;
   extern __shared__ int32_t s_tiles[];  // [B + 1]
@@ -883,7 +892,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(DecodePara
   const int rr = blockIdx.y * p.subs + sub;
   if (sub >= p.subs || kvh >= p.hkv || rr >= R) return;
   const int lo = range_lo(rr, R, NT), hi = range_lo(rr + 1, R, NT);
-  run_range<HD, HR, T, kF8, kLanePages, NBUF>(p, s_tiles, kvh, rr, R, NT, lo, hi);
+  run_range<HD, HR, T, kF8, kLanePages, NBUF, kExtras>(p, s_tiles, kvh, rr, R, NT, lo, hi);
 }
 
 // Merge of two partial states (max, weight, accumulator) in the base-2 domain.
@@ -1039,16 +1048,25 @@ constexpr int kNbuf = kRowBytes<HD, kF8> <= 64 ? 4 : kRowBytes<HD, kF8> <= 128 ?
 // Rows of the MFMA layout that hold used columns (4 columns per row).
 inline int head_rows(int cols) { return cols <= 4 ? 1 : cols <= 8 ? 2 : 4; }
 
-template <int HD, int HR, typename T, bool kF8, int WAVES>
-static int launch_partial_w(const DecodeParams &p, const Grid &g, hipStream_t st) {
+template <int HD, int HR, typename T, bool kF8, int WAVES, bool kExtras>
+static void launch_partial_x(const DecodeParams &p, const Grid &g, hipStream_t st) {
   dim3 grid(g.gx, g.gy);
   const size_t lds = (size_t)(p.batch + 1) * sizeof(int32_t);
   if (p.ps_log2 >= 4)
-    hipLaunchKernelGGL((split_partial_kernel<HD, HR, T, kF8, false, kNbuf<HD, kF8>, WAVES>),
-                       grid, dim3(WAVES * 64), lds, st, p);
+    hipLaunchKernelGGL(
+        (split_partial_kernel<HD, HR, T, kF8, false, kNbuf<HD, kF8>, WAVES, kExtras>), grid,
+        dim3(WAVES * 64), lds, st, p);
   else
-    hipLaunchKernelGGL((split_partial_kernel<HD, HR, T, kF8, true, 2, WAVES>), grid,
+    hipLaunchKernelGGL((split_partial_kernel<HD, HR, T, kF8, true, 2, WAVES, kExtras>), grid,
                        dim3(WAVES * 64), lds, st, p);
+}
+
+template <int HD, int HR, typename T, bool kF8, int WAVES>
+static int launch_partial_w(const DecodeParams &p, const Grid &g, hipStream_t st) {
+  if (p.window_left >= 0 || p.softcap > 0.f || p.sinks)
+    launch_partial_x<HD, HR, T, kF8, WAVES, true>(p, g, st);
+  else
+    launch_partial_x<HD, HR, T, kF8, WAVES, false>(p, g, st);
   return hipGetLastError() == hipSuccess ? MXFA_OK : MXFA_ELAUNCH;
 }
 
