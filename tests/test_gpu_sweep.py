@@ -5,8 +5,9 @@ including 0 and lengths shorter than the query tokens), a query token count
 with QL x GQ <= 16, causal or not, fp16/bf16, an fp8 cache or not, strided q
 and out, a head-major or token-major cache, and a split count, then compares
 the HIP result with the reference port (fp32; exactly dequantised caches for
-fp8) at the north-star tolerances. Seeds are fixed: every run checks the same
-cases.
+fp8) at the north-star tolerances. A second sweep adds a sliding window,
+attention sinks and/or soft-capping to every case (the extended kernel
+instantiation). Seeds are fixed: every run checks the same cases.
 """
 
 from __future__ import annotations
@@ -41,19 +42,48 @@ def draw(seed: int) -> dict:
                 head_major=r.random() < 0.25, ns=r.choice([None, None, 1, 3, 17, 300]))
 
 
-def expected(q, kc, vc, bt, sl, scale, causal) -> torch.Tensor:
+def draw_extras(seed: int, hq: int) -> dict:
+    """Window, sinks and soft-cap for the extended sweep: at least one is on."""
+    r = random.Random(10_000 + seed)
+    while True:
+        window = r.choice([-1, -1, 0, 1, 15, 16, 100, 2000])
+        sinks = None
+        if r.random() < 0.5:
+            vals = [r.uniform(-3.0, 4.0) for _ in range(hq)]
+            if r.random() < 0.3:
+                vals[r.randrange(hq)] = float("-inf")
+            if r.random() < 0.2:
+                vals[r.randrange(hq)] = 25.0
+            sinks = torch.tensor(vals, dtype=torch.float32)
+        softcap = r.choice([0.0, 0.0, 1.0, 10.0, 50.0])
+        if window >= 0 or sinks is not None or softcap > 0:
+            return dict(window=window, sinks=sinks, softcap=softcap)
+
+
+def expected(q, kc, vc, bt, sl, scale, causal, window=-1, sinks=None,
+             softcap=0.0) -> torch.Tensor:
     out = torch.zeros(q.shape, dtype=torch.float32)
     for i in range(q.shape[0]):
         if int(sl[i]) == 0:  # the reference raises on an empty sequence; the kernel gives 0
             continue
         out[i:i + 1] = reference_port.attention_kvcache(
             q[i:i + 1].float(), kc.float(), vc.float(), cache_seqlens=sl[i:i + 1].clone(),
-            block_table=bt[i:i + 1], softmax_scale=scale, causal=causal).float()
+            block_table=bt[i:i + 1], softmax_scale=scale, causal=causal, window_left=window,
+            sinks=sinks, softcap=softcap).float()
     return out
 
 
 @pytest.mark.parametrize("seed", range(150))
 def test_random_contract_sweep(device, seed):
+    run_case(device, seed, extended=False)
+
+
+@pytest.mark.parametrize("seed", range(150, 300))
+def test_random_extended_sweep(device, seed):
+    run_case(device, seed, extended=True)
+
+
+def run_case(device, seed: int, extended: bool):
     c = draw(seed)
     hq = c["hkv"] * c["gq"]
     b = make_paged_batch(c["batch"], hq, c["hkv"], c["hd"], c["dtype"],
@@ -62,7 +92,8 @@ def test_random_contract_sweep(device, seed):
     kc, vc = b.k_cache, b.v_cache
     if c["fp8"]:
         kc, vc = kc.to(FP8), vc.to(FP8)
-    ref = expected(b.q, kc, vc, b.block_table, b.cache_seqlens, b.scale, c["causal"])
+    extras = draw_extras(seed, hq) if extended else dict(window=-1, sinks=None, softcap=0.0)
+    ref = expected(b.q, kc, vc, b.block_table, b.cache_seqlens, b.scale, c["causal"], **extras)
     kd, vd = kc.to(device), vc.to(device)
     if c["head_major"]:  # [pages, HKV, PS, HD] storage viewed as [pages, PS, HKV, HD]
         kd = kd.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
@@ -76,12 +107,15 @@ def test_random_contract_sweep(device, seed):
         obuf = torch.zeros(c["batch"], c["ql"], hq + 5, c["hd"], device=device, dtype=c["dtype"])
         out = obuf[:, :, 1:1 + hq]
     kw = {} if c["ns"] is None else dict(num_splits=c["ns"])
+    sinks = extras["sinks"]
     got = native.paged_decode_split(q, kd, vd, b.block_table.to(device),
                                     b.cache_seqlens.to(device), b.scale, out=out,
-                                    causal=c["causal"], **kw)
+                                    causal=c["causal"], window_left=extras["window"],
+                                    sinks=None if sinks is None else sinks.to(device),
+                                    softcap=extras["softcap"], **kw)
     torch.cuda.synchronize()
     err = (got.float().cpu() - ref).abs().max().item()
-    assert err <= TOL[c["dtype"]], (c, err)
+    assert err <= TOL[c["dtype"]], (c, extras, err)
     if out is not None:  # nothing written outside the slice
         assert torch.equal(obuf[:, :, :1].cpu(), torch.zeros_like(obuf[:, :, :1].cpu()))
         assert torch.equal(obuf[:, :, 1 + hq:].cpu(), torch.zeros_like(obuf[:, :, 1 + hq:].cpu()))
