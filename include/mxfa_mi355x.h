@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define MXFA_ABI_VERSION 6
+#define MXFA_ABI_VERSION 7
 
 /* Return codes. */
 #define MXFA_OK 0
@@ -130,9 +130,13 @@ int mxfa_split_decode_launch(const void *q, int64_t q_stride_b, int64_t q_stride
  * a softmax with one extra zero-valued column (the "s_aux" of vLLM's
  * FlashAttention). softcap > 0 caps every scaled score s to softcap *
  * tanh(s / softcap) before the mask and softmax (FlashAttention's softcap); 0
- * means none. The reference has none of these: its guards hand windows to the
- * vendor (integrations/vllm/vllm_plugin.py:236-247), drop s_aux (:335-339)
- * and its API rejects softcap (mxflashattn/validation.py:56-76). kv_dtype is dtype (16-bit caches) or
+ * means none. alibi_slopes, if not null, holds one fp32 slope per query head
+ * (HQ values, 4-byte aligned): -slope * |p - j| is added to the score of the
+ * query at position p and key j, after the cap (FlashAttention's
+ * alibi_slopes). The reference has none of these: its guards hand windows and
+ * ALiBi to the vendor (integrations/vllm/vllm_plugin.py:220-247), it drops
+ * s_aux (:335-339), and its API rejects softcap and ALiBi
+ * (mxflashattn/validation.py:56-76). kv_dtype is dtype (16-bit caches) or
  * MXFA_DTYPE_FP8_E4M3 with k_scale/v_scale as in mxfa_split_decode_fp8_launch.
  * Workspace: mxfa_split_decode_workspace_size(batch, q_heads * q_len, ...).
  * Partial and combine run as one call. Other arguments as
@@ -142,9 +146,9 @@ int mxfa_split_decode_launch(const void *q, int64_t q_stride_b, int64_t q_stride
  */
 int mxfa_split_decode_multi_launch(
     const void *q, int64_t q_stride_b, int64_t q_stride_t, int64_t q_stride_h, int q_len,
-    int causal, int window_left, const float *sinks, float softcap, const void *k_cache,
-    const void *v_cache, int64_t cache_stride_page, int64_t cache_stride_token,
-    int64_t cache_stride_head, const int32_t *block_table,
+    int causal, int window_left, const float *sinks, float softcap, const float *alibi_slopes,
+    const void *k_cache, const void *v_cache, int64_t cache_stride_page,
+    int64_t cache_stride_token, int64_t cache_stride_head, const int32_t *block_table,
     int64_t bt_stride, const int32_t *seqlens, int seqlen_add, void *out, int64_t out_stride_b,
     int64_t out_stride_t, int64_t out_stride_h, void *workspace, size_t workspace_bytes,
     float scale, int batch, int q_heads, int kv_heads, int head_dim, int page_size,

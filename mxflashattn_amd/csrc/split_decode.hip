@@ -52,6 +52,7 @@ struct SplitArgs {
   int window_left;  // sliding window (keys >= position - window_left), -1: none
   const float *sinks;  // per query head softmax sink logits, nullptr: none
   float softcap;       // logit soft-capping (0: none)
+  const float *alibi;  // per query head ALiBi slopes, nullptr: none
 };
 
 struct WsLayout {
@@ -115,7 +116,8 @@ static int check_split_args(const SplitArgs &a) {
   if (a.ql > 1 && !((a.o_st >= (int64_t)a.hq * a.o_sh && a.o_sh >= a.hd) ||
                     (a.o_sh >= (int64_t)a.ql * a.o_st && a.o_st >= a.hd)))
     return MXFA_EINVAL;
-  if (((uintptr_t)a.k_scale & 3u) || ((uintptr_t)a.v_scale & 3u) || ((uintptr_t)a.sinks & 3u))
+  if (((uintptr_t)a.k_scale & 3u) || ((uintptr_t)a.v_scale & 3u) || ((uintptr_t)a.sinks & 3u) ||
+      ((uintptr_t)a.alibi & 3u))
     return MXFA_EINVAL;
   if (!a.ws || !aligned16(a.ws)) return MXFA_EWORKSPACE;
   if (a.ws_bytes < ws_layout(a.batch, a.hq * a.ql, a.hd, a.num_splits).bytes)
@@ -158,6 +160,7 @@ static DecodeParams make_params(const SplitArgs &a, const Grid &g) {
   p.window_left = a.window_left;
   p.sinks = a.sinks;
   p.softcap = a.softcap;
+  p.alibi = a.alibi;
   p.heads_per_wg = g.heads_per_wg;
   p.subs = g.subs;
   p.ps_log2 = ilog2_exact(a.ps);
@@ -266,6 +269,7 @@ static SplitArgs split_args(const void *q, int64_t q_stride_b, int64_t q_stride_
   a.window_left = -1;
   a.sinks = nullptr;
   a.softcap = 0.f;
+  a.alibi = nullptr;
   return a;
 }
 
@@ -401,8 +405,8 @@ int mxfa_split_decode_combine_launch(void *workspace, size_t workspace_bytes, vo
 
 int mxfa_split_decode_multi_launch(
     const void *q, int64_t q_stride_b, int64_t q_stride_t, int64_t q_stride_h, int q_len,
-    int causal, int window_left, const float *sinks, float softcap, const void *k_cache,
-    const void *v_cache, int64_t cache_stride_page,
+    int causal, int window_left, const float *sinks, float softcap, const float *alibi_slopes,
+    const void *k_cache, const void *v_cache, int64_t cache_stride_page,
     int64_t cache_stride_token, int64_t cache_stride_head, const int32_t *block_table,
     int64_t bt_stride, const int32_t *seqlens, int seqlen_add, void *out, int64_t out_stride_b,
     int64_t out_stride_t, int64_t out_stride_h, void *workspace, size_t workspace_bytes,
@@ -423,6 +427,7 @@ int mxfa_split_decode_multi_launch(
   a.window_left = window_left;
   a.sinks = sinks;
   a.softcap = softcap;
+  a.alibi = alibi_slopes;
   return run_split(a, true, (hipStream_t)stream);
 }
 

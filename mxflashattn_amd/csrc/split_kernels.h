@@ -115,6 +115,7 @@ struct DecodeParams {
   const float *sinks;    // per query head logit added once to each denominator (nullptr: none)
   float scale_log2;
   float softcap;         // logit soft-capping: s -> softcap * tanh(s / softcap) (0: none)
+  const float *alibi;    // per query head ALiBi slope: s -= slope * |query pos - key pos| (nullptr: none)
   int seqlen_add;
   int batch;
   int hkv;
@@ -503,8 +504,8 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
     if (p.v_scale) v_scale = ((ConstF32)p.v_scale)[0];
   }
   const int ns = p.num_ranges;  // workspace stride
-  // kExtras: a sliding window, soft-capping and/or sinks are on (the loop
-  // without them carries no trace of any). Soft-capping of the scaled score s = acc * scale *
+  // kExtras: a sliding window, soft-capping, ALiBi and/or sinks are on (the
+  // loop without them carries no trace of any). Soft-capping of the scaled score s = acc * scale *
   // k_scale: the base-2 score becomes cap_out * tanh(acc * cap_in) (no
   // division by the scale, so scale 0 stays 0).
   const bool capped = kExtras && p.softcap > 0.f;
@@ -525,6 +526,13 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   const int ct = col / gq, cg = col - (col / gq) * gq;
   const int c_hide = p.causal ? p.ql - 1 - ct : 0;
   const int c_reach = p.window_left >= 0 ? p.ql - ct + p.window_left : 0x3fffffff;
+  // ALiBi: base-2 slope of this lane's column; the query of column (ct, cg)
+  // sits QL - ct keys before the sequence end, so key k (L - k = rel) is
+  // |rel - (QL - ct)| positions away from it.
+  const bool alibi = kExtras && p.alibi != nullptr;
+  const float slope2 =
+      alibi && col < nc ? ((ConstF32)p.alibi)[kvh * gq + cg] * kLog2e : 0.f;
+  const int qdist = p.ql - ct;
   const int q_off =
       col < nc ? ct * (int)p.q_st + cg * (int)p.q_sh + row * (kF8 ? 32 : 16) : kOffOut;
   const int q_bytes = (p.ql - 1) * (int)p.q_st + (gq - 1) * (int)p.q_sh + HD * 2;
@@ -743,6 +751,13 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
 #pragma unroll
         for (int i = 0; i < 4; ++i) x[i] = cap_out * tanh_exp2((acc0[i] + acc1[i]) * cap_in);
       }
+      if (alibi) {  // wave-uniform; after the cap, as FlashAttention applies it
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int dist = abs(d.rem - (4 * row + i) - qdist);
+          x[i] -= slope2 * (float)dist;
+        }
+      }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -867,8 +882,8 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   });
 }
 
-// kExtras: the call has a sliding window, soft-capping or sinks (the host picks
-// the instantiation; without them the kernel is the plain one).
+// kExtras: the call has a sliding window, soft-capping, ALiBi or sinks (the host
+// picks the instantiation; without them the kernel is the plain one).
 template <int HD, int HR, typename T, bool kF8, bool kLanePages, int NBUF, int WAVES,
           bool kExtras>
 __global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(DecodeParams p) {
@@ -1063,7 +1078,7 @@ static void launch_partial_x(const DecodeParams &p, const Grid &g, hipStream_t s
 
 template <int HD, int HR, typename T, bool kF8, int WAVES>
 static int launch_partial_w(const DecodeParams &p, const Grid &g, hipStream_t st) {
-  if (p.window_left >= 0 || p.softcap > 0.f || p.sinks)
+  if (p.window_left >= 0 || p.softcap > 0.f || p.sinks || p.alibi)
     launch_partial_x<HD, HR, T, kF8, WAVES, true>(p, g, st);
   else
     launch_partial_x<HD, HR, T, kF8, WAVES, false>(p, g, st);

@@ -231,10 +231,10 @@ def _decode_forward_graph(query: torch.Tensor, kv_cache: torch.Tensor, attn_meta
 def _native_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: Any,
                    output: torch.Tensor, softmax_scale: float, k_scale: Any, v_scale: Any,
                    fp8: bool, window_left: int, sinks: Any = None,
-                   softcap: float = 0.0) -> torch.Tensor:
+                   softcap: float = 0.0, alibi_slopes: Any = None) -> torch.Tensor:
     """One-token decode straight on the HIP kernels, for what the public API
     (like the reference's) does not take: an fp8 (e4m3fn) cache, a sliding
-    window, attention sinks, logit soft-capping."""
+    window, attention sinks, logit soft-capping, ALiBi."""
     _no_cascade(attn_metadata)
     if int(attn_metadata.max_query_len) != 1:
         raise DecoderAdapterBlocked(
@@ -251,7 +251,8 @@ def _native_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: A
                               _int32_on(attn_metadata.block_table, query.device),
                               _int32_on(attn_metadata.seq_lens.reshape(-1), query.device),
                               softmax_scale, out=target, window_left=window_left,
-                              sinks=sinks, softcap=softcap, **scales)
+                              sinks=sinks, softcap=softcap, alibi_slopes=alibi_slopes,
+                              **scales)
     event = {"path": "mi355x_split_decode", "operation": "paged_decode_split",
              "fallback": "false"}
     if fp8:
@@ -262,6 +263,8 @@ def _native_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: A
         event["sinks"] = "true"
     if softcap > 0:
         event["softcap"] = str(softcap)
+    if alibi_slopes is not None:
+        event["alibi"] = "true"
     record_event(event)
     return output
 
@@ -270,7 +273,7 @@ def forward_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: A
                    output: torch.Tensor, *, softmax_scale: float, kv_cache_dtype: str = "auto",
                    k_scale: Any = None, v_scale: Any = None,
                    window_left: int = -1, sinks: Any = None,
-                   softcap: float = 0.0) -> torch.Tensor:
+                   softcap: float = 0.0, alibi_slopes: Any = None) -> torch.Tensor:
     """The decode body of the backend's ``forward``: one-token paged decode into
     vLLM's output buffer, with the dispatch event the reference plugin records
     (integrations/vllm/vllm_plugin.py:297-299,399-431). Raises
@@ -280,11 +283,13 @@ def forward_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: A
     per-tensor k_scale / v_scale, window_left >= 0 with the layer's sliding
     window (the query at position i sees keys >= i - window_left), and sinks
     (float32 [HQ]) with the layer's attention sinks, softcap > 0 with its logit
-    soft-capping; the reference has none of these."""
+    soft-capping, alibi_slopes (float32 [HQ]) with its ALiBi slopes; the
+    reference has none of these."""
     fp8 = kv_cache_dtype in ("fp8", "fp8_e4m3")
-    if fp8 or window_left >= 0 or sinks is not None or softcap > 0:
+    if (fp8 or window_left >= 0 or sinks is not None or softcap > 0
+            or alibi_slopes is not None):
         return _native_decode(query, kv_cache, attn_metadata, output, softmax_scale, k_scale,
-                              v_scale, fp8, window_left, sinks, softcap)
+                              v_scale, fp8, window_left, sinks, softcap, alibi_slopes)
     result, _ = decode_forward(query, kv_cache, attn_metadata, softmax_scale=softmax_scale,
                                causal=bool(attn_metadata.causal))
     info = get_last_dispatch_info()

@@ -13,7 +13,8 @@ MXFA_WIDE_CONTRACT=1 widens the guards to what the kernels take: head dim 256,
 1..16 query heads per kv head, fp8 (e4m3fn) caches with per-tensor
 k_descale / v_descale (a scalar, or a tensor expanded from one), and q of
 [B, QL, HQ, D] with QL x GQ <= 16 (draft-token verification, with the call's
-causal flag).
+causal flag). It also takes a sliding window, soft-capping and ALiBi slopes of
+one per query head ([HQ]; a per-sequence [B, HQ] table is handed back).
 
 ``mx_kvcache_compat`` replaces ``_mx_kvcache_compat`` (:319-349): it drops
 vLLM-only keyword arguments, tries the native route, else the original vendor
@@ -93,8 +94,8 @@ def window_for_kernel(window: Any, causal: bool, ql: int) -> tuple[int, bool] | 
 def _guard(args: tuple, kwargs: dict, wide: bool = False,
            descales: tuple = (None, None)) -> tuple[str | None, tuple]:
     """(reason, (q, k_cache, v_cache, block_table, seqlens, window_left, causal,
-    softcap)); reason None = take it. Sliding windows and soft-capping are taken
-    under the wider contract."""
+    softcap, alibi_slopes)); reason None = take it. Sliding windows, soft-capping
+    and per-head ALiBi slopes are taken under the wider contract."""
     q = args[0] if args else kwargs.get("q")
     if q is None or q.dim() not in (3, 4):
         return "query_rank", ()
@@ -102,8 +103,11 @@ def _guard(args: tuple, kwargs: dict, wide: bool = False,
     sl = kwargs.get("cache_seqlens")
     if bt is None or sl is None or sl.shape[0] != q.shape[0]:
         return "block_table_or_seqlens", ()
-    if kwargs.get("alibi_slopes") is not None:
-        return "alibi", ()
+    alibi = kwargs.get("alibi_slopes")
+    if alibi is not None:
+        alibi = _sinks_for_kernel(alibi, q) if wide else None
+        if alibi is None:
+            return "alibi", ()
     ql = q.shape[1] if q.dim() == 4 else 1
     causal = bool(kwargs.get("causal", False))
     window = kwargs.get("window_size")
@@ -149,7 +153,7 @@ def _guard(args: tuple, kwargs: dict, wide: bool = False,
         return "page_size", ()
     if q.device.type != "cuda":
         return "device", ()
-    return None, (q, k_cache, v_cache, bt, sl, window_left, causal, softcap)
+    return None, (q, k_cache, v_cache, bt, sl, window_left, causal, softcap, alibi)
 
 
 def try_native_decode(args: tuple, kwargs: dict, k_descale: Any = None,
@@ -174,7 +178,7 @@ def try_native_decode(args: tuple, kwargs: dict, k_descale: Any = None,
 
 def _native_decode(picked: tuple, kwargs: dict, k_descale: Any, v_descale: Any,
                    sinks: Any = None) -> torch.Tensor:
-    q, k_cache, v_cache, bt, sl, window_left, causal, softcap = picked
+    q, k_cache, v_cache, bt, sl, window_left, causal, softcap, alibi = picked
     hq, hd = q.shape[-2], q.shape[-1]
     # An explicit 0.0 is a scale (uniform weights), not "use the default".
     scale = kwargs.get("softmax_scale")
@@ -194,7 +198,8 @@ def _native_decode(picked: tuple, kwargs: dict, k_descale: Any, v_descale: Any,
         scales = {"k_scale": k_descale, "v_scale": v_descale}
     result = native.paged_decode_split(q4, k_cache, v_cache, bt, sl, scale, out=out,
                                        num_splits=ns, causal=causal, window_left=window_left,
-                                       sinks=sinks, softcap=softcap, **scales)
+                                       sinks=sinks, softcap=softcap, alibi_slopes=alibi,
+                                       **scales)
     if provided is not None and out is None:
         provided.copy_(result.reshape_as(provided))
         result = provided
@@ -208,7 +213,8 @@ def _native_decode(picked: tuple, kwargs: dict, k_descale: Any, v_descale: Any,
 
 
 def _sinks_for_kernel(s_aux: Any, q: Any) -> torch.Tensor | None:
-    """vLLM's s_aux as the kernel's sinks (float32 [HQ] on q's GPU), or None."""
+    """A per-query-head vector (vLLM's s_aux, FlashAttention's alibi_slopes)
+    as the kernel takes it (float32 [HQ] on q's GPU), or None when it is not one."""
     if not (isinstance(s_aux, torch.Tensor) and isinstance(q, torch.Tensor)):
         return None
     if s_aux.dim() != 1 or s_aux.shape[0] != q.shape[-2] or s_aux.device != q.device:

@@ -10,9 +10,9 @@ argument" failure is retried once with the untouched functions. The reference
 also swaps ``flash_attn_varlen_func`` there; prefill is not on this path, so it
 stays vLLM's. Encoder layers (``attn_type`` "encoder" / "encoder_only", which
 the reference sends to its dense API and on to the vendor kernel) run vLLM's
-own forward, and so do layers with ALiBi slopes, and sliding-window,
-attention-sink or soft-capped layers unless the wider contract is on (then the
-kernel applies the window, the sinks and the cap); the reference's forward
+own forward, and so do sliding-window, attention-sink, soft-capped and ALiBi
+layers unless the wider contract is on (then the kernel applies the window, the
+sinks, the cap and the slopes); the reference's forward
 sends all of them to its decoder regardless. Otherwise the forward runs ``decode_forward`` (public
 API) and falls back to vLLM for prefill. The KV-cache update uses the HIP append kernel
 (``reshape_and_cache_flash``).
@@ -24,6 +24,7 @@ from __future__ import annotations
 
 import os
 
+import torch
 from vllm.v1.attention.backends.flash_attn import (  # noqa: F401  (requires vLLM)
     FlashAttentionBackend,
     FlashAttentionImpl,
@@ -75,19 +76,31 @@ def _layer_window(impl) -> int:
     return -1 if mapped is None else mapped[0]
 
 
-def _layer_sinks(impl, query):
-    """The layer's attention sinks (vLLM keeps them per query head) as the
-    kernel's float32 [HQ], or None."""
-    sinks = getattr(impl, "sinks", None)
-    return None if sinks is None else native_decode._sinks_for_kernel(sinks, query)
+def _layer_vector(impl, name: str, query):
+    """A per-query-head vector of the layer (vLLM's attention sinks, ALiBi
+    slopes) as the kernel's float32 [HQ] on the query's GPU: (vector, usable).
+    The slopes are fixed at construction and may live on the host, so a device
+    copy of them is kept on the layer; sinks are a weight, taken where they are."""
+    value = getattr(impl, name, None)
+    if value is None:
+        return None, True
+    if (name == "alibi_slopes" and isinstance(value, torch.Tensor)
+            and isinstance(query, torch.Tensor) and value.device != query.device):
+        cached = getattr(impl, "_mxfa_alibi_slopes", None)
+        if cached is None or cached[0] is not value or cached[1].device != query.device:
+            cached = (value, value.to(device=query.device, dtype=torch.float32).contiguous())
+            impl._mxfa_alibi_slopes = cached
+        value = cached[1]
+    vector = native_decode._sinks_for_kernel(value, query)
+    return vector, vector is not None
 
 
 def _layer_option(impl) -> str | None:
     """An option of the layer that the decode kernel does not compute (vLLM's
     FlashAttentionImpl applies them in its own forward), or None. Sliding
-    windows, attention sinks and soft-capping are computed under the wider
-    contract."""
-    if getattr(impl, "alibi_slopes", None) is not None:
+    windows, attention sinks, soft-capping and ALiBi are computed under the
+    wider contract."""
+    if getattr(impl, "alibi_slopes", None) is not None and not native_decode.wide_contract():
         return "alibi"
     window = getattr(impl, "sliding_window", None)
     if (window is not None and not native_decode._no_window(window, True, 1)
@@ -131,6 +144,14 @@ class MXFlashAttnImpl(FlashAttentionImpl):
             record_event({"path": "vendor_direct", "operation": "encoder", "fallback": "false"})
             return result
         option = _layer_option(self)
+        sinks, alibi = (None, True), (None, True)
+        if option is None:
+            sinks = _layer_vector(self, "sinks", query)
+            alibi = _layer_vector(self, "alibi_slopes", query)
+            if not sinks[1]:
+                option = "attention_sinks"  # not one float per query head on this GPU
+            elif not alibi[1]:
+                option = "alibi"
         if option is None and (output_scale is not None or output_block_scale is not None):
             option = "output_quantization"  # vLLM's forward decides (it raises for it)
         if option is not None:
@@ -153,7 +174,7 @@ class MXFlashAttnImpl(FlashAttentionImpl):
                                   k_scale=getattr(layer, "_k_scale", None),
                                   v_scale=getattr(layer, "_v_scale", None),
                                   window_left=_layer_window(self),
-                                  sinks=_layer_sinks(self, query),
+                                  sinks=sinks[0], alibi_slopes=alibi[0],
                                   softcap=float(getattr(self, "logits_soft_cap", 0.0) or 0.0))
         except DecoderAdapterBlocked as exc:
             record_event({"path": "vendor_prefill_or_blocked", "reason": str(exc)})

@@ -24,7 +24,7 @@ LIB_PATH = Path(
     os.environ.get("MXFLASHATTN_AMD_LIB")
     or Path(__file__).resolve().parent / "_lib" / "libmxfa_mi355x.so"
 )
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 MXFA_OK = 0
 MXFA_EUNSUPPORTED = -1
@@ -96,8 +96,8 @@ _SIGNATURES = {
     "mxfa_split_decode_fp8_partial_launch": (_i, _SPLIT_ARGS + [_p, _p, _p]),
     "mxfa_split_decode_multi_launch": (
         _i,
-        [_p, _i64, _i64, _i64, _i, _i, _i, _p, _f, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i,
-         _p, _i64,
+        [_p, _i64, _i64, _i64, _i, _i, _i, _p, _f, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p,
+         _i, _p, _i64,
          _i64, _i64, _p, _sz, _f, _i, _i, _i, _i, _i, _i, _i, _i, _i, _p, _p, _i, _p],
     ),
     "mxfa_split_decode_combine_launch": (
@@ -369,7 +369,7 @@ def _prepare(q, k_cache, v_cache, block_table, cache_seqlens, out):
 
 def _launch_multi(q, k_cache, v_cache, block_table, cache_seqlens, out, workspace, ws_bytes,
                   softmax_scale, num_splits, seqlen_add, stream, causal, k_scale, v_scale,
-                  window_left, sinks, softcap):
+                  window_left, sinks, softcap, alibi_slopes):
     if q.dim() == 3:
         q, out = q.unsqueeze(1), out.unsqueeze(1)
     batch, ql, hq, hd = q.shape
@@ -378,7 +378,8 @@ def _launch_multi(q, k_cache, v_cache, block_table, cache_seqlens, out, workspac
     fp8 = k_cache.dtype == FP8_DTYPE
     rc = library().mxfa_split_decode_multi_launch(
         q.data_ptr(), qs[0], qs[1], qs[2], ql, int(bool(causal)), int(window_left),
-        _sinks_ptr(sinks, q), float(softcap), k_cache.data_ptr(),
+        _sinks_ptr(sinks, q), float(softcap), _sinks_ptr(alibi_slopes, q, "alibi_slopes"),
+        k_cache.data_ptr(),
         v_cache.data_ptr(), cs[0], cs[1], cs[2], block_table.data_ptr(), block_table.stride(0),
         cache_seqlens.data_ptr(), seqlen_add, out.data_ptr(), os_[0], os_[1], os_[2], workspace,
         ws_bytes, float(softmax_scale), batch, hq, hkv, hd, ps, block_table.shape[1], pages,
@@ -388,16 +389,17 @@ def _launch_multi(q, k_cache, v_cache, block_table, cache_seqlens, out, workspac
     _check(rc, "mxfa_split_decode_multi_launch")
 
 
-def _sinks_ptr(sinks, q: torch.Tensor) -> int:
-    """Device address of per-query-head sink logits: float32 [HQ], contiguous,
-    on q's GPU; None gives 0 (no sinks)."""
-    if sinks is None:
+def _sinks_ptr(values, q: torch.Tensor, name: str = "sinks") -> int:
+    """Device address of a per-query-head float32 vector (sinks, ALiBi
+    slopes): [HQ], contiguous, on q's GPU; None gives 0 (none)."""
+    if values is None:
         return 0
-    if (not isinstance(sinks, torch.Tensor) or sinks.dtype != torch.float32
-            or sinks.device != q.device or sinks.dim() != 1 or sinks.shape[0] != q.shape[-2]
-            or not sinks.is_contiguous()):
-        raise ValueError(f"sinks must be a contiguous float32 [{q.shape[-2]}] tensor on {q.device}")
-    return sinks.data_ptr()
+    if (not isinstance(values, torch.Tensor) or values.dtype != torch.float32
+            or values.device != q.device or values.dim() != 1 or values.shape[0] != q.shape[-2]
+            or not values.is_contiguous()):
+        raise ValueError(f"{name} must be a contiguous float32 [{q.shape[-2]}] tensor on "
+                         f"{q.device}")
+    return values.data_ptr()
 
 
 def default_num_splits(q: torch.Tensor, k_cache: torch.Tensor, block_table: torch.Tensor) -> int:
@@ -423,6 +425,7 @@ def paged_decode_split(
     window_left: int = -1,
     sinks: torch.Tensor | None = None,
     softcap: float = 0.0,
+    alibi_slopes: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Split-KV paged decode on the current stream; returns ``out`` shaped like q.
 
@@ -439,6 +442,8 @@ def paged_decode_split(
     sinks: float32 [HQ] per-head logits on the scale of the scaled scores,
     each added once to its row's softmax denominator (vLLM's s_aux).
     softcap > 0: every scaled score s becomes softcap * tanh(s / softcap).
+    alibi_slopes: float32 [HQ]; -slope * |p - j| is added to the score of the
+    query at position p and key j, after the cap.
     num_splits: balanced work ranges per kv head (default: split_heuristic).
     """
     if int(window_left) < -1:
@@ -454,10 +459,11 @@ def paged_decode_split(
     ql = q.shape[1] if q.dim() == 4 else 1
     ws_bytes = workspace_size(q.shape[0], q.shape[-2] * ql, q.shape[-1], num_splits)
     ws = WORKSPACE.get(q.device, stream, ws_bytes)
-    if ql > 1 or window_left >= 0 or sinks is not None or softcap > 0:
+    if ql > 1 or window_left >= 0 or sinks is not None or softcap > 0 or (
+            alibi_slopes is not None):
         _launch_multi(q, k_cache, v_cache, block_table, cache_seqlens, out, ws.data_ptr(),
                       ws_bytes, softmax_scale, num_splits, seqlen_add, stream, causal, k_scale,
-                      v_scale, window_left, sinks, softcap)
+                      v_scale, window_left, sinks, softcap, alibi_slopes)
         return out
     args = _launch_args(q, k_cache, v_cache, block_table, cache_seqlens, out, ws.data_ptr(),
                         ws_bytes, softmax_scale, num_splits, seqlen_add, stream)

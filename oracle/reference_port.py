@@ -29,6 +29,11 @@ softcap > 0 caps every scaled score s to softcap * tanh(s / softcap) before the
 masks (FlashAttention's softcap); the reference rejects it
 (validation.py:56-76). Pinned by its limits: a tiny cap gives uniform weights
 (the mean of the visible V rows), a huge one no change.
+
+alibi_slopes (float32 [HQ]) adds -slope * |p - j| to the score of the query
+at position p and key j, after the cap and before the masks (FlashAttention's
+alibi_slopes); the reference rejects them (validation.py:56-76). Pinned by
+zero slopes and by a zero query, whose weights are exactly e^(-slope*|p-j|).
 """
 
 from __future__ import annotations
@@ -41,7 +46,8 @@ import torch
 def attention_single(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
                      softmax_scale: float | None = None, causal: bool = False,
                      window_left: int = -1, sinks: torch.Tensor | None = None,
-                     softcap: float = 0.0) -> torch.Tensor:
+                     softcap: float = 0.0,
+                     alibi_slopes: torch.Tensor | None = None) -> torch.Tensor:
     """q [Lq, HQ, D], k/v [Lk, HKV, D] -> [Lq, HQ, D] in q.dtype (reference.py:8-40)."""
     if q.shape[0] == 0:
         return q.clone()
@@ -61,6 +67,9 @@ def attention_single(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     # query i sits at key position i + (Lk - Lq).
     qpos = torch.arange(lq).unsqueeze(1) + (lk - lq)
     kpos = torch.arange(lk).unsqueeze(0)
+    if alibi_slopes is not None:
+        dist = (qpos - kpos).abs().float().unsqueeze(0)  # [1, Lq, Lk]
+        scores = scores - alibi_slopes.float().view(hq, 1, 1) * dist
     if causal:  # it may not see later keys
         scores = scores.masked_fill((kpos > qpos).unsqueeze(0), float("-inf"))
     if window_left >= 0:  # nor keys more than window_left before it
@@ -110,7 +119,8 @@ def attention_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
                       k: torch.Tensor | None = None, v: torch.Tensor | None = None,
                       softmax_scale: float | None = None, causal: bool = False,
                       window_left: int = -1, sinks: torch.Tensor | None = None,
-                      softcap: float = 0.0) -> torch.Tensor:
+                      softcap: float = 0.0,
+                      alibi_slopes: torch.Tensor | None = None) -> torch.Tensor:
     """Decode/append against a dense or paged cache (reference.py:88-139).
 
     Mutates the caches (append) and cache_seqlens (+= S_new) like the reference.
@@ -137,7 +147,7 @@ def attention_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
             vb = gather_pages(v_cache, row, total)
         outs.append(attention_single(q[b], kb, vb, softmax_scale=softmax_scale, causal=causal,
                                      window_left=window_left, sinks=sinks,
-                                     softcap=softcap))
+                                     softcap=softcap, alibi_slopes=alibi_slopes))
     if k is not None:
         cache_seqlens.add_(s_new)
     return torch.stack(outs) if outs else q.clone()

@@ -196,7 +196,7 @@ def test_fp8_decode_rejects_misaligned_scale_pointers(lib):
 def multi_args(**over):
     """A well-formed argument tuple for mxfa_split_decode_multi_launch (QL = 2)."""
     a = dict(q=FAKE, q_sb=2 * 32 * 128, q_st=32 * 128, q_sh=128, ql=2, causal=1, window=-1,
-             sinks=None, softcap=0.0, k=FAKE, v=FAKE,
+             sinks=None, softcap=0.0, alibi=None, k=FAKE, v=FAKE,
              c_sp=16 * 8 * 128, c_st=8 * 128, c_sh=128, bt=FAKE, bt_stride=64, seqlens=FAKE,
              seqlen_add=0, out=FAKE, o_sb=2 * 32 * 128, o_st=32 * 128, o_sh=128, ws=FAKE,
              ws_bytes=1 << 30, scale=0.088, batch=32, hq=32, hkv=8, hd=128, ps=16, btw=64,
@@ -217,6 +217,7 @@ def multi_args(**over):
     (dict(sinks=FAKE + 2), -2), (dict(sinks=FAKE, ws_bytes=1000), -3),   # sink pointer
     (dict(softcap=-1.0), -2), (dict(softcap=float("nan")), -2), (dict(softcap=float("inf")), -2),
     (dict(softcap=30.0, ws_bytes=1000), -3),
+    (dict(alibi=FAKE + 1), -2), (dict(alibi=FAKE, ws_bytes=1000), -3),
 ])
 def test_multi_launch_rejects_before_launching(lib, over, code):
     assert lib.mxfa_split_decode_multi_launch(*multi_args(**over)) == code

@@ -139,13 +139,13 @@ def test_plugin_path_with_fp8_cache_matches_oracle(device):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("with_sinks", [False, True], ids=["plain", "sinks_softcap"])
+@pytest.mark.parametrize("with_sinks", [False, True], ids=["plain", "sinks_softcap_alibi"])
 @pytest.mark.parametrize("kv_dtype", ["auto", "fp8"])
 def test_adapter_window_decode_matches_oracle(device, kv_dtype, with_sinks):
     """forward_decode with a layer's sliding window and attention sinks (the
     backend under the wider contract), on a vLLM-layout cache [2, blocks, PS,
     HKV, HD], against the port's windowed attention with sinks; fp8 caches on
-    their exactly decoded values."""
+    their exactly decoded values. The second case adds soft-capping and ALiBi."""
     from types import SimpleNamespace
 
     from mxflashattn_amd.integrations.vllm import decoder_adapter
@@ -176,17 +176,19 @@ def test_adapter_window_decode_matches_oracle(device, kv_dtype, with_sinks):
     scale = hd ** -0.5
     sinks = torch.linspace(-2.0, 2.0, hq) if with_sinks else None
     cap = 3.0 if with_sinks else 0.0
+    slopes = torch.pow(2.0, -torch.arange(1, hq + 1, dtype=torch.float32)) if with_sinks else None
     for window in (-1, 0, 17, 100, 5000):
         out = torch.full((4, hq * hd), float("nan"), dtype=torch.bfloat16, device=device)
         decoder_adapter.forward_decode(q.to(device), dev_cache.to(device), meta, out,
                                        softmax_scale=scale, kv_cache_dtype=kv_dtype,
                                        k_scale=one, v_scale=one, window_left=window,
                                        sinks=None if sinks is None else sinks.to(device),
-                                       softcap=cap)
+                                       softcap=cap,
+                                       alibi_slopes=None if slopes is None else slopes.to(device))
         torch.cuda.synchronize()
         want = reference_port.attention_kvcache(
             q.unsqueeze(1), ref_cache[0], ref_cache[1], cache_seqlens=lengths.clone(),
             block_table=table, softmax_scale=scale, window_left=window, sinks=sinks,
-            softcap=cap)
+            softcap=cap, alibi_slopes=slopes)
         err = (out.float().cpu() - want.reshape(4, -1).float()).abs().max().item()
         assert err <= 1.6e-2, (window, err)

@@ -233,7 +233,7 @@ def test_fp8_reshape_and_cache_keeps_nan_and_saturates_inf(device):
 
 
 def port_expected(b, causal: bool, window_left: int = -1, sinks=None,
-                  softcap: float = 0.0) -> torch.Tensor:
+                  softcap: float = 0.0, alibi=None) -> torch.Tensor:
     """fp32 restatement of reference.attention_kvcache (bottom-right causal mask;
     window_left >= 0 adds the sliding window of the port, pinned in test_oracle)."""
     from oracle import reference_port
@@ -247,7 +247,8 @@ def port_expected(b, causal: bool, window_left: int = -1, sinks=None,
             cpu.q[i:i + 1].float(), cpu.k_cache.float(), cpu.v_cache.float(),
             cache_seqlens=cpu.cache_seqlens[i:i + 1].clone(), block_table=cpu.block_table[i:i + 1],
             softmax_scale=cpu.scale, causal=causal, window_left=window_left,
-            sinks=None if sinks is None else sinks.cpu(), softcap=softcap).float()
+            sinks=None if sinks is None else sinks.cpu(), softcap=softcap,
+            alibi_slopes=None if alibi is None else alibi.cpu()).float()
     return out
 
 
@@ -562,3 +563,82 @@ def test_softcap_with_fp8_caches(device):
     # k_scale 2 doubles every score before the cap: the port on 2 * K.
     b8.k_cache = (b8.k_cache.float() * 2).to(torch.bfloat16)
     assert max_err(got, port_expected(b8, False, -1, None, 4.0)) <= TOL[torch.bfloat16]
+
+
+# ---------------------------------------------------------------------------
+# ALiBi: s -= slope[h] * |query position - key position|, after the cap.
+
+
+def alibi_slopes(hq: int, device, sign: float = 1.0) -> torch.Tensor:
+    # The geometric slopes of the ALiBi paper, 2^(-8 (h + 1) / HQ), optionally negated
+    # (a bias that grows with distance drives the running maximum up tile after tile).
+    h = torch.arange(1, hq + 1, dtype=torch.float32)
+    return (sign * torch.pow(2.0, -8.0 * h / hq)).to(device)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("ql,gq,causal,window,with_sinks,cap",
+                         [(1, 4, False, -1, False, 0.0), (1, 8, True, -1, False, 0.0),
+                          (3, 4, True, -1, False, 0.0), (2, 8, False, -1, False, 0.0),
+                          (2, 4, True, 40, True, 0.0), (2, 4, True, -1, False, 5.0),
+                          (1, 1, False, 200, True, 30.0)])
+def test_alibi_matches_reference(device, dtype, head_dim, ql, gq, causal, window, with_sinks,
+                                 cap):
+    lengths = torch.tensor([1, 17, 300, 0, 1000, 2100])
+    b = make_paged_batch(6, 2 * gq, 2, head_dim, dtype, lengths, seed=111).to(device)
+    b = with_query_tokens(b, ql, 112)
+    slopes = alibi_slopes(2 * gq, device)
+    sinks = sink_values(2 * gq, device) if with_sinks else None
+    expected = port_expected(b, causal, window, sinks, cap, slopes)
+    for ns in (None, 1, 9):
+        kw = {} if ns is None else dict(num_splits=ns)
+        got = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table,
+                                        b.cache_seqlens, b.scale, causal=causal,
+                                        window_left=window, sinks=sinks, softcap=cap,
+                                        alibi_slopes=slopes, **kw)
+        torch.cuda.synchronize()
+        assert torch.isfinite(got.float()).all()
+        assert max_err(got, expected) <= TOL[dtype], (ns, max_err(got, expected))
+
+
+def test_alibi_with_negative_slopes_and_zero_slopes(device):
+    lengths = torch.tensor([5, 700, 3000])
+    b = make_paged_batch(3, 8, 2, 128, torch.bfloat16, lengths, seed=113).to(device)
+    for slopes in (alibi_slopes(8, device, -0.05), torch.zeros(8, device=device)):
+        expected = port_expected(b, False, -1, None, 0.0, slopes)
+        for ns in (None, 1, 7):
+            kw = {} if ns is None else dict(num_splits=ns)
+            got = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table,
+                                            b.cache_seqlens, b.scale, alibi_slopes=slopes,
+                                            **kw)
+            torch.cuda.synchronize()
+            assert max_err(got, expected) <= TOL[torch.bfloat16], (ns, slopes[0].item())
+    # Zero slopes take the extended instantiation and still match the plain one.
+    plain = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table,
+                                      b.cache_seqlens, b.scale)
+    torch.cuda.synchronize()
+    assert max_err(got, plain.float()) <= TOL[torch.bfloat16]
+
+
+def test_alibi_with_fp8_caches(device):
+    b = make_paged_batch(4, 8, 2, 128, torch.bfloat16, torch.tensor([3, 64, 500, 1200]),
+                         seed=114).to(device)
+    k8, v8 = fp8_caches(b, device)
+    b8 = type(b)(b.q, k8.cpu().float().to(torch.bfloat16).to(device),
+                 v8.cpu().float().to(torch.bfloat16).to(device), b.block_table, b.cache_seqlens,
+                 b.scale)
+    slopes = alibi_slopes(8, device)
+    got = native.paged_decode_split(b.q, k8, v8, b.block_table, b.cache_seqlens, b.scale,
+                                    alibi_slopes=slopes)
+    torch.cuda.synchronize()
+    assert max_err(got, port_expected(b8, False, -1, None, 0.0, slopes)) <= TOL[torch.bfloat16]
+
+
+def test_alibi_slopes_are_checked_on_the_host(device):
+    b = make_paged_batch(2, 8, 2, 64, torch.bfloat16, torch.tensor([10, 20]), seed=115).to(device)
+    for bad in (torch.zeros(7, device=device), torch.zeros(8, device=device, dtype=torch.float16),
+                torch.zeros(8), torch.zeros(16, device=device)[::2]):
+        with pytest.raises(ValueError, match="alibi_slopes"):
+            native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table,
+                                      b.cache_seqlens, b.scale, alibi_slopes=bad)

@@ -561,3 +561,36 @@ def test_softcap_on_two_keys_by_hand():
     out = reference_port.attention_single(q, k, v, softmax_scale=scale, softcap=cap)
     assert out[0, 0, 1].item() == pytest.approx(w[0] / sum(w), abs=1e-6)
     assert out[0, 0, 2].item() == pytest.approx(w[1] / sum(w), abs=1e-6)
+
+
+# ALiBi slopes: an extension with no reference counterpart.
+
+def test_zero_alibi_slopes_change_nothing():
+    b = make_paged_batch(2, 8, 2, 64, torch.float32, torch.tensor([30, 200]), seed=71, q_len=2)
+    args = dict(cache_seqlens=b.cache_seqlens, block_table=b.block_table, causal=True)
+    plain = reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache, **args)
+    zero = reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache,
+                                            alibi_slopes=torch.zeros(8), **args)
+    torch.testing.assert_close(plain, zero)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_alibi_weights_of_a_zero_query_by_hand(causal):
+    # All raw scores 0: key j of the query at position p weighs e^(-s|p-j|);
+    # with one-hot V rows the output is those weights, normalised.
+    n, ql, hd = 6, 2, 8
+    slopes = torch.tensor([0.5, 1.25])
+    q = torch.zeros(ql, 2, hd)
+    k = torch.randn(n, 1, hd)
+    v = torch.zeros(n, 1, hd)
+    for j in range(n):
+        v[j, 0, j] = 1.0
+    out = reference_port.attention_single(q, k, v, causal=causal, alibi_slopes=slopes)
+    for t in range(ql):
+        p = n - ql + t
+        for h in range(2):
+            keys = [j for j in range(n) if j <= p or not causal]
+            w = {j: math.exp(-float(slopes[h]) * abs(p - j)) for j in keys}
+            total = sum(w.values())
+            for j in range(n):
+                assert out[t, h, j].item() == pytest.approx(w.get(j, 0.0) / total, abs=1e-6)

@@ -187,6 +187,18 @@ def test_wide_guard_takes_soft_capping(monkeypatch):
             "softcap"
 
 
+def test_wide_guard_takes_alibi_slopes_of_one_per_query_head(monkeypatch):
+    monkeypatch.delenv("MXFA_WIDE_CONTRACT", raising=False)
+    slopes = torch.pow(2.0, -torch.arange(1, 17, dtype=torch.float64))
+    kwargs = dict(kv_kwargs(), alibi_slopes=slopes)
+    assert native_decode._guard((q_of(),), kwargs)[0] == "alibi"
+    assert native_decode._guard((q_of(),), kwargs, True)[0] == "device"  # every other passed
+    assert native_decode._sinks_for_kernel(slopes, q_of()).dtype == torch.float32
+    for bad in (torch.zeros(1, 16), torch.zeros(15), [0.5] * 16):  # per sequence, short, list
+        assert native_decode._guard((q_of(),), dict(kv_kwargs(), alibi_slopes=bad),
+                                    True)[0] == "alibi"
+
+
 def test_wide_guard_takes_sliding_windows(monkeypatch):
     monkeypatch.setenv("MXFA_WIDE_CONTRACT", "1")
     for window, causal, ql, reason in (((127, 0), True, 1, "device"),
@@ -388,7 +400,7 @@ def _picked_guard(monkeypatch):
                                                          kwargs["v_cache"],
                                                          kwargs["block_table"],
                                                          kwargs["cache_seqlens"], -1, False,
-                                                         0.0)))
+                                                         0.0, None)))
     monkeypatch.setenv("MXFA_NATIVE_DECODE", "1")
     monkeypatch.setattr(native_decode.native, "default_num_splits", lambda *a: 4)
 

@@ -226,6 +226,41 @@ def test_soft_capped_layers_decode_here_under_the_wider_contract(plugin, monkeyp
     assert seen[0]["softcap"] == 50.0
 
 
+def test_alibi_layers_decode_here_under_the_wider_contract(plugin, monkeypatch):
+    # vLLM builds the slopes on the host; the kernel gets one device copy per layer.
+    mod, _ = plugin
+    seen = []
+    monkeypatch.setattr(mod, "forward_decode", lambda *a, **k: seen.append(k) or "decoded")
+    monkeypatch.setenv("MXFA_WIDE_CONTRACT", "1")
+    impl = mod.MXFlashAttnImpl()
+    impl.sliding_window, impl.logits_soft_cap = (-1, -1), 0.0
+    impl.alibi_slopes = torch.pow(2.0, -torch.arange(1, 9, dtype=torch.float32))
+    query = torch.zeros(4, 8, 64, device="meta")
+    for _ in range(2):
+        assert impl.forward(None, query, None, None, "kv", "meta", "out") == "decoded"
+    assert seen[0]["alibi_slopes"].device.type == "meta"
+    assert seen[0]["alibi_slopes"].shape == (8,)
+    assert seen[1]["alibi_slopes"] is seen[0]["alibi_slopes"]  # copied once
+
+
+@pytest.mark.parametrize("attr,value,reason", [
+    ("alibi_slopes", torch.zeros(4, 8), "alibi"),      # per sequence: vLLM's
+    ("sinks", torch.zeros(7), "attention_sinks"),
+])
+def test_per_head_vectors_of_another_shape_run_vllms_forward(plugin, monkeypatch, attr, value,
+                                                             reason):
+    mod, _ = plugin
+    monkeypatch.setattr(mod, "forward_decode",
+                        lambda *a, **k: pytest.fail("must not reach the decode adapter"))
+    monkeypatch.setenv("MXFA_WIDE_CONTRACT", "1")
+    impl = mod.MXFlashAttnImpl()
+    impl.sliding_window, impl.logits_soft_cap = (-1, -1), 0.0
+    setattr(impl, attr, value)
+    assert impl.forward(None, torch.zeros(4, 8, 64), None, None, "kv", "meta", "out") == \
+        "vendor_kvcache"
+    assert backend.get_dispatch_events()[-1]["fallback_reason"] == reason
+
+
 def test_layer_defaults_reach_the_adapter(plugin, monkeypatch):
     mod, _ = plugin
     monkeypatch.setattr(mod, "forward_decode", lambda *a, **k: "decoded")
@@ -250,9 +285,9 @@ def test_decode_goes_through_the_adapter_with_layer_scales(plugin, monkeypatch):
     assert _forward(mod, mod.MXFlashAttnImpl(kv_cache_dtype="fp8"), layer=layer) == "decoded"
     assert seen == [
         dict(softmax_scale=0.125, kv_cache_dtype="auto", k_scale="ks", v_scale="vs",
-             window_left=-1, sinks=None, softcap=0.0),
+             window_left=-1, sinks=None, alibi_slopes=None, softcap=0.0),
         dict(softmax_scale=0.125, kv_cache_dtype="fp8", k_scale="ks", v_scale="vs",
-             window_left=-1, sinks=None, softcap=0.0)]
+             window_left=-1, sinks=None, alibi_slopes=None, softcap=0.0)]
     with pytest.raises(ValueError, match="output buffer"):
         _forward(mod, output=None)
 
