@@ -7,7 +7,8 @@ and out, a head-major or token-major cache, and a split count, then compares
 the HIP result with the reference port (fp32; exactly dequantised caches for
 fp8) at the north-star tolerances. A second sweep adds a sliding window,
 attention sinks and/or soft-capping to every case (the extended kernel
-instantiation). Seeds are fixed: every run checks the same cases.
+instantiation), and ALiBi slopes to about half of them (drawn from a stream of
+their own). Seeds are fixed: every run checks the same cases.
 """
 
 from __future__ import annotations
@@ -43,7 +44,8 @@ def draw(seed: int) -> dict:
 
 
 def draw_extras(seed: int, hq: int) -> dict:
-    """Window, sinks and soft-cap for the extended sweep: at least one is on."""
+    """Window, sinks and soft-cap for the extended sweep (at least one is on),
+    and ALiBi slopes or None."""
     r = random.Random(10_000 + seed)
     while True:
         window = r.choice([-1, -1, 0, 1, 15, 16, 100, 2000])
@@ -57,11 +59,20 @@ def draw_extras(seed: int, hq: int) -> dict:
             sinks = torch.tensor(vals, dtype=torch.float32)
         softcap = r.choice([0.0, 0.0, 1.0, 10.0, 50.0])
         if window >= 0 or sinks is not None or softcap > 0:
-            return dict(window=window, sinks=sinks, softcap=softcap)
+            break
+    a = random.Random(20_000 + seed)
+    alibi = None
+    if a.random() < 0.5:  # geometric slopes, or arbitrary ones of either sign
+        if a.random() < 0.5:
+            alibi = torch.pow(2.0, -8.0 * torch.arange(1, hq + 1, dtype=torch.float32) / hq)
+        else:
+            alibi = torch.tensor([a.uniform(-0.02, 0.5) for _ in range(hq)],
+                                 dtype=torch.float32)
+    return dict(window=window, sinks=sinks, softcap=softcap, alibi=alibi)
 
 
 def expected(q, kc, vc, bt, sl, scale, causal, window=-1, sinks=None,
-             softcap=0.0) -> torch.Tensor:
+             softcap=0.0, alibi=None) -> torch.Tensor:
     out = torch.zeros(q.shape, dtype=torch.float32)
     for i in range(q.shape[0]):
         if int(sl[i]) == 0:  # the reference raises on an empty sequence; the kernel gives 0
@@ -69,7 +80,7 @@ def expected(q, kc, vc, bt, sl, scale, causal, window=-1, sinks=None,
         out[i:i + 1] = reference_port.attention_kvcache(
             q[i:i + 1].float(), kc.float(), vc.float(), cache_seqlens=sl[i:i + 1].clone(),
             block_table=bt[i:i + 1], softmax_scale=scale, causal=causal, window_left=window,
-            sinks=sinks, softcap=softcap).float()
+            sinks=sinks, softcap=softcap, alibi_slopes=alibi).float()
     return out
 
 
@@ -92,7 +103,8 @@ def run_case(device, seed: int, extended: bool):
     kc, vc = b.k_cache, b.v_cache
     if c["fp8"]:
         kc, vc = kc.to(FP8), vc.to(FP8)
-    extras = draw_extras(seed, hq) if extended else dict(window=-1, sinks=None, softcap=0.0)
+    extras = (draw_extras(seed, hq) if extended
+              else dict(window=-1, sinks=None, softcap=0.0, alibi=None))
     ref = expected(b.q, kc, vc, b.block_table, b.cache_seqlens, b.scale, c["causal"], **extras)
     kd, vd = kc.to(device), vc.to(device)
     if c["head_major"]:  # [pages, HKV, PS, HD] storage viewed as [pages, PS, HKV, HD]
@@ -107,12 +119,13 @@ def run_case(device, seed: int, extended: bool):
         obuf = torch.zeros(c["batch"], c["ql"], hq + 5, c["hd"], device=device, dtype=c["dtype"])
         out = obuf[:, :, 1:1 + hq]
     kw = {} if c["ns"] is None else dict(num_splits=c["ns"])
-    sinks = extras["sinks"]
+    sinks, alibi = extras["sinks"], extras["alibi"]
     got = native.paged_decode_split(q, kd, vd, b.block_table.to(device),
                                     b.cache_seqlens.to(device), b.scale, out=out,
                                     causal=c["causal"], window_left=extras["window"],
                                     sinks=None if sinks is None else sinks.to(device),
-                                    softcap=extras["softcap"], **kw)
+                                    softcap=extras["softcap"],
+                                    alibi_slopes=None if alibi is None else alibi.to(device), **kw)
     torch.cuda.synchronize()
     err = (got.float().cpu() - ref).abs().max().item()
     assert err <= TOL[c["dtype"]], (c, extras, err)
