@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define MXFA_ABI_VERSION 7
+#define MXFA_ABI_VERSION 8
 
 /* Return codes. */
 #define MXFA_OK 0
@@ -118,7 +118,11 @@ int mxfa_split_decode_launch(const void *q, int64_t q_stride_b, int64_t q_stride
  * Decode with q_len query tokens per sequence (1 <= q_len, q_len * HQ/HKV <=
  * 16), for speculative decoding: q and out are [B, q_len, HQ, HD] with strides
  * (stride_b, stride_t, stride_h, 1). Token t of sequence b sits at position
- * L_b - q_len + t, L_b = seqlens[b] + seqlen_add; with causal != 0 it attends
+ * L_b - q_len + t, L_b = seqlens[b] + seqlen_add; here seqlen_add may be
+ * negative (>= -2^30; an L_b below 0 counts as 0), so a caller can run the
+ * tokens [a, e) of a longer causal query as q_len = e - a tokens with
+ * seqlen_add lowered by (its q_len) - e: positions, masks and distances stay
+ * those of the whole query. With causal != 0 it attends
  * keys [0, L_b - q_len + t] (bottom-right aligned, as
  * mxflashattn/reference.py:31-35), else all L_b keys; a token with no key gets
  * zeros (the reference's nan_to_num). window_left >= 0 is a sliding window:

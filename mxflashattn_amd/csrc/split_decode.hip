@@ -53,6 +53,7 @@ struct SplitArgs {
   const float *sinks;  // per query head softmax sink logits, nullptr: none
   float softcap;       // logit soft-capping (0: none)
   const float *alibi;  // per query head ALiBi slopes, nullptr: none
+  int min_seqlen_add;  // 0, or -2^30 where lengths below zero count as 0
 };
 
 struct WsLayout {
@@ -72,7 +73,7 @@ static int check_split_args(const SplitArgs &a) {
   if (!a.q || !a.k || !a.v || !a.bt || !a.seqlens || !a.out) return MXFA_EINVAL;
   if (a.batch <= 0 || a.hq <= 0 || a.hkv <= 0 || a.btw <= 0 || a.num_pages <= 0)
     return MXFA_EINVAL;
-  if (a.num_splits <= 0 || a.seqlen_add < 0) return MXFA_EINVAL;
+  if (a.num_splits <= 0 || a.seqlen_add < a.min_seqlen_add) return MXFA_EINVAL;
   if (!(a.scale == a.scale) || a.scale == INFINITY || a.scale == -INFINITY) return MXFA_EINVAL;
   if (!supported_hd(a.hd)) return MXFA_EUNSUPPORTED;
   if (a.hq % a.hkv != 0) return MXFA_EUNSUPPORTED;
@@ -270,6 +271,7 @@ static SplitArgs split_args(const void *q, int64_t q_stride_b, int64_t q_stride_
   a.sinks = nullptr;
   a.softcap = 0.f;
   a.alibi = nullptr;
+  a.min_seqlen_add = 0;
   return a;
 }
 
@@ -428,6 +430,7 @@ int mxfa_split_decode_multi_launch(
   a.sinks = sinks;
   a.softcap = softcap;
   a.alibi = alibi_slopes;
+  a.min_seqlen_add = -(1 << 30);  // a window on the tokens before the cache end
   return run_split(a, true, (hipStream_t)stream);
 }
 

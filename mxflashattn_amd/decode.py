@@ -33,11 +33,13 @@ from .dispatch import DecodeRoute
 _ACCEL = {"cuda"}
 
 
-def _query_length_reason(q: torch.Tensor, kv_heads: int) -> str | None:
-    """q is [B, QL, HQ, D]: QL query tokens x GQ heads fill the kernel's columns."""
+def _query_length_reason(q: torch.Tensor, kv_heads: int, causal: bool) -> str | None:
+    """q is [B, QL, HQ, D]: QL query tokens x GQ heads fill the kernel's columns,
+    or, for a causal query, up to four launches of them (token chunks)."""
     ql, gq = q.shape[1], q.shape[-2] // kv_heads
-    if ql < 1 or ql * gq > native.KERNEL_COLUMNS:
-        return f"query_length_{ql}_times_gqa_{gq}_exceeds_{native.KERNEL_COLUMNS}"
+    limit = native.CHUNKED_COLUMNS if causal else native.KERNEL_COLUMNS
+    if ql < 1 or ql * gq > limit:
+        return f"query_length_{ql}_times_gqa_{gq}_exceeds_{limit}"
     return None
 
 
@@ -81,7 +83,7 @@ def _dense_table(batch: int, pages_per_seq: int, device: torch.device) -> torch.
 def route_kvcache(q, k_cache, v_cache, k, v, cache_seqlens, block_table, scale,
                   causal) -> DecodeRoute:
     reason = _common_reason(q, k_cache.shape[2], q.shape[-1]) or _query_length_reason(
-        q, k_cache.shape[2])
+        q, k_cache.shape[2], bool(causal))
     if reason is not None:
         return DecodeRoute(reason)
     if k_cache.stride(-1) != 1 or v_cache.stride() != k_cache.stride():
@@ -116,7 +118,8 @@ def route_kvcache(q, k_cache, v_cache, k, v, cache_seqlens, block_table, scale,
 
 
 def route_dense(q, k, v, scale, causal) -> DecodeRoute:
-    reason = _common_reason(q, k.shape[2], q.shape[-1]) or _query_length_reason(q, k.shape[2])
+    reason = _common_reason(q, k.shape[2], q.shape[-1]) or _query_length_reason(
+        q, k.shape[2], bool(causal))
     if reason is not None:
         return DecodeRoute(reason)
     kc, vc = _dense_as_pages(k), _dense_as_pages(v)

@@ -12,8 +12,8 @@ not a power of two. The caller then runs the original implementation.
 MXFA_WIDE_CONTRACT=1 widens the guards to what the kernels take: head dim 256,
 1..16 query heads per kv head, fp8 (e4m3fn) caches with per-tensor
 k_descale / v_descale (a scalar, or a tensor expanded from one), and q of
-[B, QL, HQ, D] with QL x GQ <= 16 (draft-token verification, with the call's
-causal flag). It also takes a sliding window, soft-capping and ALiBi slopes of
+[B, QL, HQ, D] (draft-token verification, with the call's causal flag; QL x
+GQ <= 16, or <= 64 for a causal query, which runs as up to four token chunks). It also takes a sliding window, soft-capping and ALiBi slopes of
 one per query head ([HQ]; a per-sequence [B, HQ] table is handed back).
 
 ``mx_kvcache_compat`` replaces ``_mx_kvcache_compat`` (:319-349): it drops
@@ -146,8 +146,9 @@ def _guard(args: tuple, kwargs: dict, wide: bool = False,
         return "head_dim", ()
     if hkv <= 0 or hq % hkv or hq // hkv not in gqa:
         return "gqa_ratio", ()
-    if q.dim() == 4 and q.shape[1] * (hq // hkv) > native.KERNEL_COLUMNS:
-        return "query_length", ()
+    columns = native.CHUNKED_COLUMNS if causal else native.KERNEL_COLUMNS
+    if q.dim() == 4 and q.shape[1] * (hq // hkv) > columns:
+        return "query_length", ()  # causal queries run as up to four token chunks
     ps = k_cache.shape[1]
     if ps <= 0 or ps & (ps - 1) or ps > 4096:
         return "page_size", ()

@@ -24,7 +24,7 @@ LIB_PATH = Path(
     os.environ.get("MXFLASHATTN_AMD_LIB")
     or Path(__file__).resolve().parent / "_lib" / "libmxfa_mi355x.so"
 )
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 MXFA_OK = 0
 MXFA_EUNSUPPORTED = -1
@@ -47,6 +47,9 @@ SUPPORTED_GQA = (2, 4, 8)
 KERNEL_HEAD_DIMS = (64, 128, 256)
 KERNEL_GQA = tuple(range(1, 17))
 KERNEL_COLUMNS = 16
+# Query tokens x GQ that the routing layers send here for a causal query: at
+# most four launches of token chunks, each reading its sequences' keys again.
+CHUNKED_COLUMNS = 4 * KERNEL_COLUMNS
 
 # Every entry point declared in include/mxfa_mi355x.h.
 EXPORTED_SYMBOLS = (
@@ -281,7 +284,8 @@ def _require_device(*tensors: torch.Tensor) -> torch.device:
     return device
 
 
-def check_decode_shapes(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
+def check_decode_shapes(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                        causal: bool = False) -> None:
     """Raise UnsupportedConfig when the kernel contract does not cover the call."""
     if q.dim() not in (3, 4) or (q.dim() == 4 and q.shape[1] < 1):
         raise UnsupportedConfig(f"q must be [B,QL,HQ,HD] or [B,HQ,HD], got {tuple(q.shape)}")
@@ -294,8 +298,9 @@ def check_decode_shapes(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
     if hkv <= 0 or hq % hkv or hq // hkv not in KERNEL_GQA:
         raise UnsupportedConfig(f"GQA ratio {hq}/{hkv} not in 1..16")
     ql = q.shape[1] if q.dim() == 4 else 1
-    if ql * (hq // hkv) > KERNEL_COLUMNS:
-        raise UnsupportedConfig(f"{ql} query tokens x GQA {hq // hkv} exceeds {KERNEL_COLUMNS}")
+    if ql * (hq // hkv) > KERNEL_COLUMNS and not causal:
+        raise UnsupportedConfig(f"{ql} query tokens x GQA {hq // hkv} exceeds {KERNEL_COLUMNS} "
+                                "(causal calls run in token chunks)")
     if q.dtype not in DTYPE_CODES:
         raise UnsupportedConfig("q must be float16 or bfloat16")
     if v_cache.dtype != k_cache.dtype or k_cache.dtype not in (q.dtype, FP8_DTYPE):
@@ -341,8 +346,20 @@ def _scale_ptr(scale, device: torch.device, name: str) -> int:
     return t.data_ptr()
 
 
-def _prepare(q, k_cache, v_cache, block_table, cache_seqlens, out):
-    check_decode_shapes(q, k_cache, v_cache)
+def token_chunks(q_len: int, per_launch: int, seqlen_add: int) -> list[tuple[int, int, int]]:
+    """(first, end, seqlen_add) of each launch of a causal query of q_len tokens
+    when one launch holds per_launch tokens. Tokens [first, end) run as the
+    last end - first tokens of sequences shortened by q_len - end keys, which
+    keeps each token's position, causal mask, window and ALiBi distances."""
+    out = []
+    for first in range(0, q_len, per_launch):
+        end = min(first + per_launch, q_len)
+        out.append((first, end, seqlen_add - (q_len - end)))
+    return out
+
+
+def _prepare(q, k_cache, v_cache, block_table, cache_seqlens, out, causal: bool = False):
+    check_decode_shapes(q, k_cache, v_cache, causal)
     batch = q.shape[0]
     hd = q.shape[-1]
     if q.stride(-1) != 1 or (q.shape[-2] > 1 and q.stride(-2) < hd) or (
@@ -431,7 +448,9 @@ def paged_decode_split(
 
     q: [B, QL, HQ, HD] or [B, HQ, HD] (any strides with a contiguous last dim);
     QL > 1 query tokens sit at the last QL positions of each sequence, and
-    ``causal`` masks the keys after each one (QL * HQ/HKV <= 16);
+    ``causal`` masks the keys after each one (QL * HQ/HKV <= 16 per launch; a
+    causal call with more runs as launches of 16 // (HQ/HKV) tokens, each
+    reading its sequences' keys again);
     caches: [pages, PS, HKV, HD] of q's dtype, or float8_e4m3fn with the
     per-tensor dequantisation scales k_scale / v_scale (float32 device scalars
     for graph capture); block_table: int32 [B, W]; cache_seqlens: int32 [B].
@@ -451,19 +470,24 @@ def paged_decode_split(
     if not (0.0 <= float(softcap) < float("inf")):
         raise ValueError(f"softcap must be finite and >= 0, got {softcap}")
     q, block_table, cache_seqlens, out = _prepare(q, k_cache, v_cache, block_table,
-                                                  cache_seqlens, out)
+                                                  cache_seqlens, out, bool(causal))
     lib = library()
     if num_splits is None:
         num_splits = default_num_splits(q, k_cache, block_table)
     stream = _stream_handle(q.device)
     ql = q.shape[1] if q.dim() == 4 else 1
-    ws_bytes = workspace_size(q.shape[0], q.shape[-2] * ql, q.shape[-1], num_splits)
+    per_launch = KERNEL_COLUMNS // (q.shape[-2] // k_cache.shape[2])
+    ws_bytes = workspace_size(q.shape[0], q.shape[-2] * min(ql, per_launch), q.shape[-1],
+                              num_splits)
     ws = WORKSPACE.get(q.device, stream, ws_bytes)
     if ql > 1 or window_left >= 0 or sinks is not None or softcap > 0 or (
             alibi_slopes is not None):
-        _launch_multi(q, k_cache, v_cache, block_table, cache_seqlens, out, ws.data_ptr(),
-                      ws_bytes, softmax_scale, num_splits, seqlen_add, stream, causal, k_scale,
-                      v_scale, window_left, sinks, softcap, alibi_slopes)
+        for first, end, add in token_chunks(ql, per_launch, int(seqlen_add)):
+            whole = first == 0 and end == ql
+            _launch_multi(q if whole else q[:, first:end], k_cache, v_cache, block_table,
+                          cache_seqlens, out if whole else out[:, first:end], ws.data_ptr(),
+                          ws_bytes, softmax_scale, num_splits, add, stream, causal, k_scale,
+                          v_scale, window_left, sinks, softcap, alibi_slopes)
         return out
     args = _launch_args(q, k_cache, v_cache, block_table, cache_seqlens, out, ws.data_ptr(),
                         ws_bytes, softmax_scale, num_splits, seqlen_add, stream)

@@ -273,6 +273,12 @@ def test_kvcache_route_declines_prefill_and_odd_pages():
     q = fake_cuda(torch.empty(4, 5, 32, 128, dtype=torch.bfloat16))
     assert decode.route_kvcache(q, cache, cache, None, None, None, torch.empty(4, 2), 0.1,
                                 False).reason.startswith("query_length_5_times_gqa_4")
+    # Causal: up to four launches of token chunks (64 columns), not a prefill.
+    assert decode.route_kvcache(q, cache, cache, None, None, None, torch.empty(4, 2), 0.1,
+                                True).reason is None
+    q17 = fake_cuda(torch.empty(4, 17, 32, 128, dtype=torch.bfloat16))
+    assert decode.route_kvcache(q17, cache, cache, None, None, None, torch.empty(4, 2), 0.1,
+                                True).reason.startswith("query_length_17_times_gqa_4_exceeds_64")
     q = fake_cuda(torch.empty(4, 2, 32, 128, dtype=torch.bfloat16))
     q16 = fake_cuda(torch.empty(4, 2, 32, 128, dtype=torch.bfloat16))
     cache2 = fake_cuda(torch.empty(10, 16, 2, 128, dtype=torch.bfloat16))  # GQ 16

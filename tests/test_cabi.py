@@ -218,6 +218,8 @@ def multi_args(**over):
     (dict(softcap=-1.0), -2), (dict(softcap=float("nan")), -2), (dict(softcap=float("inf")), -2),
     (dict(softcap=30.0, ws_bytes=1000), -3),
     (dict(alibi=FAKE + 1), -2), (dict(alibi=FAKE, ws_bytes=1000), -3),
+    (dict(seqlen_add=-(1 << 30) - 1), -2),                          # below the negative floor
+    (dict(seqlen_add=-(1 << 30), ws_bytes=1000), -3),               # a negative add is taken
 ])
 def test_multi_launch_rejects_before_launching(lib, over, code):
     assert lib.mxfa_split_decode_multi_launch(*multi_args(**over)) == code
@@ -317,6 +319,19 @@ def test_python_shape_contract(hq, hkv, hd, dtype, ps, match):
     cache = torch.zeros(4, ps, hkv, hd, dtype=dtype)
     with pytest.raises(native.UnsupportedConfig, match=match):
         native.check_decode_shapes(q, cache, cache)
+
+
+def test_causal_queries_past_sixteen_columns_run_in_token_chunks():
+    q = torch.zeros(2, 5, 16, 64, dtype=torch.bfloat16)   # 5 tokens x GQ 4 = 20 columns
+    cache = torch.zeros(4, 16, 4, 64, dtype=torch.bfloat16)
+    with pytest.raises(native.UnsupportedConfig, match="exceeds"):
+        native.check_decode_shapes(q, cache, cache)
+    native.check_decode_shapes(q, cache, cache, causal=True)
+    # 4 tokens per launch; each chunk ends where its sequences are cut.
+    assert native.token_chunks(5, 4, 0) == [(0, 4, -1), (4, 5, 0)]
+    assert native.token_chunks(7, 2, 3) == [(0, 2, -2), (2, 4, 0), (4, 6, 2), (6, 7, 3)]
+    assert native.token_chunks(3, 16, 0) == [(0, 3, 0)]
+    assert native.token_chunks(16, 1, 0)[0] == (0, 1, -15)
 
 
 @pytest.mark.parametrize("hq,hkv,hd,cache_dtype", [

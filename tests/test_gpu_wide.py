@@ -642,3 +642,85 @@ def test_alibi_slopes_are_checked_on_the_host(device):
         with pytest.raises(ValueError, match="alibi_slopes"):
             native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table,
                                       b.cache_seqlens, b.scale, alibi_slopes=bad)
+
+
+# ---------------------------------------------------------------------------
+# Causal queries past the 16 kernel columns: launches of token chunks.
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("ql,gq", [(5, 4), (8, 4), (3, 8), (4, 8), (2, 16), (3, 16), (9, 2),
+                                   (17, 1)])
+@pytest.mark.parametrize("extras", [False, True], ids=["plain", "extras"])
+def test_causal_queries_past_sixteen_columns(device, dtype, head_dim, ql, gq, extras):
+    # Lengths shorter than QL: a chunk whose sequences end before position 0
+    # sees no key, as the tokens of one launch would.
+    lengths = torch.tensor([1, 3, 6, 17, 300, 0, 1000])
+    b = make_paged_batch(7, 2 * gq, 2, head_dim, dtype, lengths, seed=130 + ql).to(device)
+    b = with_query_tokens(b, ql, 131)
+    window, cap, sinks, slopes = -1, 0.0, None, None
+    if extras:
+        window, cap = 40, 5.0
+        sinks, slopes = sink_values(2 * gq, device), alibi_slopes(2 * gq, device)
+    expected = port_expected(b, True, window, sinks, cap, slopes)
+    for ns in (None, 1, 9):
+        kw = {} if ns is None else dict(num_splits=ns)
+        got = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table,
+                                        b.cache_seqlens, b.scale, causal=True, window_left=window,
+                                        sinks=sinks, softcap=cap, alibi_slopes=slopes, **kw)
+        torch.cuda.synchronize()
+        assert torch.isfinite(got.float()).all()
+        assert max_err(got, expected) <= TOL[dtype], (ns, max_err(got, expected))
+        assert torch.equal(got[5].cpu(), torch.zeros_like(got[5].cpu()))
+
+
+def test_chunked_causal_query_fp8_strided_and_seqlen_add(device):
+    # 6 tokens x GQ 4 (two launches) on an fp8 cache, q and out as slices of
+    # wider buffers, lengths given as cache_seqlens + seqlen_add.
+    b = make_paged_batch(4, 8, 2, 128, torch.bfloat16, torch.tensor([3, 64, 500, 1200]),
+                         seed=133).to(device)
+    b = with_query_tokens(b, 6, 134)
+    k8, v8 = fp8_caches(b, device)
+    b8 = type(b)(b.q, k8.cpu().float().to(torch.bfloat16).to(device),
+                 v8.cpu().float().to(torch.bfloat16).to(device), b.block_table, b.cache_seqlens,
+                 b.scale)
+    expected = port_expected(b8, True)
+    wide = torch.randn(4, 6, 11, 128, device=device).to(torch.bfloat16)
+    wide[:, :, 2:10] = b.q
+    obuf = torch.zeros(4, 6, 13, 128, device=device, dtype=torch.bfloat16)
+    shorter = (b.cache_seqlens - 2).clamp_min(0).to(torch.int32)
+    got = native.paged_decode_split(wide[:, :, 2:10], k8, v8, b.block_table, shorter, b.scale,
+                                    out=obuf[:, :, 1:9], causal=True, seqlen_add=2)
+    torch.cuda.synchronize()
+    assert max_err(got, expected) <= TOL[torch.bfloat16]
+    assert torch.equal(obuf[:, :, :1].cpu(), torch.zeros_like(obuf[:, :, :1].cpu()))
+    assert torch.equal(obuf[:, :, 9:].cpu(), torch.zeros_like(obuf[:, :, 9:].cpu()))
+
+
+def test_chunked_causal_query_through_the_api(device):
+    """flash_attn_with_kvcache with five new tokens per sequence at GQ 4
+    (20 columns, two launches): append, causal decode, lengths advanced."""
+    import mxflashattn_amd as mx
+    from oracle import reference_port
+
+    b = make_paged_batch(3, 16, 4, 128, torch.bfloat16, torch.tensor([2, 90, 400]),
+                         block_table_width=40, seed=135)
+    g = torch.Generator().manual_seed(136)
+    q = torch.randn(3, 5, 16, 128, generator=g).to(torch.bfloat16)
+    k_new = torch.randn(3, 5, 4, 128, generator=g).to(torch.bfloat16)
+    v_new = torch.randn(3, 5, 4, 128, generator=g).to(torch.bfloat16)
+    kc, vc, sl = b.k_cache.clone(), b.v_cache.clone(), b.cache_seqlens.clone()
+    expected = reference_port.attention_kvcache(
+        q.float(), kc.float(), vc.float(), cache_seqlens=sl, block_table=b.block_table,
+        k=k_new.float(), v=v_new.float(), softmax_scale=b.scale, causal=True).float()
+    gpu = b.to(device)
+    lens = gpu.cache_seqlens.clone()
+    out = mx.flash_attn_with_kvcache(q.to(device), gpu.k_cache, gpu.v_cache, k=k_new.to(device),
+                                     v=v_new.to(device), cache_seqlens=lens,
+                                     block_table=gpu.block_table, softmax_scale=b.scale,
+                                     causal=True)
+    torch.cuda.synchronize()
+    assert mx.get_last_dispatch_info().backend == mx.BACKEND_MI355X
+    assert max_err(out, expected) <= TOL[torch.bfloat16]
+    assert lens.cpu().tolist() == (b.cache_seqlens + 5).tolist()

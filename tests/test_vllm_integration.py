@@ -324,7 +324,9 @@ def test_guard_wide_contract_opt_in(monkeypatch):
         return native_decode._guard((q,), kwargs, native_decode.wide_contract())[0]
 
     assert call_ql(4, 32, 8) == "device"       # 4 tokens x GQ 4 = 16 columns
-    assert call_ql(5, 32, 8) == "query_length"
+    assert call_ql(5, 32, 8) == "device"       # causal: two token chunks
+    assert call_ql(16, 32, 8) == "device"      # 64 columns, four chunks
+    assert call_ql(17, 32, 8) == "query_length"
     monkeypatch.delenv("MXFA_WIDE_CONTRACT")
     assert call_ql(2, 32, 8) == "query_length"  # the reference's guard
 
