@@ -205,6 +205,9 @@ WIDE = {
     # same KV bytes as one token.
     "wide_q4_config2": dict(batch=32, q_heads=32, kv_heads=8, head_dim=128,
                             dtype=torch.bfloat16, lengths=(1024, 8192), q_len=4, causal=True),
+    # Eight draft tokens at GQ 4: 32 columns, two launches of four tokens.
+    "wide_q8_config2": dict(batch=32, q_heads=32, kv_heads=8, head_dim=128,
+                            dtype=torch.bfloat16, lengths=(1024, 8192), q_len=8, causal=True),
     # Config 2 with a 1024-key sliding window (the local layers of models that
     # alternate local and global attention): each sequence reads its last
     # 1024 keys, 1/4.5 of the full call's bytes.
