@@ -724,3 +724,43 @@ def test_chunked_causal_query_through_the_api(device):
     assert mx.get_last_dispatch_info().backend == mx.BACKEND_MI355X
     assert max_err(out, expected) <= TOL[torch.bfloat16]
     assert lens.cpu().tolist() == (b.cache_seqlens + 5).tolist()
+
+
+def test_graph_replays_of_a_chunked_causal_query_follow_the_lengths(device):
+    # 6 tokens x GQ 4 (two launches) with ALiBi, captured once; between replays
+    # the lengths change in place, and every replay must match an eager call
+    # on the same lengths (each chunk reads them on the device).
+    # The table is as wide as the longest length here (1600); unused entries
+    # name page 0, which the port reads the same way.
+    b = make_paged_batch(4, 16, 4, 128, torch.bfloat16, torch.tensor([900, 5, 1600, 64]),
+                         seed=137).to(device)
+    b = with_query_tokens(b, 6, 138)
+    slopes = alibi_slopes(16, device)
+    lens = b.cache_seqlens.clone()
+    stream = torch.cuda.Stream(device)
+    out = torch.empty_like(b.q)
+
+    def call(target):
+        native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table, lens, b.scale,
+                                  out=target, causal=True, alibi_slopes=slopes)
+
+    with torch.cuda.stream(stream):
+        call(out)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        call(out)
+    for i, new in enumerate(([900, 5, 1600, 64], [3, 700, 1200, 17], [0, 6, 1, 1600])):
+        lens.copy_(torch.tensor(new, dtype=torch.int32))
+        torch.cuda.synchronize()
+        eager = torch.empty_like(out)
+        with torch.cuda.stream(stream):
+            call(eager)
+        out.fill_(float("nan"))
+        with torch.cuda.stream(stream):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), (i, new)
+        b.cache_seqlens = lens.clone()
+        assert max_err(out, port_expected(b, True, -1, None, 0.0, slopes)) \
+            <= TOL[torch.bfloat16], (i, new)
