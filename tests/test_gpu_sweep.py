@@ -8,7 +8,9 @@ the HIP result with the reference port (fp32; exactly dequantised caches for
 fp8) at the north-star tolerances. A second sweep adds a sliding window,
 attention sinks and/or soft-capping to every case (the extended kernel
 instantiation), and ALiBi slopes to about half of them (drawn from a stream of
-their own). Seeds are fixed: every run checks the same cases.
+their own). A third sweep redraws each case as a causal query of more than 16
+columns (QL x GQ up to 64: launches of token chunks), with the extras of the
+second sweep on half of them. Seeds are fixed: every run checks the same cases.
 """
 
 from __future__ import annotations
@@ -94,8 +96,23 @@ def test_random_extended_sweep(device, seed):
     run_case(device, seed, extended=True)
 
 
-def run_case(device, seed: int, extended: bool):
+@pytest.mark.parametrize("seed", range(300, 360))
+def test_random_chunked_sweep(device, seed):
+    run_case(device, seed, extended=seed % 2 == 0, chunked_query=True)
+
+
+def chunked(c: dict, seed: int) -> dict:
+    """The case as a causal query past the kernel's 16 columns (GQ >= 2)."""
+    r = random.Random(30_000 + seed)
+    gq = c["gq"] if c["gq"] >= 2 else r.choice([2, 4, 8])
+    ql = r.choice([q for q in range(16 // gq + 1, 64 // gq + 1)])
+    return dict(c, gq=gq, ql=ql, causal=True)
+
+
+def run_case(device, seed: int, extended: bool, chunked_query: bool = False):
     c = draw(seed)
+    if chunked_query:
+        c = chunked(c, seed)
     hq = c["hkv"] * c["gq"]
     b = make_paged_batch(c["batch"], hq, c["hkv"], c["hd"], c["dtype"],
                          torch.tensor(c["lengths"]), page_size=c["ps"], seed=1000 + seed,
@@ -119,6 +136,8 @@ def run_case(device, seed: int, extended: bool):
         obuf = torch.zeros(c["batch"], c["ql"], hq + 5, c["hd"], device=device, dtype=c["dtype"])
         out = obuf[:, :, 1:1 + hq]
     kw = {} if c["ns"] is None else dict(num_splits=c["ns"])
+    if chunked_query:
+        assert c["ql"] * c["gq"] > 16 and c["causal"]
     sinks, alibi = extras["sinks"], extras["alibi"]
     got = native.paged_decode_split(q, kd, vd, b.block_table.to(device),
                                     b.cache_seqlens.to(device), b.scale, out=out,
