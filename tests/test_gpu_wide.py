@@ -347,6 +347,26 @@ def test_dense_query_tokens_through_flash_attn_func(device, sq, sk, causal):
     assert max_err(out, expected) <= TOL[torch.float16]
 
 
+@pytest.mark.parametrize("sq,sk", [(5, 70), (9, 70), (16, 70), (9, 7)])
+def test_dense_causal_query_past_sixteen_columns_through_flash_attn_func(device, sq, sk):
+    """flash_attn_func, GQ 4, causal, 20 to 64 columns: token chunks on the HIP
+    kernels, bottom-right mask kept (sq > sk leaves the first rows empty)."""
+    import mxflashattn_amd as mx
+    from oracle import reference_port
+
+    g = torch.Generator().manual_seed(140 + sq)
+    q = torch.randn(3, sq, 8, 64, generator=g).to(torch.float16)
+    k = torch.randn(3, sk, 2, 64, generator=g).to(torch.float16)
+    v = torch.randn(3, sk, 2, 64, generator=g).to(torch.float16)
+    expected = reference_port.attention_batched(q.float(), k.float(), v.float(),
+                                                softmax_scale=0.125, causal=True).float()
+    out = mx.flash_attn_func(q.to(device), k.to(device), v.to(device), softmax_scale=0.125,
+                             causal=True)
+    torch.cuda.synchronize()
+    assert mx.get_last_dispatch_info().backend == mx.BACKEND_MI355X
+    assert max_err(out, expected) <= TOL[torch.float16]
+
+
 # ---------------------------------------------------------------------------
 # Sliding window (window_left): keys before position - window_left are dropped;
 # each sequence's tiles start at the first tile the window reaches.
