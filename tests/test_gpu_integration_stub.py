@@ -1,4 +1,4 @@
-"""The reference-side ctypes stub printed in INTEGRATION.md, run as written.
+"""The reference-side ctypes stub printed in the integration guide, run as written.
 
 The stub is what a maintainer would put in the reference's plugin in place of
 its mxmmain.so load (integrations/vllm/vllm_plugin.py:171-182,286-289). This
@@ -26,7 +26,7 @@ def _stub_source() -> str:
     text = DOC.read_text(encoding="utf-8")
     section = text[text.index("## 3."):]
     block = re.search(r"```python\n(.*?)```", section, re.S)
-    assert block, "INTEGRATION.md section 3 has no python block"
+    assert block, f"{DOC.name} section 3 has no python block"
     return block.group(1)
 
 
