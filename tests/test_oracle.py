@@ -594,3 +594,36 @@ def test_alibi_weights_of_a_zero_query_by_hand(causal):
             total = sum(w.values())
             for j in range(n):
                 assert out[t, h, j].item() == pytest.approx(w.get(j, 0.0) / total, abs=1e-6)
+
+
+@pytest.mark.parametrize("extras", [False, True])
+def test_token_chunks_of_a_causal_query_equal_the_whole_query(extras):
+    # The identity behind running a causal query past the kernel's 16 columns
+    # as several launches: rows [a, e) of the whole query equal a query of
+    # those tokens on sequences shortened by QL - e keys (lengths below the
+    # chunk's tokens leave rows without keys, zeros in both).
+    from mxflashattn_amd import native
+
+    ql, gq = 7, 4
+    b = make_paged_batch(4, 2 * gq, 2, 64, torch.float32, torch.tensor([3, 9, 40, 130]),
+                         seed=151, q_len=ql)
+    kw = dict(block_table=b.block_table, softmax_scale=b.scale, causal=True)
+    if extras:
+        kw.update(window_left=5, softcap=2.0, sinks=torch.linspace(-1.0, 1.0, 2 * gq),
+                  alibi_slopes=torch.pow(2.0, -torch.arange(1, 2 * gq + 1, dtype=torch.float32)))
+    rows = []
+    for i in range(b.batch):
+        lens = b.cache_seqlens[i:i + 1]
+        one = dict(kw, block_table=b.block_table[i:i + 1])
+        whole = reference_port.attention_kvcache(b.q[i:i + 1], b.k_cache, b.v_cache,
+                                                 cache_seqlens=lens.clone(), **one)
+        for first, end, add in native.token_chunks(ql, 16 // gq, 0):
+            short = (lens + add).clamp_min(0)
+            if int(short) == 0:  # no key for any of these tokens
+                assert torch.all(whole[:, first:end] == 0), (i, first)
+                continue
+            part = reference_port.attention_kvcache(b.q[i:i + 1, first:end], b.k_cache,
+                                                    b.v_cache, cache_seqlens=short.clone(), **one)
+            torch.testing.assert_close(part, whole[:, first:end], rtol=1e-5, atol=1e-6)
+            rows.append((i, first))
+    assert len(rows) >= 6
