@@ -144,8 +144,8 @@ def flash_attn_varlen_func(
             "deterministic": deterministic,
             "return_attn_probs": return_attn_probs,
         },
-        decode_route=decode.route_varlen(q, k, v, q_offsets, k_offsets, max_seqlen_k, scale,
-                                         causal),
+        decode_route=decode.route_varlen(q, k, v, cu_seqlens_k, q_offsets, k_offsets,
+                                         max_seqlen_k, scale, causal),
     )
 
 
@@ -165,9 +165,16 @@ def flash_attn_with_kvcache(
     rotary_cos: torch.Tensor | None = None,
     rotary_sin: torch.Tensor | None = None,
     return_softmax_lse: bool = False,
+    *,
+    out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Decode against a dense [B, S, HKV, D] or paged [P, PS, HKV, D] cache, with
-    optional append of k/v (advances cache_seqlens in place). mxflashattn/api.py:151-286."""
+    optional append of k/v (advances cache_seqlens in place). mxflashattn/api.py:151-286.
+
+    ``out`` (keyword only; not in the reference's signature, as in vLLM's
+    FlashAttention fork) is a tensor of q's shape, dtype and device that
+    receives the result and is returned; the MI355X route writes into it
+    directly, other backends copy their result into it."""
     validate_softmax_scale(softmax_scale)
     if rotary_cos is not None or rotary_sin is not None:
         raise NotImplementedError("rotary embeddings are not supported")
@@ -222,6 +229,13 @@ def flash_attn_with_kvcache(
             raise ValueError("block_table must be on the same device as q")
     elif k_cache.shape[0] != q.shape[0]:
         raise ValueError("dense cache batch dimension must match q")
+    if out is not None:
+        if not isinstance(out, torch.Tensor):
+            raise TypeError("out must be a torch.Tensor")
+        if out.shape != q.shape or out.dtype != q.dtype or out.device != q.device:
+            raise ValueError("out must match q's shape, dtype and device")
+        if out.stride(-1) != 1:
+            raise ValueError("out must have a contiguous last dimension")
 
     # Checks that read cache_seqlens / block_table back to the host cost a
     # device synchronisation per call; they run only when asked for
@@ -230,7 +244,7 @@ def flash_attn_with_kvcache(
         _strict_checks(k_cache, k, cache_seqlens, block_table)
 
     scale = _resolved_scale(q.shape[-1], softmax_scale)
-    return dispatch(
+    result = dispatch(
         "flash_attn_with_kvcache",
         q,
         (q, k_cache, v_cache, k, v, cache_seqlens, block_table, scale, causal),
@@ -251,8 +265,12 @@ def flash_attn_with_kvcache(
             "alibi_slopes": alibi_slopes,
         },
         decode_route=decode.route_kvcache(q, k_cache, v_cache, k, v, cache_seqlens, block_table,
-                                          scale, causal),
+                                          scale, causal, out=out),
     )
+    if out is not None and result is not out:
+        out.copy_(result)
+        return out
+    return result
 
 
 def _strict_checks(k_cache, k, cache_seqlens, block_table) -> None:

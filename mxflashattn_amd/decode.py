@@ -81,7 +81,9 @@ def _dense_table(batch: int, pages_per_seq: int, device: torch.device) -> torch.
 
 
 def route_kvcache(q, k_cache, v_cache, k, v, cache_seqlens, block_table, scale,
-                  causal) -> DecodeRoute:
+                  causal, out: torch.Tensor | None = None) -> DecodeRoute:
+    """``out`` (q's shape and dtype, last dim contiguous) receives the result
+    in place; otherwise the run allocates it."""
     reason = _common_reason(q, k_cache.shape[2], q.shape[-1]) or _query_length_reason(
         q, k_cache.shape[2], bool(causal))
     if reason is not None:
@@ -92,11 +94,16 @@ def route_kvcache(q, k_cache, v_cache, k, v, cache_seqlens, block_table, scale,
         kc, vc = _dense_as_pages(k_cache), _dense_as_pages(v_cache)
         if kc is None or vc is None:
             return DecodeRoute("dense_cache_not_viewable_as_pages")
+        width = kc.shape[0] // q.shape[0]
     else:
         ps = k_cache.shape[1]
         if ps & (ps - 1) or ps > 4096:
             return DecodeRoute(f"page_size_{ps}_not_a_power_of_two_up_to_4096")
         kc, vc = k_cache, v_cache
+        width = block_table.shape[1]
+    reason = native.layout_reason(q, kc, vc, width)
+    if reason is not None:
+        return DecodeRoute(reason)
     if k is not None and (k.stride(-1) != 1 or v.stride(-1) != 1):
         k, v = k.contiguous(), v.contiguous()
 
@@ -108,11 +115,11 @@ def route_kvcache(q, k_cache, v_cache, k, v, cache_seqlens, block_table, scale,
         new = 0 if k is None else k.shape[1]
         if new:
             native.append_kv(k, v, kc, vc, table, cache_seqlens)
-        out = native.paged_decode_split(q, kc, vc, table, cache_seqlens, scale, seqlen_add=new,
-                                        causal=causal)
+        result = native.paged_decode_split(q, kc, vc, table, cache_seqlens, scale,
+                                           seqlen_add=new, causal=causal, out=out)
         if new:
             cache_seqlens.add_(new)
-        return out
+        return result
 
     return DecodeRoute(None, run)
 
@@ -125,6 +132,9 @@ def route_dense(q, k, v, scale, causal) -> DecodeRoute:
     kc, vc = _dense_as_pages(k), _dense_as_pages(v)
     if kc is None or vc is None or kc.stride(-1) != 1 or vc.stride() != kc.stride():
         return DecodeRoute("dense_kv_not_viewable_as_pages")
+    reason = native.layout_reason(q, kc, vc, kc.shape[0] // q.shape[0])
+    if reason is not None:
+        return DecodeRoute(reason)
 
     def run() -> torch.Tensor:
         batch = q.shape[0]
@@ -135,8 +145,12 @@ def route_dense(q, k, v, scale, causal) -> DecodeRoute:
     return DecodeRoute(None, run)
 
 
-def route_varlen(q, k, v, q_offsets: list[int], k_offsets: list[int], max_seqlen_k: int, scale,
-                 causal) -> DecodeRoute:
+def route_varlen(q, k, v, cu_seqlens_k: torch.Tensor, q_offsets: list[int], k_offsets: list[int],
+                 max_seqlen_k: int, scale, causal) -> DecodeRoute:
+    """Packed decode: sequence b's keys are rows [cu_k[b], cu_k[b+1]) of k/v,
+    read in place as one-token pages. The block table and lengths are built
+    on the device from ``cu_seqlens_k`` (no host-to-device copy) when every
+    sequence has its query row, the usual decode batch."""
     reason = _common_reason(q, k.shape[1], q.shape[-1])
     if reason is not None:
         return DecodeRoute(reason)
@@ -147,22 +161,29 @@ def route_varlen(q, k, v, q_offsets: list[int], k_offsets: list[int], max_seqlen
         return DecodeRoute("kv_layout_not_supported")
     # Sequences with a query row, in row order.
     rows = [i for i, n in enumerate(q_lens) if n == 1]
+    if not rows:
+        return DecodeRoute("varlen_without_query_rows")
+    kc = k.unsqueeze(1)  # [T, 1, HKV, D]: one token per page
+    vc = v.unsqueeze(1)
+    # Table width from the offsets themselves: a max_seqlen_k smaller than a
+    # sequence would otherwise cut that sequence short.
+    width = max(1, max(k_offsets[i + 1] - k_offsets[i] for i in rows))
+    reason = native.layout_reason(q.unsqueeze(1), kc, vc, width)
+    if reason is not None:
+        return DecodeRoute(reason)
 
     def run() -> torch.Tensor:
         device = q.device
-        starts = torch.tensor([k_offsets[i] for i in rows], dtype=torch.int32, device=device)
-        lengths = torch.tensor([k_offsets[i + 1] - k_offsets[i] for i in rows],
-                               dtype=torch.int32, device=device)
-        # Table width from the offsets themselves: a max_seqlen_k smaller than a
-        # sequence would otherwise cut that sequence short.
-        width = max(1, max(k_offsets[i + 1] - k_offsets[i] for i in rows))
+        cu = cu_seqlens_k.to(torch.int32)
+        starts, lengths = cu[:-1], cu[1:] - cu[:-1]
+        if len(rows) != len(q_lens):
+            pick = torch.as_tensor(rows, dtype=torch.int64).pin_memory().to(device,
+                                                                          non_blocking=True)
+            starts, lengths = starts.index_select(0, pick), lengths.index_select(0, pick)
         table = starts.unsqueeze(1) + torch.arange(width, dtype=torch.int32,
                                                    device=device).unsqueeze(0)
-        kc = k.unsqueeze(1)  # [T, 1, HKV, D]: one token per page
-        vc = v.unsqueeze(1)
-        out = native.paged_decode_split(q.unsqueeze(1), kc, vc, table, lengths, scale)
+        out = native.paged_decode_split(q.unsqueeze(1), kc, vc, table, lengths.contiguous(),
+                                        scale)
         return out.squeeze(1)
 
-    if not rows:
-        return DecodeRoute("varlen_without_query_rows")
     return DecodeRoute(None, run)

@@ -127,12 +127,30 @@ def _int32_on(t: torch.Tensor, device: torch.device) -> torch.Tensor:
     return t.to(device=device, dtype=torch.int32)
 
 
+def _rows_out(out: torch.Tensor | None, q: torch.Tensor) -> torch.Tensor | None:
+    """The first rows of vLLM's output buffer ([tokens, heads*dim] or
+    [tokens, heads, dim]) viewed as q's [B, QL, HQ, D], or None when they
+    cannot be viewed so (the result is then copied)."""
+    if out is None or out.dtype != q.dtype or out.device != q.device:
+        return None
+    rows = q.shape[0] * q.shape[1]
+    if out.shape[0] < rows or out[0].numel() != q.shape[2] * q.shape[3]:
+        return None
+    try:
+        return out[:rows].view(q.shape)
+    except RuntimeError:
+        return None
+
+
 def decode_forward(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: Any, *,
-                   softmax_scale: float, causal: bool = True) -> tuple[torch.Tensor, Any]:
+                   softmax_scale: float, causal: bool = True,
+                   out: torch.Tensor | None = None) -> tuple[torch.Tensor, Any]:
     """Run one-token paged decode; returns ([tokens, heads*dim], layout or None).
 
     vLLM writes the new token into the cache before attention, so k/v are
-    omitted and seq_lens describes the populated cache.
+    omitted and seq_lens describes the populated cache. ``out`` (vLLM's output
+    buffer) receives the result in place when its rows can be viewed as the
+    query; the returned tensor is then a view of it.
     """
     if os.getenv("MXFLASHATTN_GRAPH_DECODE", "0") == "1":
         _no_cascade(attn_metadata)
@@ -152,7 +170,7 @@ def decode_forward(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: A
         if mql != 1 and not has_padded_decode and not has_split_decode:
             raise DecoderAdapterBlocked(f"only_single_token_decode_supported:max_query_len={mql}")
         return _decode_forward_graph(query, kv_cache, attn_metadata,
-                                     softmax_scale=softmax_scale, causal=causal)
+                                     softmax_scale=softmax_scale, causal=causal, out=out)
     if _transparent_enabled():
         _no_cascade(attn_metadata)
         if int(attn_metadata.max_query_len) != 1:
@@ -167,7 +185,7 @@ def decode_forward(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: A
         block_table = _int32_on(attn_metadata.block_table, query.device)
         result = flash_attn_with_kvcache(q, key_cache, value_cache, cache_seqlens=cache_seqlens,
                                          block_table=block_table, softmax_scale=softmax_scale,
-                                         causal=causal)
+                                         causal=causal, **_out_kw(out, q))
         return result.reshape(n, -1), None
     layout = (inspect_layout(query, kv_cache, attn_metadata) if STRICT_LAYOUT
               else fast_layout(query, kv_cache, attn_metadata))
@@ -189,13 +207,19 @@ def decode_forward(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: A
         q, key_cache, value_cache,
         cache_seqlens=_int32_on(attn_metadata.seq_lens, query.device),
         block_table=_int32_on(attn_metadata.block_table, query.device),
-        softmax_scale=softmax_scale, causal=causal,
+        softmax_scale=softmax_scale, causal=causal, **_out_kw(out, q),
     )
     return result.reshape(layout.num_actual_tokens, -1), layout
 
 
+def _out_kw(out: torch.Tensor | None, q: torch.Tensor) -> dict:
+    view = _rows_out(out, q)
+    return {} if view is None else {"out": view}
+
+
 def _decode_forward_graph(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: Any, *,
-                          softmax_scale: float, causal: bool = True):
+                          softmax_scale: float, causal: bool = True,
+                          out: torch.Tensor | None = None):
     """Static-shape (graph) decode: prefer the split decode metadata when present,
     else one query row per metadata row (capture padding stays out of the call)."""
     key_cache, value_cache = kv_cache.unbind(0)
@@ -224,6 +248,7 @@ def _decode_forward_graph(query: torch.Tensor, kv_cache: torch.Tensor, attn_meta
     result = flash_attn_with_kvcache(
         q, key_cache, value_cache, cache_seqlens=cache_seqlens.contiguous(),
         block_table=block_table.contiguous(), softmax_scale=softmax_scale, causal=causal,
+        **_out_kw(out, q),
     )
     return result.reshape(q.shape[0] * q.shape[1], -1), None
 
@@ -291,7 +316,7 @@ def forward_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: A
         return _native_decode(query, kv_cache, attn_metadata, output, softmax_scale, k_scale,
                               v_scale, fp8, window_left, sinks, softcap, alibi_slopes)
     result, _ = decode_forward(query, kv_cache, attn_metadata, softmax_scale=softmax_scale,
-                               causal=bool(attn_metadata.causal))
+                               causal=bool(attn_metadata.causal), out=output)
     info = get_last_dispatch_info()
     if info is None:
         raise RuntimeError("MXFlashAttn decoder returned without dispatch evidence")
@@ -302,7 +327,8 @@ def forward_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: A
         raise RuntimeError(
             f"MXFlashAttn decoder output size mismatch: target={tuple(target.shape)} "
             f"result={tuple(result.shape)}")
-    target.copy_(result.reshape_as(target))
+    if result.data_ptr() != target.data_ptr():  # not written in place
+        target.copy_(result.reshape_as(target))
     return output
 
 

@@ -209,10 +209,18 @@ class _Workspace:
 
     A launch on one stream never shares its workspace with another stream's
     launches, so calls on different streams cannot race on it.
+
+    A HIP graph captured on a stream keeps the workspace address of the
+    capture in its kernel arguments. When a later call needs a larger buffer,
+    the smaller one is therefore never released: it moves to a keep-alive list
+    for the life of the process, so replays of earlier captures still write
+    into memory that nothing else owns. Growth doubles, so the retired buffers
+    together stay smaller than the live one.
     """
 
     def __init__(self) -> None:
         self._buffers: dict[tuple[int, int], torch.Tensor] = {}
+        self._retired: list[torch.Tensor] = []
         self._lock = threading.Lock()
 
     def get(self, device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
@@ -223,13 +231,14 @@ class _Workspace:
                 size = max(nbytes, 1 << 20)
                 if buf is not None:
                     size = max(size, buf.numel() * 2)
+                    self._retired.append(buf)
                 buf = torch.empty(size, dtype=torch.uint8, device=device)
                 self._buffers[key] = buf
             return buf
 
-    def clear(self) -> None:
+    def retired_bytes(self) -> int:
         with self._lock:
-            self._buffers.clear()
+            return sum(t.numel() for t in self._retired)
 
 
 WORKSPACE = _Workspace()
@@ -310,6 +319,45 @@ def check_decode_shapes(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
         raise UnsupportedConfig(f"page size {ps} is not a power of two <= 4096")
 
 
+# Limits of the C ABI (csrc/split_decode.hip check_split_args): sequences per
+# launch (the tile prefix sums live in LDS), keys per table row, and the
+# 16-byte alignment of the cache fragments.
+MAX_BATCH = 16000
+MAX_KV_HEADS = 65535
+MAX_TABLE_KEYS = 1 << 30
+
+
+def layout_reason(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                  block_table_width: int) -> str | None:
+    """Why the kernels cannot take these tensors as laid out, or None.
+
+    Reads shapes, strides and addresses only (never device data). q itself is
+    copied when its layout does not suit the kernel, so only the caches and
+    the sizes matter here."""
+    batch, hd = q.shape[0], q.shape[-1]
+    ps, hkv = k_cache.shape[1], k_cache.shape[2]
+    esz = k_cache.element_size()
+    if batch > MAX_BATCH:
+        return f"batch_{batch}_exceeds_{MAX_BATCH}"
+    if hkv > MAX_KV_HEADS:
+        return f"kv_heads_{hkv}_exceeds_{MAX_KV_HEADS}"
+    max_len = block_table_width * ps
+    if max_len > MAX_TABLE_KEYS or batch * ((max_len + 15) // 16) >= 1 << 31:
+        return "block_table_capacity_exceeds_kernel_limit"
+    if k_cache.stride(-1) != 1 or v_cache.stride() != k_cache.stride():
+        return "cache_layout_not_supported"
+    if k_cache.data_ptr() % 16 or v_cache.data_ptr() % 16:
+        return "cache_not_16_byte_aligned"
+    sp, st, sh = k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)
+    if min(sp, st, sh) < 0 or any((s * esz) % 16 for s in (sp, st, sh)):
+        return "cache_strides_not_multiples_of_16_bytes"
+    if ps > 1 and st < hd:
+        return "cache_token_rows_overlap"
+    if (15 * st + hd) * esz >= 1 << 30 or (ps - 1) * st * esz >= 1 << 32 or sh * esz >= 1 << 32:
+        return "cache_strides_exceed_kernel_limit"
+    return None
+
+
 def _launch_args(q, k_cache, v_cache, block_table, cache_seqlens, out, workspace, ws_bytes,
                  softmax_scale, num_splits, seqlen_add, stream=None):
     batch, hq, hd = q.shape[0], q.shape[-2], q.shape[-1]
@@ -324,7 +372,40 @@ def _launch_args(q, k_cache, v_cache, block_table, cache_seqlens, out, workspace
     )
 
 
-_SCALARS: dict[tuple[int, float], torch.Tensor] = {}
+class _ScalarCache:
+    """Device float32 scalars for scales passed as Python floats.
+
+    Each is made by a fill kernel on the current stream (no host-to-device
+    copy and no synchronisation) and kept for the life of the process, since
+    a captured graph holds its address. A value first seen while the stream is
+    capturing is refused: a fill recorded into a graph runs only at replay,
+    so eager calls would read the scalar before it exists. At most ``limit``
+    distinct values are kept per device; past that, float scales are refused
+    with a clear error (pass a float32 device tensor instead).
+    """
+
+    def __init__(self, limit: int = 64) -> None:
+        self.limit = limit
+        self._values: dict[tuple[int, float], torch.Tensor] = {}
+        self._lock = threading.Lock()
+
+    def ptr(self, value: float, device: torch.device, name: str) -> int:
+        key = (device.index or 0, value)
+        with self._lock:
+            t = self._values.get(key)
+            if t is None:
+                if torch.cuda.is_current_stream_capturing():
+                    raise ValueError(f"{name}={value} is first used inside graph capture; pass "
+                                     "a float32 device tensor, or make one eager call first")
+                if sum(1 for k in self._values if k[0] == key[0]) >= self.limit:
+                    raise ValueError(f"{name}: more than {self.limit} distinct float scales on "
+                                     f"{device}; pass a float32 device tensor")
+                t = self._values[key] = torch.full((1,), value, dtype=torch.float32,
+                                                   device=device)
+            return t.data_ptr()
+
+
+_SCALARS = _ScalarCache()
 
 
 def _scale_ptr(scale, device: torch.device, name: str) -> int:
@@ -339,11 +420,7 @@ def _scale_ptr(scale, device: torch.device, name: str) -> int:
         if scale.numel() != 1 and any(st != 0 for st in scale.stride()):
             raise UnsupportedConfig(f"{name} must be one per-tensor scale")
         return scale.data_ptr()
-    key = (device.index or 0, float(scale))
-    t = _SCALARS.get(key)
-    if t is None:
-        t = _SCALARS[key] = torch.tensor([float(scale)], dtype=torch.float32, device=device)
-    return t.data_ptr()
+    return _SCALARS.ptr(float(scale), device, name)
 
 
 def token_chunks(q_len: int, per_launch: int, seqlen_add: int) -> list[tuple[int, int, int]]:
@@ -363,8 +440,11 @@ def _prepare(q, k_cache, v_cache, block_table, cache_seqlens, out, causal: bool 
     batch = q.shape[0]
     hd = q.shape[-1]
     if q.stride(-1) != 1 or (q.shape[-2] > 1 and q.stride(-2) < hd) or (
-            q.dim() == 4 and q.shape[1] > 1 and q.stride(1) % 8):
-        q = q.contiguous()
+            q.dim() == 4 and q.shape[1] > 1 and q.stride(1) % 8) or q.data_ptr() % 16 or (
+            any(s % 8 for s in q.stride()[:-1])):
+        # The kernel reads q in 16-byte fragments: 16-byte aligned, strides
+        # in multiples of 8 elements. A packed copy always is.
+        q = q.clone(memory_format=torch.contiguous_format)
     if k_cache.stride(-1) != 1 or v_cache.stride() != k_cache.stride():
         raise UnsupportedConfig("k_cache and v_cache must share strides with a contiguous last dim")
     if k_cache.shape[1] > 1 and k_cache.stride(1) < hd:
@@ -465,6 +545,16 @@ def paged_decode_split(
     query at position p and key j, after the cap.
     num_splits: balanced work ranges per kv head (default: split_heuristic).
     """
+    if out is not None and (out.data_ptr() % 8 or any(st % 4 for st in out.stride()[:-1])):
+        # The kernels store 8-byte pieces of each output row; a view that is
+        # not laid out for that gets the result through a packed copy.
+        final = out
+        result = paged_decode_split(
+            q, k_cache, v_cache, block_table, cache_seqlens, softmax_scale,
+            num_splits=num_splits, seqlen_add=seqlen_add, k_scale=k_scale, v_scale=v_scale,
+            causal=causal, window_left=window_left, sinks=sinks, softcap=softcap,
+            alibi_slopes=alibi_slopes)
+        return final.copy_(result)
     if int(window_left) < -1:
         raise ValueError(f"window_left must be >= -1, got {window_left}")
     if not (0.0 <= float(softcap) < float("inf")):

@@ -312,6 +312,6 @@ def test_dense_cache_page_view(seq, page):
 def test_varlen_route_declines_multi_token_queries():
     q = fake_cuda(torch.empty(3, 8, 64, dtype=torch.float16))
     k = fake_cuda(torch.empty(5, 2, 64, dtype=torch.float16))
-    assert decode.route_varlen(q, k, k, [0, 2, 3], [0, 3, 5], 3, 0.1,
+    assert decode.route_varlen(q, k, k, k, [0, 2, 3], [0, 3, 5], 3, 0.1,
                                False).reason == "varlen_query_length_above_one"
-    assert decode.route_varlen(q, k, k, [0, 1, 2, 3], [0, 1, 3, 5], 3, 0.1, False).reason is None
+    assert decode.route_varlen(q, k, k, k, [0, 1, 2, 3], [0, 1, 3, 5], 3, 0.1, False).reason is None

@@ -16,6 +16,11 @@ checks that a plausible mistake would fail:
       on independently gathered K/V, per query head against kv head h // GQ
     - GQA mapping: kv heads with constant, distinct V rows give every query head
       exactly its group's constant
+  reference_port.attention_varlen
+    - each packed segment, an empty-query segment among them, equals float64
+      library attention over that segment's keys with an independently built
+      bottom-right causal mask (rows that see no key are zeros); moving a
+      segment boundary by one key changes the result
   c_oracle.paged_decode_f64
     - agreement with reference_port (fp32) and with a float64 SDPA
     - a peaked query (q = 40 * k_j) returns V_j
@@ -627,3 +632,56 @@ def test_token_chunks_of_a_causal_query_equal_the_whole_query(extras):
             torch.testing.assert_close(part, whole[:, first:end], rtol=1e-5, atol=1e-6)
             rows.append((i, first))
     assert len(rows) >= 6
+
+
+def varlen_library(q, k, v, cu_q, cu_k, scale, causal):
+    """Per segment: float64 library attention with a mask built from positions
+    (query i of a segment sits at key position i + Lk - Lq); rows that see no
+    key are zeros."""
+    rows = []
+    for i in range(len(cu_q) - 1):
+        qs, ks = q[cu_q[i]:cu_q[i + 1]], k[cu_k[i]:cu_k[i + 1]]
+        vs = v[cu_k[i]:cu_k[i + 1]]
+        lq, lk = qs.shape[0], ks.shape[0]
+        if lq == 0:
+            continue
+        group = qs.shape[1] // ks.shape[1]
+        qh = qs.double().permute(1, 0, 2).unsqueeze(0)
+        kh = ks.double().repeat_interleave(group, dim=1).permute(1, 0, 2).unsqueeze(0)
+        vh = vs.double().repeat_interleave(group, dim=1).permute(1, 0, 2).unsqueeze(0)
+        allowed = torch.ones(lq, lk, dtype=torch.bool)
+        if causal:
+            pos = torch.arange(lq).unsqueeze(1) + (lk - lq)
+            allowed = torch.arange(lk).unsqueeze(0) <= pos
+        o = F.scaled_dot_product_attention(qh, kh, vh, attn_mask=allowed, scale=scale)
+        o = torch.nan_to_num(o, nan=0.0)[0].permute(1, 0, 2)
+        o[~allowed.any(dim=1)] = 0.0
+        rows.append(o)
+    return torch.cat(rows, dim=0)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_varlen_port_matches_library_attention_per_segment(causal):
+    torch.manual_seed(17)
+    cu_q = [0, 2, 2, 3, 7]     # segment 1 has no query row
+    cu_k = [0, 3, 7, 8, 10]    # segment 3: four queries over two keys
+    q = torch.randn(7, 4, 64)
+    k = torch.randn(10, 2, 64)
+    v = torch.randn(10, 2, 64)
+    out = reference_port.attention_varlen(q, k, v, cu_q, cu_k, softmax_scale=0.3, causal=causal)
+    assert out.shape == q.shape
+    expected = varlen_library(q, k, v, cu_q, cu_k, 0.3, causal)
+    torch.testing.assert_close(out.double(), expected, atol=1e-5, rtol=1e-5)
+    if causal:  # the first two queries of segment 3 see no key
+        assert torch.equal(out[3:5], torch.zeros_like(out[3:5]))
+
+
+def test_varlen_port_segment_boundaries_matter():
+    torch.manual_seed(18)
+    cu_q, cu_k = [0, 1, 2], [0, 5, 9]
+    q, k, v = torch.randn(2, 2, 64), torch.randn(9, 1, 64), torch.randn(9, 1, 64)
+    out = reference_port.attention_varlen(q, k, v, cu_q, cu_k)
+    shifted = reference_port.attention_varlen(q, k, v, cu_q, [0, 4, 9])
+    assert not torch.allclose(out[0], shifted[0]) and not torch.allclose(out[1], shifted[1])
+    torch.testing.assert_close(out.double(), varlen_library(q, k, v, cu_q, cu_k, 64 ** -0.5,
+                                                            False), atol=1e-5, rtol=1e-5)
