@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define MXFA_ABI_VERSION 8
+#define MXFA_ABI_VERSION 9
 
 /* Return codes. */
 #define MXFA_OK 0
@@ -42,6 +42,7 @@ extern "C" {
 #define MXFA_EINVAL (-2)       /* null pointer, non-positive size, misaligned pointer or stride */
 #define MXFA_EWORKSPACE (-3)   /* workspace missing or smaller than mxfa_split_decode_workspace_size */
 #define MXFA_ELAUNCH (-4)      /* the HIP runtime rejected a kernel launch */
+#define MXFA_ESCRATCH (-5)     /* the call needs more than MXFA_SCRATCH_BYTES (no-allocation entry point) */
 
 /* Element types. */
 #define MXFA_DTYPE_F16 0
@@ -113,6 +114,31 @@ int mxfa_split_decode_launch(const void *q, int64_t q_stride_b, int64_t q_stride
                              int q_heads, int kv_heads, int head_dim, int page_size,
                              int block_table_width, int num_pages, int dtype, int num_splits,
                              void *stream);
+
+/*
+ * mxfa_split_decode_launch without the workspace arguments, for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * and harnesses that forbid hipMalloc). No reference counterpart.
+ *
+ * The workspace is the library's own device array of MXFA_SCRATCH_BYTES, one
+ * per GPU, held until the process ends; calls needing more
+ * (mxfa_split_decode_workspace_size > MXFA_SCRATCH_BYTES) return
+ * MXFA_ESCRATCH. Nothing in it must start at zero (every byte a call reads was
+ * written earlier in that call). Every call on one GPU shares that GPU's
+ * array: calls that overlap in time on one GPU (different streams) race and
+ * give wrong results; serialise them on one stream. Same arguments, kernels
+ * and results as mxfa_split_decode_launch otherwise.
+ */
+#define MXFA_SCRATCH_BYTES ((size_t)8 << 20)
+int mxfa_split_decode_noalloc_launch(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                                     const void *k_cache, const void *v_cache,
+                                     int64_t cache_stride_page, int64_t cache_stride_token,
+                                     int64_t cache_stride_head, const int32_t *block_table,
+                                     int64_t bt_stride, const int32_t *seqlens, int seqlen_add,
+                                     void *out, int64_t out_stride_b, int64_t out_stride_h,
+                                     float scale, int batch, int q_heads, int kv_heads,
+                                     int head_dim, int page_size, int block_table_width,
+                                     int num_pages, int dtype, int num_splits, void *stream);
 
 /*
  * Decode with q_len query tokens per sequence (1 <= q_len, q_len * HQ/HKV <=

@@ -8,9 +8,36 @@
 // workspace allocation (csrc_native/m1_binding.cpp:94-97) and the split count
 // of integrations/vllm/vllm_plugin.py:271-276.
 
+#include <mutex>
+
 #include "split_kernels.h"
 
 namespace mxfa {
+
+// Workspace of mxfa_split_decode_noalloc_launch: one array per GPU (each
+// device holds its own copy at its own address), alive until the process
+// ends. Host code never passes `scratch` itself to a kernel: its host-side
+// name is a stand-in, not a device address. scratch_address() looks the
+// address up once per device, with that device current.
+static __device__ __align__(256) unsigned char scratch[MXFA_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mutex;
+static void *g_scratch_ptr[kMaxScratchDevices];
+
+static int scratch_address(void **ptr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
+    return MXFA_ELAUNCH;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return MXFA_ELAUNCH;
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return MXFA_OK;
+}
 
 int launch_partial_64(const DecodeParams &p, const Grid &g, int dtype, bool fp8, hipStream_t st);
 int launch_partial_128(const DecodeParams &p, const Grid &g, int dtype, bool fp8, hipStream_t st);
@@ -327,6 +354,9 @@ const char *mxfa_strerror(int code) {
     case MXFA_EINVAL: return "invalid argument (null pointer, size, alignment or stride)";
     case MXFA_EWORKSPACE: return "workspace missing or too small";
     case MXFA_ELAUNCH: return "kernel launch failed";
+    case MXFA_ESCRATCH:
+      return "the call needs more workspace than the no-allocation entry point's 8 MiB "
+             "(use mxfa_split_decode_launch with a workspace)";
   }
   return "unknown error";
 }
@@ -367,6 +397,28 @@ int mxfa_split_decode_workspace_size(int batch, int q_heads, int head_dim, int n
 
 int mxfa_split_decode_launch(MXFA_SPLIT_PARAMS, void *stream) {
   return run_split(split_args(MXFA_SPLIT_ARGS), true, (hipStream_t)stream);
+}
+
+int mxfa_split_decode_noalloc_launch(
+    const void *q, int64_t q_stride_b, int64_t q_stride_h, const void *k_cache,
+    const void *v_cache, int64_t cache_stride_page, int64_t cache_stride_token,
+    int64_t cache_stride_head, const int32_t *block_table, int64_t bt_stride,
+    const int32_t *seqlens, int seqlen_add, void *out, int64_t out_stride_b,
+    int64_t out_stride_h, float scale, int batch, int q_heads, int kv_heads, int head_dim,
+    int page_size, int block_table_width, int num_pages, int dtype, int num_splits,
+    void *stream) {
+  if (batch <= 0 || q_heads <= 0 || head_dim <= 0 || num_splits <= 0) return MXFA_EINVAL;
+  const size_t need = ws_layout(batch, q_heads, head_dim, num_splits).bytes;
+  if (need > MXFA_SCRATCH_BYTES) return MXFA_ESCRATCH;
+  void *ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != MXFA_OK) return rc;
+  return run_split(split_args(q, q_stride_b, q_stride_h, k_cache, v_cache, cache_stride_page,
+                              cache_stride_token, cache_stride_head, block_table, bt_stride,
+                              seqlens, seqlen_add, out, out_stride_b, out_stride_h, ws,
+                              MXFA_SCRATCH_BYTES, scale, batch, q_heads, kv_heads, head_dim,
+                              page_size, block_table_width, num_pages, dtype, num_splits),
+                   true, (hipStream_t)stream);
 }
 
 int mxfa_split_decode_partial_launch(MXFA_SPLIT_PARAMS, void *stream) {

@@ -24,13 +24,16 @@ LIB_PATH = Path(
     os.environ.get("MXFLASHATTN_AMD_LIB")
     or Path(__file__).resolve().parent / "_lib" / "libmxfa_mi355x.so"
 )
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 MXFA_OK = 0
 MXFA_EUNSUPPORTED = -1
 MXFA_EINVAL = -2
 MXFA_EWORKSPACE = -3
 MXFA_ELAUNCH = -4
+MXFA_ESCRATCH = -5
+# Workspace of mxfa_split_decode_noalloc_launch (the library's own device array).
+SCRATCH_BYTES = 8 << 20
 
 DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
 DTYPE_FP8_E4M3 = 2
@@ -59,6 +62,7 @@ EXPORTED_SYMBOLS = (
     "mxfa_split_heuristic_fp8",
     "mxfa_split_decode_workspace_size",
     "mxfa_split_decode_launch",
+    "mxfa_split_decode_noalloc_launch",
     "mxfa_split_decode_partial_launch",
     "mxfa_split_decode_combine_launch",
     "mxfa_split_decode_fp8_launch",
@@ -94,6 +98,7 @@ _SIGNATURES = {
     "mxfa_split_heuristic_fp8": (_i, [_i, _i, _i, _i, _i, _i, _i, ctypes.POINTER(_i)]),
     "mxfa_split_decode_workspace_size": (_i, [_i, _i, _i, _i, ctypes.POINTER(_sz)]),
     "mxfa_split_decode_launch": (_i, _SPLIT_ARGS + [_p]),
+    "mxfa_split_decode_noalloc_launch": (_i, _SPLIT_ARGS[:15] + _SPLIT_ARGS[17:] + [_p]),
     "mxfa_split_decode_partial_launch": (_i, _SPLIT_ARGS + [_p]),
     "mxfa_split_decode_fp8_launch": (_i, _SPLIT_ARGS + [_p, _p, _p]),
     "mxfa_split_decode_fp8_partial_launch": (_i, _SPLIT_ARGS + [_p, _p, _p]),
@@ -588,6 +593,35 @@ def paged_decode_split(
     else:
         rc = lib.mxfa_split_decode_launch(*args)
         _check(rc, "mxfa_split_decode_launch")
+    return out
+
+
+def paged_decode_split_noalloc(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    cache_seqlens: torch.Tensor,
+    softmax_scale: float,
+    *,
+    out: torch.Tensor,
+    num_splits: int | None = None,
+    seqlen_add: int = 0,
+) -> torch.Tensor:
+    """One-token decode of 16-bit caches through mxfa_split_decode_noalloc_launch:
+    the workspace is the library's own device array (SCRATCH_BYTES per GPU), so
+    the launch allocates nothing; ``out`` is required. Calls that overlap in
+    time on one GPU share that array and must not run concurrently."""
+    if k_cache.dtype == FP8_DTYPE or (q.dim() == 4 and q.shape[1] != 1):
+        raise UnsupportedConfig("the no-allocation entry point takes one-token 16-bit decode")
+    q, block_table, cache_seqlens, out = _prepare(q, k_cache, v_cache, block_table,
+                                                  cache_seqlens, out)
+    if num_splits is None:
+        num_splits = default_num_splits(q, k_cache, block_table)
+    args = _launch_args(q, k_cache, v_cache, block_table, cache_seqlens, out, 0, 0,
+                        softmax_scale, num_splits, seqlen_add)
+    rc = library().mxfa_split_decode_noalloc_launch(*args[:15], *args[17:])
+    _check(rc, "mxfa_split_decode_noalloc_launch")
     return out
 
 

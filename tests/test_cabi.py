@@ -44,7 +44,7 @@ def test_library_loads_and_reports_header_abi(lib):
 
 def test_every_header_function_is_exported_and_bound(lib):
     declared = header_functions()
-    assert len(declared) == len(set(declared)) == 14
+    assert len(declared) == len(set(declared)) == 15
     for name in declared:
         assert hasattr(lib, name), name
     assert set(declared) == set(native.EXPORTED_SYMBOLS) == set(native._SIGNATURES)
@@ -53,15 +53,18 @@ def test_every_header_function_is_exported_and_bound(lib):
 def test_return_codes_match_header():
     d = header_defines()
     assert (d["MXFA_OK"], d["MXFA_EUNSUPPORTED"], d["MXFA_EINVAL"], d["MXFA_EWORKSPACE"],
-            d["MXFA_ELAUNCH"]) == (native.MXFA_OK, native.MXFA_EUNSUPPORTED, native.MXFA_EINVAL,
-                                   native.MXFA_EWORKSPACE, native.MXFA_ELAUNCH)
+            d["MXFA_ELAUNCH"], d["MXFA_ESCRATCH"]) == (
+                native.MXFA_OK, native.MXFA_EUNSUPPORTED, native.MXFA_EINVAL,
+                native.MXFA_EWORKSPACE, native.MXFA_ELAUNCH, native.MXFA_ESCRATCH)
+    assert native.SCRATCH_BYTES == 8 << 20
     assert native.DTYPE_CODES == {torch.float16: d["MXFA_DTYPE_F16"],
                                   torch.bfloat16: d["MXFA_DTYPE_BF16"]}
 
 
 def test_strerror_is_distinct_per_code(lib):
-    texts = {code: lib.mxfa_strerror(code).decode() for code in (0, -1, -2, -3, -4)}
-    assert len(set(texts.values())) == 5
+    texts = {code: lib.mxfa_strerror(code).decode() for code in (0, -1, -2, -3, -4, -5)}
+    assert len(set(texts.values())) == 6
+    assert "8 MiB" in texts[-5]
     assert "unsupported" in texts[-1]
     assert lib.mxfa_strerror(-99).decode()
 
@@ -354,3 +357,14 @@ def test_python_shape_contract_rejects_mixed_and_fnuz_caches():
     fnuz = torch.zeros(4, 16, 2, 64, dtype=torch.float8_e4m3fnuz)
     with pytest.raises(native.UnsupportedConfig):
         native.check_decode_shapes(q, fnuz, fnuz)
+
+
+def test_no_alloc_entry_refuses_oversized_and_invalid_calls_before_launch(lib):
+    # 32 heads x 300 ranges x 2 x 128 floats is more than the 8 MiB array; the
+    # size check runs before any HIP call, so no GPU is needed.
+    fn = lib.mxfa_split_decode_noalloc_launch
+    args = [1, 0, 0, 1, 1, 0, 0, 0, 1, 0, 1, 0, 1, 0, 0, 0.1, 2, 32, 8, 128, 16, 4, 8, 1, 300,
+            None]
+    assert fn(*args) == native.MXFA_ESCRATCH
+    args[16] = 0  # batch
+    assert fn(*args) == native.MXFA_EINVAL

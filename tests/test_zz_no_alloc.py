@@ -1,0 +1,58 @@
+"""mxfa_split_decode_noalloc_launch against mxfa_split_decode_launch (GPU).
+
+The no-allocation entry point runs the same kernels with the library's own
+device array as workspace, so its output must equal the workspace entry
+point's bit for bit. Two calls in a row, the second with a smaller input (the
+array keeps the first call's contents), then a size beyond the array, which
+must be refused before any launch.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from mxflashattn_amd import native
+from mxflashattn_amd.workloads import CONFIGS, make_paged_batch
+
+pytestmark = pytest.mark.gpu
+
+
+def decode_both(b, num_splits=None):
+    with_ws = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table,
+                                        b.cache_seqlens, b.scale, num_splits=num_splits)
+    no_alloc = torch.full_like(b.q, float("nan"))
+    native.paged_decode_split_noalloc(b.q, b.k_cache, b.v_cache, b.block_table,
+                                      b.cache_seqlens, b.scale, out=no_alloc,
+                                      num_splits=num_splits)
+    torch.cuda.synchronize()
+    return with_ws, no_alloc
+
+
+def test_no_alloc_matches_workspace_entry_point_on_two_calls(device):
+    first = make_paged_batch(**CONFIGS["config2_qwen3_4b"], device=device)
+    second = make_paged_batch(3, 16, 4, 64, torch.float16, torch.tensor([5, 700, 33]),
+                              seed=61).to(device)
+    for b in (first, second):  # the second call is the smaller one
+        ws_bytes = native.workspace_size(b.batch, b.q_heads, b.head_dim,
+                                         native.default_num_splits(b.q, b.k_cache,
+                                                                   b.block_table))
+        assert ws_bytes <= native.SCRATCH_BYTES
+        with_ws, no_alloc = decode_both(b)
+        assert torch.equal(with_ws, no_alloc)
+    # A split count that crosses every sequence, on the smaller input.
+    with_ws, no_alloc = decode_both(second, num_splits=40)
+    assert torch.equal(with_ws, no_alloc)
+
+
+def test_no_alloc_refuses_inputs_beyond_its_array(device):
+    b = make_paged_batch(2, 32, 8, 128, torch.bfloat16, torch.tensor([100, 200]),
+                         seed=62).to(device)
+    splits = 300  # 32 heads x 300 ranges x 2 x 128 floats: 9.8 MB > 8 MiB
+    assert native.workspace_size(b.batch, 32, 128, splits) > native.SCRATCH_BYTES
+    out = torch.zeros_like(b.q)
+    with pytest.raises(RuntimeError, match="8 MiB"):
+        native.paged_decode_split_noalloc(b.q, b.k_cache, b.v_cache, b.block_table,
+                                          b.cache_seqlens, b.scale, out=out, num_splits=splits)
+    torch.cuda.synchronize()
+    assert torch.equal(out, torch.zeros_like(out))  # nothing was launched
