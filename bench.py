@@ -8,8 +8,10 @@ in HBM. The KV pool is rotated across copies
 totalling >= 1 GB so the 256 MB Infinity Cache cannot serve repeated reads.
 Prints ONE JSON line:
 
-  value        effective KV GB/s = sum_b 4*L_b*HKV*HD / (us per call), the
-               calls replayed from a HIP graph (no host launch overhead)
+  value        effective KV GB/s = sum_b 4*L_b*HKV*HD / (us per call); us per
+               call is the median of 10 timed regions of exactly --steps
+               calls, each region one replay of a HIP graph holding those
+               calls (no host launch overhead); timed_calls counts them all
   us_per_call_eager  the same calls launched one by one from Python, median of
                per-call HIP events
   us_per_call_warm   graph replays on one KV pool, never rotated (cache-warm
@@ -105,36 +107,36 @@ def time_calls(fn, pools, steps: int, warmup: int, stream) -> tuple[float, float
     return statistics.median(per), first.elapsed_time(last) * 1e3 / steps
 
 
-def time_graph(fn, pools, steps: int, warmup: int, stream) -> float:
-    """Mean us per call of ``steps`` calls replayed from HIP graphs on ``stream``.
+def time_graph(fn, pools, calls: int, warmup: int, stream, rounds: int = 10) -> tuple[float, int]:
+    """(median us per call, calls timed) of ``rounds`` timed regions on ``stream``.
 
-    One graph holds a block of calls that walks the pool rotation; it is
-    replayed until ``steps`` calls have run, between two events on the stream
-    the kernels run on. The workspace is allocated by the eager warmup on the
-    same stream, so nothing is allocated inside the capture.
+    Each timed region is exactly ``calls`` calls: one replay of a HIP graph
+    that holds ``calls`` calls walking the pool rotation, between two events
+    on the stream the kernels run on. The regions run back to back and the
+    median region is reported. ``warmup`` eager calls on the same stream
+    come first (they also size the workspace there, so nothing is allocated
+    inside the capture), then one untimed replay.
     """
     with torch.cuda.stream(stream):
         for i in range(warmup):
             fn(*pools[i % len(pools)])
     torch.cuda.synchronize()
-    block = len(pools) * max(1, 16 // len(pools))
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
-        for i in range(block):
+        for i in range(calls):
             fn(*pools[i % len(pools)])
-    reps = max(1, steps // block)
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(rounds)]
     with torch.cuda.stream(stream):
-        graph.replay()  # warm the graph
-        torch.cuda.synchronize()
-        first = torch.cuda.Event(enable_timing=True)
-        last = torch.cuda.Event(enable_timing=True)
-        first.record(stream)
-        for _ in range(reps):
+        graph.replay()  # untimed
+        for first, last in events:
+            first.record(stream)
             graph.replay()
-        last.record(stream)
+            last.record(stream)
     torch.cuda.synchronize()
     del graph
-    return first.elapsed_time(last) * 1e3 / (reps * block)
+    per_call = [a.elapsed_time(b) * 1e3 / calls for a, b in events]
+    return statistics.median(per_call), calls * rounds
 
 
 def measure_workload(name: str, spec: dict, device, steps: int, warmup: int) -> dict:
@@ -155,11 +157,11 @@ def measure_workload(name: str, spec: dict, device, steps: int, warmup: int) -> 
 
     us_eager, us_eager_mean = time_calls(call, pools, steps, warmup, stream)
     side = torch.cuda.Stream(device)
-    us_graph = time_graph(call, pools, steps, warmup, side)
+    us_graph, timed_calls = time_graph(call, pools, steps, warmup, side)
     # Warm: the same graph replays on one pool that is never rotated, so a
     # working set under the 256 MB Infinity Cache is partly served from it.
     # Reported beside the rotated figure of record, never as `value`.
-    us_warm = time_graph(call, pools[:1], steps, 0, side)
+    us_warm, _ = time_graph(call, pools[:1], steps, 0, side)
 
     # The dominant kernel alone: partial-only launches, same inputs and stream.
     ws = torch.empty(native.workspace_size(base.batch, base.q_heads, base.head_dim, ns),
@@ -171,7 +173,7 @@ def measure_workload(name: str, spec: dict, device, steps: int, warmup: int) -> 
 
     # The partial-only entry point takes one token and no window.
     single = base.q.shape[1] == 1 and window < 0
-    us_partial = time_graph(partial, pools, steps, warmup, side) if single else None
+    us_partial = time_graph(partial, pools, steps, warmup, side)[0] if single else None
     kv = base.kv_bytes()
     alg = base.algorithmic_bytes()
     gbs = kv / (us_graph * 1e-6) / 1e9
@@ -191,6 +193,7 @@ def measure_workload(name: str, spec: dict, device, steps: int, warmup: int) -> 
         "partial_kernel_gb_s": round(alg / (us_partial * 1e-6) / 1e9, 1) if us_partial else None,
         "num_splits": ns,
         "rotation_copies": len(pools),
+        "timed_calls": timed_calls,
     }
     del pools, base
     torch.cuda.empty_cache()
@@ -280,13 +283,13 @@ def main() -> int:
         for name, cspec in {**CELLS, **CONFIGS}.items():
             if name == args.workload:
                 continue
-            cells[name] = measure_workload(name, cspec, device, 100, 10)
+            cells[name] = measure_workload(name, cspec, device, 64, 10)
             print(f"[bench] {name}: {cells[name]}", file=sys.stderr, flush=True)
 
     wide = {}
     if not args.no_wide:
         for name, wspec in WIDE.items():
-            wide[name] = measure_workload(name, wspec, device, 100, 10)
+            wide[name] = measure_workload(name, wspec, device, 64, 10)
             print(f"[bench] {name}: {wide[name]}", file=sys.stderr, flush=True)
 
     decode = None
@@ -345,6 +348,9 @@ def main() -> int:
             "parallelism": "single_gpu",
         },
         "us_per_call": main_res["us_per_call"],
+        "timed_calls": main_res["timed_calls"],
+        "timing": (f"median of 10 timed regions of exactly {args.steps} calls each, every region "
+                   "one HIP-graph replay over the rotated KV pools"),
         "us_per_call_eager": main_res["us_per_call_eager"],
         "kv_gb_s_eager": main_res["kv_gb_s_eager"],
         "us_per_call_warm": main_res["us_per_call_warm"],
@@ -361,6 +367,10 @@ def main() -> int:
             "kernel": kernel,
             "kernel_us": kernel_us,
             "algorithmic_bytes": main_res["algorithmic_bytes"],
+            # The whole call (partial kernel, combine kernel and the launch
+            # between them) against the same peak.
+            "call_achieved": main_res["alg_gb_s"],
+            "call_frac": round(main_res["alg_gb_s"] / HBM_PEAK_GBS, 4),
         },
         "cpu_baseline": cpu,
         "cells": cells,
@@ -368,6 +378,12 @@ def main() -> int:
         "decode_step": decode,
         "decode_step_fp8": decode_fp8,
     }
+    summary = {args.workload: main_res, **cells}
+    for name in sorted(summary):
+        res = summary[name]
+        print(f"[cells] {name:28s} {res['us_per_call']:9.2f} us/call "
+              f"{res['pct_hbm_peak']:6.2f} % of 8 TB/s", file=sys.stderr)
+    sys.stderr.flush()
     print(json.dumps(line))
     return 0
 

@@ -371,8 +371,11 @@ __device__ __forceinline__ float head_of_row(float x, int row) {
   return v;
 }
 
-// Exclusive prefix sum of per-sequence tile counts into s[0..B] (LDS), all threads.
-template <int kThreads>
+// Exclusive prefix sum of per-sequence tile counts into s[0..B] (LDS), all
+// threads. The lengths are read from memory once: the first pass parks each
+// tile count in s[b], the second turns them into prefix sums in place. Without
+// a window (kWindow false) every sequence starts at its tile 0.
+template <int kThreads, bool kWindow>
 __device__ __forceinline__ void tile_prefix(const DecodeParams &p, int32_t *s, int *wave_tot) {
   const int B = p.batch;
   const int per = (B + kThreads - 1) / kThreads;
@@ -380,8 +383,12 @@ __device__ __forceinline__ void tile_prefix(const DecodeParams &p, int32_t *s, i
   int local = 0;
   for (int i = 0; i < per; ++i) {
     const int b = b0 + i;
-    if (b < B) local += tiles_of(seq_len_of(p.seqlens, b, p.seqlen_add, p.max_len), p.ql,
-                                 p.window_left);
+    if (b < B) {
+      const int L = seq_len_of(p.seqlens, b, p.seqlen_add, p.max_len);
+      const int n = kWindow ? tiles_of(L, p.ql, p.window_left) : (L + kTile - 1) / kTile;
+      s[b] = n;
+      local += n;
+    }
   }
   // Inclusive scan of `local` across the workgroup.
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -396,11 +403,12 @@ __device__ __forceinline__ void tile_prefix(const DecodeParams &p, int32_t *s, i
   int base = 0;
   for (int w = 0; w < wave; ++w) base += wave_tot[w];
   int run = base + x - local;  // exclusive prefix of this thread's first element
-  for (int i = 0; i < per; ++i) {
+  for (int i = 0; i < per; ++i) {  // each thread rewrites only its own entries
     const int b = b0 + i;
     if (b < B) {
+      const int n = s[b];
       s[b] = run;
-      run += tiles_of(seq_len_of(p.seqlens, b, p.seqlen_add, p.max_len), p.ql, p.window_left);
+      run += n;
     }
   }
   if (threadIdx.x == kThreads - 1) s[B] = base + x;
@@ -538,22 +546,31 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   const int q_bytes = (p.ql - 1) * (int)p.q_st + (gq - 1) * (int)p.q_sh + HD * 2;
   auto q_step = [](int cc) { return kF8 ? (cc >> 1) * 128 + (cc & 1) * 16 : cc * 64; };
 
-  // Sequence holding tile lo: largest b with s[b] <= lo (then s[b+1] > lo).
+  // Sequence holding tile lo: the largest b < B with s[b] <= lo (then
+  // s[b+1] > lo). s is nondecreasing and s[0] = 0 <= lo, so the lanes whose
+  // probe passes form a prefix: each round narrows [a, a + n) to one of 64
+  // steps (one round for B <= 64, three for B <= 16000).
   int pb;
   {
-    int a = 0, z = B - 1;
-    while (a < z) {
-      const int mid = (a + z + 1) >> 1;
-      if (s_tiles[mid] <= lo) a = mid;
-      else z = mid - 1;
+    int a = 0, n = B;
+    while (n > 1) {
+      const int step = (n + 63) >> 6;
+      const int idx = a + lane * step;
+      const bool ok = idx < a + n && s_tiles[idx] <= lo;
+      const int cnt = __builtin_popcountll(__builtin_amdgcn_ballot_w64(ok));
+      const int na = a + (cnt - 1) * step;
+      n = min(step, a + n - na);
+      a = na;
     }
     pb = rfl(a);
   }
-  // Cursor of the tile builder (runs NBUF tiles ahead of the math).
+  // Cursor of the tile builder (runs NBUF tiles ahead of the math). Without a
+  // window every sequence starts at its tile 0, so the first page id does not
+  // wait for the length.
   int p_start = rfl(s_tiles[pb]);
   int p_end = rfl(s_tiles[pb + 1]);
   int p_len = seq_len_of(p.seqlens, pb, p.seqlen_add, p.max_len);
-  int p_first = first_tile_of(p_len, p.ql, p.window_left);  // tile of the sequence at p_start
+  int p_first = kExtras ? first_tile_of(p_len, p.ql, p.window_left) : 0;  // tile at p_start
   ConstI32 p_bt = as_const(p.bt + (int64_t)pb * p.bt_stride);
 
   auto make_tile = [&](int t, Tile &d, int (&lpg)[NPG]) {
@@ -575,7 +592,7 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
         p_end = rfl(s_tiles[pb + 1]);
       } while (t >= p_end);
       p_len = seq_len_of(p.seqlens, pb, p.seqlen_add, p.max_len);
-      p_first = first_tile_of(p_len, p.ql, p.window_left);
+      p_first = kExtras ? first_tile_of(p_len, p.ql, p.window_left) : 0;
       p_bt = as_const(p.bt + (int64_t)pb * p.bt_stride);
     }
     d.b = pb;
@@ -891,7 +908,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(DecodePara
   extern __shared__ int32_t s_tiles[];  // [B + 1]
   __shared__ int s_wave_tot[WAVES];
 
-  tile_prefix<kThreads>(p, s_tiles, s_wave_tot);  // ends with a barrier
+  tile_prefix<kThreads, kExtras>(p, s_tiles, s_wave_tot);  // ends with a barrier
   zero_empty<HD, kThreads>(p, s_tiles);
   const int B = p.batch;
   if (blockIdx.x == 0 && blockIdx.y == 0) {
