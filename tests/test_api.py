@@ -1,10 +1,14 @@
-"""Public API contract on the CPU (mirrors the reference's tests/test_api.py).
+"""Public API on the CPU: the argument contract, the explicit fallback, and
+the MI355X route's qualification.
 
-Host tensors never qualify for the MI355X decode backend, so these calls go
-through the rest of the dispatch chain: the explicit PyTorch path behind
-MXFLASHATTN_ALLOW_FALLBACK=1, or BackendUnavailableError without it. The
-decode routes' own qualification logic is checked at the end without a GPU.
+Host tensors never take the MI355X route, so a valid call here goes down the
+rest of the chain: with MXFLASHATTN_ALLOW_FALLBACK=1 to the PyTorch path (its
+results are checked against properties and the oracle port), without it to
+BackendUnavailableError. The messages matched below are the reference's
+(mxflashattn/api.py, mxflashattn/validation.py), which callers match on.
 """
+
+import math
 
 import pytest
 import torch
@@ -13,212 +17,240 @@ import mxflashattn_amd.dispatch as dispatch
 from mxflashattn_amd import (
     BackendUnavailableError,
     decode,
-    fallback,
     flash_attn_func,
     flash_attn_varlen_func,
     flash_attn_with_kvcache,
     get_last_dispatch_info,
 )
+from oracle import reference_port
 
 pytestmark = pytest.mark.filterwarnings(
     "ignore:MXFlashAttn is using the PyTorch reference path:RuntimeWarning")
 
 
-def tensors(batch=1, q_len=2, kv_len=3, q_heads=2, kv_heads=1, head_dim=64):
-    q = torch.randn(batch, q_len, q_heads, head_dim, dtype=torch.float32)
-    k = torch.randn(batch, kv_len, kv_heads, head_dim, dtype=torch.float32)
-    v = torch.randn_like(k)
-    return q, k, v
+@pytest.fixture
+def fallback(monkeypatch):
+    """The PyTorch path is the only backend: no vendor wheel, no extension."""
+    monkeypatch.setenv("MXFLASHATTN_ALLOW_FALLBACK", "1")
+    monkeypatch.setattr(dispatch, "_flash_attn_function", lambda operation: None)
+    monkeypatch.setattr(dispatch, "_native_extension", lambda: None)
+    return monkeypatch
 
 
-def test_native_backend_is_required_unless_fallback_is_explicit(monkeypatch):
-    q, k, v = tensors()
+def rand(*shape, seed=0, dtype=torch.float32):
+    return torch.randn(*shape, generator=torch.Generator().manual_seed(seed)).to(dtype)
+
+
+def i32(values):
+    return torch.tensor(values, dtype=torch.int32)
+
+
+# --- argument contract ------------------------------------------------------
+
+Q4, K4 = rand(2, 3, 4, 64), rand(2, 5, 2, 64)
+QD, KD = rand(2, 1, 4, 64), rand(2, 6, 2, 64)  # decode against a dense cache
+SL = i32([3, 4])
+
+CONTRACT = [
+    ("dropout", lambda: flash_attn_func(Q4, K4, K4, dropout_p=0.2), NotImplementedError,
+     "dropout is not supported"),
+    ("window", lambda: flash_attn_func(Q4, K4, K4, window_size=(8, 0)), NotImplementedError,
+     "local window attention is not supported"),
+    ("softcap", lambda: flash_attn_func(Q4, K4, K4, softcap=30.0), NotImplementedError,
+     "soft-capping is not supported"),
+    ("alibi", lambda: flash_attn_func(Q4, K4, K4, alibi_slopes=torch.ones(4)),
+     NotImplementedError, "alibi_slopes are not supported"),
+    ("probs", lambda: flash_attn_func(Q4, K4, K4, return_attn_probs=True), NotImplementedError,
+     "return_attn_probs is not supported"),
+    ("deterministic", lambda: flash_attn_func(Q4, K4, K4, deterministic=True),
+     NotImplementedError, "deterministic mode"),
+    ("nan scale", lambda: flash_attn_func(Q4, K4, K4, softmax_scale=math.nan), ValueError,
+     "softmax_scale must be finite"),
+    ("text scale", lambda: flash_attn_func(Q4, K4, K4, softmax_scale="x"), TypeError,
+     "finite number or None"),
+    ("rank", lambda: flash_attn_func(Q4[0], K4, K4), ValueError, "rank 4"),
+    ("head dim", lambda: flash_attn_func(rand(1, 1, 2, 96), rand(1, 2, 1, 96),
+                                         rand(1, 2, 1, 96)), ValueError, "head dimension"),
+    ("gqa", lambda: flash_attn_func(rand(1, 1, 3, 64), rand(1, 2, 2, 64), rand(1, 2, 2, 64)),
+     ValueError, "divisible by the number of kv heads"),
+    ("int dtype", lambda: flash_attn_func(Q4.int(), K4.int(), K4.int()), TypeError,
+     "supported dtypes"),
+    ("rotary", lambda: flash_attn_with_kvcache(QD, KD, KD, cache_seqlens=SL,
+                                               rotary_cos=torch.zeros(1)),
+     NotImplementedError, "rotary embeddings are not supported"),
+    ("lse", lambda: flash_attn_with_kvcache(QD, KD, KD, cache_seqlens=SL,
+                                            return_softmax_lse=True),
+     NotImplementedError, "return_softmax_lse is not supported"),
+    ("no lengths", lambda: flash_attn_with_kvcache(QD, KD, KD), ValueError,
+     "cache_seqlens is required"),
+    ("lengths shape", lambda: flash_attn_with_kvcache(QD, KD, KD, cache_seqlens=i32([3])),
+     ValueError, "one value per batch item"),
+    ("lengths dtype", lambda: flash_attn_with_kvcache(QD, KD, KD, cache_seqlens=SL.float()),
+     TypeError, "int32 or int64"),
+    ("table rows", lambda: flash_attn_with_kvcache(QD, KD, KD, cache_seqlens=SL,
+                                                   block_table=torch.zeros(3, 1,
+                                                                           dtype=torch.int32)),
+     ValueError, "one row per batch item"),
+    ("page size", lambda: flash_attn_with_kvcache(QD, torch.empty(2, 0, 2, 64),
+                                                  torch.empty(2, 0, 2, 64),
+                                                  cache_seqlens=SL,
+                                                  block_table=i32([[0], [1]])),
+     ValueError, "page size must be positive"),
+    ("half append", lambda: flash_attn_with_kvcache(QD, KD, KD, k=rand(2, 1, 2, 64),
+                                                    cache_seqlens=SL),
+     ValueError, "both be provided"),
+    ("out shape", lambda: flash_attn_with_kvcache(QD, KD, KD, cache_seqlens=SL,
+                                                  out=torch.empty(2, 1, 4, 32)),
+     ValueError, "out must match"),
+    ("varlen coverage", lambda: flash_attn_varlen_func(rand(3, 2, 64), rand(3, 1, 64),
+                                                       rand(3, 1, 64), i32([0, 2]), i32([0, 3]),
+                                                       2, 3), ValueError, "cover all tokens"),
+    ("varlen empty keys", lambda: flash_attn_varlen_func(rand(2, 2, 64), rand(2, 1, 64),
+                                                         rand(2, 1, 64), i32([0, 1, 2]),
+                                                         i32([0, 2, 2]), 1, 2),
+     ValueError, "key/value sequences must be non-empty"),
+    ("varlen too long", lambda: flash_attn_varlen_func(rand(1, 2, 64), rand(4, 1, 64),
+                                                       rand(4, 1, 64), i32([0, 1]),
+                                                       i32([0, 4]), 1, 3),
+     ValueError, "longer than max_seqlen"),
+    ("varlen decreasing", lambda: flash_attn_varlen_func(rand(2, 2, 64), rand(3, 1, 64),
+                                                         rand(3, 1, 64), i32([0, 2, 2]),
+                                                         i32([0, 3, 2, 3]), 2, 3),
+     ValueError, "same batch size|non-decreasing"),
+    ("varlen device", lambda: flash_attn_varlen_func(
+        rand(1, 2, 64), rand(1, 1, 64), rand(1, 1, 64),
+        torch.tensor([0, 1], dtype=torch.int32, device="meta"), i32([0, 1]), 1, 1),
+     ValueError, "same device as q"),
+]
+
+
+@pytest.mark.parametrize("name,call,error,text", CONTRACT, ids=[c[0] for c in CONTRACT])
+def test_contract_errors(fallback, name, call, error, text):
+    with pytest.raises(error, match=text):
+        call()
+
+
+# --- the fallback switch ------------------------------------------------------
+
+def test_without_the_switch_the_chain_refuses(monkeypatch):
     monkeypatch.delenv("MXFLASHATTN_ALLOW_FALLBACK", raising=False)
     monkeypatch.setattr(dispatch, "_flash_attn_function", lambda operation: None)
     monkeypatch.setattr(dispatch, "_native_extension", lambda: None)
-    with pytest.raises(BackendUnavailableError, match="MXFLASHATTN_ALLOW_FALLBACK=1"):
-        flash_attn_func(q, k, v)
+    for call in (lambda: flash_attn_func(Q4, K4, K4),
+                 lambda: flash_attn_with_kvcache(QD, KD, KD, cache_seqlens=SL)):
+        with pytest.raises(BackendUnavailableError, match="MXFLASHATTN_ALLOW_FALLBACK=1"):
+            call()
 
 
-def test_explicit_reference_fallback_runs_and_records_reason(monkeypatch):
-    q, k, v = tensors()
-    monkeypatch.setenv("MXFLASHATTN_ALLOW_FALLBACK", "1")
-    monkeypatch.setattr(dispatch, "_flash_attn_function", lambda operation: None)
-    monkeypatch.setattr(dispatch, "_native_extension", lambda: None)
+def test_with_the_switch_the_reference_path_runs_and_says_why(fallback):
     with pytest.warns(RuntimeWarning, match="native_backend_requires_accelerator_tensor"):
-        output = flash_attn_func(q, k, v, causal=True)
-    assert output.shape == q.shape
-    assert torch.isfinite(output).all()
+        out = flash_attn_with_kvcache(QD, KD, KD, cache_seqlens=SL)
     info = get_last_dispatch_info()
-    assert info.backend == "reference"
-    assert info.fallback_reason
-    # The MI355X route names why it declined the call.
-    assert "mi355x_split_decode:requires_accelerator_tensor" in info.fallback_reason
+    assert (info.backend, info.operation) == ("reference", "flash_attn_with_kvcache")
+    reasons = info.fallback_reason.split(";")
+    assert "native_backend_requires_accelerator_tensor" in reasons
+    assert "mi355x_split_decode:requires_accelerator_tensor" in reasons
+    assert out.shape == QD.shape and torch.isfinite(out).all()
 
 
-def test_causal_attention_handles_query_longer_than_key_without_nan(monkeypatch):
-    monkeypatch.setenv("MXFLASHATTN_ALLOW_FALLBACK", "1")
-    q = torch.randn(1, 3, 2, 64)
-    k = torch.randn(1, 1, 1, 64)
-    v = torch.randn_like(k)
-    output = flash_attn_func(q, k, v, causal=True)
-    assert torch.isfinite(output).all()
-    torch.testing.assert_close(output[:, :2], torch.zeros_like(output[:, :2]))
-    torch.testing.assert_close(output[:, 2:], v.expand(-1, -1, 2, -1))
+# --- results of the fallback path -------------------------------------------
+
+@pytest.mark.parametrize("seed", range(4))
+def test_paged_cache_equals_the_gathered_dense_cache(fallback, seed):
+    # Random tables over a shuffled pool: the paged call equals the dense call
+    # on the rows gathered in table order.
+    g = torch.Generator().manual_seed(seed)
+    ps, pages, hkv = 4, 13, 2
+    lengths = torch.randint(1, 4 * ps + 1, (3,), generator=g)
+    k_cache, v_cache = rand(pages, ps, hkv, 64, seed=seed), rand(pages, ps, hkv, 64, seed=99)
+    table = torch.randperm(pages, generator=g)[:12].view(3, 4).to(torch.int32)
+    q = rand(3, 1, 6, 64, seed=seed + 7)
+    paged = flash_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens=lengths.to(torch.int32),
+                                    block_table=table)
+    for b in range(3):
+        n = int(lengths[b])
+        rows = [k_cache[table[b, t // ps], t % ps] for t in range(n)]
+        vrows = [v_cache[table[b, t // ps], t % ps] for t in range(n)]
+        dense = flash_attn_func(q[b:b + 1], torch.stack(rows)[None], torch.stack(vrows)[None])
+        torch.testing.assert_close(paged[b:b + 1], dense)
 
 
-def test_varlen_attention_supports_gqa_and_unequal_sequences(monkeypatch):
-    monkeypatch.setenv("MXFLASHATTN_ALLOW_FALLBACK", "1")
-    q = torch.randn(3, 2, 64)
-    k = torch.randn(5, 1, 64)
-    v = torch.randn_like(k)
-    cu_q = torch.tensor([0, 2, 3], dtype=torch.int32)
-    cu_k = torch.tensor([0, 3, 5], dtype=torch.int32)
-    output = flash_attn_varlen_func(q, k, v, cu_q, cu_k, max_seqlen_q=2, max_seqlen_k=3)
-    assert output.shape == q.shape
-    assert torch.isfinite(output).all()
-    # Row 2 is sequence 1's only query: attention over keys 3..4.
-    expected = fallback.attention_batched(q[None, 2:3], k[None, 3:5], v[None, 3:5])[0]
-    torch.testing.assert_close(output[2:3], expected)
+@pytest.mark.parametrize("paged", [True, False])
+def test_append_writes_the_new_rows_then_attends_over_them(fallback, paged):
+    q, k_new, v_new = rand(2, 1, 4, 64, seed=1), rand(2, 2, 2, 64, seed=2), rand(2, 2, 2, 64,
+                                                                                   seed=3)
+    lengths = i32([3, 5])
+    if paged:
+        k_cache, v_cache = rand(6, 4, 2, 64, seed=4), rand(6, 4, 2, 64, seed=5)
+        table = i32([[5, 0], [2, 4]])
+    else:
+        k_cache, v_cache = rand(2, 8, 2, 64, seed=4), rand(2, 8, 2, 64, seed=5)
+        table = None
+    k_before, v_before = k_cache.clone(), v_cache.clone()
+    out = flash_attn_with_kvcache(q, k_cache, v_cache, k=k_new, v=v_new, cache_seqlens=lengths,
+                                  block_table=table)
+    assert lengths.tolist() == [5, 7]
+    # The port on the untouched caches does the same append and attention.
+    expected = reference_port.attention_kvcache(q, k_before, v_before, k=k_new, v=v_new,
+                                                cache_seqlens=i32([3, 5]), block_table=table)
+    torch.testing.assert_close(out, expected)
+    torch.testing.assert_close(k_cache, k_before)  # the port appended the same rows
+    for b, old in enumerate((3, 5)):
+        for t in range(2):
+            pos = old + t
+            row = k_cache[table[b, pos // 4], pos % 4] if paged else k_cache[b, pos]
+            assert torch.equal(row, k_new[b, t])
 
 
-def test_varlen_rejects_cumulative_lengths_that_do_not_cover_tokens(monkeypatch):
-    monkeypatch.setenv("MXFLASHATTN_ALLOW_FALLBACK", "1")
-    q = torch.randn(2, 1, 64)
-    k = torch.randn(2, 1, 64)
-    cu = torch.tensor([0, 1], dtype=torch.int32)
-    with pytest.raises(ValueError, match="cover all tokens"):
-        flash_attn_varlen_func(q, k, k, cu, cu, max_seqlen_q=1, max_seqlen_k=1)
+def test_causal_rows_without_a_visible_key_are_zero(fallback):
+    # Four queries at the end of three keys: query i sits at key position
+    # i - 1, so query 0 sees nothing and query j > 0 sees keys 0..j-1.
+    q, k, v = rand(1, 4, 2, 64, seed=8), rand(1, 3, 1, 64, seed=9), rand(1, 3, 1, 64, seed=10)
+    out = flash_attn_func(q, k, v, causal=True)
+    assert torch.equal(out[0, 0], torch.zeros_like(out[0, 0]))
+    for j in range(1, 4):
+        alone = flash_attn_func(q[:, j:j + 1], k[:, :j], v[:, :j])
+        torch.testing.assert_close(out[:, j:j + 1], alone)
 
 
-def test_varlen_rejects_empty_key_sequences(monkeypatch):
-    monkeypatch.setenv("MXFLASHATTN_ALLOW_FALLBACK", "1")
-    q = torch.randn(2, 1, 64)
-    k = torch.randn(1, 1, 64)
-    cu_q = torch.tensor([0, 1, 2], dtype=torch.int32)
-    cu_k = torch.tensor([0, 0, 1], dtype=torch.int32)
-    with pytest.raises(ValueError, match="key/value sequences must be non-empty"):
-        flash_attn_varlen_func(q, k, k, cu_q, cu_k, max_seqlen_q=1, max_seqlen_k=1)
+def test_varlen_segments_are_independent_calls(fallback):
+    cu_q, cu_k = [0, 1, 4, 6], [0, 5, 7, 12]
+    q, k, v = rand(6, 4, 128, seed=11), rand(12, 2, 128, seed=12), rand(12, 2, 128, seed=13)
+    out = flash_attn_varlen_func(q, k, v, i32(cu_q), i32(cu_k), max_seqlen_q=3, max_seqlen_k=5,
+                                 causal=True)
+    for i in range(3):
+        qs, ks = slice(cu_q[i], cu_q[i + 1]), slice(cu_k[i], cu_k[i + 1])
+        alone = flash_attn_func(q[None, qs], k[None, ks], v[None, ks], causal=True)[0]
+        torch.testing.assert_close(out[qs], alone)
 
 
-def test_varlen_rejects_cumulative_lengths_on_a_different_device(monkeypatch):
-    monkeypatch.setenv("MXFLASHATTN_ALLOW_FALLBACK", "1")
-    q = torch.randn(1, 1, 64)
-    k = torch.randn(1, 1, 64)
-    cu = torch.tensor([0, 1], device="meta", dtype=torch.int32)
-    with pytest.raises(ValueError, match="same device as q"):
-        flash_attn_varlen_func(q, k, k, cu, cu, max_seqlen_q=1, max_seqlen_k=1)
+def test_an_explicit_zero_scale_averages_v(fallback):
+    q, k, v = rand(1, 1, 2, 64, seed=14), rand(1, 5, 1, 64, seed=15), rand(1, 5, 1, 64, seed=16)
+    out = flash_attn_func(q, k, v, softmax_scale=0.0)
+    torch.testing.assert_close(out[0, 0, 0], v[0, :, 0].mean(dim=0))
+    assert not torch.allclose(out, flash_attn_func(q, k, v))  # 0.0 is not "default"
 
 
-def test_varlen_rejects_sequences_longer_than_max_seqlen(monkeypatch):
-    monkeypatch.setenv("MXFLASHATTN_ALLOW_FALLBACK", "1")
-    q = torch.randn(1, 1, 64)
-    k = torch.randn(3, 1, 64)
-    with pytest.raises(ValueError, match="longer than max_seqlen"):
-        flash_attn_varlen_func(q, k, k, torch.tensor([0, 1], dtype=torch.int32),
-                               torch.tensor([0, 3], dtype=torch.int32), max_seqlen_q=1,
-                               max_seqlen_k=2)
+def test_out_receives_the_result(fallback):
+    out = torch.full_like(QD, math.nan)
+    got = flash_attn_with_kvcache(QD, KD, KD, cache_seqlens=SL, out=out)
+    assert got is out
+    torch.testing.assert_close(out, flash_attn_with_kvcache(QD, KD, KD, cache_seqlens=SL))
 
 
-def test_kvcache_rejects_zero_page_size(monkeypatch):
-    monkeypatch.setenv("MXFLASHATTN_ALLOW_FALLBACK", "1")
-    q = torch.randn(1, 1, 1, 64)
-    k_cache = torch.empty(1, 0, 1, 64)
-    v_cache = torch.empty_like(k_cache)
-    with pytest.raises(ValueError, match="page size must be positive"):
-        flash_attn_with_kvcache(q, k_cache, v_cache,
-                                cache_seqlens=torch.tensor([1], dtype=torch.int32),
-                                block_table=torch.tensor([[0]], dtype=torch.int32))
-
-
-def test_paged_kv_cache_reads_blocks_in_table_order(monkeypatch):
-    monkeypatch.setenv("MXFLASHATTN_ALLOW_FALLBACK", "1")
-    q = torch.randn(1, 1, 2, 64)
-    k_cache = torch.randn(2, 2, 1, 64)
-    v_cache = torch.randn_like(k_cache)
-    output = flash_attn_with_kvcache(q, k_cache, v_cache,
-                                     cache_seqlens=torch.tensor([3], dtype=torch.int32),
-                                     block_table=torch.tensor([[1, 0]], dtype=torch.int32))
-    expected_k = torch.cat((k_cache[1], k_cache[0, :1]), dim=0).unsqueeze(0)
-    expected_v = torch.cat((v_cache[1], v_cache[0, :1]), dim=0).unsqueeze(0)
-    torch.testing.assert_close(output, flash_attn_func(q, expected_k, expected_v))
-
-
-def test_paged_kv_cache_appends_and_advances_sequence_length(monkeypatch):
-    monkeypatch.setenv("MXFLASHATTN_ALLOW_FALLBACK", "1")
-    q, k_new, v_new = tensors(q_len=1, kv_len=1)
-    k_cache = torch.zeros(2, 2, 1, 64)
-    v_cache = torch.zeros_like(k_cache)
-    k_cache[0] = torch.randn_like(k_cache[0])
-    v_cache[0] = torch.randn_like(v_cache[0])
-    cache_seqlens = torch.tensor([2], dtype=torch.int32)
-    output = flash_attn_with_kvcache(q, k_cache, v_cache, k=k_new, v=v_new,
-                                     cache_seqlens=cache_seqlens,
-                                     block_table=torch.tensor([[0, 1]], dtype=torch.int32))
-    assert output.shape == q.shape
-    assert cache_seqlens.tolist() == [3]
-    torch.testing.assert_close(k_cache[1, 0], k_new[0, 0])
-    torch.testing.assert_close(v_cache[1, 0], v_new[0, 0])
-
-
-def test_dense_kv_cache_appends_and_advances_sequence_length(monkeypatch):
-    monkeypatch.setenv("MXFLASHATTN_ALLOW_FALLBACK", "1")
-    q, k_new, v_new = tensors(q_len=1, kv_len=1)
-    k_cache = torch.zeros(1, 4, 1, 64)
-    v_cache = torch.zeros_like(k_cache)
-    k_cache[:, :2] = torch.randn(1, 2, 1, 64)
-    v_cache[:, :2] = torch.randn(1, 2, 1, 64)
-    cache_seqlens = torch.tensor([2], dtype=torch.int32)
-    flash_attn_with_kvcache(q, k_cache, v_cache, k=k_new, v=v_new, cache_seqlens=cache_seqlens)
-    assert cache_seqlens.tolist() == [3]
-    torch.testing.assert_close(k_cache[0, 2], k_new[0, 0])
-    torch.testing.assert_close(v_cache[0, 2], v_new[0, 0])
-
-
-def test_unsupported_flash_attention_options_fail_clearly(monkeypatch):
-    monkeypatch.setenv("MXFLASHATTN_ALLOW_FALLBACK", "1")
-    q, k, v = tensors()
-    with pytest.raises(NotImplementedError, match="dropout"):
-        flash_attn_func(q, k, v, dropout_p=0.1)
-    q1, kc, vc = tensors(q_len=1)
-    sl = torch.tensor([2], dtype=torch.int32)
-    with pytest.raises(NotImplementedError, match="rotary"):
-        flash_attn_with_kvcache(q1, kc, vc, cache_seqlens=sl, rotary_cos=torch.zeros(1))
-    with pytest.raises(NotImplementedError, match="return_softmax_lse"):
-        flash_attn_with_kvcache(q1, kc, vc, cache_seqlens=sl, return_softmax_lse=True)
-
-
-def test_explicit_zero_scale_is_preserved_and_nonfinite_scale_is_rejected(monkeypatch):
-    monkeypatch.setenv("MXFLASHATTN_ALLOW_FALLBACK", "1")
-    q, k, v = tensors()
-    zero_scale = flash_attn_func(q, k, v, softmax_scale=0.0)
-    expected = fallback.attention_batched(q, k, v, softmax_scale=0.0)
-    default_scale = flash_attn_func(q, k, v)
-    torch.testing.assert_close(zero_scale, expected)
-    assert not torch.allclose(zero_scale, default_scale)
-    with pytest.raises(ValueError, match="softmax_scale must be finite"):
-        flash_attn_func(q, k, v, softmax_scale=float("nan"))
-
-
-def test_kvcache_requires_cache_seqlens_and_matching_table(monkeypatch):
-    monkeypatch.setenv("MXFLASHATTN_ALLOW_FALLBACK", "1")
-    q, kc, vc = tensors(q_len=1)
-    with pytest.raises(ValueError, match="cache_seqlens is required"):
-        flash_attn_with_kvcache(q, kc, vc)
-    with pytest.raises(ValueError, match="one row per batch item"):
-        flash_attn_with_kvcache(q, kc, vc, cache_seqlens=torch.tensor([1], dtype=torch.int32),
-                                block_table=torch.zeros(2, 1, dtype=torch.int32))
-
-
-def test_strict_validation_reads_lengths_back(monkeypatch):
-    monkeypatch.setenv("MXFLASHATTN_ALLOW_FALLBACK", "1")
-    monkeypatch.setenv("MXFLASHATTN_STRICT_VALIDATION", "1")
-    q, kc, vc = tensors(q_len=1)
-    with pytest.raises(ValueError, match="exceeds dense cache capacity"):
-        flash_attn_with_kvcache(q, kc, vc, cache_seqlens=torch.tensor([4], dtype=torch.int32))
-    with pytest.raises(ValueError, match="out-of-range page index"):
-        flash_attn_with_kvcache(q, kc, vc, cache_seqlens=torch.tensor([2], dtype=torch.int32),
-                                block_table=torch.tensor([[5]], dtype=torch.int32))
+@pytest.mark.parametrize("lengths,table,text", [
+    ([7, 1], None, "exceeds dense cache capacity"),
+    ([0, 2], None, "at least one cached or appended"),
+    ([-1, 2], None, "non-negative"),
+    ([2, 5], [[0, 1], [1, 2]], "enough pages"),
+    ([2, 1], [[9, 0], [1, 2]], "out-of-range page index"),
+])
+def test_strict_validation_reads_lengths_and_tables_back(fallback, lengths, table, text):
+    fallback.setenv("MXFLASHATTN_STRICT_VALIDATION", "1")
+    caches = (KD, KD) if table is None else (rand(3, 2, 2, 64), rand(3, 2, 2, 64))
+    with pytest.raises(ValueError, match=text):
+        flash_attn_with_kvcache(QD, *caches, cache_seqlens=i32(lengths),
+                                block_table=None if table is None else i32(table))
 
 
 # --- qualification of the MI355X decode route (no kernel runs here) --------
