@@ -70,9 +70,41 @@ def _run(cmd: list[str]) -> None:
         )
 
 
+TORCH_OP_SOURCE = CSRC_DIR / "torch_op.cpp"
+
+
+def torch_op_path() -> Path:
+    import sysconfig
+
+    return LIB_DIR / ("_mxfa_torch" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def torch_op_command(output: Path) -> list[str]:
+    """g++ line of the torch operator (host code only, no device code): it
+    includes torch's and HIP's headers and links torch and the C-ABI library,
+    found next to it at run time ($ORIGIN)."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    torch_lib = Path(torch.__file__).resolve().parent / "lib"
+    abi = int(torch.compiled_with_cxx11_abi())
+    return ["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-fvisibility=hidden",
+            f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-D__HIP_PLATFORM_AMD__=1",
+            "-DTORCH_EXTENSION_NAME=_mxfa_torch", "-DTORCH_API_INCLUDE_EXTENSION_H",
+            *[f"-I{p}" for p in cpp_extension.include_paths()],
+            f"-I{sysconfig.get_paths()['include']}", f"-I{rocm}/include", f"-I{INCLUDE_DIR}",
+            str(TORCH_OP_SOURCE), f"-L{torch_lib}", f"-L{LIB_DIR}", "-lmxfa_mi355x", "-lc10",
+            "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-ltorch_python",
+            f"-Wl,-rpath,{torch_lib}", "-Wl,-rpath,$ORIGIN", "-o", str(output)]
+
+
 def build(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compile the library; always recompiles (one hipcc per source, in
-    parallel, then one link). Returns the library path."""
+    """Compile the library and the torch operator in front of it; always
+    recompiles (one hipcc per source, in parallel, then one link, then the
+    operator). Returns the library path."""
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     obj_dir = LIB_DIR / "obj"
     obj_dir.mkdir(exist_ok=True)
@@ -88,6 +120,13 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     tmp = LIB_PATH.with_suffix(".so.tmp")
     _run(link_command(objs, tmp))
     os.replace(tmp, LIB_PATH)
+    op = torch_op_path()
+    op_tmp = op.with_suffix(".tmp")
+    cmd = torch_op_command(op_tmp)
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    _run(cmd)
+    os.replace(op_tmp, op)
     return LIB_PATH
 
 

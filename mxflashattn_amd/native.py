@@ -163,6 +163,38 @@ def library() -> ctypes.CDLL:
         return lib
 
 
+_op_lock = threading.Lock()
+_op: object | None = None
+# False forces the ctypes path (for comparisons); the operator is used when built.
+USE_TORCH_OP = True
+
+
+def torch_op():
+    """The torch operator in front of the C ABI (``csrc/torch_op.cpp``), or
+    None when it is not built. It takes the common one-token decode in C++
+    and hands every other call back (returns None) to the ctypes path."""
+    global _op
+    if _op is None:
+        with _op_lock:
+            if _op is None:
+                import importlib.util
+                import sysconfig
+
+                library()  # the operator links this library: load and check it first
+                path = LIB_PATH.parent / ("_mxfa_torch" + sysconfig.get_config_var("EXT_SUFFIX"))
+                module = False
+                if path.exists():
+                    spec = importlib.util.spec_from_file_location("_mxfa_torch", path)
+                    module = importlib.util.module_from_spec(spec)
+                    spec.loader.exec_module(module)
+                    if module.abi_version() != ABI_VERSION:
+                        raise NativeLibraryError(
+                            f"torch operator ABI {module.abi_version()} does not match "
+                            f"{ABI_VERSION}")
+                _op = module
+    return _op or None
+
+
 def unavailable_reason() -> str | None:
     """None when the library loads, else the reason it does not."""
     try:
@@ -247,6 +279,13 @@ class _Workspace:
 
 
 WORKSPACE = _Workspace()
+
+
+def retired_workspace_bytes() -> int:
+    """Bytes of workspaces replaced by larger ones and kept alive, over the
+    ctypes path's cache and the torch operator's."""
+    op = torch_op()
+    return WORKSPACE.retired_bytes() + (op.workspace_bytes()[1] if op is not None else 0)
 
 
 def _dtype_code(t: torch.Tensor) -> int:
@@ -550,6 +589,15 @@ def paged_decode_split(
     query at position p and key j, after the cap.
     num_splits: balanced work ranges per kv head (default: split_heuristic).
     """
+    if (USE_TORCH_OP and k_scale is None and v_scale is None and window_left < 0
+            and sinks is None and softcap == 0 and alibi_slopes is None
+            and (q.dim() == 3 or q.shape[1] == 1)):
+        op = torch_op()
+        if op is not None:
+            result = op.decode(q, k_cache, v_cache, block_table, cache_seqlens,
+                               float(softmax_scale), out, num_splits or 0, int(seqlen_add))
+            if result is not None:
+                return result
     if out is not None and (out.data_ptr() % 8 or any(st % 4 for st in out.stride()[:-1])):
         # The kernels store 8-byte pieces of each output row; a view that is
         # not laid out for that gets the result through a packed copy.

@@ -271,11 +271,11 @@ def test_workspace_growth_after_capture_keeps_captured_buffer(device):
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
         call(small, out)
-    retired = native.WORKSPACE.retired_bytes()
+    retired = native.retired_workspace_bytes()
     with torch.cuda.stream(stream):
         big = call(large)  # needs a larger workspace on the same stream
     torch.cuda.synchronize()
-    assert native.WORKSPACE.retired_bytes() > retired  # the workspace grew
+    assert native.retired_workspace_bytes() > retired  # the workspace grew
     # Fresh allocations of the retired size must not alias the captured buffer.
     fillers = [torch.full((1 << 20,), 3, dtype=torch.uint8, device=device) for _ in range(8)]
     torch.cuda.synchronize()
@@ -290,3 +290,25 @@ def test_workspace_growth_after_capture_keeps_captured_buffer(device):
     assert max_err(eager, port_kvcache(small)) <= TOL[torch.bfloat16]
     assert max_err(big, port_kvcache(large)) <= TOL[torch.bfloat16]
     del graph
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+def test_torch_operator_and_ctypes_paths_agree_bitwise(device, monkeypatch, dtype):
+    """The C++ operator (csrc/torch_op.cpp) takes the common one-token call;
+    the ctypes binding takes it when the operator is switched off. Same C ABI,
+    same kernels: the outputs are the same bits, with a strided q and out."""
+    assert native.torch_op() is not None, "the torch operator is not built"
+    b = make_paged_batch(7, 32, 8, 128, dtype, torch.tensor([1, 17, 300, 2, 2049, 64, 5]),
+                         seed=71).to(device)
+    q = fused_qkv_query(b, device).view(b.batch, 1, 32, 128)
+    outs = []
+    for use_op in (True, False):
+        monkeypatch.setattr(native, "USE_TORCH_OP", use_op)
+        buf = torch.full((b.batch, 1, 40, 128), 3.0, device=device, dtype=dtype)
+        got = native.paged_decode_split(q, b.k_cache, b.v_cache, b.block_table,
+                                        b.cache_seqlens, b.scale, out=buf[:, :, 4:36])
+        torch.cuda.synchronize()
+        assert got.data_ptr() == buf[:, :, 4:36].data_ptr()
+        outs.append(buf.clone())
+    assert torch.equal(outs[0], outs[1])
+    assert max_err(outs[0][:, :, 4:36], port_kvcache(b)) <= TOL[dtype]
