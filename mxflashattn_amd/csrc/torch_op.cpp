@@ -146,8 +146,10 @@ py::object decode(const at::Tensor &q, const at::Tensor &k_cache, const at::Tens
     bhd_strides(out, o_sb, o_sh);
   }
   void *stream = (void *)c10::hip::getCurrentHIPStream(device.index()).stream();
+  // num_splits < 0: the heuristic's count; 0 is invalid (the binding's path reports it).
+  if (num_splits == 0 || num_splits > 65535) return py::none();
   int ns = (int)num_splits;
-  if (ns <= 0 && mxfa_split_heuristic((int)batch, (int)hq, (int)hkv, (int)hd, (int)ps,
+  if (ns < 0 && mxfa_split_heuristic((int)batch, (int)hq, (int)hkv, (int)hd, (int)ps,
                                       (int)block_table.size(1), num_cus(device.index()),
                                       &ns) != MXFA_OK)
     return py::none();
@@ -174,7 +176,7 @@ PYBIND11_MODULE(_mxfa_torch, m) {
   m.doc() = "torch operator in front of libmxfa_mi355x's split decode C ABI";
   m.def("decode", &decode, py::arg("q"), py::arg("k_cache"), py::arg("v_cache"),
         py::arg("block_table"), py::arg("cache_seqlens"), py::arg("scale"),
-        py::arg("out") = py::none(), py::arg("num_splits") = 0, py::arg("seqlen_add") = 0);
+        py::arg("out") = py::none(), py::arg("num_splits") = -1, py::arg("seqlen_add") = 0);
   m.def("abi_version", &mxfa_abi_version);
   m.def("workspace_bytes", &workspace_bytes,
         "(bytes of live workspaces, bytes of workspaces replaced by larger ones)");

@@ -595,7 +595,8 @@ def paged_decode_split(
         op = torch_op()
         if op is not None:
             result = op.decode(q, k_cache, v_cache, block_table, cache_seqlens,
-                               float(softmax_scale), out, num_splits or 0, int(seqlen_add))
+                               float(softmax_scale), out,
+                               -1 if num_splits is None else int(num_splits), int(seqlen_add))
             if result is not None:
                 return result
     if out is not None and (out.data_ptr() % 8 or any(st % 4 for st in out.stride()[:-1])):

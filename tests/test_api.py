@@ -347,3 +347,29 @@ def test_varlen_route_declines_multi_token_queries():
     assert decode.route_varlen(q, k, k, k, [0, 2, 3], [0, 3, 5], 3, 0.1,
                                False).reason == "varlen_query_length_above_one"
     assert decode.route_varlen(q, k, k, k, [0, 1, 2, 3], [0, 1, 3, 5], 3, 0.1, False).reason is None
+
+
+@pytest.mark.parametrize("case,reason", [
+    ("batch", "batch_16001_exceeds_16000"),
+    ("misaligned cache", "cache_not_16_byte_aligned"),
+    ("cache strides", "cache_strides_not_multiples_of_16_bytes"),
+    ("table capacity", "block_table_capacity_exceeds_kernel_limit"),
+])
+def test_kvcache_route_declines_what_the_kernels_cannot_address(case, reason):
+    # Calls the C ABI would reject are handed down the chain with a reason,
+    # before any launch (the ABI's limits: csrc/split_decode.hip).
+    batch, width = (16001, 2) if case == "batch" else (4, 2)
+    if case == "table capacity":
+        width = (1 << 30) // 16 + 1
+    q = fake_cuda(torch.empty(batch, 1, 8, 64, dtype=torch.float16))
+    base = torch.empty(10 * 16 * 2 * 64 + 8, dtype=torch.float16)
+    if case == "misaligned cache":
+        cache = base[4:4 + 10 * 16 * 2 * 64].view(10, 16, 2, 64)  # 8-byte offset
+    elif case == "cache strides":
+        cache = torch.empty(10, 16, 2, 68, dtype=torch.float16)[..., :64]  # 136-byte rows
+    else:
+        cache = base[:10 * 16 * 2 * 64].view(10, 16, 2, 64)
+    cache = fake_cuda(cache)
+    table = torch.empty(batch, 1, dtype=torch.int32).expand(batch, width)  # shape only
+    route = decode.route_kvcache(q, cache, cache, None, None, None, table, 0.1, False)
+    assert route.reason == reason
