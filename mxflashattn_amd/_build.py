@@ -101,15 +101,19 @@ def torch_op_command(output: Path) -> list[str]:
             f"-Wl,-rpath,{torch_lib}", "-Wl,-rpath,$ORIGIN", "-o", str(output)]
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> Path:
+def build(verbose: bool = False, jobs: int | None = None, lib_path: Path = LIB_PATH,
+          extra: tuple[str, ...] = (), torch_op: bool = True) -> Path:
     """Compile the library and the torch operator in front of it; always
     recompiles (one hipcc per source, in parallel, then one link, then the
-    operator). Returns the library path."""
-    LIB_DIR.mkdir(parents=True, exist_ok=True)
-    obj_dir = LIB_DIR / "obj"
+    operator). ``lib_path`` and ``extra`` hipcc flags give other builds of the
+    same sources (the profiling build of wave_timeline). Returns the library
+    path."""
+    lib_dir = lib_path.parent
+    lib_dir.mkdir(parents=True, exist_ok=True)
+    obj_dir = lib_dir / "obj"
     obj_dir.mkdir(exist_ok=True)
     objs = [obj_dir / (Path(name).stem + ".o") for name in SOURCES]
-    cmds = [compile_command(CSRC_DIR / name, obj) for name, obj in zip(SOURCES, objs)]
+    cmds = [compile_command(CSRC_DIR / name, obj, extra) for name, obj in zip(SOURCES, objs)]
     if verbose:
         for cmd in cmds:
             print(" ".join(cmd), flush=True)
@@ -117,9 +121,11 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
         for future in [pool.submit(_run, cmd) for cmd in cmds]:
             future.result()
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+    tmp = lib_path.with_suffix(".so.tmp")
     _run(link_command(objs, tmp))
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, lib_path)
+    if not torch_op:
+        return lib_path
     op = torch_op_path()
     op_tmp = op.with_suffix(".tmp")
     cmd = torch_op_command(op_tmp)
@@ -127,7 +133,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
         print(" ".join(cmd), flush=True)
     _run(cmd)
     os.replace(op_tmp, op)
-    return LIB_PATH
+    return lib_path
 
 
 if __name__ == "__main__":

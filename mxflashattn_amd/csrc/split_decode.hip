@@ -153,6 +153,10 @@ static int check_split_args(const SplitArgs &a) {
   return MXFA_OK;
 }
 
+#ifdef MXFA_WAVE_STAMPS
+static unsigned long long *g_wave_stamps = nullptr;
+#endif
+
 static DecodeParams make_params(const SplitArgs &a, const Grid &g) {
   const WsLayout w = ws_layout(a.batch, a.hq * a.ql, a.hd, a.num_splits);
   const int64_t esz = a.fp8 ? 1 : 2;
@@ -195,6 +199,9 @@ static DecodeParams make_params(const SplitArgs &a, const Grid &g) {
   p.max_len = a.btw * a.ps;
   p.num_pages = a.num_pages;
   p.num_ranges = a.num_splits;
+#ifdef MXFA_WAVE_STAMPS
+  p.stamps = g_wave_stamps;
+#endif
   return p;
 }
 
@@ -345,6 +352,14 @@ using namespace mxfa;
 extern "C" {
 
 int mxfa_abi_version(void) { return MXFA_ABI_VERSION; }
+
+#ifdef MXFA_WAVE_STAMPS
+// Profiling builds only (not part of the C ABI): device buffer of 65536 x 8
+// words that later partial-kernel launches stamp, or nullptr to stop.
+void mxfa_wave_stamps_set(void *device_buffer) {
+  g_wave_stamps = (unsigned long long *)device_buffer;
+}
+#endif
 
 const char *mxfa_strerror(int code) {
   switch (code) {

@@ -129,6 +129,9 @@ struct DecodeParams {
   int max_len;  // block_table_width * page_size
   int num_pages;
   int num_ranges;
+#ifdef MXFA_WAVE_STAMPS
+  unsigned long long *stamps;  // profiling builds: 8 words per wave (see wave_stamp)
+#endif
 };
 
 struct Grid {
@@ -475,6 +478,27 @@ struct Tile {
   int flags;
   int pg;  // page id (block-table entry), page-uniform tiles only
 };
+
+// Profiling builds (-DMXFA_WAVE_STAMPS) record, per wave, the real-time clock
+// (100 MHz) at kernel entry [0], after the tile scan [1], when the first
+// tiles' loads are issued [2] and at the end [3], with the tiles [4], a valid
+// flag [5], the workgroup [6] and the kv head [7]. Other builds compile none
+// of it.
+__device__ __forceinline__ void wave_stamp(const DecodeParams &p, int slot,
+                                           unsigned long long value) {
+#ifdef MXFA_WAVE_STAMPS
+  const unsigned wave = ((blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+  if (p.stamps && (threadIdx.x & 63) == 0 && wave < 65536) p.stamps[wave * 8 + slot] = value;
+#endif
+}
+
+__device__ __forceinline__ unsigned long long wave_clock() {
+#ifdef MXFA_WAVE_STAMPS
+  return __builtin_amdgcn_s_memrealtime();
+#else
+  return 0;
+#endif
+}
 
 // One wave: the tiles [lo, hi) of kv head kvh, range rr of R. HR = DPP rows
 // holding used columns (GQ*QL <= 4 HR), T = element type of q, out and the MFMA
@@ -874,6 +898,7 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   });
   const int ntiles = hi - lo;
   int t = lo;
+  wave_stamp(p, 2, wave_clock());
   auto step = [&](auto kc) {
     constexpr int k = decltype(kc)::value;
     constexpr int kn = (k + NBUF - 1) % NBUF;  // holds tile t + NBUF - 1
@@ -908,6 +933,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(DecodePara
   extern __shared__ int32_t s_tiles[];  // [B + 1]
   __shared__ int s_wave_tot[WAVES];
 
+  const unsigned long long t_entry = wave_clock();
   tile_prefix<kThreads, kExtras>(p, s_tiles, s_wave_tot);  // ends with a barrier
   zero_empty<HD, kThreads>(p, s_tiles);
   const int B = p.batch;
@@ -924,7 +950,14 @@ __global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(DecodePara
   const int rr = blockIdx.y * p.subs + sub;
   if (sub >= p.subs || kvh >= p.hkv || rr >= R) return;
   const int lo = range_lo(rr, R, NT), hi = range_lo(rr + 1, R, NT);
+  wave_stamp(p, 0, t_entry);
+  wave_stamp(p, 1, wave_clock());
   run_range<HD, HR, T, kF8, kLanePages, NBUF, kExtras>(p, s_tiles, kvh, rr, R, NT, lo, hi);
+  wave_stamp(p, 3, wave_clock());
+  wave_stamp(p, 4, hi - lo);
+  wave_stamp(p, 5, 1);
+  wave_stamp(p, 6, blockIdx.y * gridDim.x + blockIdx.x);
+  wave_stamp(p, 7, kvh);
 }
 
 // Merge of two partial states (max, weight, accumulator) in the base-2 domain.
