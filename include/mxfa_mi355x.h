@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define MXFA_ABI_VERSION 9
+#define MXFA_ABI_VERSION 10
 
 /* Return codes. */
 #define MXFA_OK 0
@@ -49,6 +49,17 @@ extern "C" {
 #define MXFA_DTYPE_BF16 1
 #define MXFA_DTYPE_FP8_E4M3 2 /* KV caches only (OCP e4m3fn) */
 
+/*
+ * num_splits value for the per-sequence kernel: one launch, no workspace.
+ * Every workgroup takes one sequence for one kv head; its four waves take
+ * every fourth 16-token tile each and merge their partial results in LDS.
+ * mxfa_split_heuristic returns it for batches of short sequences (judged by
+ * the block table's capacity, block_table_width * page_size), where it skips
+ * the tile scan and the second launch. Callers may also pass it themselves.
+ * No reference counterpart (the reference always launches partial + combine).
+ */
+#define MXFA_SPLITS_PER_SEQUENCE (-1)
+
 /* ABI version of the loaded library (MXFA_ABI_VERSION). No reference counterpart. */
 int mxfa_abi_version(void);
 
@@ -60,7 +71,12 @@ const char *mxfa_strerror(int code);
  * work split itself happens on the device: the 16-token tiles of all
  * sequences are laid end to end and cut into num_splits equal ranges (fewer
  * when there are fewer tiles), and every (kv head, range) pair is one wave, so
- * the per-CU load is even for any length mix. Integer-only, reads no device data. Replaces the Python loop at
+ * the per-CU load is even for any length mix. When the block table's capacity
+ * C = block_table_width * page_size bounds every sequence to a few tiles
+ * (page_size >= 16 and, for head rows of <= 128 bytes, C <= 768 tokens with
+ * batch * kv_heads * ceil(C / 16) <= 16384; for 256-byte rows C <= 384 with the
+ * same bound; never for longer rows), it returns MXFA_SPLITS_PER_SEQUENCE
+ * instead. Integer-only, reads no device data. Replaces the Python loop at
  * integrations/vllm/vllm_plugin.py:271-276 (NP doubling until B*HKV*NP >= 2048,
  * c_len = ceil(BTW*PS/NP)).
  */
@@ -81,7 +97,8 @@ int mxfa_split_heuristic_fp8(int batch, int q_heads, int kv_heads, int head_dim,
  * per-call at::empty of ows/mdws at csrc_native/m1_binding.cpp:94-96. Layout:
  * piece outputs fp32 [HKV, num_splits, 2, GQ, HD], piece base-2 LSEs fp32
  * [HKV, num_splits, 2, GQ] (HKV * GQ = q_heads), tile prefix sums int32
- * [batch + 1]. Its contents between calls do not matter.
+ * [batch + 1]. Its contents between calls do not matter. 0 bytes for
+ * MXFA_SPLITS_PER_SEQUENCE (the workspace arguments may then be null and 0).
  */
 int mxfa_split_decode_workspace_size(int batch, int q_heads, int head_dim, int num_splits,
                                      size_t *bytes);
@@ -91,7 +108,8 @@ int mxfa_split_decode_workspace_size(int batch, int q_heads, int head_dim, int n
  * first seqlens[b] + seqlen_add tokens of sequence b, gathered through block_table.
  * Two launches on `stream`: the split partial kernel (it writes every sequence
  * that lies inside one work range, zero for empty sequences, and the pieces of
- * the others to the workspace), then the LSE combine kernel. A sequence of
+ * the others to the workspace), then the LSE combine kernel; with num_splits =
+ * MXFA_SPLITS_PER_SEQUENCE one launch of the per-sequence kernel. A sequence of
  * length 0 yields zeros. Calls that share a workspace must not run concurrently.
  *
  * Replaces mxfa_paged_decode_split_launch (csrc_native/m1_kernel.cpp:1206-1211)
@@ -192,7 +210,8 @@ int mxfa_split_decode_multi_launch(
  * LSE of every piece of the other sequences, with the tile prefix sums, to the
  * workspace. Followed by mxfa_split_decode_combine_launch on the same stream it
  * is the same computation as mxfa_split_decode_launch; alone it lets a caller
- * time the dominant kernel or schedule the two stages itself.
+ * time the dominant kernel or schedule the two stages itself. With num_splits
+ * = MXFA_SPLITS_PER_SEQUENCE it runs the per-sequence kernel, the whole call.
  * Counterpart of the paged_decode_v3 launch inside launch_split
  * (csrc_native/m1_kernel.cpp:985-999).
  */
@@ -212,7 +231,9 @@ int mxfa_split_decode_partial_launch(const void *q, int64_t q_stride_b, int64_t 
  * a work range end. The workspace must have been filled by
  * mxfa_split_decode_partial_launch with the same batch, heads, head_dim and
  * num_splits, earlier on the same stream; a workspace holding anything else
- * gives wrong numbers (never an out-of-bounds access).
+ * gives wrong numbers (never an out-of-bounds access). With num_splits =
+ * MXFA_SPLITS_PER_SEQUENCE there is nothing to merge: it returns MXFA_OK and
+ * launches nothing.
  * Counterpart of the split_combine launch (csrc_native/m1_kernel.cpp:1000-1001,
  * kernel :861-888).
  */

@@ -13,4 +13,8 @@ int launch_combine_64(const CombineParams &c, int dtype, hipStream_t st) {
   return launch_combine_hd<64>(c, dtype, st);
 }
 
+int launch_seq_64(const DecodeParams &p, int dtype, bool fp8, hipStream_t st) {
+  return launch_seq_hd<64>(p, dtype, fp8, st);
+}
+
 }  // namespace mxfa

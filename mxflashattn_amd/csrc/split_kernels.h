@@ -49,6 +49,11 @@
 // across the XCDs' separate L2s): sequences that cross a range end fold their
 // pieces with base-2 LSE weights.
 //
+// Per-sequence kernel (one launch, for batches of short sequences): one
+// workgroup per (sequence, kv head); its waves take every S-th tile of the
+// sequence through the same per-wave loop and merge their pieces in LDS, so
+// there is no tile scan, no workspace and no second launch.
+//
 // Several query tokens per sequence (QL, decode with draft tokens): token t
 // sits at position L - QL + t and, with the causal mask, sees keys
 // [0, L - QL + t] (the bottom-right alignment of the reference's mask).
@@ -500,13 +505,21 @@ __device__ __forceinline__ unsigned long long wave_clock() {
 #endif
 }
 
-// One wave: the tiles [lo, hi) of kv head kvh, range rr of R. HR = DPP rows
+// One wave: the tiles [lo, hi) of kv head kvh, range rr. HR = DPP rows
 // holding used columns (GQ*QL <= 4 HR), T = element type of q, out and the MFMA
 // operands, kF8 = e4m3fn caches. Accumulator lane (r, c) holds columns
 // 4r..4r+3, dims c*VD + jb in block jb.
-template <int HD, int HR, typename T, bool kF8, bool kLanePages, int NBUF, bool kExtras>
+//
+// kSeq (per-sequence workgroups): p describes one sequence (batch 1), the wave
+// takes its tiles lo, lo + stride, ... below hi = the sequence's tile count,
+// and writes its one piece (normalised output, base-2 LSE) to LDS at lds_o
+// [C][HD] and lds_lse [C] for the workgroup to merge; s_tiles is not read.
+template <int HD, int HR, typename T, bool kF8, bool kLanePages, int NBUF, bool kExtras,
+          bool kSeq>
 __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *s_tiles, int kvh,
-                                          int rr, int R, int NT, int lo, int hi) {
+                                          int rr, int lo, int hi, int stride, float *lds_o,
+                                          float *lds_lse) {
+  const int tstep = kSeq ? stride : 1;  // tile index step between the wave's tiles
   using E = Elem<T>;
   constexpr int NCH = HD / 32;               // MFMA steps over the head dim
   constexpr int NKL = kF8 ? HD / 64 : NCH;   // 16-byte K loads per lane and tile
@@ -574,8 +587,8 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   // s[b+1] > lo). s is nondecreasing and s[0] = 0 <= lo, so the lanes whose
   // probe passes form a prefix: each round narrows [a, a + n) to one of 64
   // steps (one round for B <= 64, three for B <= 16000).
-  int pb;
-  {
+  int pb = 0;
+  if constexpr (!kSeq) {
     int a = 0, n = B;
     while (n > 1) {
       const int step = (n + 63) >> 6;
@@ -591,13 +604,18 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   // Cursor of the tile builder (runs NBUF tiles ahead of the math). Without a
   // window every sequence starts at its tile 0, so the first page id does not
   // wait for the length.
-  int p_start = rfl(s_tiles[pb]);
-  int p_end = rfl(s_tiles[pb + 1]);
+  int p_start = kSeq ? 0 : rfl(s_tiles[pb]);
+  int p_end = kSeq ? hi : rfl(s_tiles[pb + 1]);
   int p_len = seq_len_of(p.seqlens, pb, p.seqlen_add, p.max_len);
   int p_first = kExtras ? first_tile_of(p_len, p.ql, p.window_left) : 0;  // tile at p_start
   ConstI32 p_bt = as_const(p.bt + (int64_t)pb * p.bt_stride);
 
   auto make_tile = [&](int t, Tile &d, int (&lpg)[NPG]) {
+    // kSeq: the page id is read before the range test, clamped into the
+    // table row, so without a window it does not wait for the length.
+    int pg_early = 0;
+    if constexpr (kSeq && !kLanePages)
+      pg_early = p_bt[min((t - p_start + p_first) * kTile, p.max_len - 1) >> p.ps_log2];
     if (t >= hi) {
       d.b = pb;
       d.tok0 = 0;
@@ -609,23 +627,30 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
       for (int i = 0; i < NPG; ++i) lpg[i] = 0;
       return;
     }
-    if (t >= p_end) {  // next sequence with tiles (rare, wave-uniform)
-      do {
-        ++pb;
-        p_start = p_end;
-        p_end = rfl(s_tiles[pb + 1]);
-      } while (t >= p_end);
-      p_len = seq_len_of(p.seqlens, pb, p.seqlen_add, p.max_len);
-      p_first = kExtras ? first_tile_of(p_len, p.ql, p.window_left) : 0;
-      p_bt = as_const(p.bt + (int64_t)pb * p.bt_stride);
+    if constexpr (!kSeq) {
+      if (t >= p_end) {  // next sequence with tiles (rare, wave-uniform)
+        do {
+          ++pb;
+          p_start = p_end;
+          p_end = rfl(s_tiles[pb + 1]);
+        } while (t >= p_end);
+        p_len = seq_len_of(p.seqlens, pb, p.seqlen_add, p.max_len);
+        p_first = kExtras ? first_tile_of(p_len, p.ql, p.window_left) : 0;
+        p_bt = as_const(p.bt + (int64_t)pb * p.bt_stride);
+      }
     }
     d.b = pb;
     d.tok0 = (t - p_start + p_first) * kTile;
     d.rem = p_len - d.tok0;
     d.valid = min(kTile, d.rem);
-    const bool seq_start = t == p_start, seq_end = d.tok0 + kTile >= p_len;
-    d.flags = ((t == lo || seq_start) ? kFirst : 0) | ((t == hi - 1 || seq_end) ? kLast : 0) |
-              (seq_start ? kSeqStart : 0) | (seq_end ? kSeqEnd : 0) | (t == lo ? kRangeStart : 0);
+    if constexpr (kSeq) {  // one piece per wave, merged in LDS
+      d.flags = (t == lo ? kFirst : 0) | (t + tstep >= hi ? kLast : 0);
+    } else {
+      const bool seq_start = t == p_start, seq_end = d.tok0 + kTile >= p_len;
+      d.flags = ((t == lo || seq_start) ? kFirst : 0) | ((t == hi - 1 || seq_end) ? kLast : 0) |
+                (seq_start ? kSeqStart : 0) | (seq_end ? kSeqEnd : 0) |
+                (t == lo ? kRangeStart : 0);
+    }
     if constexpr (kLanePages) {
       // Per-lane page ids: [0] for this lane's K token, [1+u] for its V tokens.
       // Token positions clamp to the last valid token.
@@ -636,7 +661,7 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
         lpg[1 + u] = p_bt[(d.tok0 + min(4 * row + u, last)) >> p.ps_log2];
       d.pg = 0;
     } else {
-      d.pg = p_bt[d.tok0 >> p.ps_log2];
+      d.pg = kSeq ? pg_early : p_bt[d.tok0 >> p.ps_log2];
     }
   };
 
@@ -721,7 +746,7 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   auto finalize = [&](const Tile &d) {
     const float dt = rows_sum(dsum);  // lane (any row, h): denominator of head h
     const int b = d.b;
-    const bool whole = piece_from_start && (d.flags & kSeqEnd);
+    const bool whole = !kSeq && piece_from_start && (d.flags & kSeqEnd);
     const int slot = piece_first_in_range ? 0 : 1;
     const int64_t pbase = ((int64_t)(kvh * ns + rr) * 2 + slot) * nc;
     static_for<4>([&](auto ic) {
@@ -747,12 +772,14 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
                              vslot * (VD * 2),
                          v, inv);
       } else {
-        float4 *dst = reinterpret_cast<float4 *>(p.ws_o + (pbase + hh) * HD + vslot * VD);
+        float4 *dst = reinterpret_cast<float4 *>(
+            (kSeq ? lds_o + hh * HD : p.ws_o + (pbase + hh) * HD) + vslot * VD);
 #pragma unroll
         for (int j = 0; j < VD / 4; ++j)
           dst[j] = make_float4(v[4 * j] * inv, v[4 * j + 1] * inv, v[4 * j + 2] * inv,
                                v[4 * j + 3] * inv);
-        if (col == 0) p.ws_lse[pbase + hh] = Dh > 0.f ? Mh + __log2f(Dh) : -INFINITY;
+        if (col == 0)
+          (kSeq ? lds_lse[hh] : p.ws_lse[pbase + hh]) = Dh > 0.f ? Mh + __log2f(Dh) : -INFINITY;
       }
     });
   };
@@ -893,27 +920,27 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   int lpg_n[NPG];
   static_for<NBUF>([&](auto ic) {
     constexpr int i = decltype(ic)::value;
-    make_tile(lo + i, sets[i].d, sets[i].lpg);
+    make_tile(lo + i * tstep, sets[i].d, sets[i].lpg);
     if constexpr (i < NBUF - 1) issue(sets[i]);
   });
-  const int ntiles = hi - lo;
+  const int ntiles = kSeq ? (hi - lo + tstep - 1) / tstep : hi - lo;
   int t = lo;
   wave_stamp(p, 2, wave_clock());
   auto step = [&](auto kc) {
     constexpr int k = decltype(kc)::value;
     constexpr int kn = (k + NBUF - 1) % NBUF;  // holds tile t + NBUF - 1
     if constexpr (kLanePages) {
-      make_tile(t + NBUF, dn, lpg_n);
+      make_tile(t + NBUF * tstep, dn, lpg_n);
       issue(sets[kn]);
     } else {
       issue(sets[kn]);
-      make_tile(t + NBUF, dn, lpg_n);
+      make_tile(t + NBUF * tstep, dn, lpg_n);
     }
     compute(sets[k]);
     sets[k].d = dn;
 #pragma unroll
     for (int i = 0; i < NPG; ++i) sets[k].lpg[i] = lpg_n[i];
-    ++t;
+    t += tstep;
   };
   int done = 0;
   for (; done + NBUF <= ntiles; done += NBUF) static_for<NBUF>(step);
@@ -952,7 +979,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(DecodePara
   const int lo = range_lo(rr, R, NT), hi = range_lo(rr + 1, R, NT);
   wave_stamp(p, 0, t_entry);
   wave_stamp(p, 1, wave_clock());
-  run_range<HD, HR, T, kF8, kLanePages, NBUF, kExtras>(p, s_tiles, kvh, rr, R, NT, lo, hi);
+  run_range<HD, HR, T, kF8, kLanePages, NBUF, kExtras, false>(p, s_tiles, kvh, rr, lo, hi, 1,
+                                                             nullptr, nullptr);
   wave_stamp(p, 3, wave_clock());
   wave_stamp(p, 4, hi - lo);
   wave_stamp(p, 5, 1);
@@ -1064,6 +1092,77 @@ __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(CombineP
   }
 }
 
+// Per-sequence workgroups (one launch, no workspace, no tile scan): workgroup
+// (x, b) takes sequence b for kv heads x*KH .. x*KH + KH - 1, KH =
+// heads_per_wg. Wave (kh, s), s < S = subs, takes tiles s, s + S, s + 2S, ...
+// of the sequence for its kv head, so its first page id is read together with
+// the length. Each wave leaves one piece (normalised output and base-2 LSE)
+// in LDS; after a barrier the workgroup folds the S pieces of every (kv head,
+// column) in wave order and rounds the output once. Waves past the sequence's
+// tiles leave an LSE of -inf and are skipped; an empty sequence gets zeros.
+// LDS: WAVES * C * (HD + 1) floats, C = GQ * QL.
+template <int HD, int HR, typename T, bool kF8, bool kLanePages, int NBUF, int WAVES, int OCC,
+          bool kExtras>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(OCC)))
+void seq_decode_kernel(DecodeParams p) {
+  using E = Elem<T>;
+  constexpr int CH = HD / 4;  // float4 chunks per head row
+  extern __shared__ float s_piece[];
+  const int nc = p.gq * p.ql;
+  const int wave = rfl(threadIdx.x >> 6);
+  const int KH = p.heads_per_wg, S = p.subs;
+  const int kh = wave % KH, sub = wave / KH;
+  const int kvh = blockIdx.x * KH + kh;
+  const int b = blockIdx.y;
+  float *const lse_base = s_piece + WAVES * nc * HD;
+  const unsigned long long t_entry = wave_clock();
+  const int L = seq_len_of(p.seqlens, b, p.seqlen_add, p.max_len);
+  const int n = L > 0 ? (kExtras ? tiles_of(L, p.ql, p.window_left) : (L + kTile - 1) / kTile)
+                      : 0;
+  if ((threadIdx.x & 63) < nc) lse_base[wave * nc + (threadIdx.x & 63)] = -INFINITY;
+  if (kvh < p.hkv && sub < n) {
+    DecodeParams v = p;  // the one sequence, as a batch of 1
+    v.q += b * p.q_sb;
+    v.bt += b * p.bt_stride;
+    v.seqlens += b;
+    v.out += b * p.o_sb;
+    v.batch = 1;
+    wave_stamp(p, 0, t_entry);
+    wave_stamp(p, 1, wave_clock());
+    run_range<HD, HR, T, kF8, kLanePages, NBUF, kExtras, true>(
+        v, nullptr, kvh, 0, sub, n, S, s_piece + wave * nc * HD, lse_base + wave * nc);
+    wave_stamp(p, 3, wave_clock());
+    wave_stamp(p, 4, (n - sub + S - 1) / S);
+    wave_stamp(p, 5, 1);
+    wave_stamp(p, 6, blockIdx.y * gridDim.x + blockIdx.x);
+    wave_stamp(p, 7, kvh);
+  }
+  __syncthreads();
+  for (int it = threadIdx.x; it < KH * nc * CH; it += WAVES * 64) {
+    const int cc = it % CH, r = it / CH;
+    const int hh = r % nc, kk = r / nc;
+    const int kv = blockIdx.x * KH + kk;
+    if (kv >= p.hkv) continue;
+    float M = -INFINITY, W = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s2 = 0; s2 < S; ++s2) {
+      const int w = s2 * KH + kk;
+      const float l = lse_base[w * nc + hh];
+      if (l == -INFINITY) continue;  // no piece (or no key seen): its output is not read
+      lse_fold(M, W, acc, l, 1.f, reinterpret_cast<const float4 *>(s_piece + (w * nc + hh) * HD)[cc]);
+    }
+    const int t = hh / p.gq, h = kv * p.gq + (hh - t * p.gq);
+    if (p.sinks) W += fast_exp2(p.sinks[h] * kLog2e - M);  // M = -inf: W = inf, out 0
+    const float inv = W > 0.f ? 1.f / W : 0.f;
+    const uint32_t w0 =
+        (uint32_t)E::narrow(acc.x * inv) | ((uint32_t)E::narrow(acc.y * inv) << 16);
+    const uint32_t w1 =
+        (uint32_t)E::narrow(acc.z * inv) | ((uint32_t)E::narrow(acc.w * inv) << 16);
+    *reinterpret_cast<uint2 *>(p.out + b * p.o_sb + t * p.o_st + h * p.o_sh + cc * 8) =
+        make_uint2(w0, w1);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Launch shapes (host side, shared by the per-head-dim compilation units).
 
@@ -1162,6 +1261,62 @@ int launch_partial_hd(const DecodeParams &p, const Grid &g, int dtype, bool fp8,
                : launch_partial_hr<HD, BF16, false>(p, g, st);
   return fp8 ? launch_partial_hr<HD, F16, true>(p, g, st)
              : launch_partial_hr<HD, F16, false>(p, g, st);
+}
+
+// Per-sequence kernel (seq_decode_kernel): grid (ceil(HKV / KH), B) of
+// kSeqWaves = KH * S waves, KH = p.heads_per_wg, S = p.subs. Four waves of one
+// kv head beat eight (one or two kv heads) on every short-context shape
+// measured. Register budget for two waves per SIMD: four per SIMD spill and
+// measured 3-7 % slower at 16-bit HD 64 (19 % at B 128, 8 kv heads, L <= 512).
+// Head dim 256 gets one wave per SIMD: its two-wave builds spilled 65-200
+// VGPRs and returned wrong outputs (max error 0.6-1.9 on a seeded case, the
+// same case right with one wave per SIMD); nothing spills with one.
+constexpr int kSeqWaves = 4;
+template <int HD>
+constexpr int kSeqOcc = HD >= 256 ? 1 : 2;
+
+// LDS bytes of the per-sequence kernel's pieces.
+inline size_t seq_lds_bytes(int hd, int cols) {
+  return (size_t)kSeqWaves * cols * (hd + 1) * sizeof(float);
+}
+
+template <int HD, int HR, typename T, bool kF8, bool kExtras>
+static void launch_seq_x(const DecodeParams &p, hipStream_t st) {
+  dim3 grid((p.hkv + p.heads_per_wg - 1) / p.heads_per_wg, p.batch);
+  const size_t lds = seq_lds_bytes(HD, p.gq * p.ql);
+  if (p.ps_log2 >= 4)
+    hipLaunchKernelGGL((seq_decode_kernel<HD, HR, T, kF8, false, kNbuf<HD, kF8>, kSeqWaves,
+                                          kSeqOcc<HD>, kExtras>),
+                       grid, dim3(kSeqWaves * 64), lds, st, p);
+  else
+    hipLaunchKernelGGL((seq_decode_kernel<HD, HR, T, kF8, true, 2, kSeqWaves, kSeqOcc<HD>,
+                                          kExtras>),
+                       grid, dim3(kSeqWaves * 64), lds, st, p);
+}
+
+template <int HD, int HR, typename T, bool kF8>
+static int launch_seq_t(const DecodeParams &p, hipStream_t st) {
+  if (p.window_left >= 0 || p.softcap > 0.f || p.sinks || p.alibi)
+    launch_seq_x<HD, HR, T, kF8, true>(p, st);
+  else
+    launch_seq_x<HD, HR, T, kF8, false>(p, st);
+  return hipGetLastError() == hipSuccess ? MXFA_OK : MXFA_ELAUNCH;
+}
+
+template <int HD, typename T, bool kF8>
+static int launch_seq_hr(const DecodeParams &p, hipStream_t st) {
+  switch (head_rows(p.gq * p.ql)) {
+    case 1: return launch_seq_t<HD, 1, T, kF8>(p, st);
+    case 2: return launch_seq_t<HD, 2, T, kF8>(p, st);
+    default: return launch_seq_t<HD, 4, T, kF8>(p, st);
+  }
+}
+
+template <int HD>
+int launch_seq_hd(const DecodeParams &p, int dtype, bool fp8, hipStream_t st) {
+  if (dtype == MXFA_DTYPE_BF16)
+    return fp8 ? launch_seq_hr<HD, BF16, true>(p, st) : launch_seq_hr<HD, BF16, false>(p, st);
+  return fp8 ? launch_seq_hr<HD, F16, true>(p, st) : launch_seq_hr<HD, F16, false>(p, st);
 }
 
 template <int HD>

@@ -5,7 +5,8 @@
 //        num_splits, seqlen_add) takes the common call (one query
 // token per sequence, caches of q's 16-bit type, int32 table and lengths,
 // every tensor on the current GPU with layouts the kernels read in place),
-// launches it on torch's current HIP stream and returns the output. For any
+// launches it on torch's current HIP stream and returns the output.
+// num_splits None is mxfa_split_heuristic's choice. For any
 // other call it launches nothing and returns None; the Python binding then
 // takes the call and gives its usual errors.
 //
@@ -105,8 +106,8 @@ bool bhd_strides(const at::Tensor &t, int64_t &sb, int64_t &sh) {
 
 py::object decode(const at::Tensor &q, const at::Tensor &k_cache, const at::Tensor &v_cache,
                   const at::Tensor &block_table, const at::Tensor &cache_seqlens, double scale,
-                  const c10::optional<at::Tensor> &out_arg, int64_t num_splits,
-                  int64_t seqlen_add) {
+                  const c10::optional<at::Tensor> &out_arg,
+                  const c10::optional<int64_t> &num_splits_arg, int64_t seqlen_add) {
   const at::ScalarType dt = q.scalar_type();
   if (dt != at::kHalf && dt != at::kBFloat16) return py::none();
   if (!q.is_cuda() || k_cache.scalar_type() != dt || v_cache.scalar_type() != dt) return py::none();
@@ -146,17 +147,23 @@ py::object decode(const at::Tensor &q, const at::Tensor &k_cache, const at::Tens
     bhd_strides(out, o_sb, o_sh);
   }
   void *stream = (void *)c10::hip::getCurrentHIPStream(device.index()).stream();
-  // num_splits < 0: the heuristic's count; 0 is invalid (the binding's path reports it).
-  if (num_splits == 0 || num_splits > 65535) return py::none();
-  int ns = (int)num_splits;
-  if (ns < 0 && mxfa_split_heuristic((int)batch, (int)hq, (int)hkv, (int)hd, (int)ps,
-                                      (int)block_table.size(1), num_cus(device.index()),
-                                      &ns) != MXFA_OK)
+  // No num_splits: the heuristic's choice. Values the C ABI rejects (0, below
+  // MXFA_SPLITS_PER_SEQUENCE, above 65535) go to the binding's path, which
+  // reports them.
+  int ns = 0;
+  if (num_splits_arg.has_value()) {
+    const int64_t v = *num_splits_arg;
+    if ((v <= 0 && v != MXFA_SPLITS_PER_SEQUENCE) || v > 65535) return py::none();
+    ns = (int)v;
+  } else if (mxfa_split_heuristic((int)batch, (int)hq, (int)hkv, (int)hd, (int)ps,
+                                  (int)block_table.size(1), num_cus(device.index()),
+                                  &ns) != MXFA_OK) {
     return py::none();
+  }
   size_t ws_bytes = 0;
   if (mxfa_split_decode_workspace_size((int)batch, (int)hq, (int)hd, ns, &ws_bytes) != MXFA_OK)
     return py::none();
-  void *ws = workspace(device, stream, ws_bytes);
+  void *ws = ws_bytes ? workspace(device, stream, ws_bytes) : nullptr;
   const int rc = mxfa_split_decode_launch(
       q.data_ptr(), q_sb, q_sh, k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0),
       k_cache.stride(1), k_cache.stride(2), block_table.data_ptr<int32_t>(), block_table.stride(0),
@@ -176,7 +183,8 @@ PYBIND11_MODULE(_mxfa_torch, m) {
   m.doc() = "torch operator in front of libmxfa_mi355x's split decode C ABI";
   m.def("decode", &decode, py::arg("q"), py::arg("k_cache"), py::arg("v_cache"),
         py::arg("block_table"), py::arg("cache_seqlens"), py::arg("scale"),
-        py::arg("out") = py::none(), py::arg("num_splits") = -1, py::arg("seqlen_add") = 0);
+        py::arg("out") = py::none(), py::arg("num_splits") = py::none(),
+        py::arg("seqlen_add") = 0);
   m.def("abi_version", &mxfa_abi_version);
   m.def("workspace_bytes", &workspace_bytes,
         "(bytes of live workspaces, bytes of workspaces replaced by larger ones)");

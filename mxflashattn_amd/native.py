@@ -24,7 +24,7 @@ LIB_PATH = Path(
     os.environ.get("MXFLASHATTN_AMD_LIB")
     or Path(__file__).resolve().parent / "_lib" / "libmxfa_mi355x.so"
 )
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 MXFA_OK = 0
 MXFA_EUNSUPPORTED = -1
@@ -32,6 +32,9 @@ MXFA_EINVAL = -2
 MXFA_EWORKSPACE = -3
 MXFA_ELAUNCH = -4
 MXFA_ESCRATCH = -5
+# num_splits value of the one-launch per-sequence kernel (MXFA_SPLITS_PER_SEQUENCE):
+# every (sequence, kv head) is one workgroup whose four waves merge in LDS.
+SPLITS_PER_SEQUENCE = -1
 # Workspace of mxfa_split_decode_noalloc_launch (the library's own device array).
 SCRATCH_BYTES = 8 << 20
 
@@ -587,7 +590,9 @@ def paged_decode_split(
     softcap > 0: every scaled score s becomes softcap * tanh(s / softcap).
     alibi_slopes: float32 [HQ]; -slope * |p - j| is added to the score of the
     query at position p and key j, after the cap.
-    num_splits: balanced work ranges per kv head (default: split_heuristic).
+    num_splits: balanced work ranges per kv head, or SPLITS_PER_SEQUENCE for
+    the one-launch per-sequence kernel (default: split_heuristic, which picks
+    the latter for batches of short sequences by the block table's capacity).
     """
     if (USE_TORCH_OP and k_scale is None and v_scale is None and window_left < 0
             and sinks is None and softcap == 0 and alibi_slopes is None
@@ -596,7 +601,8 @@ def paged_decode_split(
         if op is not None:
             result = op.decode(q, k_cache, v_cache, block_table, cache_seqlens,
                                float(softmax_scale), out,
-                               -1 if num_splits is None else int(num_splits), int(seqlen_add))
+                               None if num_splits is None else int(num_splits),
+                               int(seqlen_add))
             if result is not None:
                 return result
     if out is not None and (out.data_ptr() % 8 or any(st % 4 for st in out.stride()[:-1])):
@@ -689,7 +695,8 @@ def split_decode_partial(
     v_scale: torch.Tensor | float | None = None,
 ) -> None:
     """Partial stage only: sequences inside one work range land in ``out``, the
-    pieces of the others in ``workspace``; ``split_decode_combine`` finishes."""
+    pieces of the others in ``workspace``; ``split_decode_combine`` finishes.
+    With num_splits = SPLITS_PER_SEQUENCE this is the whole call (one kernel)."""
     q, block_table, cache_seqlens, out = _prepare(q, k_cache, v_cache, block_table,
                                                   cache_seqlens, out)
     _require_device(q, workspace)

@@ -70,10 +70,17 @@ def test_strerror_is_distinct_per_code(lib):
 
 
 def heuristic_closed_form(b, hq, hkv, hd, ps, btw, cus, elem_bytes=2):
-    # One wave per (kv head, range): a workgroup has max(4, min(HKV, 8 for head
-    # rows of <= 128 bytes, else 4)) waves = min(HKV, waves) kv heads x
-    # waves // that sub-ranges, one workgroup per CU.
-    waves = max(4, min(hkv, 8 if hd * elem_bytes <= 128 else 4))
+    # Short sequences by the table's capacity C = btw * ps (page size >= 16,
+    # B * HKV * ceil(C / 16) <= 16384, C <= 768 for head rows of <= 128 bytes,
+    # C <= 384 for 256-byte rows): the per-sequence kernel.
+    cap, row = btw * ps, hd * elem_bytes
+    if (ps >= 16 and b * hkv * -(-cap // 16) <= 16384
+            and ((row <= 128 and cap <= 768) or (row <= 256 and cap <= 384))):
+        return native.SPLITS_PER_SEQUENCE
+    # Otherwise one wave per (kv head, range): a workgroup has max(4, min(HKV,
+    # 8 for head rows of <= 128 bytes, else 4)) waves = min(HKV, waves) kv heads
+    # x waves // that sub-ranges, one workgroup per CU.
+    waves = max(4, min(hkv, 8 if row <= 128 else 4))
     kh = min(hkv, waves)
     subs = waves // kh
     gx = -(-hkv // kh)
@@ -86,7 +93,18 @@ def heuristic_closed_form(b, hq, hkv, hd, ps, btw, cus, elem_bytes=2):
     (32, 32, 8, 128, 16, 512, 256),    # config 2: 256 CUs x 8 waves / 8 kv heads
     (32, 32, 16, 128, 16, 512, 256),   # GQ2: 16 kv heads, two workgroups per range
     (32, 32, 4, 64, 16, 512, 256),     # GQ8 HD64: two sub-ranges per workgroup
-    (1, 2, 1, 64, 16, 1, 256),         # one tile in total
+    (1, 2, 1, 64, 16, 1, 256),         # one tile in total: per sequence
+    (1, 2, 1, 64, 8, 2, 256),          # one tile, pages of 8: split
+    (4, 8, 2, 64, 16, 32, 256),        # config 1's table: per sequence
+    (128, 16, 8, 64, 16, 32, 256),     # config 3: B * HKV * 32 tiles past the bound
+    (64, 32, 8, 64, 16, 32, 256),      # on the work bound
+    (64, 32, 8, 64, 16, 48, 256),      # C 768: past the work bound
+    (32, 32, 8, 64, 16, 48, 256),      # C 768 inside it
+    (32, 32, 8, 64, 16, 49, 256),      # C 784
+    (8, 32, 8, 128, 16, 24, 256),      # 256-byte rows, C 384
+    (8, 32, 8, 128, 16, 25, 256),      # C 400
+    (8, 32, 8, 128, 64, 6, 256),       # C 384 in pages of 64
+    (8, 16, 4, 256, 16, 4, 256),       # 512-byte rows: always split
     (256, 16, 8, 64, 16, 64, 256),
     (4, 32, 4, 128, 256, 128, 304),    # other CU count
     (16384, 64, 8, 128, 16, 4096, 256),
@@ -110,7 +128,14 @@ def test_split_heuristic_known_values():
     assert native.split_heuristic(32, 32, 8, 64, 16, 512, 256) == 256
     assert native.split_heuristic(32, 32, 16, 128, 16, 512, 256) == 64
     assert native.split_heuristic(4, 8, 2, 64, 16, 128, 256) == 512
-    assert native.split_heuristic(1, 2, 1, 64, 16, 1, 256) == 1
+    assert native.split_heuristic(1, 2, 1, 64, 16, 1, 256) == native.SPLITS_PER_SEQUENCE
+    assert native.SPLITS_PER_SEQUENCE == -1
+    # config 1 (table of 32 pages of 16) and config 3 (B128, 8 kv heads, same table).
+    assert native.split_heuristic(4, 8, 2, 64, 16, 32, 256) == -1
+    assert native.split_heuristic(128, 16, 8, 64, 16, 32, 256) == 256
+    # fp8 HD 128 has 128-byte rows: the 16-bit HD 64 bounds.
+    assert native.split_heuristic(32, 32, 8, 128, 16, 48, 256, True) == -1
+    assert native.split_heuristic(32, 32, 8, 128, 16, 48, 256) == 128
     # fp8 config 2: eight waves hold all 8 kv heads, one workgroup per range.
     assert native.split_heuristic(32, 32, 8, 128, 16, 512, 256, True) == 256
     assert native.split_heuristic(32, 32, 4, 128, 16, 512, 256, True) == 256
@@ -139,6 +164,14 @@ def test_workspace_size_rejects_bad_sizes(lib):
     assert lib.mxfa_split_decode_workspace_size(0, 32, 128, 4, ctypes.byref(out)) == -2
     assert lib.mxfa_split_decode_workspace_size(1, 32, 128, 0, ctypes.byref(out)) == -2
     assert lib.mxfa_split_decode_workspace_size(1, 32, 128, 4, None) == -2
+    assert lib.mxfa_split_decode_workspace_size(1, 32, 128, -2, ctypes.byref(out)) == -2
+
+
+def test_per_sequence_kernel_needs_no_workspace(lib):
+    assert native.workspace_size(32, 32, 128, native.SPLITS_PER_SEQUENCE) == 0
+    # Nothing to merge: the combine stage returns at once, launching nothing.
+    assert lib.mxfa_split_decode_combine_launch(None, 0, None, 0, 0, 32, 32, 8, 128, 1, -1,
+                                                None) == native.MXFA_OK
 
 
 FAKE = 0x100000  # 16-byte aligned, never dereferenced: every case below fails a host check
@@ -165,6 +198,13 @@ def decode_args(**over):
     (dict(o_sh=130), -2), (dict(out=FAKE + 2), -2),
     (dict(c_st=64), -2), (dict(q_sh=64), -2),  # overlapping rows
     (dict(ws=None), -3), (dict(ws=FAKE + 8), -3), (dict(ws_bytes=1000), -3),
+    # num_splits: ranges >= 1 or the per-sequence kernel (-1), which needs no
+    # workspace but keeps every other check; its pieces live in LDS (64 KB at
+    # most: HD 256 with 16 columns does not fit).
+    (dict(ns=-2), -2), (dict(ns=-1, batch=0), -2), (dict(ns=-1, hd=96), -1),
+    (dict(ns=-1, q=FAKE + 2), -2), (dict(ns=-1, ws=None, ws_bytes=0, out=None), -2),
+    (dict(ns=-1, hd=256, hq=128, q_sb=128 * 256, q_sh=256, o_sb=128 * 256, o_sh=256,
+          c_sp=16 * 8 * 256, c_st=8 * 256, c_sh=256), -1),
 ])
 def test_decode_launch_rejects_before_launching(lib, over, code):
     assert lib.mxfa_split_decode_launch(*decode_args(**over)) == code

@@ -48,8 +48,9 @@ def test_cells_ragged_match_oracle(device, dtype, head_dim, gq):
     lengths = torch.tensor([1, 15, 16, 17, 300, 1000])
     b = make_paged_batch(6, 2 * gq, 2, head_dim, dtype, lengths, seed=11 + gq).to(device)
     expected = oracle_out(b)
-    # num_splits: one range per kv head, a few, and more ranges than tiles.
-    for ns in (None, 1, 3, 16, 200):
+    # num_splits: one range per kv head, a few, more ranges than tiles, and
+    # the per-sequence kernel.
+    for ns in (None, 1, 3, 16, 200, native.SPLITS_PER_SEQUENCE):
         kw = {} if ns is None else dict(num_splits=ns)
         got = run_native(b, **kw)
         assert torch.isfinite(got.float()).all()
@@ -65,6 +66,8 @@ def test_page_sizes(device, page_size, head_dim):
     expected = oracle_out(b)
     assert max_err(run_native(b), expected) <= TOL[torch.float16]
     assert max_err(run_native(b, num_splits=12), expected) <= TOL[torch.float16]
+    assert max_err(run_native(b, num_splits=native.SPLITS_PER_SEQUENCE),
+                   expected) <= TOL[torch.float16]
 
 
 def test_single_token_returns_v_row_exactly(device):
@@ -199,7 +202,7 @@ def test_kv_head_counts(device, hq, hkv, head_dim):
     lengths = torch.tensor([1, 40, 700, 16, 33])
     b = make_paged_batch(5, hq, hkv, head_dim, torch.bfloat16, lengths, seed=21).to(device)
     expected = oracle_out(b)
-    for ns in (None, 1, 2, 5, 64):
+    for ns in (None, 1, 2, 5, 64, native.SPLITS_PER_SEQUENCE):
         kw = {} if ns is None else dict(num_splits=ns)
         assert max_err(run_native(b, **kw), expected) <= TOL[torch.bfloat16], ns
 
@@ -211,6 +214,7 @@ def test_back_to_back_calls_of_changing_shapes_share_the_workspace(device):
         (6, 32, 8, 128, torch.bfloat16, torch.tensor([900, 17, 2048, 1, 300, 64]), 40),
         (3, 16, 4, 64, torch.float16, torch.tensor([4000, 5, 129]), 200),
         (6, 32, 8, 128, torch.bfloat16, torch.tensor([900, 17, 2048, 1, 300, 64]), 7),
+        (3, 16, 4, 64, torch.float16, torch.tensor([4000, 5, 129]), native.SPLITS_PER_SEQUENCE),
     ]
     batches = [make_paged_batch(*s[:6], seed=30 + i).to(device) for i, s in enumerate(shapes)]
     expected = [oracle_out(b) for b in batches]
@@ -270,7 +274,8 @@ def test_partial_then_combine_equals_one_launch(device):
     assert max_err(one[keep], oracle_out(sub)) <= TOL[torch.bfloat16]
 
 
-def test_graph_replays_match_eager(device):
+@pytest.mark.parametrize("ns", [None, native.SPLITS_PER_SEQUENCE], ids=["split", "per_seq"])
+def test_graph_replays_match_eager(device, ns):
     # One decode call captured in a HIP graph (the workspace allocated by an
     # eager call on the capture stream first) and replayed several times with
     # unrelated eager work between replays: every replay equals the eager call.
@@ -280,13 +285,13 @@ def test_graph_replays_match_eager(device):
     out = torch.empty_like(b.q)
     with torch.cuda.stream(stream):
         native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
-                                  b.scale, out=out)
+                                  b.scale, out=out, num_splits=ns)
         eager = out.clone()
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
         native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
-                                  b.scale, out=out)
+                                  b.scale, out=out, num_splits=ns)
     for i in range(4):
         out.fill_(float("nan"))
         with torch.cuda.stream(stream):
@@ -334,7 +339,7 @@ def test_maximum_batch(device):
     expected = torch.from_numpy(c_oracle.paged_decode_f64(
         b.q.cpu(), b.k_cache.cpu(), b.v_cache.cpu(), b.block_table.cpu(), b.cache_seqlens.cpu(),
         b.scale)).reshape(b.q.shape)
-    for ns in (None, 4096):
+    for ns in (None, 4096, native.SPLITS_PER_SEQUENCE):
         kw = {} if ns is None else dict(num_splits=ns)
         assert max_err(run_native(b, **kw), expected) <= TOL[torch.float16]
 
@@ -347,6 +352,8 @@ def test_most_splits_and_largest_page(device):
     expected = oracle_out(b)
     assert max_err(run_native(b, num_splits=65535), expected) <= TOL[torch.bfloat16]
     assert max_err(run_native(b), expected) <= TOL[torch.bfloat16]
+    assert max_err(run_native(b, num_splits=native.SPLITS_PER_SEQUENCE),
+                   expected) <= TOL[torch.bfloat16]
 
 
 def test_long_context(device):

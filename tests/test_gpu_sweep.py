@@ -10,7 +10,10 @@ attention sinks and/or soft-capping to every case (the extended kernel
 instantiation), and ALiBi slopes to about half of them (drawn from a stream of
 their own). A third sweep redraws each case as a causal query of more than 16
 columns (QL x GQ up to 64: launches of token chunks), with the extras of the
-second sweep on half of them. Seeds are fixed: every run checks the same cases.
+second sweep on half of them. A fourth runs cases of all three kinds through
+the per-sequence kernel (num_splits = SPLITS_PER_SEQUENCE), whose pieces live
+in LDS: a launch of 16 columns at head dim 256 does not fit and must be
+refused. Seeds are fixed: every run checks the same cases.
 """
 
 from __future__ import annotations
@@ -101,6 +104,12 @@ def test_random_chunked_sweep(device, seed):
     run_case(device, seed, extended=seed % 2 == 0, chunked_query=True)
 
 
+@pytest.mark.parametrize("seed", range(360, 480))
+def test_random_per_sequence_sweep(device, seed):
+    run_case(device, seed, extended=seed % 3 == 1, chunked_query=seed % 3 == 2,
+             per_sequence=True)
+
+
 def chunked(c: dict, seed: int) -> dict:
     """The case as a causal query past the kernel's 16 columns (GQ >= 2)."""
     r = random.Random(30_000 + seed)
@@ -109,10 +118,13 @@ def chunked(c: dict, seed: int) -> dict:
     return dict(c, gq=gq, ql=ql, causal=True)
 
 
-def run_case(device, seed: int, extended: bool, chunked_query: bool = False):
+def run_case(device, seed: int, extended: bool, chunked_query: bool = False,
+             per_sequence: bool = False):
     c = draw(seed)
     if chunked_query:
         c = chunked(c, seed)
+    if per_sequence:
+        c = dict(c, ns=native.SPLITS_PER_SEQUENCE)
     hq = c["hkv"] * c["gq"]
     b = make_paged_batch(c["batch"], hq, c["hkv"], c["hd"], c["dtype"],
                          torch.tensor(c["lengths"]), page_size=c["ps"], seed=1000 + seed,
@@ -139,6 +151,13 @@ def run_case(device, seed: int, extended: bool, chunked_query: bool = False):
     if chunked_query:
         assert c["ql"] * c["gq"] > 16 and c["causal"]
     sinks, alibi = extras["sinks"], extras["alibi"]
+    cols = min(c["ql"], 16 // c["gq"]) * c["gq"]  # query columns of one launch
+    if per_sequence and 4 * cols * (c["hd"] + 1) * 4 > 64 << 10:
+        with pytest.raises(native.UnsupportedConfig, match="mxfa_split_decode"):
+            native.paged_decode_split(q, kd, vd, b.block_table.to(device),
+                                      b.cache_seqlens.to(device), b.scale, out=out,
+                                      causal=c["causal"], window_left=extras["window"], **kw)
+        return
     got = native.paged_decode_split(q, kd, vd, b.block_table.to(device),
                                     b.cache_seqlens.to(device), b.scale, out=out,
                                     causal=c["causal"], window_left=extras["window"],

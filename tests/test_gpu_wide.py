@@ -36,6 +36,13 @@ def max_err(actual: torch.Tensor, expected: torch.Tensor) -> float:
     return (actual.double().cpu() - expected.double().cpu()).abs().max().item()
 
 
+def per_sequence(head_dim: int, gq: int, ql: int = 1) -> tuple:
+    """(SPLITS_PER_SEQUENCE,) when one launch's pieces fit the per-sequence
+    kernel's 64 KB of LDS (4 waves x columns x (HD + 1) floats), else ()."""
+    cols = min(ql, 16 // gq) * gq
+    return (native.SPLITS_PER_SEQUENCE,) if 16 * cols * (head_dim + 1) <= 64 << 10 else ()
+
+
 def decode(b, k_cache=None, v_cache=None, **kw) -> torch.Tensor:
     out = native.paged_decode_split(b.q, b.k_cache if k_cache is None else k_cache,
                                     b.v_cache if v_cache is None else v_cache, b.block_table,
@@ -51,7 +58,7 @@ def test_group_sizes_and_head_dims(device, dtype, head_dim, gq):
     lengths = torch.tensor([1, 17, 300, 0, 1000])
     b = make_paged_batch(5, 2 * gq, 2, head_dim, dtype, lengths, seed=30 + gq).to(device)
     expected = f64_expected(b)
-    for ns in (None, 1, 7, 64):
+    for ns in (None, 1, 7, 64) + per_sequence(head_dim, gq):
         kw = {} if ns is None else dict(num_splits=ns)
         got = decode(b, **kw)
         assert torch.isfinite(got.float()).all()
@@ -110,7 +117,7 @@ def test_fp8_cache_matches_oracle(device, dtype, head_dim, gq):
     k8, v8 = fp8_caches(b, device)
     expected = fp8_expected(b, k8, v8, 2.0, 0.5)
     ks, vs = scalar(2.0, device), scalar(0.5, device)
-    for ns in (None, 1, 5, 40):
+    for ns in (None, 1, 5, 40) + per_sequence(head_dim, gq):
         kw = {} if ns is None else dict(num_splits=ns)
         got = decode(b, k8, v8, k_scale=ks, v_scale=vs, **kw)
         assert torch.isfinite(got.float()).all()
@@ -269,7 +276,7 @@ def test_query_tokens_match_reference(device, dtype, head_dim, ql, gq, causal):
     b = make_paged_batch(6, 2 * gq, 2, head_dim, dtype, lengths, seed=60 + ql).to(device)
     b = with_query_tokens(b, ql, 61)
     expected = port_expected(b, causal)
-    for ns in (None, 1, 9, 64):
+    for ns in (None, 1, 9, 64, native.SPLITS_PER_SEQUENCE):
         kw = {} if ns is None else dict(num_splits=ns)
         got = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table,
                                         b.cache_seqlens, b.scale, causal=causal, **kw)
@@ -384,7 +391,7 @@ def test_window_matches_reference(device, dtype, head_dim, window, ql, gq, causa
     if ql == 1:
         b.q = b.q[:, 0]  # [B, HQ, HD]: the one-token form takes the window too
     expected = port_expected(b if ql > 1 else with_query_tokens_view(b), causal, window)
-    for ns in (None, 1, 9, 64):
+    for ns in (None, 1, 9, 64, native.SPLITS_PER_SEQUENCE):
         kw = {} if ns is None else dict(num_splits=ns)
         got = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table,
                                         b.cache_seqlens, b.scale, causal=causal,
@@ -469,7 +476,7 @@ def test_sinks_match_reference(device, dtype, head_dim, ql, gq, causal, window):
     b = with_query_tokens(b, ql, 91)
     sinks = sink_values(2 * gq, device)
     expected = port_expected(b, causal, window, sinks)
-    for ns in (None, 1, 9, 64):
+    for ns in (None, 1, 9, 64, native.SPLITS_PER_SEQUENCE):
         kw = {} if ns is None else dict(num_splits=ns)
         got = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table,
                                         b.cache_seqlens, b.scale, causal=causal,
@@ -559,7 +566,7 @@ def test_softcap_matches_reference(device, dtype, head_dim, cap, ql, gq, causal,
     b.q = (b.q.float() * 3).to(dtype)  # scores of a few units, where the cap bites
     sinks = sink_values(2 * gq, device) if with_sinks else None
     expected = port_expected(b, causal, window, sinks, cap)
-    for ns in (None, 1, 9):
+    for ns in (None, 1, 9) + per_sequence(head_dim, gq, ql):
         kw = {} if ns is None else dict(num_splits=ns)
         got = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table,
                                         b.cache_seqlens, b.scale, causal=causal,
@@ -611,7 +618,7 @@ def test_alibi_matches_reference(device, dtype, head_dim, ql, gq, causal, window
     slopes = alibi_slopes(2 * gq, device)
     sinks = sink_values(2 * gq, device) if with_sinks else None
     expected = port_expected(b, causal, window, sinks, cap, slopes)
-    for ns in (None, 1, 9):
+    for ns in (None, 1, 9) + per_sequence(head_dim, gq, ql):
         kw = {} if ns is None else dict(num_splits=ns)
         got = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table,
                                         b.cache_seqlens, b.scale, causal=causal,
@@ -627,7 +634,7 @@ def test_alibi_with_negative_slopes_and_zero_slopes(device):
     b = make_paged_batch(3, 8, 2, 128, torch.bfloat16, lengths, seed=113).to(device)
     for slopes in (alibi_slopes(8, device, -0.05), torch.zeros(8, device=device)):
         expected = port_expected(b, False, -1, None, 0.0, slopes)
-        for ns in (None, 1, 7):
+        for ns in (None, 1, 7, native.SPLITS_PER_SEQUENCE):
             kw = {} if ns is None else dict(num_splits=ns)
             got = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table,
                                             b.cache_seqlens, b.scale, alibi_slopes=slopes,
@@ -684,7 +691,7 @@ def test_causal_queries_past_sixteen_columns(device, dtype, head_dim, ql, gq, ex
         window, cap = 40, 5.0
         sinks, slopes = sink_values(2 * gq, device), alibi_slopes(2 * gq, device)
     expected = port_expected(b, True, window, sinks, cap, slopes)
-    for ns in (None, 1, 9):
+    for ns in (None, 1, 9) + per_sequence(head_dim, gq, ql):
         kw = {} if ns is None else dict(num_splits=ns)
         got = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table,
                                         b.cache_seqlens, b.scale, causal=True, window_left=window,

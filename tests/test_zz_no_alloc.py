@@ -43,6 +43,9 @@ def test_no_alloc_matches_workspace_entry_point_on_two_calls(device):
     # A split count that crosses every sequence, on the smaller input.
     with_ws, no_alloc = decode_both(second, num_splits=40)
     assert torch.equal(with_ws, no_alloc)
+    # The per-sequence kernel uses no workspace at all.
+    with_ws, no_alloc = decode_both(second, num_splits=native.SPLITS_PER_SEQUENCE)
+    assert torch.equal(with_ws, no_alloc)
 
 
 def test_no_alloc_refuses_inputs_beyond_its_array(device):
