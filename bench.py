@@ -2,7 +2,8 @@
 """Decode-attention benchmark on one MI355X (BASELINE.json metric).
 
 One step = one split-KV paged decode call (two kernels: the split partial
-kernel, then the LSE combine of the sequences that cross a work-range end)
+kernel, then the LSE combine of the sequences that cross a work-range end; one
+per-sequence kernel where the split heuristic picks it for short sequences)
 over the whole synthetic batch of the named workload, inputs already resident
 in HBM. The KV pool is rotated across copies
 totalling >= 1 GB so the 256 MB Infinity Cache cannot serve repeated reads.
@@ -324,6 +325,8 @@ def main() -> int:
     # token, no window); otherwise the whole call, both kernels.
     achieved = main_res["partial_kernel_gb_s"]
     kernel, kernel_us = "split_partial_kernel", main_res["partial_kernel_us"]
+    if main_res["num_splits"] == -1:  # SPLITS_PER_SEQUENCE: one kernel is the whole call
+        kernel = "seq_decode_kernel"
     if achieved is None:
         achieved = main_res["alg_gb_s"]
         kernel, kernel_us = "split_partial_kernel + split_combine_kernel", main_res["us_per_call"]
