@@ -72,11 +72,11 @@ const char *mxfa_strerror(int code);
  * sequences are laid end to end and cut into num_splits equal ranges (fewer
  * when there are fewer tiles), and every (kv head, range) pair is one wave, so
  * the per-CU load is even for any length mix. When the block table's capacity
- * C = block_table_width * page_size bounds every sequence to a few tiles
- * (page_size >= 16 and, for head rows of <= 128 bytes, C <= 768 tokens with
- * batch * kv_heads * ceil(C / 16) <= 16384; for 256-byte rows C <= 384 with the
- * same bound; never for longer rows), it returns MXFA_SPLITS_PER_SEQUENCE
- * instead. Integer-only, reads no device data. Replaces the Python loop at
+ * C = block_table_width * page_size bounds every sequence to a few tiles, it
+ * returns MXFA_SPLITS_PER_SEQUENCE instead: page_size >= 16, W = batch *
+ * kv_heads * ceil(C / 16) <= 16384, and either head rows of <= 128 bytes with
+ * C <= 768 tokens, or 256-byte rows with C <= 384 (or C <= 512 when batch *
+ * kv_heads >= 64), and W <= 8192 at head dim 256; never for longer rows. Integer-only, reads no device data. Replaces the Python loop at
  * integrations/vllm/vllm_plugin.py:271-276 (NP doubling until B*HKV*NP >= 2048,
  * c_len = ceil(BTW*PS/NP)).
  */

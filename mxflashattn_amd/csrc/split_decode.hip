@@ -365,17 +365,21 @@ static int split_heuristic(int batch, int q_heads, int kv_heads, int head_dim, i
     return MXFA_EINVAL;
   const int row_bytes = head_dim * elem_bytes;
   const int64_t cap = (int64_t)block_table_width * page_size;
-  // Short sequences (by the table's capacity, the one bound known without
+  // Short sequences (by the table's capacity C, the one bound known without
   // reading the lengths): the per-sequence kernel, whose four waves per (b,
   // kv head) finish a few tiles each sooner than the split path's tile scan
-  // and second launch. Bounds measured on MI355X with lengths U[C/2, C] at
-  // B 1..128, 1, 2 or 8 kv heads, GQ 4: inside them as fast or up to 1.8x
-  // faster; past them slower (128-byte rows at C 1024, or at B 128 with 8 kv
-  // heads and C 512; 256-byte rows at C 512 with small batches).
+  // and second launch. Bounds from MI355X sweeps (lengths U[C/2, C], B 1..128,
+  // 1, 2 or 8 kv heads, GQ 4): inside them 0.99-1.9x the split path's speed;
+  // past them it loses (128-byte rows at C 1024 for most batches, B * HKV >=
+  // 512 at C 768; 256-byte rows at C 768, or C 512 with B * HKV < 64; head
+  // dim 256, one wave per SIMD, at B * HKV = 1024).
   const int64_t seq_tiles = (cap + kTile - 1) / kTile;
-  const int64_t seq_work = (int64_t)batch * kv_heads * seq_tiles;
-  if (page_size >= kTile && seq_work <= 16384 &&
-      ((row_bytes <= 128 && cap <= 768) || (row_bytes <= 256 && cap <= 384))) {
+  const int64_t units = (int64_t)batch * kv_heads;
+  const int64_t seq_work = units * seq_tiles;
+  const bool short_rows = row_bytes <= 128 && cap <= 768;
+  const bool mid_rows = row_bytes <= 256 && (cap <= 384 || (cap <= 512 && units >= 64)) &&
+                        (head_dim < 256 || seq_work <= 8192);
+  if (page_size >= kTile && seq_work <= 16384 && (short_rows || mid_rows)) {
     *num_splits = MXFA_SPLITS_PER_SEQUENCE;
     return MXFA_OK;
   }

@@ -70,12 +70,16 @@ def test_strerror_is_distinct_per_code(lib):
 
 
 def heuristic_closed_form(b, hq, hkv, hd, ps, btw, cus, elem_bytes=2):
-    # Short sequences by the table's capacity C = btw * ps (page size >= 16,
-    # B * HKV * ceil(C / 16) <= 16384, C <= 768 for head rows of <= 128 bytes,
-    # C <= 384 for 256-byte rows): the per-sequence kernel.
+    # Short sequences by the table's capacity C = btw * ps: page size >= 16,
+    # W = B * HKV * ceil(C / 16) <= 16384, and head rows of <= 128 bytes with
+    # C <= 768, or 256-byte rows with C <= 384 (C <= 512 from B * HKV = 64 on)
+    # and W <= 8192 at head dim 256: the per-sequence kernel.
     cap, row = btw * ps, hd * elem_bytes
-    if (ps >= 16 and b * hkv * -(-cap // 16) <= 16384
-            and ((row <= 128 and cap <= 768) or (row <= 256 and cap <= 384))):
+    units = b * hkv
+    work = units * -(-cap // 16)
+    mid = (row <= 256 and (cap <= 384 or (cap <= 512 and units >= 64))
+           and (hd < 256 or work <= 8192))
+    if ps >= 16 and work <= 16384 and ((row <= 128 and cap <= 768) or mid):
         return native.SPLITS_PER_SEQUENCE
     # Otherwise one wave per (kv head, range): a workgroup has max(4, min(HKV,
     # 8 for head rows of <= 128 bytes, else 4)) waves = min(HKV, waves) kv heads
@@ -103,6 +107,11 @@ def heuristic_closed_form(b, hq, hkv, hd, ps, btw, cus, elem_bytes=2):
     (32, 32, 8, 64, 16, 49, 256),      # C 784
     (8, 32, 8, 128, 16, 24, 256),      # 256-byte rows, C 384
     (8, 32, 8, 128, 16, 25, 256),      # C 400
+    (8, 32, 8, 128, 16, 32, 256),      # C 512, B * HKV 64
+    (4, 32, 8, 128, 16, 32, 256),      # C 512, B * HKV 32
+    (128, 16, 8, 128, 16, 32, 256),    # C 512 past the work bound
+    (32, 16, 8, 256, 16, 16, 256),     # HD 256 (fp8: 256-byte rows), W 4096
+    (128, 16, 8, 256, 16, 16, 256),    # W 16384: past the HD 256 bound
     (8, 32, 8, 128, 64, 6, 256),       # C 384 in pages of 64
     (8, 16, 4, 256, 16, 4, 256),       # 512-byte rows: always split
     (256, 16, 8, 64, 16, 64, 256),
