@@ -76,7 +76,11 @@ const char *mxfa_strerror(int code);
  * returns MXFA_SPLITS_PER_SEQUENCE instead: page_size >= 16, W = batch *
  * kv_heads * ceil(C / 16) <= 16384, and either head rows of <= 128 bytes with
  * C <= 768 tokens, or 256-byte rows with C <= 384 (or C <= 512 when batch *
- * kv_heads >= 64), and W <= 8192 at head dim 256; never for longer rows. Integer-only, reads no device data. Replaces the Python loop at
+ * kv_heads >= 64), and W <= 8192 at head dim 256; never for longer rows, nor
+ * when the kernel's 64 KB of LDS cannot hold q_heads / kv_heads columns at this
+ * head dim (16 at head dim 256). For mxfa_split_decode_multi_launch pass
+ * q_heads * q_len as q_heads (the columns of one launch); the range count
+ * does not depend on it. Integer-only, reads no device data. Replaces the Python loop at
  * integrations/vllm/vllm_plugin.py:271-276 (NP doubling until B*HKV*NP >= 2048,
  * c_len = ceil(BTW*PS/NP)).
  */

@@ -329,7 +329,7 @@ static Grid seq_grid(int hkv, int batch) {
 
 static int launch_seq(const SplitArgs &a, hipStream_t st) {
   // The pieces live in LDS: at most 64 KB per workgroup (HD 256 with 16 columns needs more).
-  if (seq_lds_bytes(a.hd, a.hq / a.hkv * a.ql) > ((size_t)64 << 10)) return MXFA_EUNSUPPORTED;
+  if (seq_lds_bytes(a.hd, a.hq / a.hkv * a.ql) > kSeqLdsMax) return MXFA_EUNSUPPORTED;
   const Grid g = seq_grid(a.hkv, a.batch);
   DecodeParams p = make_params(a, g);
   p.num_ranges = 0;
@@ -379,7 +379,10 @@ static int split_heuristic(int batch, int q_heads, int kv_heads, int head_dim, i
   const bool short_rows = row_bytes <= 128 && cap <= 768;
   const bool mid_rows = row_bytes <= 256 && (cap <= 384 || (cap <= 512 && units >= 64)) &&
                         (head_dim < 256 || seq_work <= 8192);
-  if (page_size >= kTile && seq_work <= 16384 && (short_rows || mid_rows)) {
+  // q_heads / kv_heads columns per launch (q_heads * q_len for the multi-token
+  // entry point) must fit the kernel's LDS.
+  const bool fits = seq_lds_bytes(head_dim, (q_heads + kv_heads - 1) / kv_heads) <= kSeqLdsMax;
+  if (page_size >= kTile && seq_work <= 16384 && fits && (short_rows || mid_rows)) {
     *num_splits = MXFA_SPLITS_PER_SEQUENCE;
     return MXFA_OK;
   }

@@ -1275,10 +1275,11 @@ constexpr int kSeqWaves = 4;
 template <int HD>
 constexpr int kSeqOcc = HD >= 256 ? 1 : 2;
 
-// LDS bytes of the per-sequence kernel's pieces.
+// LDS bytes of the per-sequence kernel's pieces, and the most it takes.
 inline size_t seq_lds_bytes(int hd, int cols) {
   return (size_t)kSeqWaves * cols * (hd + 1) * sizeof(float);
 }
+constexpr size_t kSeqLdsMax = (size_t)64 << 10;
 
 template <int HD, int HR, typename T, bool kF8, bool kExtras>
 static void launch_seq_x(const DecodeParams &p, hipStream_t st) {

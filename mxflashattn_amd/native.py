@@ -547,8 +547,15 @@ def _sinks_ptr(values, q: torch.Tensor, name: str = "sinks") -> int:
 
 
 def default_num_splits(q: torch.Tensor, k_cache: torch.Tensor, block_table: torch.Tensor) -> int:
-    return split_heuristic(q.shape[0], q.shape[-2], k_cache.shape[2], q.shape[-1],
-                           k_cache.shape[1], block_table.shape[1], num_cus(q.device.index or 0),
+    """The heuristic's count for q ([B, HQ, HD] or [B, QL, HQ, HD]). It is
+    asked for the columns of one launch, HQ times the query tokens a launch
+    takes (QL, or 16 / GQ of them for longer causal queries), which decide
+    whether the per-sequence kernel's LDS holds them."""
+    hq, hkv = q.shape[-2], k_cache.shape[2]
+    ql = q.shape[1] if q.dim() == 4 else 1
+    tokens = min(ql, max(1, KERNEL_COLUMNS // max(1, hq // hkv)))
+    return split_heuristic(q.shape[0], hq * tokens, hkv, q.shape[-1], k_cache.shape[1],
+                           block_table.shape[1], num_cus(q.device.index or 0),
                            k_cache.dtype == FP8_DTYPE)
 
 

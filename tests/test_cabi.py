@@ -74,12 +74,15 @@ def heuristic_closed_form(b, hq, hkv, hd, ps, btw, cus, elem_bytes=2):
     # W = B * HKV * ceil(C / 16) <= 16384, and head rows of <= 128 bytes with
     # C <= 768, or 256-byte rows with C <= 384 (C <= 512 from B * HKV = 64 on)
     # and W <= 8192 at head dim 256: the per-sequence kernel.
+    # Its LDS (4 waves x columns x (HD + 1) floats, columns = HQ / HKV) must
+    # stay within 64 KB.
     cap, row = btw * ps, hd * elem_bytes
     units = b * hkv
     work = units * -(-cap // 16)
     mid = (row <= 256 and (cap <= 384 or (cap <= 512 and units >= 64))
            and (hd < 256 or work <= 8192))
-    if ps >= 16 and work <= 16384 and ((row <= 128 and cap <= 768) or mid):
+    fits = 16 * -(-hq // hkv) * (hd + 1) <= 64 << 10
+    if ps >= 16 and work <= 16384 and fits and ((row <= 128 and cap <= 768) or mid):
         return native.SPLITS_PER_SEQUENCE
     # Otherwise one wave per (kv head, range): a workgroup has max(4, min(HKV,
     # 8 for head rows of <= 128 bytes, else 4)) waves = min(HKV, waves) kv heads
@@ -112,6 +115,9 @@ def heuristic_closed_form(b, hq, hkv, hd, ps, btw, cus, elem_bytes=2):
     (128, 16, 8, 128, 16, 32, 256),    # C 512 past the work bound
     (32, 16, 8, 256, 16, 16, 256),     # HD 256 (fp8: 256-byte rows), W 4096
     (128, 16, 8, 256, 16, 16, 256),    # W 16384: past the HD 256 bound
+    (8, 120, 8, 256, 16, 16, 256),     # HD 256, 15 columns: the LDS holds them
+    (8, 128, 8, 256, 16, 16, 256),     # HD 256, 16 columns: it does not
+    (8, 128, 8, 128, 16, 16, 256),     # HD 128, 16 columns: it does
     (8, 32, 8, 128, 64, 6, 256),       # C 384 in pages of 64
     (8, 16, 4, 256, 16, 4, 256),       # 512-byte rows: always split
     (256, 16, 8, 64, 16, 64, 256),
@@ -145,6 +151,9 @@ def test_split_heuristic_known_values():
     # fp8 HD 128 has 128-byte rows: the 16-bit HD 64 bounds.
     assert native.split_heuristic(32, 32, 8, 128, 16, 48, 256, True) == -1
     assert native.split_heuristic(32, 32, 8, 128, 16, 48, 256) == 128
+    # fp8 HD 256 (256-byte rows): 15 columns fit the per-sequence kernel's LDS, 16 do not.
+    assert native.split_heuristic(8, 120, 8, 256, 16, 16, 256, True) == -1
+    assert native.split_heuristic(8, 128, 8, 256, 16, 16, 256, True) > 0
     # fp8 config 2: eight waves hold all 8 kv heads, one workgroup per range.
     assert native.split_heuristic(32, 32, 8, 128, 16, 512, 256, True) == 256
     assert native.split_heuristic(32, 32, 4, 128, 16, 512, 256, True) == 256

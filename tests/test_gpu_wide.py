@@ -125,6 +125,21 @@ def test_fp8_cache_matches_oracle(device, dtype, head_dim, gq):
         assert torch.equal(got[3].cpu(), torch.zeros_like(got[3].cpu()))
 
 
+@pytest.mark.parametrize("gq", [15, 16])
+def test_fp8_head_dim_256_short_table_takes_the_kernel_that_fits(device, gq):
+    # A table of 16 pages of 16 (256 tokens) puts fp8 HD 256 (256-byte rows) in
+    # the per-sequence kernel's range, whose LDS holds 15 columns at this head
+    # dim but not 16: the default count must pick a kernel that runs.
+    lengths = torch.tensor([3, 256, 100, 17, 0])
+    b = make_paged_batch(5, 2 * gq, 2, 256, torch.bfloat16, lengths, block_table_width=16,
+                         seed=56 + gq).to(device)
+    k8, v8 = fp8_caches(b, device)
+    ns = native.default_num_splits(b.q, k8, b.block_table)
+    assert (ns == native.SPLITS_PER_SEQUENCE) == (gq == 15)
+    got = decode(b, k8, v8, k_scale=scalar(2.0, device), v_scale=scalar(0.5, device))
+    assert max_err(got, fp8_expected(b, k8, v8, 2.0, 0.5)) <= TOL[torch.bfloat16]
+
+
 @pytest.mark.parametrize("page_size", [1, 8, 32])
 def test_fp8_small_and_large_pages(device, page_size):
     b = make_paged_batch(3, 8, 2, 128, torch.bfloat16, torch.tensor([5, 200, 999]),
