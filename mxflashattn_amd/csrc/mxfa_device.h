@@ -47,6 +47,12 @@ struct Elem<BF16> {
 
 // DPP control row_newbcast:n = 0x150 + n (lane n of each 16-lane row to the row).
 constexpr int kDppRowNewBcast0 = 0x150;
+// row_shr:n = 0x110 + n (lane i of a row takes lane i - n of the same row);
+// row_bcast:15 / row_bcast:31 (lane 15 of each row to the next row / lane 31
+// to rows 2 and 3).
+constexpr int kDppRowShr0 = 0x110;
+constexpr int kDppRowBcast15 = 0x142;
+constexpr int kDppRowBcast31 = 0x143;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -259,6 +259,9 @@ static int launch_combine(void *ws, void *out, const float *sinks, int64_t o_sb,
   c.num_ranges = ns;
   c.heads_per_block = combine_heads_per_block(batch, hq * ql, hd, ns);
   c.sinks = sinks;
+#ifdef MXFA_WAVE_STAMPS
+  c.stamps = g_wave_stamps ? g_wave_stamps + kStampCombineBase : nullptr;
+#endif
   switch (hd) {
     case 64: return launch_combine_64(c, dtype, st);
     case 128: return launch_combine_128(c, dtype, st);
@@ -408,8 +411,10 @@ extern "C" {
 int mxfa_abi_version(void) { return MXFA_ABI_VERSION; }
 
 #ifdef MXFA_WAVE_STAMPS
-// Profiling builds only (not part of the C ABI): device buffer of 65536 x 8
-// words that later partial-kernel launches stamp, or nullptr to stop.
+// Profiling builds only (not part of the C ABI): device buffer of
+// kStampWaves x kStampWords words for the partial and per-sequence kernels'
+// waves, then kStampCombineBlocks x kStampCombineWords for the combine
+// kernel's blocks, that later launches stamp; nullptr stops.
 void mxfa_wave_stamps_set(void *device_buffer) {
   g_wave_stamps = (unsigned long long *)device_buffer;
 }

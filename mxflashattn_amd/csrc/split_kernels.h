@@ -135,7 +135,7 @@ struct DecodeParams {
   int num_pages;
   int num_ranges;
 #ifdef MXFA_WAVE_STAMPS
-  unsigned long long *stamps;  // profiling builds: 8 words per wave (see wave_stamp)
+  unsigned long long *stamps;  // profiling builds: kStampWords words per wave (see wave_stamp)
 #endif
 };
 
@@ -156,7 +156,62 @@ struct CombineParams {
   int num_ranges;
   int heads_per_block;  // a power of two; heads_per_block * HD / 4 <= kCombineThreads
   const float *sinks;   // as DecodeParams::sinks
+#ifdef MXFA_WAVE_STAMPS
+  unsigned long long *stamps;  // profiling builds: kStampCombineWords words per block
+#endif
 };
+
+// Profiling builds (-DMXFA_WAVE_STAMPS) record, per wave (kStampWords words
+// each), the real-time clock (100 MHz) at kernel entry [0], after the tile
+// scan [1], when the first tiles' loads are issued [2] and at the end [3],
+// with the tiles [4], a valid flag [5], the workgroup [6] and the kv head [7];
+// then when the lengths have arrived [8], when the range's first sequence is
+// known [9], when the first page id has arrived [10] and when the first
+// tile's data has arrived [11]. The combine kernel records per block, after
+// the waves' words, entry [0], prefix sums read [1], pieces folded [2] and
+// end [3]. Other builds compile none of it.
+constexpr int kStampWords = 16;
+constexpr int kStampWaves = 65536;
+constexpr int kStampCombineWords = 4;
+constexpr long kStampCombineBase = (long)kStampWaves * kStampWords;
+constexpr int kStampCombineBlocks = 65536;
+
+__device__ __forceinline__ unsigned long long wave_clock() {
+#ifdef MXFA_WAVE_STAMPS
+  return __builtin_amdgcn_s_memrealtime();
+#else
+  return 0;
+#endif
+}
+
+__device__ __forceinline__ void wave_stamp(const DecodeParams &p, int slot,
+                                           unsigned long long value) {
+#ifdef MXFA_WAVE_STAMPS
+  const unsigned wave = ((blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+  if (p.stamps && (threadIdx.x & 63) == 0 && wave < kStampWaves)
+    p.stamps[wave * kStampWords + slot] = value;
+#endif
+}
+
+// The clock once `dep` exists (profiling builds): the empty asm statement
+// uses the value, so the clock read cannot move ahead of its computation.
+template <typename V>
+__device__ __forceinline__ void wave_stamp_after(const DecodeParams &p, int slot, V dep) {
+#ifdef MXFA_WAVE_STAMPS
+  asm volatile("" ::"v"(dep));
+  wave_stamp(p, slot, wave_clock());
+#endif
+}
+
+// Combine-kernel stamps (profiling builds): thread 0 of each block, once `dep` exists.
+template <typename V>
+__device__ __forceinline__ void block_stamp_after(const CombineParams &c, int slot, V dep) {
+#ifdef MXFA_WAVE_STAMPS
+  asm volatile("" ::"v"(dep));
+  if (c.stamps && threadIdx.x == 0 && blockIdx.x < kStampCombineBlocks)
+    c.stamps[blockIdx.x * kStampCombineWords + slot] = wave_clock();
+#endif
+}
 
 // Block tables and lengths are read-only for the whole call; reading them
 // through the constant address space lets wave-uniform lookups use scalar
@@ -189,11 +244,18 @@ __device__ __forceinline__ int tiles_of(int L, int ql, int window_left) {
 }
 
 // First tile of range r out of R over NT tiles, and the range holding tile t.
+// Both stay in 32-bit unsigned division while the product fits (every
+// benchmark shape: r * NT < 2^31), which is a few instructions where the
+// 64-bit division is a long software sequence on the prologue's critical path.
 __device__ __forceinline__ int range_lo(int r, int R, int NT) {
-  return (int)(((int64_t)r * NT) / R);
+  const int64_t x = (int64_t)r * NT;
+  if (x < 0x7fffffff) return (int)((uint32_t)x / (uint32_t)R);
+  return (int)(x / R);
 }
 __device__ __forceinline__ int range_of(int t, int R, int NT) {
-  return (int)((((int64_t)t + 1) * R - 1) / NT);
+  const int64_t x = ((int64_t)t + 1) * R - 1;
+  if (x < 0x7fffffff) return (int)((uint32_t)x / (uint32_t)NT);
+  return (int)(x / NT);
 }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_srd(const char *base, int bytes) {
@@ -379,37 +441,62 @@ __device__ __forceinline__ float head_of_row(float x, int row) {
   return v;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave with DPP moves only (no
+// LDS permutes): a Hillis-Steele scan inside each 16-lane row (row_shr 1, 2,
+// 4, 8), then the row totals carried across rows (row_bcast:15 into rows 1
+// and 3, row_bcast:31 into rows 2 and 3). Lanes a move leaves unwritten add 0.
+__device__ __forceinline__ int wave_scan_incl(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, kDppRowShr0 + 1, 0xf, 0xf, true);
+  x += __builtin_amdgcn_update_dpp(0, x, kDppRowShr0 + 2, 0xf, 0xf, true);
+  x += __builtin_amdgcn_update_dpp(0, x, kDppRowShr0 + 4, 0xf, 0xf, true);
+  x += __builtin_amdgcn_update_dpp(0, x, kDppRowShr0 + 8, 0xf, 0xf, true);
+  x += __builtin_amdgcn_update_dpp(0, x, kDppRowBcast15, 0xa, 0xf, false);
+  x += __builtin_amdgcn_update_dpp(0, x, kDppRowBcast31, 0xc, 0xf, false);
+  return x;
+}
+
 // Exclusive prefix sum of per-sequence tile counts into s[0..B] (LDS), all
-// threads. The lengths are read from memory once: the first pass parks each
-// tile count in s[b], the second turns them into prefix sums in place. Without
-// a window (kWindow false) every sequence starts at its tile 0.
+// threads. The lengths are read from memory once, eight loads in flight per
+// thread: the first pass parks each tile count in s[b], the second turns them
+// into prefix sums in place. Without a window (kWindow false) every sequence
+// starts at its tile 0.
 template <int kThreads, bool kWindow>
 __device__ __forceinline__ void tile_prefix(const DecodeParams &p, int32_t *s, int *wave_tot) {
+  constexpr int kWaves = kThreads / 64;
+  constexpr int kBatchLoads = 8;
   const int B = p.batch;
   const int per = (B + kThreads - 1) / kThreads;
   const int b0 = threadIdx.x * per;
   int local = 0;
-  for (int i = 0; i < per; ++i) {
-    const int b = b0 + i;
-    if (b < B) {
-      const int L = seq_len_of(p.seqlens, b, p.seqlen_add, p.max_len);
-      const int n = kWindow ? tiles_of(L, p.ql, p.window_left) : (L + kTile - 1) / kTile;
-      s[b] = n;
-      local += n;
+  for (int i0 = 0; i0 < per; i0 += kBatchLoads) {
+    int n[kBatchLoads];
+#pragma unroll
+    for (int j = 0; j < kBatchLoads; ++j) {
+      const int b = b0 + i0 + j;
+      n[j] = 0;
+      if (i0 + j < per && b < B) {
+        const int L = seq_len_of(p.seqlens, b, p.seqlen_add, p.max_len);
+        n[j] = kWindow ? tiles_of(L, p.ql, p.window_left) : (L + kTile - 1) / kTile;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kBatchLoads; ++j) {
+      const int b = b0 + i0 + j;
+      if (i0 + j < per && b < B) {
+        s[b] = n[j];
+        local += n[j];
+      }
     }
   }
+  wave_stamp_after(p, 8, local);
   // Inclusive scan of `local` across the workgroup.
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int x = local;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(x, off, 64);
-    if (lane >= off) x += y;
-  }
+  const int x = wave_scan_incl(local);
   if (lane == 63) wave_tot[wave] = x;
   __syncthreads();
   int base = 0;
-  for (int w = 0; w < wave; ++w) base += wave_tot[w];
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) base += w < wave ? wave_tot[w] : 0;
   int run = base + x - local;  // exclusive prefix of this thread's first element
   for (int i = 0; i < per; ++i) {  // each thread rewrites only its own entries
     const int b = b0 + i;
@@ -483,27 +570,6 @@ struct Tile {
   int flags;
   int pg;  // page id (block-table entry), page-uniform tiles only
 };
-
-// Profiling builds (-DMXFA_WAVE_STAMPS) record, per wave, the real-time clock
-// (100 MHz) at kernel entry [0], after the tile scan [1], when the first
-// tiles' loads are issued [2] and at the end [3], with the tiles [4], a valid
-// flag [5], the workgroup [6] and the kv head [7]. Other builds compile none
-// of it.
-__device__ __forceinline__ void wave_stamp(const DecodeParams &p, int slot,
-                                           unsigned long long value) {
-#ifdef MXFA_WAVE_STAMPS
-  const unsigned wave = ((blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
-  if (p.stamps && (threadIdx.x & 63) == 0 && wave < 65536) p.stamps[wave * 8 + slot] = value;
-#endif
-}
-
-__device__ __forceinline__ unsigned long long wave_clock() {
-#ifdef MXFA_WAVE_STAMPS
-  return __builtin_amdgcn_s_memrealtime();
-#else
-  return 0;
-#endif
-}
 
 // One wave: the tiles [lo, hi) of kv head kvh, range rr. HR = DPP rows
 // holding used columns (GQ*QL <= 4 HR), T = element type of q, out and the MFMA
@@ -600,6 +666,7 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
       a = na;
     }
     pb = rfl(a);
+    wave_stamp_after(p, 9, pb);
   }
   // Cursor of the tile builder (runs NBUF tiles ahead of the math). Without a
   // window every sequence starts at its tile 0, so the first page id does not
@@ -740,6 +807,9 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   for (int cc = 0; cc < NCH; ++cc) qf[cc] = make_uint4(0u, 0u, 0u, 0u);
   bool piece_from_start = false;
   bool piece_first_in_range = false;
+#ifdef MXFA_WAVE_STAMPS
+  bool stamp_data = true;  // the first tile's data not yet stamped
+#endif
   // V slot of this lane: the VD dims it holds (and writes) start at vslot*VD.
   const int vslot = kShareV ? 2 * (col & 7) + (col >> 3) : col;
 
@@ -835,6 +905,12 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
       x[i] = valid ? x[i] : -INFINITY;
       need |= x[i] > m + kRescaleLog2;
     }
+#ifdef MXFA_WAVE_STAMPS
+    if (stamp_data) {
+      wave_stamp_after(p, 11, x[0]);
+      stamp_data = false;
+    }
+#endif
     if (__builtin_amdgcn_ballot_w64(need) != 0) {
       // Rare, wave-uniform: move the reference of each head to the wave's
       // tile maximum when it passed the reference by more than kRescaleLog2.
@@ -923,6 +999,7 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
     make_tile(lo + i * tstep, sets[i].d, sets[i].lpg);
     if constexpr (i < NBUF - 1) issue(sets[i]);
   });
+  wave_stamp_after(p, 10, sets[0].d.pg);
   const int ntiles = kSeq ? (hi - lo + tstep - 1) / tstep : hi - lo;
   int t = lo;
   wave_stamp(p, 2, wave_clock());
@@ -1028,14 +1105,22 @@ __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(CombineP
   const int vh = (blockIdx.x % nblk) * H + (threadIdx.x % CB) / CH;
   const int cc = threadIdx.x % CH;
   const int g = threadIdx.x / CB;
+  block_stamp_after(p, 0, g);
   const int NT = p.ws_s[p.batch];
   const int sb = p.ws_s[b], se = p.ws_s[b + 1];
+  block_stamp_after(p, 1, NT + sb + se);
   // Prefix sums that do not describe tiles inside [0, NT) (a workspace the
   // partial kernel did not fill) are skipped, so every index stays in range.
-  if (se <= sb || sb < 0 || se > NT) return;
+  if (se <= sb || sb < 0 || se > NT) {
+    block_stamp_after(p, 3, sb);
+    return;
+  }
   const int R = min(p.num_ranges, NT);
   const int ra = range_of(sb, R, NT), rb = range_of(se - 1, R, NT);
-  if (ra == rb) return;
+  if (ra == rb) {
+    block_stamp_after(p, 3, ra);
+    return;
+  }
   const int slot_a = (range_lo(ra, R, NT) == sb) ? 0 : 1;
   const int ns = p.num_ranges;
   const bool live = vh < nv;  // the last block of a sequence may run past the rows
@@ -1059,6 +1144,7 @@ __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(CombineP
       for (int i = 0; i < kUnroll; ++i) lse_fold(M, W, acc, l[i], 1.f, ov[i]);
     }
   }
+  block_stamp_after(p, 2, M);
   float *red = s_red + threadIdx.x * 6;
   red[0] = M;
   red[1] = W;
@@ -1090,6 +1176,7 @@ __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(CombineP
     *reinterpret_cast<uint2 *>(p.out + b * p.o_sb + t * p.o_st + h * p.o_sh + cc * 8) =
         make_uint2(w0, w1);
   }
+  block_stamp_after(p, 3, W);
 }
 
 // Per-sequence workgroups (one launch, no workspace, no tile scan): workgroup
