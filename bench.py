@@ -12,7 +12,9 @@ Prints ONE JSON line:
   value        effective KV GB/s = sum_b 4*L_b*HKV*HD / (us per call); us per
                call is the median of 10 timed regions of exactly --steps
                calls, each region one replay of a HIP graph holding those
-               calls (no host launch overhead); timed_calls counts them all
+               calls (no host launch overhead), after 100 ms of untimed
+               replays (clock ramp after the idle input build); timed_calls
+               counts them all
   us_per_call_eager  the same calls launched one by one from Python, median of
                per-call HIP events
   us_per_call_warm   graph replays on one KV pool, never rotated (cache-warm
@@ -21,9 +23,11 @@ Prints ONE JSON line:
                bytes (KV + q + out + used block-table entries + lengths) / its
                average duration (HIP events around graph replays of
                partial-only launches, on the launch stream), against 8 TB/s
-  cpu_baseline fp32 torch-CPU restatement of reference.attention_kvcache
-               (oracle.reference_port) on the host cores, bounded sample of the
-               workload, plus config 1 (the reference's CPU-runnable case)
+  cpu_baseline the reference's own CPU implementation of the path (its ATen
+               backend csrc/mxmac, built from its sources into oracle/_ref)
+               on the host cores, bounded sample of the workload, plus config 1
+               (the reference's CPU-runnable case); the fp32 restatement
+               (oracle.reference_port) is timed beside it
   cells        the six GQ x HD cells of config 2 and configs 1, 3, 4
   wide         shapes beyond the reference's contract at config 2's batch and
                lengths: fp8 (e4m3fn) caches, head dim 256, GQ 1 and 16,
@@ -55,6 +59,7 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "decode-attn effective KV GB/s (% of HBM peak) + µs/call, B=32 GQ4 HD128 bf16"
 MAIN_WORKLOAD = "config2_qwen3_4b"
 ROTATE_BYTES = 1 << 30
+WARM_MS = 100.0  # untimed graph replays right before every timed region
 
 
 def parse_args() -> argparse.Namespace:
@@ -116,7 +121,7 @@ def time_graph(fn, pools, calls: int, warmup: int, stream, rounds: int = 10) -> 
     on the stream the kernels run on. The regions run back to back and the
     median region is reported. ``warmup`` eager calls on the same stream
     come first (they also size the workspace there, so nothing is allocated
-    inside the capture), then one untimed replay.
+    inside the capture), then untimed replays for at least WARM_MS.
     """
     with torch.cuda.stream(stream):
         for i in range(warmup):
@@ -128,8 +133,16 @@ def time_graph(fn, pools, calls: int, warmup: int, stream, rounds: int = 10) -> 
             fn(*pools[i % len(pools)])
     events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
               for _ in range(rounds)]
+    # Untimed replays for at least WARM_MS first: after the host has built
+    # the inputs the GPU has idled, and the first ~15 ms of work after an
+    # idle spell run 3-10 % slower while clocks ramp up.
+    t_end = time.perf_counter() + WARM_MS / 1e3
     with torch.cuda.stream(stream):
-        graph.replay()  # untimed
+        while True:
+            graph.replay()
+            torch.cuda.synchronize()
+            if time.perf_counter() >= t_end:
+                break
         for first, last in events:
             first.record(stream)
             graph.replay()
@@ -201,8 +214,9 @@ def measure_workload(name: str, spec: dict, device, steps: int, warmup: int) -> 
     return res
 
 
-def _time_port(spec: dict, reps: int) -> tuple[float, object]:
-    """Median seconds per call of the fp32 CPU restatement on one batch."""
+def _time_cpu(spec: dict, reps: int, ref) -> tuple[float, object]:
+    """Median seconds per call on one batch (CPU tensors): the reference's own
+    ATen build (oracle/_ref) when ``ref`` is given, else the fp32 restatement."""
     from mxflashattn_amd.workloads import make_paged_batch
     from oracle import reference_port
 
@@ -210,18 +224,26 @@ def _time_port(spec: dict, reps: int) -> tuple[float, object]:
     times = []
     for i in range(reps + 1):
         t0 = time.perf_counter()
-        reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache,
-                                         cache_seqlens=b.cache_seqlens.clone(),
-                                         block_table=b.block_table, softmax_scale=b.scale)
+        if ref is not None:
+            ref.flash_attn_with_kvcache(b.q, b.k_cache, b.v_cache, None, None,
+                                        b.cache_seqlens.clone(), b.block_table, b.scale, False)
+        else:
+            reference_port.attention_kvcache(b.q, b.k_cache, b.v_cache,
+                                             cache_seqlens=b.cache_seqlens.clone(),
+                                             block_table=b.block_table, softmax_scale=b.scale)
         if i:
             times.append(time.perf_counter() - t0)
     return statistics.median(times), b
 
 
 def cpu_baseline(name: str, spec: dict, reps: int) -> dict:
-    """Time the fp32 CPU restatement on the same batch (CPU tensors), and on
-    config 1, the reference's CPU-runnable case."""
+    """Time the reference's own CPU implementation of the path (its ATen
+    backend, csrc/mxmac, built into oracle/_ref; kind "reference") on the same
+    batch, and on config 1, the reference's CPU-runnable case. The fp32
+    restatement (oracle.reference_port, kind "port") is timed beside it, and
+    stands in for it where oracle/_ref was not built."""
     from mxflashattn_amd.workloads import CONFIGS
+    from oracle import ref_aten
 
     # The host cores this process may use; a GPU box's share is capped by
     # OMP_NUM_THREADS whatever os.cpu_count() reports.
@@ -230,15 +252,19 @@ def cpu_baseline(name: str, spec: dict, reps: int) -> dict:
     if cap.isdigit() and int(cap) > 0:
         cores = min(cores, int(cap))
     torch.set_num_threads(max(1, cores))
-    med, b = _time_port(spec, reps)
-    med1, b1 = _time_port(CONFIGS["config1_cpu_ref"], 50)
-    return {
+    ref = ref_aten.load()
+    kind = "reference" if ref is not None else "port"
+    med, b = _time_cpu(spec, reps, ref)
+    med1, b1 = _time_cpu(CONFIGS["config1_cpu_ref"], 50, ref)
+    res = {
         "value": round(b.kv_bytes() / med / 1e9, 3),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
-        "kind": "port",
+        "kind": kind,
         "sample": (f"{name} full batch (B={b.batch}, {b.total_tokens()} tokens), "
-                   f"median of {reps} calls after 1 warmup; {med * 1e3:.1f} ms per call"),
+                   f"median of {reps} calls after 1 warmup; {med * 1e3:.1f} ms per call"
+                   + ("; the reference's csrc/mxmac flash_attn_with_kvcache built from its "
+                      "sources (oracle/_ref)" if ref is not None else "")),
         "ms_per_call": round(med * 1e3, 2),
         "config1_cpu_ref": {
             "ms_per_call": round(med1 * 1e3, 3),
@@ -246,6 +272,14 @@ def cpu_baseline(name: str, spec: dict, reps: int) -> dict:
             "sample": f"B={b1.batch}, {b1.total_tokens()} tokens, median of 50 calls",
         },
     }
+    if ref is not None:
+        reps_p = min(reps, 3)
+        med_p, _ = _time_cpu(spec, reps_p, None)
+        res["port"] = {"ms_per_call": round(med_p * 1e3, 2),
+                       "value": round(b.kv_bytes() / med_p / 1e9, 3),
+                       "sample": (f"oracle.reference_port.attention_kvcache, same batch, median "
+                                  f"of {reps_p} calls after 1 warmup")}
+    return res
 
 
 def load_traffic(workload: str) -> float | None:
@@ -353,7 +387,8 @@ def main() -> int:
         "us_per_call": main_res["us_per_call"],
         "timed_calls": main_res["timed_calls"],
         "timing": (f"median of 10 timed regions of exactly {args.steps} calls each, every region "
-                   "one HIP-graph replay over the rotated KV pools"),
+                   "one HIP-graph replay over the rotated KV pools, after "
+                   f"{args.warmup} eager warmup calls and {WARM_MS:.0f} ms of untimed replays"),
         "us_per_call_eager": main_res["us_per_call_eager"],
         "kv_gb_s_eager": main_res["kv_gb_s_eager"],
         "us_per_call_warm": main_res["us_per_call_warm"],

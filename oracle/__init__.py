@@ -11,6 +11,11 @@ Modules:
   c_oracle        ctypes wrapper of decode_ref.c: fp64 paged decode and
                   bitwise block-table / slot-mapping appends.
   split_model     fp64 NumPy model of the split partials and their LSE merge.
+  build_ref       compiles the reference's own ATen implementation of the path
+                  (csrc/mxmac) into oracle/_ref/ with one g++ line.
+  ref_aten        loads that build (None where it was not built); it pins
+                  reference_port (tests/test_oracle_ref.py) and is the
+                  "reference" CPU baseline of bench.py.
 
 How each function is pinned (golden vectors, closed forms, invariants) is
 listed in tests/test_oracle.py; every function here has at least one check
