@@ -27,13 +27,17 @@ ARCH = "gfx950"
 
 # Packed-fp32 VALU forms are disabled for every device pass: hipcc forms them
 # from plain float code, and some of their forms have given wrong results on
-# MI355X boxes with no error raised.
+# MI355X boxes with no error raised. Kernel arguments ahead of the parameter
+# struct (what each kernel's first loads need) are preloaded into SGPRs at
+# wave launch, so those loads do not wait for a kernarg-segment read.
 HIPCC_FLAGS = (
     f"--offload-arch={ARCH}",
     "-O3",
     "-std=c++17",
     "-fPIC",
     "-mcode-object-version=5",
+    "-mllvm",
+    "-amdgpu-kernarg-preload-count=16",
     "-Xclang",
     "-target-feature",
     "-Xclang",

@@ -456,15 +456,16 @@ __device__ __forceinline__ int wave_scan_incl(int x) {
 }
 
 // Exclusive prefix sum of per-sequence tile counts into s[0..B] (LDS), all
-// threads. The lengths are read from memory once, eight loads in flight per
+// threads (seqlens and B are the kernel's preloaded leading arguments, equal
+// to p.seqlens and p.batch). The lengths are read from memory once, eight loads in flight per
 // thread: the first pass parks each tile count in s[b], the second turns them
 // into prefix sums in place. Without a window (kWindow false) every sequence
 // starts at its tile 0.
 template <int kThreads, bool kWindow>
-__device__ __forceinline__ void tile_prefix(const DecodeParams &p, int32_t *s, int *wave_tot) {
+__device__ __forceinline__ void tile_prefix(const DecodeParams &p, const int32_t *seqlens, int B,
+                                            int32_t *s, int *wave_tot) {
   constexpr int kWaves = kThreads / 64;
   constexpr int kBatchLoads = 8;
-  const int B = p.batch;
   const int per = (B + kThreads - 1) / kThreads;
   const int b0 = threadIdx.x * per;
   int local = 0;
@@ -475,7 +476,7 @@ __device__ __forceinline__ void tile_prefix(const DecodeParams &p, int32_t *s, i
       const int b = b0 + i0 + j;
       n[j] = 0;
       if (i0 + j < per && b < B) {
-        const int L = seq_len_of(p.seqlens, b, p.seqlen_add, p.max_len);
+        const int L = seq_len_of(seqlens, b, p.seqlen_add, p.max_len);
         n[j] = kWindow ? tiles_of(L, p.ql, p.window_left) : (L + kTile - 1) / kTile;
       }
     }
@@ -1032,15 +1033,17 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
 // picks the instantiation; without them the kernel is the plain one).
 template <int HD, int HR, typename T, bool kF8, bool kLanePages, int NBUF, int WAVES,
           bool kExtras>
-__global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(DecodeParams p) {
+__global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(const int32_t *seqlens,
+                                                                        int batch,
+                                                                        DecodeParams p) {
   constexpr int kThreads = WAVES * 64;
   extern __shared__ int32_t s_tiles[];  // [B + 1]
   __shared__ int s_wave_tot[WAVES];
 
   const unsigned long long t_entry = wave_clock();
-  tile_prefix<kThreads, kExtras>(p, s_tiles, s_wave_tot);  // ends with a barrier
+  tile_prefix<kThreads, kExtras>(p, seqlens, batch, s_tiles, s_wave_tot);  // ends with a barrier
   zero_empty<HD, kThreads>(p, s_tiles);
-  const int B = p.batch;
+  const int B = batch;
   if (blockIdx.x == 0 && blockIdx.y == 0) {
     for (int i = threadIdx.x; i <= B; i += kThreads) p.ws_s[i] = s_tiles[i];
   }
@@ -1091,7 +1094,9 @@ __device__ __forceinline__ void lse_fold(float &M, float &W, float4 &A, float m2
 constexpr int kCombineThreads = 256;
 
 template <int HD, typename T>
-__global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(CombineParams p) {
+__global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(const int32_t *ws_s,
+                                                                         int batch, int nblk,
+                                                                         CombineParams p) {
   using E = Elem<T>;
   constexpr int CH = HD / 4;  // float4 chunks per head
   constexpr int kUnroll = 8;
@@ -1100,14 +1105,13 @@ __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(CombineP
   const int CB = H * CH;
   const int groups = kCombineThreads / CB;
   const int nv = p.hq * p.ql;  // (query token, head) rows per sequence
-  const int nblk = (nv + H - 1) / H;
-  const int b = blockIdx.x / nblk;
+  const int b = blockIdx.x / nblk;  // nblk = ceil(nv / H) blocks per sequence
   const int vh = (blockIdx.x % nblk) * H + (threadIdx.x % CB) / CH;
   const int cc = threadIdx.x % CH;
   const int g = threadIdx.x / CB;
   block_stamp_after(p, 0, g);
-  const int NT = p.ws_s[p.batch];
-  const int sb = p.ws_s[b], se = p.ws_s[b + 1];
+  const int NT = ws_s[batch];
+  const int sb = ws_s[b], se = ws_s[b + 1];
   block_stamp_after(p, 1, NT + sb + se);
   // Prefix sums that do not describe tiles inside [0, NT) (a workspace the
   // partial kernel did not fill) are skipped, so every index stays in range.
@@ -1191,7 +1195,8 @@ __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(CombineP
 template <int HD, int HR, typename T, bool kF8, bool kLanePages, int NBUF, int WAVES, int OCC,
           bool kExtras>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(OCC)))
-void seq_decode_kernel(DecodeParams p) {
+void seq_decode_kernel(const int32_t *seqlens, const int32_t *bt, int64_t bt_stride, int max_len,
+                       int seqlen_add, int ps_log2, DecodeParams p) {
   using E = Elem<T>;
   constexpr int CH = HD / 4;  // float4 chunks per head row
   extern __shared__ float s_piece[];
@@ -1203,15 +1208,18 @@ void seq_decode_kernel(DecodeParams p) {
   const int b = blockIdx.y;
   float *const lse_base = s_piece + WAVES * nc * HD;
   const unsigned long long t_entry = wave_clock();
-  const int L = seq_len_of(p.seqlens, b, p.seqlen_add, p.max_len);
+  const int L = seq_len_of(seqlens, b, seqlen_add, max_len);
   const int n = L > 0 ? (kExtras ? tiles_of(L, p.ql, p.window_left) : (L + kTile - 1) / kTile)
                       : 0;
   if ((threadIdx.x & 63) < nc) lse_base[wave * nc + (threadIdx.x & 63)] = -INFINITY;
   if (kvh < p.hkv && sub < n) {
     DecodeParams v = p;  // the one sequence, as a batch of 1
     v.q += b * p.q_sb;
-    v.bt += b * p.bt_stride;
-    v.seqlens += b;
+    v.bt = bt + b * bt_stride;  // the preloaded copies: the first page id waits on no kernarg load
+    v.seqlens = seqlens + b;
+    v.max_len = max_len;
+    v.seqlen_add = seqlen_add;
+    v.ps_log2 = ps_log2;
     v.out += b * p.o_sb;
     v.batch = 1;
     wave_stamp(p, 0, t_entry);
@@ -1306,10 +1314,10 @@ static void launch_partial_x(const DecodeParams &p, const Grid &g, hipStream_t s
   if (p.ps_log2 >= 4)
     hipLaunchKernelGGL(
         (split_partial_kernel<HD, HR, T, kF8, false, kNbuf<HD, kF8>, WAVES, kExtras>), grid,
-        dim3(WAVES * 64), lds, st, p);
+        dim3(WAVES * 64), lds, st, p.seqlens, p.batch, p);
   else
     hipLaunchKernelGGL((split_partial_kernel<HD, HR, T, kF8, true, 2, WAVES, kExtras>), grid,
-                       dim3(WAVES * 64), lds, st, p);
+                       dim3(WAVES * 64), lds, st, p.seqlens, p.batch, p);
 }
 
 template <int HD, int HR, typename T, bool kF8, int WAVES>
@@ -1375,11 +1383,13 @@ static void launch_seq_x(const DecodeParams &p, hipStream_t st) {
   if (p.ps_log2 >= 4)
     hipLaunchKernelGGL((seq_decode_kernel<HD, HR, T, kF8, false, kNbuf<HD, kF8>, kSeqWaves,
                                           kSeqOcc<HD>, kExtras>),
-                       grid, dim3(kSeqWaves * 64), lds, st, p);
+                       grid, dim3(kSeqWaves * 64), lds, st, p.seqlens, p.bt, p.bt_stride,
+                       p.max_len, p.seqlen_add, p.ps_log2, p);
   else
     hipLaunchKernelGGL((seq_decode_kernel<HD, HR, T, kF8, true, 2, kSeqWaves, kSeqOcc<HD>,
                                           kExtras>),
-                       grid, dim3(kSeqWaves * 64), lds, st, p);
+                       grid, dim3(kSeqWaves * 64), lds, st, p.seqlens, p.bt, p.bt_stride,
+                       p.max_len, p.seqlen_add, p.ps_log2, p);
 }
 
 template <int HD, int HR, typename T, bool kF8>
@@ -1413,9 +1423,11 @@ int launch_combine_hd(const CombineParams &c, int dtype, hipStream_t st) {
   const int nblk = (c.hq * c.ql + c.heads_per_block - 1) / c.heads_per_block;
   dim3 grid(c.batch * nblk);
   if (dtype == MXFA_DTYPE_BF16)
-    hipLaunchKernelGGL((split_combine_kernel<HD, BF16>), grid, dim3(kCombineThreads), 0, st, c);
+    hipLaunchKernelGGL((split_combine_kernel<HD, BF16>), grid, dim3(kCombineThreads), 0, st,
+                       c.ws_s, c.batch, nblk, c);
   else
-    hipLaunchKernelGGL((split_combine_kernel<HD, F16>), grid, dim3(kCombineThreads), 0, st, c);
+    hipLaunchKernelGGL((split_combine_kernel<HD, F16>), grid, dim3(kCombineThreads), 0, st,
+                       c.ws_s, c.batch, nblk, c);
   return hipGetLastError() == hipSuccess ? MXFA_OK : MXFA_ELAUNCH;
 }
 
