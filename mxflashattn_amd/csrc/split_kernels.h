@@ -469,16 +469,26 @@ __device__ __forceinline__ void tile_prefix(const DecodeParams &p, const int32_t
   const int per = (B + kThreads - 1) / kThreads;
   const int b0 = threadIdx.x * per;
   int local = 0;
-  for (int i0 = 0; i0 < per; i0 += kBatchLoads) {
+  if (per == 1) {  // up to one sequence per thread (B <= kThreads): one load
+    const int b = b0;
+    if (b < B) {
+      const int L = seq_len_of(seqlens, b, p.seqlen_add, p.max_len);
+      local = kWindow ? tiles_of(L, p.ql, p.window_left) : (L + kTile - 1) / kTile;
+      s[b] = local;
+    }
+  }
+  for (int i0 = 0; per > 1 && i0 < per; i0 += kBatchLoads) {
+    // Branch-free, so a thread's loads all go out together (entries past the
+    // batch read sequence 0 and count nothing).
     int n[kBatchLoads];
 #pragma unroll
     for (int j = 0; j < kBatchLoads; ++j) {
       const int b = b0 + i0 + j;
-      n[j] = 0;
-      if (i0 + j < per && b < B) {
-        const int L = seq_len_of(seqlens, b, p.seqlen_add, p.max_len);
-        n[j] = kWindow ? tiles_of(L, p.ql, p.window_left) : (L + kTile - 1) / kTile;
-      }
+      const bool live = i0 + j < per && b < B;
+      const int L = seq_len_of(seqlens, live ? b : 0, p.seqlen_add, p.max_len);
+      const int t = kWindow ? (L > 0 ? tiles_of(L, p.ql, p.window_left) : 0)
+                            : (L + kTile - 1) / kTile;
+      n[j] = live ? t : 0;
     }
 #pragma unroll
     for (int j = 0; j < kBatchLoads; ++j) {

@@ -12,7 +12,10 @@ bench workloads on that build and prints one JSON line per workload with the
 medians, over six calls, of (µs after the partial kernel's first wave entry):
 
   entry_last       the last wave's entry
-  lengths_med      lengths arrived, median wave
+  lengths_med      lengths arrived, median wave (waves with no sequence to
+                   read pass at once)
+  lengths_wg_med   the lengths' round trip: per workgroup, the last wave's
+                   arrival after the first wave's entry; median workgroup
   prologue_med     tile scan done, median wave
   search_med       range's first sequence known, median wave
   page_id_med      first page id arrived, median wave
@@ -73,9 +76,13 @@ def _summary(stamps, combine) -> dict:
         groups = np.unique(wg)
         wg_speed = np.array([speed[wg == g].mean() for g in groups])
         wg_end = np.array([end[wg == g].max() for g in groups])
+        lengths = rel(8)
+        lengths_wg = np.array([lengths[wg == g].max() - entry[wg == g].min() for g in groups])
         row = dict(
             waves=len(d), tiles_med=float(np.median(tiles)), entry_last=float(entry.max()),
-            lengths_med=float(np.median(rel(8))), prologue_med=float(np.median(pro)),
+            lengths_med=float(np.median(lengths)),
+            lengths_wg_med=float(np.median(lengths_wg)) if d[:, 8].any() else 0.0,
+            prologue_med=float(np.median(pro)),
             search_med=float(np.median(rel(9))), page_id_med=float(np.median(rel(10))),
             loop_med=float(np.median(loop)), loop_last=float(loop.max()),
             data_med=float(np.median(rel(11))), data_last=float(rel(11).max()),
