@@ -591,11 +591,13 @@ struct Tile {
 // takes its tiles lo, lo + stride, ... below hi = the sequence's tile count,
 // and writes its one piece (normalised output, base-2 LSE) to LDS at lds_o
 // [C][HD] and lds_lse [C] for the workgroup to merge; s_tiles is not read.
+// Without a window and with page-uniform tiles, pg_first is the page id of
+// tile lo, already read by the caller.
 template <int HD, int HR, typename T, bool kF8, bool kLanePages, int NBUF, bool kExtras,
           bool kSeq>
 __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *s_tiles, int kvh,
                                           int rr, int lo, int hi, int stride, float *lds_o,
-                                          float *lds_lse) {
+                                          float *lds_lse, int pg_first = 0) {
   const int tstep = kSeq ? stride : 1;  // tile index step between the wave's tiles
   using E = Elem<T>;
   constexpr int NCH = HD / 32;               // MFMA steps over the head dim
@@ -1008,6 +1010,9 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   static_for<NBUF>([&](auto ic) {
     constexpr int i = decltype(ic)::value;
     make_tile(lo + i * tstep, sets[i].d, sets[i].lpg);
+    // The caller's page id of the first tile replaces make_tile's read,
+    // which is then dead code.
+    if constexpr (i == 0 && kSeq && !kLanePages && !kExtras) sets[0].d.pg = pg_first;
     if constexpr (i < NBUF - 1) issue(sets[i]);
   });
   wave_stamp_after(p, 10, sets[0].d.pg);
@@ -1104,24 +1109,26 @@ __device__ __forceinline__ void lse_fold(float &M, float &W, float4 &A, float m2
 constexpr int kCombineThreads = 256;
 
 template <int HD, typename T>
-__global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(const int32_t *ws_s,
-                                                                         int batch, int nblk,
-                                                                         CombineParams p) {
+__global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(
+    const int32_t *ws_s, const float *ws_o, const float *ws_lse, int batch, int nblk, int H,
+    int hq, int ql, int gq, int ns, CombineParams p) {
   using E = Elem<T>;
   constexpr int CH = HD / 4;  // float4 chunks per head
   constexpr int kUnroll = 8;
   __shared__ float s_red[kCombineThreads * 6];
-  const int H = p.heads_per_block;
+  // Everything up to the piece loads comes from the leading arguments (the
+  // CombineParams fields of the same names, preloaded into SGPRs): the
+  // prefix sums are read at once and the pieces right after them.
+  const int b = blockIdx.x / nblk;  // nblk = ceil(nv / H) blocks per sequence
+  const int NT = ws_s[batch];
+  const int sb = ws_s[b], se = ws_s[b + 1];
   const int CB = H * CH;
   const int groups = kCombineThreads / CB;
-  const int nv = p.hq * p.ql;  // (query token, head) rows per sequence
-  const int b = blockIdx.x / nblk;  // nblk = ceil(nv / H) blocks per sequence
+  const int nv = hq * ql;  // (query token, head) rows per sequence
   const int vh = (blockIdx.x % nblk) * H + (threadIdx.x % CB) / CH;
   const int cc = threadIdx.x % CH;
   const int g = threadIdx.x / CB;
   block_stamp_after(p, 0, g);
-  const int NT = ws_s[batch];
-  const int sb = ws_s[b], se = ws_s[b + 1];
   block_stamp_after(p, 1, NT + sb + se);
   // Prefix sums that do not describe tiles inside [0, NT) (a workspace the
   // partial kernel did not fill) are skipped, so every index stays in range.
@@ -1129,18 +1136,17 @@ __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(const in
     block_stamp_after(p, 3, sb);
     return;
   }
-  const int R = min(p.num_ranges, NT);
+  const int R = min(ns, NT);
   const int ra = range_of(sb, R, NT), rb = range_of(se - 1, R, NT);
   if (ra == rb) {
     block_stamp_after(p, 3, ra);
     return;
   }
   const int slot_a = (range_lo(ra, R, NT) == sb) ? 0 : 1;
-  const int ns = p.num_ranges;
   const bool live = vh < nv;  // the last block of a sequence may run past the rows
-  const int t = live ? vh / p.hq : 0, h = live ? vh - t * p.hq : 0;
-  const int kvh = h / p.gq, hh = t * p.gq + (h - kvh * p.gq);  // piece column
-  const int nc = p.gq * p.ql;
+  const int t = live ? vh / hq : 0, h = live ? vh - t * hq : 0;
+  const int kvh = h / gq, hh = t * gq + (h - kvh * gq);  // piece column
+  const int nc = gq * ql;
   float M = -INFINITY, W = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   if (live) {
@@ -1151,8 +1157,8 @@ __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(const in
       for (int i = 0; i < kUnroll; ++i) {
         const int q = min(q0 + i * groups, rb);
         const int64_t ps = ((int64_t)(kvh * ns + q) * 2 + (q == ra ? slot_a : 0)) * nc + hh;
-        l[i] = (q0 + i * groups <= rb) ? p.ws_lse[ps] : -INFINITY;
-        ov[i] = reinterpret_cast<const float4 *>(p.ws_o + ps * HD)[cc];
+        l[i] = (q0 + i * groups <= rb) ? ws_lse[ps] : -INFINITY;
+        ov[i] = reinterpret_cast<const float4 *>(ws_o + ps * HD)[cc];
       }
 #pragma unroll
       for (int i = 0; i < kUnroll; ++i) lse_fold(M, W, acc, l[i], 1.f, ov[i]);
@@ -1210,15 +1216,30 @@ void seq_decode_kernel(const int32_t *seqlens, const int32_t *bt, int64_t bt_str
   using E = Elem<T>;
   constexpr int CH = HD / 4;  // float4 chunks per head row
   extern __shared__ float s_piece[];
-  const int nc = p.gq * p.ql;
+  // One kv head per workgroup (the launcher's shape): wave s takes tiles s,
+  // s + WAVES, ... of the sequence.
+  constexpr int KH = 1, S = WAVES;
   const int wave = rfl(threadIdx.x >> 6);
-  const int KH = p.heads_per_wg, S = p.subs;
-  const int kh = wave % KH, sub = wave / KH;
-  const int kvh = blockIdx.x * KH + kh;
+  const int sub = wave;
+  const int kvh = blockIdx.x;
   const int b = blockIdx.y;
-  float *const lse_base = s_piece + WAVES * nc * HD;
   const unsigned long long t_entry = wave_clock();
-  const int L = seq_len_of(seqlens, b, seqlen_add, max_len);
+  // The length and (no window, page-uniform tiles) the first tile's page id
+  // first: their addresses need only the preloaded leading arguments, so
+  // both loads go out with the kernel-argument loads.
+  const int len_raw = as_const(seqlens)[b];
+  int pg_first = 0;
+  if constexpr (!kExtras && !kLanePages)
+    pg_first = as_const(bt + (int64_t)b * bt_stride)[min(sub * kTile, max_len - 1) >> ps_log2];
+  // One wait for all of them and for the arguments the first K/V loads need
+  // (otherwise each is read where first used, one round trip after another).
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::"s"(len_raw), "s"(pg_first), "s"(p.q), "s"(p.k), "s"(p.v), "s"(p.sp_bytes),
+               "s"(p.st_bytes), "s"(p.hkv));
+  const int nc = p.gq * p.ql;
+  float *const lse_base = s_piece + WAVES * nc * HD;
+  int L = len_raw + seqlen_add;
+  L = L < 0 ? 0 : (L > max_len ? max_len : L);
   const int n = L > 0 ? (kExtras ? tiles_of(L, p.ql, p.window_left) : (L + kTile - 1) / kTile)
                       : 0;
   if ((threadIdx.x & 63) < nc) lse_base[wave * nc + (threadIdx.x & 63)] = -INFINITY;
@@ -1235,7 +1256,7 @@ void seq_decode_kernel(const int32_t *seqlens, const int32_t *bt, int64_t bt_str
     wave_stamp(p, 0, t_entry);
     wave_stamp(p, 1, wave_clock());
     run_range<HD, HR, T, kF8, kLanePages, NBUF, kExtras, true>(
-        v, nullptr, kvh, 0, sub, n, S, s_piece + wave * nc * HD, lse_base + wave * nc);
+        v, nullptr, kvh, 0, sub, n, S, s_piece + wave * nc * HD, lse_base + wave * nc, pg_first);
     wave_stamp(p, 3, wave_clock());
     wave_stamp(p, 4, (n - sub + S - 1) / S);
     wave_stamp(p, 5, 1);
@@ -1388,7 +1409,8 @@ constexpr size_t kSeqLdsMax = (size_t)64 << 10;
 
 template <int HD, int HR, typename T, bool kF8, bool kExtras>
 static void launch_seq_x(const DecodeParams &p, hipStream_t st) {
-  dim3 grid((p.hkv + p.heads_per_wg - 1) / p.heads_per_wg, p.batch);
+  // The kernel assumes one kv head per workgroup and kSeqWaves waves on it.
+  dim3 grid(p.hkv, p.batch);
   const size_t lds = seq_lds_bytes(HD, p.gq * p.ql);
   if (p.ps_log2 >= 4)
     hipLaunchKernelGGL((seq_decode_kernel<HD, HR, T, kF8, false, kNbuf<HD, kF8>, kSeqWaves,
@@ -1422,6 +1444,7 @@ static int launch_seq_hr(const DecodeParams &p, hipStream_t st) {
 
 template <int HD>
 int launch_seq_hd(const DecodeParams &p, int dtype, bool fp8, hipStream_t st) {
+  if (p.heads_per_wg != 1 || p.subs != kSeqWaves) return MXFA_ELAUNCH;  // the kernel's shape
   if (dtype == MXFA_DTYPE_BF16)
     return fp8 ? launch_seq_hr<HD, BF16, true>(p, st) : launch_seq_hr<HD, BF16, false>(p, st);
   return fp8 ? launch_seq_hr<HD, F16, true>(p, st) : launch_seq_hr<HD, F16, false>(p, st);
@@ -1434,10 +1457,12 @@ int launch_combine_hd(const CombineParams &c, int dtype, hipStream_t st) {
   dim3 grid(c.batch * nblk);
   if (dtype == MXFA_DTYPE_BF16)
     hipLaunchKernelGGL((split_combine_kernel<HD, BF16>), grid, dim3(kCombineThreads), 0, st,
-                       c.ws_s, c.batch, nblk, c);
+                       c.ws_s, c.ws_o, c.ws_lse, c.batch, nblk, c.heads_per_block, c.hq, c.ql,
+                       c.gq, c.num_ranges, c);
   else
     hipLaunchKernelGGL((split_combine_kernel<HD, F16>), grid, dim3(kCombineThreads), 0, st,
-                       c.ws_s, c.batch, nblk, c);
+                       c.ws_s, c.ws_o, c.ws_lse, c.batch, nblk, c.heads_per_block, c.hq, c.ql,
+                       c.gq, c.num_ranges, c);
   return hipGetLastError() == hipSuccess ? MXFA_OK : MXFA_ELAUNCH;
 }
 
