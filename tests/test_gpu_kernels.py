@@ -344,6 +344,37 @@ def test_maximum_batch(device):
         assert max_err(run_native(b, **kw), expected) <= TOL[torch.float16]
 
 
+@pytest.mark.parametrize("batch", [257, 513, 1024, 4353])
+@pytest.mark.parametrize("kv_heads,head_dim,dtype", [(2, 128, torch.bfloat16),
+                                                     (8, 64, torch.float16)],
+                         ids=["4wave", "8wave"])
+@pytest.mark.parametrize("window", [-1, 20])
+def test_batches_past_one_length_per_thread(device, batch, kv_heads, head_dim, dtype, window):
+    # The tile scan reads one length per thread up to the workgroup's
+    # threads (256 for four-wave, 512 for eight-wave workgroups) and batches
+    # of eight loads past that: 257 and 513 sit one past each size, 4353
+    # needs two rounds of eight per thread in the four-wave kernel. A window
+    # takes the extended instantiation's tile count.
+    g = torch.Generator().manual_seed(batch + head_dim)
+    lengths = torch.randint(0, 48, (batch,), generator=g)
+    b = make_paged_batch(batch, 2 * kv_heads, kv_heads, head_dim, dtype, lengths,
+                         seed=batch).to(device)
+    cpu = b.to("cpu")
+    # Empty sequences (one in ten) give zero rows; the oracle, like the
+    # reference, rejects them, so it runs them at length 1 and those rows
+    # are cleared.
+    empty = cpu.cache_seqlens == 0
+    expected = reference_port.attention_kvcache(
+        cpu.q, cpu.k_cache, cpu.v_cache, cache_seqlens=cpu.cache_seqlens.clamp(min=1),
+        block_table=cpu.block_table, softmax_scale=cpu.scale, window_left=window)
+    expected[empty] = 0
+    assert empty.any()
+    for ns in (None, 1000):
+        kw = {} if ns is None else dict(num_splits=ns)
+        out = run_native(b, window_left=window, **kw)
+        assert max_err(out, expected) <= TOL[dtype], ns
+
+
 def test_most_splits_and_largest_page(device):
     # 65535 ranges (the maximum; more than there are tiles, so R = NT) and
     # 4096-token pages.
