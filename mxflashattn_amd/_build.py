@@ -29,7 +29,11 @@ ARCH = "gfx950"
 # from plain float code, and some of their forms have given wrong results on
 # MI355X boxes with no error raised. Kernel arguments ahead of the parameter
 # struct (what each kernel's first loads need) are preloaded into SGPRs at
-# wave launch, so those loads do not wait for a kernarg-segment read.
+# wave launch, so those loads do not wait for a kernarg-segment read. MFMA
+# results and accumulators live in VGPRs where the kernel fits 256 of them:
+# with accumulation registers the compiler put the QK scores and the PV
+# accumulators in the same ones and copied the accumulators out and back on
+# every tile (40 copies per tile at 16-bit HD 64).
 HIPCC_FLAGS = (
     f"--offload-arch={ARCH}",
     "-O3",
@@ -38,6 +42,8 @@ HIPCC_FLAGS = (
     "-mcode-object-version=5",
     "-mllvm",
     "-amdgpu-kernarg-preload-count=16",
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form",
     "-Xclang",
     "-target-feature",
     "-Xclang",

@@ -686,9 +686,19 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   // wait for the length.
   int p_start = kSeq ? 0 : rfl(s_tiles[pb]);
   int p_end = kSeq ? hi : rfl(s_tiles[pb + 1]);
+  ConstI32 p_bt = as_const(p.bt + (int64_t)pb * p.bt_stride);
+  // Split kernel without a window: the first tile's page id needs only
+  // p_start, so its load goes out before the length's (the scheduling barrier
+  // keeps that order) and the two share one round trip. Issued after, it
+  // would wait for the length: the compiler uses the length at once. The
+  // position is clamped into the table row (an empty range at the batch end
+  // may start past its sequence's last page).
+  if constexpr (!kSeq && !kLanePages && !kExtras) {
+    pg_first = p_bt[min((lo - p_start) * kTile, p.max_len - 1) >> p.ps_log2];
+    __builtin_amdgcn_sched_barrier(0);
+  }
   int p_len = seq_len_of(p.seqlens, pb, p.seqlen_add, p.max_len);
   int p_first = kExtras ? first_tile_of(p_len, p.ql, p.window_left) : 0;  // tile at p_start
-  ConstI32 p_bt = as_const(p.bt + (int64_t)pb * p.bt_stride);
 
   auto make_tile = [&](int t, Tile &d, int (&lpg)[NPG]) {
     // kSeq: the page id is read before the range test, clamped into the
@@ -745,7 +755,17 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
     }
   };
 
+  // In the split kernel the page id is read one pipeline step before issue()
+  // uses it; the empty asm keeps the clamp (and so the wait for that read)
+  // here instead of letting the compiler clamp it right after the read and
+  // stall there. (The per-sequence kernel measured better without it.)
   auto clamp_page = [&](int pg) -> int {
+    if constexpr (!kSeq) {
+      if constexpr (kLanePages)
+        asm volatile("" : "+v"(pg));  // per-lane page ids
+      else
+        asm volatile("" : "+s"(pg));
+    }
     pg = pg < 0 ? 0 : pg;
     return pg >= p.num_pages ? p.num_pages - 1 : pg;
   };
@@ -761,9 +781,11 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
 
   auto issue = [&](Set &s) {
     const Tile &d = s.d;
+    // rfl: the size is wave-uniform; without it the compiler may keep it in a
+    // VGPR and wrap the q loads in a loop over distinct descriptors.
     const __amdgpu_buffer_rsrc_t rq =
         make_srd(p.q + (int64_t)d.b * p.q_sb + (int64_t)kvh * gq * p.q_sh,
-                 (d.flags & kFirst) ? q_bytes : 0);
+                 rfl((d.flags & kFirst) ? q_bytes : 0));
     if (d.flags & kFirst) {  // wave-uniform; q is loaded once per piece
 #pragma unroll
       for (int cc = 0; cc < NCH; ++cc) s.q[cc] = buf_load16<0>(rq, q_off + q_step(cc));
@@ -1010,9 +1032,9 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   static_for<NBUF>([&](auto ic) {
     constexpr int i = decltype(ic)::value;
     make_tile(lo + i * tstep, sets[i].d, sets[i].lpg);
-    // The caller's page id of the first tile replaces make_tile's read,
-    // which is then dead code.
-    if constexpr (i == 0 && kSeq && !kLanePages && !kExtras) sets[0].d.pg = pg_first;
+    // The page id of the first tile read above (or by the caller) replaces
+    // make_tile's read, which is then dead code.
+    if constexpr (i == 0 && !kLanePages && !kExtras) sets[0].d.pg = pg_first;
     if constexpr (i < NBUF - 1) issue(sets[i]);
   });
   wave_stamp_after(p, 10, sets[0].d.pg);
