@@ -323,6 +323,7 @@ static SplitArgs split_args(const void *q, int64_t q_stride_b, int64_t q_stride_
 // Per-sequence launch shape: one kv head per workgroup, kSeqWaves waves on it.
 static Grid seq_grid(int hkv, int batch) {
   Grid g;
+  g.waves = kSeqWaves;
   g.heads_per_wg = 1;
   g.subs = kSeqWaves;
   g.gx = hkv;

@@ -139,8 +139,10 @@ struct DecodeParams {
 #endif
 };
 
+// Launch shape: workgroups of `waves` waves (a kernel instantiation), of which
+// heads_per_wg x subs are used (kv head, sub-range); gx x gy workgroups.
 struct Grid {
-  int heads_per_wg, subs, gx, gy;
+  int waves, heads_per_wg, subs, gx, gy;
 };
 
 struct CombineParams {
@@ -1320,9 +1322,10 @@ void seq_decode_kernel(const int32_t *seqlens, const int32_t *bt, int64_t bt_str
 template <int HD, bool kF8>
 constexpr int kRowBytes = HD * (kF8 ? 1 : 2);
 
-// Waves per workgroup: one wave per kv head (KH = min(HKV, max) kv heads per
-// workgroup), at least 4 waves (S = 4 / KH sub-ranges when HKV < 4), at most
-// 8 for rows of up to 128 bytes and 4 for longer rows; one workgroup per CU.
+// Waves per workgroup: one wave per kv head (KH = min(HKV, waves) kv heads per
+// workgroup, S = waves / KH sub-ranges when HKV < 4); 4 waves for HKV <= 4,
+// else 8 for rows of up to 128 bytes and 4 for longer rows; one workgroup per
+// CU. Waves past KH x S (HKV 3, 5, 6, 7) leave at once.
 // Measured on MI355X (one call, config-2 lengths): with 256-byte rows
 // eight-wave workgroups run as two generations of four waves per CU (the
 // second wave on each SIMD issues its first loads only when the first
@@ -1337,13 +1340,13 @@ constexpr int kMaxWaves = kRowBytes<HD, kF8> <= 128 ? 8 : 4;
 
 inline int waves_for(int row_bytes, int hkv) {
   const int most = row_bytes <= 128 ? 8 : 4;
-  const int kh = hkv < most ? hkv : most;
-  return kh >= kMinWaves ? kh : kMinWaves;
+  return hkv > kMinWaves ? most : kMinWaves;
 }
 
 // Workgroups of `waves` waves: min(HKV, waves) kv heads x waves / that sub-ranges.
 inline Grid grid_for(int hkv, int num_splits, int waves) {
   Grid g;
+  g.waves = waves;
   g.heads_per_wg = hkv < waves ? hkv : waves;
   g.subs = waves / g.heads_per_wg;
   g.gx = (hkv + g.heads_per_wg - 1) / g.heads_per_wg;
@@ -1382,11 +1385,16 @@ static int launch_partial_w(const DecodeParams &p, const Grid &g, hipStream_t st
   return hipGetLastError() == hipSuccess ? MXFA_OK : MXFA_ELAUNCH;
 }
 
+// The kernel is the grid's wave count; a grid the instantiations cannot run
+// (more waves than the row size has, or its heads and sub-ranges past the
+// waves) is refused: its extra kv heads would go uncomputed.
 template <int HD, int HR, typename T, bool kF8>
 static int launch_partial_t(const DecodeParams &p, const Grid &g, hipStream_t st) {
+  if (g.heads_per_wg * g.subs > g.waves) return MXFA_ELAUNCH;
   if constexpr (kMaxWaves<HD, kF8> == 8) {
-    if (g.heads_per_wg * g.subs == 8) return launch_partial_w<HD, HR, T, kF8, 8>(p, g, st);
+    if (g.waves == 8) return launch_partial_w<HD, HR, T, kF8, 8>(p, g, st);
   }
+  if (g.waves != 4) return MXFA_ELAUNCH;
   return launch_partial_w<HD, HR, T, kF8, 4>(p, g, st);
 }
 

@@ -84,10 +84,10 @@ def heuristic_closed_form(b, hq, hkv, hd, ps, btw, cus, elem_bytes=2):
     fits = 16 * -(-hq // hkv) * (hd + 1) <= 64 << 10
     if ps >= 16 and work <= 16384 and fits and ((row <= 128 and cap <= 768) or mid):
         return native.SPLITS_PER_SEQUENCE
-    # Otherwise one wave per (kv head, range): a workgroup has max(4, min(HKV,
-    # 8 for head rows of <= 128 bytes, else 4)) waves = min(HKV, waves) kv heads
-    # x waves // that sub-ranges, one workgroup per CU.
-    waves = max(4, min(hkv, 8 if row <= 128 else 4))
+    # Otherwise one wave per (kv head, range): a workgroup has 4 waves for
+    # HKV <= 4, else 8 for head rows of <= 128 bytes and 4 for longer ones;
+    # min(HKV, waves) kv heads x waves // that sub-ranges, one workgroup per CU.
+    waves = 4 if hkv <= 4 else (8 if row <= 128 else 4)
     kh = min(hkv, waves)
     subs = waves // kh
     gx = -(-hkv // kh)
@@ -99,7 +99,9 @@ def heuristic_closed_form(b, hq, hkv, hd, ps, btw, cus, elem_bytes=2):
 @pytest.mark.parametrize("args", [
     (32, 32, 8, 128, 16, 512, 256),    # config 2: 256 CUs x 8 waves / 8 kv heads
     (32, 32, 16, 128, 16, 512, 256),   # GQ2: 16 kv heads, two workgroups per range
-    (32, 32, 4, 64, 16, 512, 256),     # GQ8 HD64: two sub-ranges per workgroup
+    (32, 32, 4, 64, 16, 512, 256),     # GQ8 HD64: four kv heads, one range per workgroup
+    (32, 24, 6, 64, 16, 512, 256),     # 6 kv heads of 8 waves: one range per workgroup
+    (32, 24, 6, 128, 16, 512, 256),    # 6 kv heads, 256-byte rows: two head groups
     (1, 2, 1, 64, 16, 1, 256),         # one tile in total: per sequence
     (1, 2, 1, 64, 8, 2, 256),          # one tile, pages of 8: split
     (4, 8, 2, 64, 16, 32, 256),        # config 1's table: per sequence

@@ -207,6 +207,35 @@ def test_kv_head_counts(device, hq, hkv, head_dim):
         assert max_err(run_native(b, **kw), expected) <= TOL[torch.bfloat16], ns
 
 
+@pytest.mark.parametrize("hkv", [5, 6, 7])
+@pytest.mark.parametrize("head_dim,fp8", [(64, False), (128, False), (64, True), (128, True)],
+                         ids=["hd64", "hd128", "fp8_hd64", "fp8_hd128"])
+def test_five_to_seven_kv_heads(device, hkv, head_dim, fp8):
+    # Rows of up to 128 bytes (16-bit HD 64, fp8 HD 64 and 128) put 5-7 kv
+    # heads in one eight-wave workgroup whose other waves leave at once;
+    # 256-byte rows split them over two four-wave head groups. The output
+    # starts as NaN, so a head no wave computes cannot pass.
+    lengths = torch.tensor([1, 40, 700, 16, 2100])
+    b = make_paged_batch(5, 2 * hkv, hkv, head_dim, torch.bfloat16, lengths,
+                         seed=60 + hkv).to(device)
+    k_cache, v_cache = b.k_cache, b.v_cache
+    if fp8:
+        k_cache = b.k_cache.cpu().to(torch.float8_e4m3fn).to(device)
+        v_cache = b.v_cache.cpu().to(torch.float8_e4m3fn).to(device)
+        expected = torch.from_numpy(c_oracle.paged_decode_fp8_f64(
+            b.q.cpu(), k_cache.cpu(), v_cache.cpu(), b.block_table.cpu(),
+            b.cache_seqlens.cpu(), b.scale, 1.0, 1.0)).reshape(b.q.shape)
+    else:
+        expected = oracle_out(b)
+    for ns in (None, 1, 5, 64, native.SPLITS_PER_SEQUENCE):
+        out = torch.full_like(b.q, float("nan"))
+        native.paged_decode_split(b.q, k_cache, v_cache, b.block_table, b.cache_seqlens,
+                                  b.scale, out=out, num_splits=ns)
+        torch.cuda.synchronize()
+        err = max_err(out, expected)
+        assert err <= TOL[torch.bfloat16], (ns, err)
+
+
 def test_back_to_back_calls_of_changing_shapes_share_the_workspace(device):
     # Every call on a stream reuses one workspace; calls of other shapes in
     # between must not leave anything a later call reads.
