@@ -13,7 +13,9 @@ columns (QL x GQ up to 64: launches of token chunks), with the extras of the
 second sweep on half of them. A fourth runs cases of all three kinds through
 the per-sequence kernel (num_splits = SPLITS_PER_SEQUENCE), whose pieces live
 in LDS: a launch of 16 columns at head dim 256 does not fit and must be
-refused. Seeds are fixed: every run checks the same cases.
+refused. A fifth draws its kv heads from 5, 6, 7, 9, 10 and 12 (workgroups
+with idle waves, two or more head groups) and mixes the other four kinds. Seeds
+are fixed: every run checks the same cases.
 """
 
 from __future__ import annotations
@@ -33,9 +35,9 @@ TOL = {torch.float16: 2e-3, torch.bfloat16: 1.6e-2}
 FP8 = torch.float8_e4m3fn
 
 
-def draw(seed: int) -> dict:
+def draw(seed: int, hkv_choices: tuple = (1, 2, 3, 4, 8)) -> dict:
     r = random.Random(seed)
-    hkv = r.choice([1, 2, 3, 4, 8])
+    hkv = r.choice(hkv_choices)
     gq = r.choice([1, 2, 3, 4, 5, 8, 16])
     ql = r.choice([q for q in (1, 1, 1, 2, 3, 4, 8) if q * gq <= 16])
     batch = r.randint(1, 9)
@@ -110,6 +112,12 @@ def test_random_per_sequence_sweep(device, seed):
              per_sequence=True)
 
 
+@pytest.mark.parametrize("seed", range(480, 600))
+def test_random_odd_kv_heads_sweep(device, seed):
+    run_case(device, seed, extended=seed % 4 == 1, chunked_query=seed % 4 == 2,
+             per_sequence=seed % 4 == 3, hkv_choices=(5, 6, 7, 9, 10, 12))
+
+
 def chunked(c: dict, seed: int) -> dict:
     """The case as a causal query past the kernel's 16 columns (GQ >= 2)."""
     r = random.Random(30_000 + seed)
@@ -119,8 +127,8 @@ def chunked(c: dict, seed: int) -> dict:
 
 
 def run_case(device, seed: int, extended: bool, chunked_query: bool = False,
-             per_sequence: bool = False):
-    c = draw(seed)
+             per_sequence: bool = False, hkv_choices: tuple = (1, 2, 3, 4, 8)):
+    c = draw(seed, hkv_choices)
     if chunked_query:
         c = chunked(c, seed)
     if per_sequence:
