@@ -461,11 +461,13 @@ __device__ __forceinline__ int wave_scan_incl(int x) {
 // threads (seqlens and B are the kernel's preloaded leading arguments, equal
 // to p.seqlens and p.batch). The lengths are read from memory once, eight loads in flight per
 // thread: the first pass parks each tile count in s[b], the second turns them
-// into prefix sums in place. Without a window (kWindow false) every sequence
-// starts at its tile 0.
+// into prefix sums in place (up to one sequence per thread, the count stays in a
+// register instead). Without a window (kWindow false) every sequence starts at
+// its tile 0. Returns the tile total s[B] (from the wave totals, so no thread
+// reads s[B] back).
 template <int kThreads, bool kWindow>
-__device__ __forceinline__ void tile_prefix(const DecodeParams &p, const int32_t *seqlens, int B,
-                                            int32_t *s, int *wave_tot) {
+__device__ __forceinline__ int tile_prefix(const DecodeParams &p, const int32_t *seqlens, int B,
+                                           int32_t *s, int *wave_tot) {
   constexpr int kWaves = kThreads / 64;
   constexpr int kBatchLoads = 8;
   const int per = (B + kThreads - 1) / kThreads;
@@ -476,7 +478,6 @@ __device__ __forceinline__ void tile_prefix(const DecodeParams &p, const int32_t
     if (b < B) {
       const int L = seq_len_of(seqlens, b, p.seqlen_add, p.max_len);
       local = kWindow ? tiles_of(L, p.ql, p.window_left) : (L + kTile - 1) / kTile;
-      s[b] = local;
     }
   }
   for (int i0 = 0; per > 1 && i0 < per; i0 += kBatchLoads) {
@@ -507,20 +508,29 @@ __device__ __forceinline__ void tile_prefix(const DecodeParams &p, const int32_t
   const int x = wave_scan_incl(local);
   if (lane == 63) wave_tot[wave] = x;
   __syncthreads();
-  int base = 0;
+  int base = 0, total = 0;
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) base += w < wave ? wave_tot[w] : 0;
+  for (int w = 0; w < kWaves; ++w) {
+    const int t = wave_tot[w];
+    base += w < wave ? t : 0;
+    total += t;
+  }
   int run = base + x - local;  // exclusive prefix of this thread's first element
-  for (int i = 0; i < per; ++i) {  // each thread rewrites only its own entries
-    const int b = b0 + i;
-    if (b < B) {
-      const int n = s[b];
-      s[b] = run;
-      run += n;
+  if (per == 1) {
+    if (b0 < B) s[b0] = run;
+  } else {
+    for (int i = 0; i < per; ++i) {  // each thread rewrites only its own entries
+      const int b = b0 + i;
+      if (b < B) {
+        const int n = s[b];
+        s[b] = run;
+        run += n;
+      }
     }
   }
-  if (threadIdx.x == kThreads - 1) s[B] = base + x;
+  if (threadIdx.x == kThreads - 1) s[B] = total;
   __syncthreads();
+  return total;
 }
 
 // Empty sequences (no tiles) get zero output; sequence b is cleared by the
@@ -667,27 +677,37 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   // Sequence holding tile lo: the largest b < B with s[b] <= lo (then
   // s[b+1] > lo). s is nondecreasing and s[0] = 0 <= lo, so the lanes whose
   // probe passes form a prefix: each round narrows [a, a + n) to one of 64
-  // steps (one round for B <= 64, three for B <= 16000).
-  int pb = 0;
+  // steps (one round for B < 64, three for B <= 16000).
+  // Cursor of the tile builder (runs NBUF tiles ahead of the math): the
+  // sequence pb and its tiles [p_start, p_end). Without a window every
+  // sequence starts at its tile 0, so the first page id does not wait for the
+  // length.
+  int pb = 0, p_start = 0, p_end = hi;
   if constexpr (!kSeq) {
-    int a = 0, n = B;
-    while (n > 1) {
-      const int step = (n + 63) >> 6;
-      const int idx = a + lane * step;
-      const bool ok = idx < a + n && s_tiles[idx] <= lo;
-      const int cnt = __builtin_popcountll(__builtin_amdgcn_ballot_w64(ok));
-      const int na = a + (cnt - 1) * step;
-      n = min(step, a + n - na);
-      a = na;
+    if (B < 64) {
+      // One round: lane l holds s[min(l, B)], so s[pb] and s[pb + 1] come
+      // from two lanes rather than from another LDS read.
+      const int v = s_tiles[min(lane, B)];
+      pb = __builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < B && v <= lo)) - 1;
+      p_start = __builtin_amdgcn_readlane(v, pb);
+      p_end = __builtin_amdgcn_readlane(v, pb + 1);
+    } else {
+      int a = 0, n = B;
+      while (n > 1) {
+        const int step = (n + 63) >> 6;
+        const int idx = a + lane * step;
+        const bool ok = idx < a + n && s_tiles[idx] <= lo;
+        const int cnt = __builtin_popcountll(__builtin_amdgcn_ballot_w64(ok));
+        const int na = a + (cnt - 1) * step;
+        n = min(step, a + n - na);
+        a = na;
+      }
+      pb = rfl(a);
+      p_start = rfl(s_tiles[pb]);
+      p_end = rfl(s_tiles[pb + 1]);
     }
-    pb = rfl(a);
     wave_stamp_after(p, 9, pb);
   }
-  // Cursor of the tile builder (runs NBUF tiles ahead of the math). Without a
-  // window every sequence starts at its tile 0, so the first page id does not
-  // wait for the length.
-  int p_start = kSeq ? 0 : rfl(s_tiles[pb]);
-  int p_end = kSeq ? hi : rfl(s_tiles[pb + 1]);
   ConstI32 p_bt = as_const(p.bt + (int64_t)pb * p.bt_stride);
   // Split kernel without a window: the first tile's page id needs only
   // p_start, so its load goes out before the length's (the scheduling barrier
@@ -1080,7 +1100,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(const int3
   __shared__ int s_wave_tot[WAVES];
 
   const unsigned long long t_entry = wave_clock();
-  tile_prefix<kThreads, kExtras>(p, seqlens, batch, s_tiles, s_wave_tot);  // ends with a barrier
+  const int NT = rfl(tile_prefix<kThreads, kExtras>(p, seqlens, batch, s_tiles, s_wave_tot));
   zero_empty<HD, kThreads>(p, s_tiles);
   const int B = batch;
   if (blockIdx.x == 0 && blockIdx.y == 0) {
@@ -1091,7 +1111,6 @@ __global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(const int3
   const int KH = p.heads_per_wg;
   const int kh = wave % KH, sub = wave / KH;
   const int kvh = blockIdx.x * KH + kh;
-  const int NT = rfl(s_tiles[B]);
   const int R = min(p.num_ranges, NT);  // every range holds >= 1 tile
   const int rr = blockIdx.y * p.subs + sub;
   if (sub >= p.subs || kvh >= p.hkv || rr >= R) return;
