@@ -125,6 +125,25 @@ def test_large_scores_do_not_overflow(device):
     assert max_err(got, expected) <= 2e-3
 
 
+@pytest.mark.parametrize("scale", [-0.125, -1.5, 1e-4, 3.0])
+@pytest.mark.parametrize("dtype,head_dim,gq", [(torch.bfloat16, 128, 4), (torch.float16, 64, 8)])
+def test_negative_tiny_and_large_scales(device, scale, dtype, head_dim, gq):
+    # Any finite scale is valid: a negative one turns the largest dot products
+    # into the smallest scores, a large one makes the softmax nearly one-hot
+    # (base-2 scores in the hundreds, the running maximum moving often).
+    b = make_paged_batch(4, 2 * gq, 2, head_dim, dtype, torch.tensor([1, 37, 600, 2000]),
+                         seed=70 + head_dim).to(device)
+    expected = torch.from_numpy(c_oracle.paged_decode_f64(
+        b.q.cpu(), b.k_cache.cpu(), b.v_cache.cpu(), b.block_table.cpu(), b.cache_seqlens.cpu(),
+        scale)).reshape(b.q.shape)
+    for ns in (None, 1, 7, native.SPLITS_PER_SEQUENCE):
+        out = torch.full_like(b.q, float("nan"))
+        native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
+                                  scale, out=out, num_splits=ns)
+        torch.cuda.synchronize()
+        assert max_err(out, expected) <= TOL[dtype], (ns, max_err(out, expected))
+
+
 def test_noncontiguous_q_and_out(device):
     b = make_paged_batch(4, 16, 4, 128, torch.float16, torch.tensor([33, 64, 1, 200]),
                          seed=8).to(device)
