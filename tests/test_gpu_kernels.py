@@ -144,6 +144,23 @@ def test_negative_tiny_and_large_scales(device, scale, dtype, head_dim, gq):
         assert max_err(out, expected) <= TOL[dtype], (ns, max_err(out, expected))
 
 
+@pytest.mark.parametrize("page_size", [4, 16])
+def test_table_slots_past_each_length_are_never_read(device, page_size):
+    # Serving frameworks pad block-table rows past a sequence's pages with -1
+    # or leave stale ids there: the result must not depend on them.
+    lengths = torch.tensor([1, 16, 17, 250, 0, 700])
+    b = make_paged_batch(6, 8, 2, 128, torch.bfloat16, lengths, page_size=page_size, seed=31,
+                         block_table_width=700 // page_size + 8).to(device)
+    used = (b.cache_seqlens.long() + page_size - 1) // page_size
+    past = torch.arange(b.block_table.shape[1], device=device)[None, :] >= used[:, None]
+    for ns in (None, 1, 3, 64, native.SPLITS_PER_SEQUENCE):
+        want = run_native(b, num_splits=ns)
+        for pad in (-1, 2**31 - 1):
+            padded = PagedBatch(b.q, b.k_cache, b.v_cache,
+                                b.block_table.masked_fill(past, pad), b.cache_seqlens, b.scale)
+            assert torch.equal(run_native(padded, num_splits=ns).cpu(), want.cpu()), (ns, pad)
+
+
 def test_noncontiguous_q_and_out(device):
     b = make_paged_batch(4, 16, 4, 128, torch.float16, torch.tensor([33, 64, 1, 200]),
                          seed=8).to(device)
