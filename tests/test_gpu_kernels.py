@@ -161,6 +161,38 @@ def test_table_slots_past_each_length_are_never_read(device, page_size):
             assert torch.equal(run_native(padded, num_splits=ns).cpu(), want.cpu()), (ns, pad)
 
 
+def test_pages_past_4_gib(device):
+    # K and V caches of about 4.4 GB each, every used page past the 4 GiB byte
+    # offset: tile addresses and append destinations need 64-bit arithmetic.
+    # The same pages in a small pool give the same result bit for bit.
+    hkv, hd, ps = 2, 128, 16
+    small = make_paged_batch(3, 8, hkv, hd, torch.bfloat16, torch.tensor([40, 700, 5]), seed=41,
+                             block_table_width=48).to(device)
+    pool = small.k_cache.shape[0]
+    num_pages = (4 << 30) // (ps * hkv * hd * 2) + 16000
+    k = torch.empty(num_pages, ps, hkv, hd, dtype=torch.bfloat16, device=device)
+    v = torch.empty_like(k)
+    k[num_pages - pool:] = small.k_cache.flip(0)  # page p -> num_pages - 1 - p
+    v[num_pages - pool:] = small.v_cache.flip(0)
+    big = PagedBatch(small.q, k, v, (num_pages - 1 - small.block_table).to(torch.int32),
+                     small.cache_seqlens, small.scale)
+    assert int(big.block_table.min()) * ps * hkv * hd * 2 >= 4 << 30
+    for ns in (None, 1, 5, native.SPLITS_PER_SEQUENCE):
+        assert torch.equal(run_native(big, num_splits=ns).cpu(),
+                           run_native(small, num_splits=ns).cpu()), ns
+    # Appends land in the same rows of the far pages.
+    k_new = torch.randn(3, 2, hkv, hd, device=device).to(torch.bfloat16)
+    v_new = torch.randn(3, 2, hkv, hd, device=device).to(torch.bfloat16)
+    kc, vc = small.k_cache.clone(), small.v_cache.clone()
+    native.append_kv(k_new, v_new, kc, vc, small.block_table, small.cache_seqlens)
+    native.append_kv(k_new, v_new, k, v, big.block_table, big.cache_seqlens)
+    torch.cuda.synchronize()
+    assert torch.equal(k[num_pages - pool:].flip(0).cpu(), kc.cpu())
+    assert torch.equal(v[num_pages - pool:].flip(0).cpu(), vc.cpu())
+    del k, v, big
+    torch.cuda.empty_cache()
+
+
 def test_noncontiguous_q_and_out(device):
     b = make_paged_batch(4, 16, 4, 128, torch.float16, torch.tensor([33, 64, 1, 200]),
                          seed=8).to(device)
