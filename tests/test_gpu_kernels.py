@@ -189,6 +189,16 @@ def test_pages_past_4_gib(device):
     torch.cuda.synchronize()
     assert torch.equal(k[num_pages - pool:].flip(0).cpu(), kc.cpu())
     assert torch.equal(v[num_pages - pool:].flip(0).cpu(), vc.cpu())
+    # The slot form (vLLM's slot_mapping), one more token per sequence.
+    pos = small.cache_seqlens.long() + 2
+    page_col = (pos // ps).view(-1, 1)
+    key, value = k_new[:, 0].contiguous(), v_new[:, 0].contiguous()
+    for table, kd, vd in ((small.block_table, kc, vc), (big.block_table, k, v)):
+        slots = table.long().gather(1, page_col).view(-1) * ps + pos % ps
+        native.reshape_and_cache(key, value, kd, vd, slots)
+    torch.cuda.synchronize()
+    assert torch.equal(k[num_pages - pool:].flip(0).cpu(), kc.cpu())
+    assert torch.equal(v[num_pages - pool:].flip(0).cpu(), vc.cpu())
     del k, v, big
     torch.cuda.empty_cache()
 
