@@ -677,35 +677,33 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   // Sequence holding tile lo: the largest b < B with s[b] <= lo (then
   // s[b+1] > lo). s is nondecreasing and s[0] = 0 <= lo, so the lanes whose
   // probe passes form a prefix: each round narrows [a, a + n) to one of 64
-  // steps (one round for B < 64, three for B <= 16000).
+  // steps, down to at most 63 candidates, which one last round settles (one
+  // round for B < 64, two up to B = 4032, three up to 16000).
   // Cursor of the tile builder (runs NBUF tiles ahead of the math): the
   // sequence pb and its tiles [p_start, p_end). Without a window every
   // sequence starts at its tile 0, so the first page id does not wait for the
   // length.
   int pb = 0, p_start = 0, p_end = hi;
   if constexpr (!kSeq) {
-    if (B < 64) {
-      // One round: lane l holds s[min(l, B)], so s[pb] and s[pb + 1] come
-      // from two lanes rather than from another LDS read.
-      const int v = s_tiles[min(lane, B)];
-      pb = __builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < B && v <= lo)) - 1;
-      p_start = __builtin_amdgcn_readlane(v, pb);
-      p_end = __builtin_amdgcn_readlane(v, pb + 1);
-    } else {
-      int a = 0, n = B;
-      while (n > 1) {
-        const int step = (n + 63) >> 6;
-        const int idx = a + lane * step;
-        const bool ok = idx < a + n && s_tiles[idx] <= lo;
-        const int cnt = __builtin_popcountll(__builtin_amdgcn_ballot_w64(ok));
-        const int na = a + (cnt - 1) * step;
-        n = min(step, a + n - na);
-        a = na;
-      }
-      pb = rfl(a);
-      p_start = rfl(s_tiles[pb]);
-      p_end = rfl(s_tiles[pb + 1]);
+    int a = 0, n = B;  // s[a] <= lo < s[a + n]
+    while (n > 63) {
+      const int step = (n + 63) >> 6;
+      const int idx = a + lane * step;
+      const bool ok = idx < a + n && s_tiles[idx] <= lo;
+      const int cnt = __builtin_popcountll(__builtin_amdgcn_ballot_w64(ok));
+      const int na = a + (cnt - 1) * step;
+      n = min(step, a + n - na);
+      a = na;
     }
+    // Last round, n <= 63: lane l holds s[min(a + l, B)], so s[pb] and
+    // s[pb + 1] come from two lanes rather than from another LDS read.
+    a = rfl(a);
+    n = rfl(n);
+    const int v = s_tiles[min(a + lane, B)];
+    const int c = __builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < n && v <= lo));
+    pb = a + c - 1;
+    p_start = __builtin_amdgcn_readlane(v, c - 1);
+    p_end = __builtin_amdgcn_readlane(v, c);
     wave_stamp_after(p, 9, pb);
   }
   ConstI32 p_bt = as_const(p.bt + (int64_t)pb * p.bt_stride);

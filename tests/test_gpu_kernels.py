@@ -451,7 +451,7 @@ def test_maximum_batch(device):
         assert max_err(run_native(b, **kw), expected) <= TOL[torch.float16]
 
 
-@pytest.mark.parametrize("batch", [257, 513, 1024, 4353])
+@pytest.mark.parametrize("batch", [63, 64, 65, 257, 513, 1024, 4032, 4033, 4353])
 @pytest.mark.parametrize("kv_heads,head_dim,dtype", [(2, 128, torch.bfloat16),
                                                      (8, 64, torch.float16)],
                          ids=["4wave", "8wave"])
@@ -460,10 +460,14 @@ def test_batches_past_one_length_per_thread(device, batch, kv_heads, head_dim, d
     # The tile scan reads one length per thread up to the workgroup's
     # threads (256 for four-wave, 512 for eight-wave workgroups) and batches
     # of eight loads past that: 257 and 513 sit one past each size, 4353
-    # needs two rounds of eight per thread in the four-wave kernel. A window
-    # takes the extended instantiation's tile count.
+    # needs two rounds of eight per thread in the four-wave kernel. The
+    # search for a range's first sequence settles up to 63 candidates in one
+    # round: 63, 64 and 65 sequences sit around that, 4032 and 4033 around
+    # the step of 63 that still leaves two rounds. A window takes the
+    # extended instantiation's tile count.
     g = torch.Generator().manual_seed(batch + head_dim)
     lengths = torch.randint(0, 48, (batch,), generator=g)
+    lengths[batch // 3] = 0
     b = make_paged_batch(batch, 2 * kv_heads, kv_heads, head_dim, dtype, lengths,
                          seed=batch).to(device)
     cpu = b.to("cpu")
