@@ -710,9 +710,9 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   // Split kernel without a window: the first tile's page id needs only
   // p_start, so its load goes out before the length's (the scheduling barrier
   // keeps that order) and the two share one round trip. Issued after, it
-  // would wait for the length: the compiler uses the length at once. The
-  // position is clamped into the table row (an empty range at the batch end
-  // may start past its sequence's last page).
+  // would wait for the length: the compiler uses the length at once. Tile lo
+  // lies inside sequence pb (lo < p_end), so the position is in the table row;
+  // the clamp keeps the read there whatever the lengths say.
   if constexpr (!kSeq && !kLanePages && !kExtras) {
     pg_first = p_bt[min((lo - p_start) * kTile, p.max_len - 1) >> p.ps_log2];
     __builtin_amdgcn_sched_barrier(0);
