@@ -139,6 +139,19 @@ def test_split_heuristic_closed_form(args):
     assert native.split_heuristic(*args, True) == heuristic_closed_form(*args, 1)
 
 
+@pytest.mark.parametrize("hd", [64, 128, 256])
+def test_split_heuristic_over_every_kv_head_count(hd):
+    # Every kv head count 1..40 with GQ 1, 2 and 4, a long table (split
+    # path) and a short one (per-sequence where it applies), 16-bit and fp8
+    # rows: the C rule and its closed form agree everywhere.
+    for hkv in range(1, 41):
+        for gq in (1, 2, 4):
+            for b, btw in ((32, 512), (8, 24)):
+                args = (b, gq * hkv, hkv, hd, 16, btw, 256)
+                assert native.split_heuristic(*args) == heuristic_closed_form(*args), args
+                assert native.split_heuristic(*args, True) == heuristic_closed_form(*args, 1), args
+
+
 def test_split_heuristic_known_values():
     assert native.split_heuristic(32, 32, 8, 128, 16, 512, 256) == 128
     assert native.split_heuristic(32, 32, 4, 64, 16, 512, 256) == 256

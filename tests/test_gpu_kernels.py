@@ -273,10 +273,13 @@ def test_fp64_oracle_agrees_with_fp32_port_on_gpu_inputs(device):
 
 @pytest.mark.parametrize("hq,hkv,head_dim", [
     (2, 1, 128), (8, 1, 64), (6, 3, 128), (24, 12, 64), (32, 16, 128), (64, 16, 64),
+    (20, 20, 64), (40, 20, 128), (40, 40, 64), (80, 40, 128),
 ])
 def test_kv_head_counts(device, hq, hkv, head_dim):
-    # Workgroups hold min(HKV, 8) kv heads x 8 // that sub-ranges: one kv head
-    # with eight sub-ranges, three heads with two, and two head groups.
+    # Workgroups hold min(HKV, waves) kv heads x waves // that sub-ranges: one
+    # kv head with four sub-ranges, three heads with one, and past 8 (128-byte
+    # rows) or 4 (256-byte rows) kv heads several head groups, the last one
+    # partly used at 20 and 40.
     lengths = torch.tensor([1, 40, 700, 16, 33])
     b = make_paged_batch(5, hq, hkv, head_dim, torch.bfloat16, lengths, seed=21).to(device)
     expected = oracle_out(b)
