@@ -606,7 +606,7 @@ struct Tile {
 // Without a window and with page-uniform tiles, pg_first is the page id of
 // tile lo, already read by the caller.
 template <int HD, int HR, typename T, bool kF8, bool kLanePages, int NBUF, bool kExtras,
-          bool kSeq>
+          bool kSeq, bool kBalance = false>
 __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *s_tiles, int kvh,
                                           int rr, int lo, int hi, int stride, float *lds_o,
                                           float *lds_lse, int pg_first = 0) {
@@ -1078,7 +1078,24 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
     t += tstep;
   };
   int done = 0;
-  for (; done + NBUF <= ntiles; done += NBUF) static_for<NBUF>(step);
+  for (; done + NBUF <= ntiles; done += NBUF) {
+    if constexpr (kBalance) {
+      // Two waves per SIMD: the older one runs ahead of its partner and the
+      // CU ends on one wave per SIMD. Each wave lowers its priority as its
+      // range shrinks (3 in the first quarter, 0 in the last), so the one
+      // behind issues first.
+      const int q = ((ntiles - done) * 4 - 1) / ntiles;
+      if (q >= 3)
+        __builtin_amdgcn_s_setprio(3);
+      else if (q == 2)
+        __builtin_amdgcn_s_setprio(2);
+      else if (q == 1)
+        __builtin_amdgcn_s_setprio(1);
+      else
+        __builtin_amdgcn_s_setprio(0);
+    }
+    static_for<NBUF>(step);
+  }
   const int rest = ntiles - done;  // < NBUF tiles, already issued into sets[0 .. rest-1]
   static_for<NBUF - 1>([&](auto jc) {
     constexpr int j = decltype(jc)::value;
@@ -1115,8 +1132,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(const int3
   const int lo = range_lo(rr, R, NT), hi = range_lo(rr + 1, R, NT);
   wave_stamp(p, 0, t_entry);
   wave_stamp(p, 1, wave_clock());
-  run_range<HD, HR, T, kF8, kLanePages, NBUF, kExtras, false>(p, s_tiles, kvh, rr, lo, hi, 1,
-                                                             nullptr, nullptr);
+  run_range<HD, HR, T, kF8, kLanePages, NBUF, kExtras, false, WAVES == 8>(
+      p, s_tiles, kvh, rr, lo, hi, 1, nullptr, nullptr);
   wave_stamp(p, 3, wave_clock());
   wave_stamp(p, 4, hi - lo);
   wave_stamp(p, 5, 1);
