@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define MXFA_ABI_VERSION 10
+#define MXFA_ABI_VERSION 11
 
 /* Return codes. */
 #define MXFA_OK 0
@@ -287,6 +287,35 @@ int mxfa_split_decode_fp8_partial_launch(const void *q, int64_t q_stride_b, int6
                                          int block_table_width, int num_pages, int dtype,
                                          int num_splits, const float *k_scale,
                                          const float *v_scale, void *stream);
+
+/*
+ * Streaming probe (a measurement aid): the split partial kernel's gather with
+ * no attention math. Same tile scan, balanced ranges, launch shape and
+ * per-tile buffer loads of K and V (q once per piece) as
+ * mxfa_split_decode_partial_launch with the same arguments, but each wave
+ * only XORs the words it loads; lane l of the wave of (kv head h, range r)
+ * writes its XOR to sink[(h * R + r) * 64 + l], R = min(num_splits, total
+ * 16-token tiles), so sink_bytes >= kv_heads * num_splits * 256. Nothing else
+ * is written. tiles_in_flight: 0 for the decode kernel's own register sets
+ * at this head dim, or 2..4 (tiles a wave holds in registers; loads go out
+ * tiles_in_flight - 1 tiles ahead). 16-bit caches, head dim 64 or 128, page
+ * size >= 16, num_splits > 0. Its time is the ceiling that the decode
+ * kernel's access pattern allows on the device.
+ *
+ * Replaces mxfa_stream_probe (csrc_native/m1_kernel.cpp:1023-1108, bound as
+ * mxmmain.stream_probe at csrc_native/m1_binding.cpp:28-35,122-123), which
+ * walks each sequence's pages with the decode kernel's row pattern; this one
+ * walks the balanced ranges the decode kernel walks.
+ */
+int mxfa_stream_probe_launch(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                             const void *k_cache, const void *v_cache,
+                             int64_t cache_stride_page, int64_t cache_stride_token,
+                             int64_t cache_stride_head, const int32_t *block_table,
+                             int64_t bt_stride, const int32_t *seqlens, int seqlen_add,
+                             uint32_t *sink, size_t sink_bytes, int batch, int q_heads,
+                             int kv_heads, int head_dim, int page_size, int block_table_width,
+                             int num_pages, int dtype, int num_splits, int tiles_in_flight,
+                             void *stream);
 
 /*
  * vLLM-style paged append: for token t with slot = slot_mapping[t] >= 0,

@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import concurrent.futures
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -63,8 +64,8 @@ def hipcc_path() -> str:
 
 
 def compile_command(source: Path, obj: Path, extra: tuple[str, ...] = ()) -> list[str]:
-    return [hipcc_path(), *HIPCC_FLAGS, *extra, f"-I{INCLUDE_DIR}", f"-I{CSRC_DIR}", "-c",
-            str(source), "-o", str(obj)]
+    return [hipcc_path(), *HIPCC_FLAGS, *extra, RESOURCE_REMARKS, f"-I{INCLUDE_DIR}",
+            f"-I{CSRC_DIR}", "-c", str(source), "-o", str(obj)]
 
 
 def link_command(objs: list[Path], output: Path) -> list[str]:
@@ -72,12 +73,46 @@ def link_command(objs: list[Path], output: Path) -> list[str]:
             str(output)]
 
 
-def _run(cmd: list[str]) -> None:
+def _run(cmd: list[str]) -> str:
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
         raise RuntimeError(
             f"hipcc failed ({result.returncode}): {' '.join(cmd)}\n{result.stdout}\n{result.stderr}"
         )
+    return result.stderr
+
+
+# Every kernel must keep its state in registers: a kernel that spills VGPRs or
+# uses private (scratch) memory for any other reason fails the build. The
+# compiler's resource-usage remarks (one block per kernel) are the record.
+RESOURCE_REMARKS = "-Rpass-analysis=kernel-resource-usage"
+_REMARK = re.compile(r"remark:\s+(Function Name|VGPRs Spill|ScratchSize \[bytes/lane\]|VGPRs|"
+                     r"AGPRs|Occupancy \[waves/SIMD\]): (\S+)")
+
+
+def resource_usage(remarks: str) -> dict[str, dict[str, str]]:
+    """Kernel name -> {field: value} from kernel-resource-usage remarks."""
+    kernels: dict[str, dict[str, str]] = {}
+    current: dict[str, str] | None = None
+    for m in _REMARK.finditer(remarks):
+        field, value = m.group(1), m.group(2)
+        if field == "Function Name":
+            current = kernels.setdefault(value, {})
+        elif current is not None:
+            current[field] = value
+    return kernels
+
+
+def check_resource_usage(source: str, remarks: str) -> dict[str, dict[str, str]]:
+    """Raise when a kernel of ``source`` spills VGPRs or uses scratch memory."""
+    kernels = resource_usage(remarks)
+    bad = [f"{name}: VGPR spills {u.get('VGPRs Spill')}, scratch "
+           f"{u.get('ScratchSize [bytes/lane]')} bytes/lane"
+           for name, u in kernels.items()
+           if u.get("VGPRs Spill", "0") != "0" or u.get("ScratchSize [bytes/lane]", "0") != "0"]
+    if bad:
+        raise RuntimeError(f"{source}: kernels spill or use scratch memory:\n" + "\n".join(bad))
+    return kernels
 
 
 TORCH_OP_SOURCE = CSRC_DIR / "torch_op.cpp"
@@ -129,8 +164,11 @@ def build(verbose: bool = False, jobs: int | None = None, lib_path: Path = LIB_P
             print(" ".join(cmd), flush=True)
     workers = jobs or min(len(cmds), os.cpu_count() or 1)
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
-        for future in [pool.submit(_run, cmd) for cmd in cmds]:
-            future.result()
+        futures = [pool.submit(_run, cmd) for cmd in cmds]
+        kernels = sum(len(check_resource_usage(name, future.result()))
+                      for name, future in zip(SOURCES, futures))
+    if kernels == 0:
+        raise RuntimeError("no kernel-resource-usage remarks from hipcc: the check saw no kernel")
     tmp = lib_path.with_suffix(".so.tmp")
     _run(link_command(objs, tmp))
     os.replace(tmp, lib_path)

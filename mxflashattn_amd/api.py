@@ -236,6 +236,8 @@ def flash_attn_with_kvcache(
             raise ValueError("out must match q's shape, dtype and device")
         if out.stride(-1) != 1:
             raise ValueError("out must have a contiguous last dimension")
+        if torch._debug_has_internal_overlap(out) == 1:
+            raise ValueError("out must not have internally overlapping memory")
 
     # Checks that read cache_seqlens / block_table back to the host cost a
     # device synchronisation per call; they run only when asked for

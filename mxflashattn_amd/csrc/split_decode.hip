@@ -25,14 +25,22 @@ constexpr int kMaxScratchDevices = 64;
 static std::mutex g_scratch_mutex;
 static void *g_scratch_ptr[kMaxScratchDevices];
 
+// The lookup enqueues no work on any stream. When a device's first call comes
+// while this thread captures a graph, the lookup runs with the thread's
+// capture mode relaxed for its duration (a global-mode capture would count a
+// first-use module load as an unsafe call), then the mode is restored.
 static int scratch_address(void **ptr) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
     return MXFA_ELAUNCH;
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if (!g_scratch_ptr[dev]) {
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    const bool swapped = hipThreadExchangeStreamCaptureMode(&mode) == hipSuccess;
     void *p = nullptr;
-    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return MXFA_ELAUNCH;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (swapped) hipThreadExchangeStreamCaptureMode(&mode);
+    if (err != hipSuccess || !p) return MXFA_ELAUNCH;
     g_scratch_ptr[dev] = p;
   }
   *ptr = g_scratch_ptr[dev];
@@ -48,6 +56,10 @@ int launch_combine_256(const CombineParams &c, int dtype, hipStream_t st);
 int launch_seq_64(const DecodeParams &p, int dtype, bool fp8, hipStream_t st);
 int launch_seq_128(const DecodeParams &p, int dtype, bool fp8, hipStream_t st);
 int launch_seq_256(const DecodeParams &p, int dtype, bool fp8, hipStream_t st);
+int launch_probe_64(const DecodeParams &p, const Grid &g, int nbuf, uint32_t *sink,
+                    hipStream_t st);
+int launch_probe_128(const DecodeParams &p, const Grid &g, int nbuf, uint32_t *sink,
+                     hipStream_t st);
 
 static bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
@@ -60,6 +72,31 @@ static int ilog2_exact(int v) {
 
 static bool supported_hd(int hd) { return hd == 64 || hd == 128 || hd == 256; }
 
+// Output rows (batch, query token, head) of `hd` contiguous elements never
+// share an element: with the dims of more than one entry sorted by stride,
+// each stride covers the whole extent of the dims below it (the innermost
+// covers a row). Different workgroups write different rows, so rows that
+// overlap (an expand()ed view, a head stride below the head dim) would race.
+static bool rows_disjoint(const int64_t (&size)[3], const int64_t (&stride)[3], int64_t hd) {
+  int64_t sz[3], sd[3];
+  int n = 0;
+  for (int i = 0; i < 3; ++i) {
+    if (size[i] <= 1) continue;
+    int j = n++;
+    for (; j > 0 && sd[j - 1] > stride[i]; --j) {
+      sz[j] = sz[j - 1];
+      sd[j] = sd[j - 1];
+    }
+    sz[j] = size[i];
+    sd[j] = stride[i];
+  }
+  int64_t extent = hd;  // elements spanned by the dims below the current one
+  for (int i = 0; i < n; ++i) {
+    if (sd[i] < extent) return false;
+    extent = sd[i] * (sz[i] - 1) + extent;
+  }
+  return true;
+}
 
 struct SplitArgs {
   const void *q;
@@ -100,7 +137,8 @@ static WsLayout ws_layout(int batch, int hq, int hd, int ns) {
   return w;
 }
 
-static int check_split_args(const SplitArgs &a) {
+// Checks common to every decode launch; the workspace is checked by the caller.
+static int check_call_args(const SplitArgs &a) {
   if (!a.q || !a.k || !a.v || !a.bt || !a.seqlens || !a.out) return MXFA_EINVAL;
   if (a.batch <= 0 || a.hq <= 0 || a.hkv <= 0 || a.btw <= 0 || a.num_pages <= 0)
     return MXFA_EINVAL;
@@ -146,13 +184,17 @@ static int check_split_args(const SplitArgs &a) {
   if (((uintptr_t)a.out & 7u) || ((a.o_sb | a.o_st | a.o_sh) & 3) || a.o_sb < 0 ||
       a.o_st < 0 || a.o_sh < 0)
     return MXFA_EINVAL;
-  // Output rows of different (query token, head) pairs must not overlap.
-  if (a.ql > 1 && !((a.o_st >= (int64_t)a.hq * a.o_sh && a.o_sh >= a.hd) ||
-                    (a.o_sh >= (int64_t)a.ql * a.o_st && a.o_st >= a.hd)))
-    return MXFA_EINVAL;
+  // Output rows of different (sequence, query token, head) triples must not overlap.
+  if (!rows_disjoint({a.batch, a.ql, a.hq}, {a.o_sb, a.o_st, a.o_sh}, a.hd)) return MXFA_EINVAL;
   if (((uintptr_t)a.k_scale & 3u) || ((uintptr_t)a.v_scale & 3u) || ((uintptr_t)a.sinks & 3u) ||
       ((uintptr_t)a.alibi & 3u))
     return MXFA_EINVAL;
+  return MXFA_OK;
+}
+
+static int check_split_args(const SplitArgs &a) {
+  const int rc = check_call_args(a);
+  if (rc != MXFA_OK) return rc;
   if (a.num_splits == MXFA_SPLITS_PER_SEQUENCE) return MXFA_OK;  // no workspace
   if (!a.ws || !aligned16(a.ws)) return MXFA_EWORKSPACE;
   if (a.ws_bytes < ws_layout(a.batch, a.hq * a.ql, a.hd, a.num_splits).bytes)
@@ -165,7 +207,8 @@ static unsigned long long *g_wave_stamps = nullptr;
 #endif
 
 static DecodeParams make_params(const SplitArgs &a, const Grid &g) {
-  const bool ws = a.num_splits > 0;  // the per-sequence kernel has no workspace
+  // The per-sequence kernel has no workspace, and the streaming probe none either.
+  const bool ws = a.num_splits > 0 && a.ws != nullptr;
   const WsLayout w = ws_layout(a.batch, a.hq * a.ql, a.hd, ws ? a.num_splits : 1);
   const int64_t esz = a.fp8 ? 1 : 2;
   DecodeParams p;
@@ -500,6 +543,34 @@ int mxfa_split_decode_noalloc_launch(
                    true, (hipStream_t)stream);
 }
 
+int mxfa_stream_probe_launch(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                             const void *k_cache, const void *v_cache,
+                             int64_t cache_stride_page, int64_t cache_stride_token,
+                             int64_t cache_stride_head, const int32_t *block_table,
+                             int64_t bt_stride, const int32_t *seqlens, int seqlen_add,
+                             uint32_t *sink, size_t sink_bytes, int batch, int q_heads,
+                             int kv_heads, int head_dim, int page_size, int block_table_width,
+                             int num_pages, int dtype, int num_splits, int tiles_in_flight,
+                             void *stream) {
+  // The probe writes no output; `out` is checked as q (same shape and strides).
+  SplitArgs a = split_args(q, q_stride_b, q_stride_h, k_cache, v_cache, cache_stride_page,
+                           cache_stride_token, cache_stride_head, block_table, bt_stride,
+                           seqlens, seqlen_add, const_cast<void *>(q), q_stride_b, q_stride_h,
+                           nullptr, 0, 1.f, batch, q_heads, kv_heads, head_dim, page_size,
+                           block_table_width, num_pages, dtype, num_splits);
+  int rc = check_call_args(a);
+  if (rc != MXFA_OK) return rc;
+  if (num_splits <= 0 || (head_dim != 64 && head_dim != 128) || page_size < kTile ||
+      (tiles_in_flight != 0 && (tiles_in_flight < 2 || tiles_in_flight > 4)))
+    return MXFA_EUNSUPPORTED;
+  if (!sink || ((uintptr_t)sink & 3u) || sink_bytes < (size_t)kv_heads * num_splits * 64 * 4)
+    return MXFA_EWORKSPACE;
+  const Grid g = grid_for(kv_heads, num_splits, waves_for(head_dim * 2, kv_heads));
+  const DecodeParams p = make_params(a, g);
+  return head_dim == 64 ? launch_probe_64(p, g, tiles_in_flight, sink, (hipStream_t)stream)
+                        : launch_probe_128(p, g, tiles_in_flight, sink, (hipStream_t)stream);
+}
+
 int mxfa_split_decode_partial_launch(MXFA_SPLIT_PARAMS, void *stream) {
   return run_split(split_args(MXFA_SPLIT_ARGS), false, (hipStream_t)stream);
 }
@@ -529,6 +600,8 @@ int mxfa_split_decode_combine_launch(void *workspace, size_t workspace_bytes, vo
   if (batch > kMaxBatch || num_splits > 65535) return MXFA_EUNSUPPORTED;
   if (!aligned16(workspace) || ((uintptr_t)out & 7u) || ((out_stride_b | out_stride_h) & 3) ||
       out_stride_b < 0 || out_stride_h < 0)
+    return MXFA_EINVAL;
+  if (!rows_disjoint({batch, 1, q_heads}, {out_stride_b, 0, out_stride_h}, head_dim))
     return MXFA_EINVAL;
   if (workspace_bytes < ws_layout(batch, q_heads, head_dim, num_splits).bytes)
     return MXFA_EWORKSPACE;

@@ -17,4 +17,9 @@ int launch_seq_64(const DecodeParams &p, int dtype, bool fp8, hipStream_t st) {
   return launch_seq_hd<64>(p, dtype, fp8, st);
 }
 
+int launch_probe_64(const DecodeParams &p, const Grid &g, int nbuf, uint32_t *sink,
+                    hipStream_t st) {
+  return launch_probe_hd<64>(p, g, nbuf, sink, st);
+}
+
 }  // namespace mxfa

@@ -605,11 +605,15 @@ struct Tile {
 // [C][HD] and lds_lse [C] for the workgroup to merge; s_tiles is not read.
 // Without a window and with page-uniform tiles, pg_first is the page id of
 // tile lo, already read by the caller.
+//
+// kProbe (the streaming probe): the same tile walk and loads, but each tile
+// only XORs the words it loaded into the returned value, with no attention
+// math and no output; other instantiations return 0.
 template <int HD, int HR, typename T, bool kF8, bool kLanePages, int NBUF, bool kExtras,
-          bool kSeq, bool kBalance = false>
-__device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *s_tiles, int kvh,
-                                          int rr, int lo, int hi, int stride, float *lds_o,
-                                          float *lds_lse, int pg_first = 0) {
+          bool kSeq, bool kBalance = false, bool kProbe = false>
+__device__ __forceinline__ uint32_t run_range(const DecodeParams &p, const int32_t *s_tiles,
+                                              int kvh, int rr, int lo, int hi, int stride,
+                                              float *lds_o, float *lds_lse, int pg_first = 0) {
   const int tstep = kSeq ? stride : 1;  // tile index step between the wave's tiles
   using E = Elem<T>;
   constexpr int NCH = HD / 32;               // MFMA steps over the head dim
@@ -720,12 +724,19 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
   int p_len = seq_len_of(p.seqlens, pb, p.seqlen_add, p.max_len);
   int p_first = kExtras ? first_tile_of(p_len, p.ql, p.window_left) : 0;  // tile at p_start
 
+  // Per-lane page ids are computed into a local array and copied to `lpg` at
+  // one point that both the padding and the real tile reach: stores to `lpg`
+  // from two branches were merged by the compiler into a store through a
+  // selected address, which kept the register sets in private memory.
   auto make_tile = [&](int t, Tile &d, int (&lpg)[NPG]) {
     // kSeq: the page id is read before the range test, clamped into the
     // table row, so without a window it does not wait for the length.
     int pg_early = 0;
     if constexpr (kSeq && !kLanePages)
       pg_early = p_bt[min((t - p_start + p_first) * kTile, p.max_len - 1) >> p.ps_log2];
+    int lp[NPG];
+#pragma unroll
+    for (int i = 0; i < NPG; ++i) lp[i] = 0;
     if (t >= hi) {
       d.b = pb;
       d.tok0 = 0;
@@ -734,7 +745,7 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
       d.flags = 0;
       d.pg = 0;
 #pragma unroll
-      for (int i = 0; i < NPG; ++i) lpg[i] = 0;
+      for (int i = 0; i < NPG; ++i) lpg[i] = lp[i];
       return;
     }
     if constexpr (!kSeq) {
@@ -765,14 +776,16 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
       // Per-lane page ids: [0] for this lane's K token, [1+u] for its V tokens.
       // Token positions clamp to the last valid token.
       const int last = d.valid - 1;
-      lpg[0] = p_bt[(d.tok0 + min(col, last)) >> p.ps_log2];
+      lp[0] = p_bt[(d.tok0 + min(col, last)) >> p.ps_log2];
 #pragma unroll
       for (int u = 0; u < U; ++u)
-        lpg[1 + u] = p_bt[(d.tok0 + min(4 * row + u, last)) >> p.ps_log2];
+        lp[1 + u] = p_bt[(d.tok0 + min(4 * row + u, last)) >> p.ps_log2];
       d.pg = 0;
     } else {
       d.pg = kSeq ? pg_early : p_bt[d.tok0 >> p.ps_log2];
     }
+#pragma unroll
+    for (int i = 0; i < NPG; ++i) lpg[i] = lp[i];
   };
 
   // In the split kernel the page id is read one pipeline step before issue()
@@ -909,8 +922,27 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
     });
   };
 
+  uint32_t probe = 0;
   auto compute = [&](Set &s) {
     const Tile &d = s.d;
+    if constexpr (kProbe) {
+#pragma unroll
+      for (int cc = 0; cc < NKL; ++cc) probe ^= s.k[cc].x ^ s.k[cc].y ^ s.k[cc].z ^ s.k[cc].w;
+      if constexpr (kShareV) {
+        probe ^= s.vr[0].x ^ s.vr[0].y ^ s.vr[0].z ^ s.vr[0].w;
+        probe ^= s.vr[1].x ^ s.vr[1].y ^ s.vr[1].z ^ s.vr[1].w;
+      } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int w = 0; w < VB / 4; ++w) probe ^= s.v[u].w[w];
+      }
+      if (d.flags & kFirst) {
+#pragma unroll
+        for (int cc = 0; cc < NCH; ++cc) probe ^= s.q[cc].x ^ s.q[cc].y ^ s.q[cc].z ^ s.q[cc].w;
+      }
+      return;
+    }
     if (d.flags & kFirst) {
       m = -INFINITY;
       dsum = 0.f;
@@ -1101,6 +1133,7 @@ __device__ __forceinline__ void run_range(const DecodeParams &p, const int32_t *
     constexpr int j = decltype(jc)::value;
     if (j < rest) compute(sets[j]);
   });
+  return probe;
 }
 
 // kExtras: the call has a sliding window, soft-capping, ALiBi or sinks (the host
@@ -1139,6 +1172,32 @@ __global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(const int3
   wave_stamp(p, 5, 1);
   wave_stamp(p, 6, blockIdx.y * gridDim.x + blockIdx.x);
   wave_stamp(p, 7, kvh);
+}
+
+// Streaming probe: split_partial_kernel's tile scan, ranges, launch shape and
+// per-tile loads (16-bit caches, page-uniform tiles, NBUF register sets) with
+// no attention math: each lane XORs the words it loads and writes that to
+// sink[(kvh * R + rr) * 64 + lane]. Its time is the ceiling the tile loop's
+// access pattern allows; it writes no output, workspace or prefix sums.
+template <int HD, typename T, int NBUF, int WAVES>
+__global__ __launch_bounds__(WAVES * 64, 1) void stream_probe_kernel(const int32_t *seqlens,
+                                                                       int batch, DecodeParams p,
+                                                                       uint32_t *sink) {
+  constexpr int kThreads = WAVES * 64;
+  extern __shared__ int32_t s_tiles[];  // [B + 1]
+  __shared__ int s_wave_tot[WAVES];
+  const int NT = rfl(tile_prefix<kThreads, false>(p, seqlens, batch, s_tiles, s_wave_tot));
+  const int wave = rfl(threadIdx.x >> 6);
+  const int KH = p.heads_per_wg;
+  const int kh = wave % KH, sub = wave / KH;
+  const int kvh = blockIdx.x * KH + kh;
+  const int R = min(p.num_ranges, NT);
+  const int rr = blockIdx.y * p.subs + sub;
+  if (sub >= p.subs || kvh >= p.hkv || rr >= R) return;
+  const int lo = range_lo(rr, R, NT), hi = range_lo(rr + 1, R, NT);
+  const uint32_t x = run_range<HD, 1, T, false, false, NBUF, false, false, WAVES == 8, true>(
+      p, s_tiles, kvh, rr, lo, hi, 1, nullptr, nullptr);
+  sink[((int64_t)kvh * R + rr) * 64 + (threadIdx.x & 63)] = x;
 }
 
 // Merge of two partial states (max, weight, accumulator) in the base-2 domain.
@@ -1512,6 +1571,42 @@ int launch_seq_hd(const DecodeParams &p, int dtype, bool fp8, hipStream_t st) {
   if (dtype == MXFA_DTYPE_BF16)
     return fp8 ? launch_seq_hr<HD, BF16, true>(p, st) : launch_seq_hr<HD, BF16, false>(p, st);
   return fp8 ? launch_seq_hr<HD, F16, true>(p, st) : launch_seq_hr<HD, F16, false>(p, st);
+}
+
+// Streaming probe launch (16-bit caches, page size >= 16): the decode
+// kernel's grid and waves; nbuf 0 takes the decode kernel's register sets.
+template <int HD, int WAVES>
+static int launch_probe_w(const DecodeParams &p, const Grid &g, int nbuf, uint32_t *sink,
+                          hipStream_t st) {
+  dim3 grid(g.gx, g.gy);
+  const size_t lds = (size_t)(p.batch + 1) * sizeof(int32_t);
+  switch (nbuf == 0 ? kNbuf<HD, false> : nbuf) {
+    case 2:
+      hipLaunchKernelGGL((stream_probe_kernel<HD, BF16, 2, WAVES>), grid, dim3(WAVES * 64), lds,
+                         st, p.seqlens, p.batch, p, sink);
+      break;
+    case 3:
+      hipLaunchKernelGGL((stream_probe_kernel<HD, BF16, 3, WAVES>), grid, dim3(WAVES * 64), lds,
+                         st, p.seqlens, p.batch, p, sink);
+      break;
+    case 4:
+      hipLaunchKernelGGL((stream_probe_kernel<HD, BF16, 4, WAVES>), grid, dim3(WAVES * 64), lds,
+                         st, p.seqlens, p.batch, p, sink);
+      break;
+    default: return MXFA_EUNSUPPORTED;
+  }
+  return hipGetLastError() == hipSuccess ? MXFA_OK : MXFA_ELAUNCH;
+}
+
+template <int HD>
+int launch_probe_hd(const DecodeParams &p, const Grid &g, int nbuf, uint32_t *sink,
+                    hipStream_t st) {
+  if (g.heads_per_wg * g.subs > g.waves || p.ps_log2 < 4) return MXFA_ELAUNCH;
+  if constexpr (kMaxWaves<HD, false> == 8) {
+    if (g.waves == 8) return launch_probe_w<HD, 8>(p, g, nbuf, sink, st);
+  }
+  if (g.waves != 4) return MXFA_ELAUNCH;
+  return launch_probe_w<HD, 4>(p, g, nbuf, sink, st);
 }
 
 template <int HD>

@@ -23,8 +23,11 @@
 #include <c10/hip/HIPStream.h>
 #include <hip/hip_runtime_api.h>
 
+#include <cstdlib>
+#include <limits>
 #include <map>
 #include <mutex>
+#include <string>
 #include <utility>
 #include <vector>
 
@@ -45,7 +48,7 @@ Workspaces &workspaces() {
   return *w;
 }
 
-void *workspace(const at::Device &device, void *stream, size_t bytes) {
+at::Tensor workspace(const at::Device &device, void *stream, size_t bytes) {
   Workspaces &w = workspaces();
   std::lock_guard<std::mutex> lock(w.mu);
   const auto key = std::make_pair((int)device.index(), stream);
@@ -58,9 +61,31 @@ void *workspace(const at::Device &device, void *stream, size_t bytes) {
     }
     at::Tensor t = at::empty({size}, at::TensorOptions().dtype(at::kByte).device(device));
     w.live[key] = t;
-    return t.data_ptr();
+    return t;
   }
-  return it->second.data_ptr();
+  return it->second;
+}
+
+// MXFA_POISON_OUTPUTS=1 (a debugging aid, read once; the Python binding reads
+// the same variable): before each launch outside graph capture the output is
+// filled with NaN and the workspace with 0xff bytes, so a row or a piece the
+// kernels fail to write shows up as NaN rather than as a stale value.
+bool poison_outputs() {
+  static const bool on = [] {
+    const char *e = std::getenv("MXFA_POISON_OUTPUTS");
+    return e != nullptr && std::string(e) == "1";
+  }();
+  return on;
+}
+
+void poison(void *stream, at::Tensor &out, at::Tensor *ws) {
+  if (!poison_outputs()) return;
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing((hipStream_t)stream, &status) != hipSuccess ||
+      status != hipStreamCaptureStatusNone)
+    return;
+  out.fill_(std::numeric_limits<float>::quiet_NaN());
+  if (ws) ws->fill_(0xff);
 }
 
 // (bytes of the live workspaces, bytes of the retired ones)
@@ -163,7 +188,10 @@ py::object decode(const at::Tensor &q, const at::Tensor &k_cache, const at::Tens
   size_t ws_bytes = 0;
   if (mxfa_split_decode_workspace_size((int)batch, (int)hq, (int)hd, ns, &ws_bytes) != MXFA_OK)
     return py::none();
-  void *ws = ws_bytes ? workspace(device, stream, ws_bytes) : nullptr;
+  at::Tensor ws_t;
+  if (ws_bytes) ws_t = workspace(device, stream, ws_bytes);
+  void *ws = ws_bytes ? ws_t.data_ptr() : nullptr;
+  poison(stream, out, ws_bytes ? &ws_t : nullptr);
   const int rc = mxfa_split_decode_launch(
       q.data_ptr(), q_sb, q_sh, k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0),
       k_cache.stride(1), k_cache.stride(2), block_table.data_ptr<int32_t>(), block_table.stride(0),

@@ -24,7 +24,7 @@ LIB_PATH = Path(
     os.environ.get("MXFLASHATTN_AMD_LIB")
     or Path(__file__).resolve().parent / "_lib" / "libmxfa_mi355x.so"
 )
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 MXFA_OK = 0
 MXFA_EUNSUPPORTED = -1
@@ -37,6 +37,14 @@ MXFA_ESCRATCH = -5
 SPLITS_PER_SEQUENCE = -1
 # Workspace of mxfa_split_decode_noalloc_launch (the library's own device array).
 SCRATCH_BYTES = 8 << 20
+
+# MXFA_POISON_OUTPUTS=1, a debugging aid (the GPU parity tests set it): before
+# every launch outside graph capture the output is filled with NaN and the
+# workspace with 0xff bytes (NaN pieces, prefix sums of -1), so a row or a
+# piece the kernels fail to write shows up as NaN instead of a stale value,
+# such as the previous call's correct answer in a block the caching allocator
+# handed back. The torch operator reads the same variable.
+POISON_OUTPUTS = os.environ.get("MXFA_POISON_OUTPUTS", "") == "1"
 
 DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
 DTYPE_FP8_E4M3 = 2
@@ -71,6 +79,7 @@ EXPORTED_SYMBOLS = (
     "mxfa_split_decode_fp8_launch",
     "mxfa_split_decode_fp8_partial_launch",
     "mxfa_split_decode_multi_launch",
+    "mxfa_stream_probe_launch",
     "mxfa_reshape_and_cache_launch",
     "mxfa_reshape_and_cache_fp8_launch",
     "mxfa_append_kv_launch",
@@ -110,6 +119,11 @@ _SIGNATURES = {
         [_p, _i64, _i64, _i64, _i, _i, _i, _p, _f, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p,
          _i, _p, _i64,
          _i64, _i64, _p, _sz, _f, _i, _i, _i, _i, _i, _i, _i, _i, _i, _p, _p, _i, _p],
+    ),
+    "mxfa_stream_probe_launch": (
+        _i,
+        [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _p, _sz, _i, _i, _i, _i, _i,
+         _i, _i, _i, _i, _i, _p],
     ),
     "mxfa_split_decode_combine_launch": (
         _i,
@@ -289,6 +303,17 @@ def retired_workspace_bytes() -> int:
     ctypes path's cache and the torch operator's."""
     op = torch_op()
     return WORKSPACE.retired_bytes() + (op.workspace_bytes()[1] if op is not None else 0)
+
+
+def _poison(out: torch.Tensor | None, ws: torch.Tensor | None = None) -> None:
+    """NaN-fill ``out`` and 0xff-fill ``ws`` when MXFA_POISON_OUTPUTS is set,
+    on the current stream, except under graph capture."""
+    if not POISON_OUTPUTS or torch.cuda.is_current_stream_capturing():
+        return
+    if out is not None:
+        out.fill_(float("nan"))
+    if ws is not None:
+        ws.fill_(0xFF)
 
 
 def _dtype_code(t: torch.Tensor) -> int:
@@ -507,6 +532,9 @@ def _prepare(q, k_cache, v_cache, block_table, cache_seqlens, out, causal: bool 
         out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     if out.shape != q.shape or out.dtype != q.dtype or out.stride(-1) != 1:
         raise ValueError("out must match q's shape and dtype with a contiguous last dim")
+    if torch._debug_has_internal_overlap(out) == 1:
+        # Different workgroups write different rows; rows sharing memory would race.
+        raise ValueError("out must not have internally overlapping memory")
     _require_device(q, out)
     return q, block_table, cache_seqlens, out
 
@@ -637,15 +665,18 @@ def paged_decode_split(
     ws_bytes = workspace_size(q.shape[0], q.shape[-2] * min(ql, per_launch), q.shape[-1],
                               num_splits)
     ws = WORKSPACE.get(q.device, stream, ws_bytes)
+    _poison(out)
     if ql > 1 or window_left >= 0 or sinks is not None or softcap > 0 or (
             alibi_slopes is not None):
         for first, end, add in token_chunks(ql, per_launch, int(seqlen_add)):
             whole = first == 0 and end == ql
+            _poison(None, ws)
             _launch_multi(q if whole else q[:, first:end], k_cache, v_cache, block_table,
                           cache_seqlens, out if whole else out[:, first:end], ws.data_ptr(),
                           ws_bytes, softmax_scale, num_splits, add, stream, causal, k_scale,
                           v_scale, window_left, sinks, softcap, alibi_slopes)
         return out
+    _poison(None, ws)
     args = _launch_args(q, k_cache, v_cache, block_table, cache_seqlens, out, ws.data_ptr(),
                         ws_bytes, softmax_scale, num_splits, seqlen_add, stream)
     if k_cache.dtype == FP8_DTYPE:
@@ -720,6 +751,32 @@ def split_decode_partial(
     else:
         rc = library().mxfa_split_decode_partial_launch(*args)
         _check(rc, "mxfa_split_decode_partial_launch")
+
+
+def stream_probe(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                 block_table: torch.Tensor, cache_seqlens: torch.Tensor, num_splits: int,
+                 sink: torch.Tensor | None = None, tiles_in_flight: int = 0) -> torch.Tensor:
+    """The streaming probe (mxfa_stream_probe_launch): the split partial
+    kernel's gather at ``num_splits`` ranges with no attention math, on the
+    current stream. Returns the sink, int32 [HKV, num_splits, 64], each lane's
+    XOR of the words its wave loaded (only what the launch's ranges cover is
+    written). ``tiles_in_flight`` 0 is the decode kernel's own pipeline depth."""
+    q, block_table, cache_seqlens, _ = _prepare(q, k_cache, v_cache, block_table,
+                                                cache_seqlens, None)
+    hkv = k_cache.shape[2]
+    if sink is None:
+        sink = torch.empty(hkv, num_splits, 64, dtype=torch.int32, device=q.device)
+    if sink.dtype != torch.int32 or not sink.is_contiguous() or sink.device != q.device:
+        raise ValueError("sink must be a contiguous int32 tensor on q's device")
+    qs, cs = q.stride(), k_cache.stride()
+    rc = library().mxfa_stream_probe_launch(
+        q.data_ptr(), qs[0], qs[-2], k_cache.data_ptr(), v_cache.data_ptr(), cs[0], cs[1], cs[2],
+        block_table.data_ptr(), block_table.stride(0), cache_seqlens.data_ptr(), 0,
+        sink.data_ptr(), sink.numel() * 4, q.shape[0], q.shape[-2], hkv, q.shape[-1],
+        k_cache.shape[1], block_table.shape[1], k_cache.shape[0], _dtype_code(q), int(num_splits),
+        int(tiles_in_flight), _stream_handle(q.device))
+    _check(rc, "mxfa_stream_probe_launch")
+    return sink
 
 
 def split_decode_combine(workspace: torch.Tensor, out: torch.Tensor, kv_heads: int,

@@ -58,9 +58,6 @@ class PagedBatch:
             return lens
         return torch.clamp(lens, max=self.window_left + self.q.shape[1])
 
-    def total_tokens(self) -> int:
-        return int(self.cache_seqlens.sum().item())
-
     def kv_bytes(self) -> int:
         """K and V bytes the call must read: sum_b 2 * A_b * HKV * HD * elem,
         A_b the attended keys (L_b without a window), elem the cache's

@@ -44,7 +44,7 @@ def test_library_loads_and_reports_header_abi(lib):
 
 def test_every_header_function_is_exported_and_bound(lib):
     declared = header_functions()
-    assert len(declared) == len(set(declared)) == 15
+    assert len(declared) == len(set(declared)) == 16
     for name in declared:
         assert hasattr(lib, name), name
     assert set(declared) == set(native.EXPORTED_SYMBOLS) == set(native._SIGNATURES)
@@ -230,6 +230,12 @@ def decode_args(**over):
     (dict(q=FAKE + 2), -2), (dict(k=FAKE + 8), -2), (dict(q_sh=100), -2), (dict(c_st=1028), -2),
     (dict(o_sh=130), -2), (dict(out=FAKE + 2), -2),
     (dict(c_st=64), -2), (dict(q_sh=64), -2),  # overlapping rows
+    # Output rows that share memory (an expand()ed view, strides below the
+    # extent of the dims inside them) would be written by different workgroups.
+    (dict(o_sh=0), -2), (dict(o_sb=0), -2), (dict(o_sh=64), -2), (dict(o_sb=31 * 128), -2),
+    # A head-major output (batch innermost) is disjoint: it passes the output
+    # checks and stops at the workspace size.
+    (dict(o_sb=128, o_sh=32 * 128, ws_bytes=1000), -3),
     (dict(ws=None), -3), (dict(ws=FAKE + 8), -3), (dict(ws_bytes=1000), -3),
     # num_splits: ranges >= 1 or the per-sequence kernel (-1), which needs no
     # workspace but keeps every other check; its pieces live in LDS (64 KB at
@@ -316,6 +322,29 @@ def test_combine_rejects_before_launching(lib):
     assert f(FAKE, ws, FAKE, 512, 64, 4, 8, 2, 64, 5, 3, None) == -1
     assert f(FAKE, ws, FAKE, 512, 64, 0, 8, 2, 64, 0, 3, None) == -2
     assert f(FAKE, ws, FAKE + 2, 512, 64, 4, 8, 2, 64, 0, 3, None) == -2
+    assert f(FAKE, ws, FAKE, 0, 64, 4, 8, 2, 64, 0, 3, None) == -2  # rows of all sequences alias
+    assert f(FAKE, ws, FAKE, 512, 0, 4, 8, 2, 64, 0, 3, None) == -2  # rows of all heads alias
+
+
+def probe_args(**over):
+    """A well-formed argument tuple for mxfa_stream_probe_launch, with overrides."""
+    a = dict(q=FAKE, q_sb=32 * 128, q_sh=128, k=FAKE, v=FAKE, c_sp=16 * 8 * 128, c_st=8 * 128,
+             c_sh=128, bt=FAKE, bt_stride=64, seqlens=FAKE, seqlen_add=0, sink=FAKE,
+             sink_bytes=1 << 30, batch=32, hq=32, hkv=8, hd=128, ps=16, btw=64, pages=4096,
+             dtype=1, ns=32, nbuf=0, stream=None)
+    a.update(over)
+    return tuple(a.values())
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(q=None), -2), (dict(k=None), -2), (dict(batch=0), -2), (dict(hq=36), -1),
+    (dict(hd=256, q_sb=32 * 256, q_sh=256, c_sp=16 * 8 * 256, c_st=8 * 256, c_sh=256), -1),
+    (dict(ps=8, c_sp=8 * 8 * 128), -1), (dict(ns=-1), -1), (dict(nbuf=1), -1), (dict(nbuf=5), -1),
+    (dict(dtype=2), -1), (dict(sink=None), -3), (dict(sink=FAKE + 2), -3),
+    (dict(sink_bytes=8 * 32 * 256 - 4), -3),
+])
+def test_stream_probe_rejects_before_launching(lib, over, code):
+    assert lib.mxfa_stream_probe_launch(*probe_args(**over)) == code
 
 
 def test_decode_workspace_boundary_is_exact(lib):

@@ -48,14 +48,17 @@ def test_config_full_size_matches_port(device, name):
     expected = port_out(b)
     api_out = mx.flash_attn_with_kvcache(b.q, b.k_cache, b.v_cache,
                                          cache_seqlens=b.cache_seqlens,
-                                         block_table=b.block_table, softmax_scale=b.scale)
+                                         block_table=b.block_table, softmax_scale=b.scale,
+                                         out=torch.full_like(b.q, float("nan")))
     torch.cuda.synchronize()
     info = mx.get_last_dispatch_info()
     assert info.backend == mx.BACKEND_MI355X and info.fallback_reason is None
+    assert torch.isfinite(api_out.float()).all()
     assert max_err(api_out, expected) <= tol, name
     for ns in (None, 1):
         got = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table,
-                                        b.cache_seqlens, b.scale, num_splits=ns)
+                                        b.cache_seqlens, b.scale, num_splits=ns,
+                                        out=torch.full_like(b.q, float("nan")))
         torch.cuda.synchronize()
         assert torch.isfinite(got.float()).all()
         assert max_err(got, expected) <= tol, (name, ns)
@@ -65,8 +68,9 @@ def test_config_full_size_matches_port(device, name):
 def test_config4_matches_fp64_oracle(device, name):
     b = make_paged_batch(**CONFIGS[name], device=device)
     got = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
-                                    b.scale)
+                                    b.scale, out=torch.full_like(b.q, float("nan")))
     torch.cuda.synchronize()
+    assert torch.isfinite(got.float()).all()
     ref = c_oracle.paged_decode_f64(b.q.cpu(), b.k_cache.cpu(), b.v_cache.cpu(),
                                     b.block_table.cpu(), b.cache_seqlens.cpu(), b.scale)
     assert max_err(got, torch.from_numpy(ref).reshape(got.shape)) <= TOL[torch.bfloat16]

@@ -34,10 +34,17 @@ def max_err(actual: torch.Tensor, expected: torch.Tensor) -> float:
     return (actual.float().cpu() - expected.float().cpu()).abs().max().item()
 
 
+def nan_like(t: torch.Tensor) -> torch.Tensor:
+    """An output buffer whose every element the kernels must overwrite."""
+    return torch.full_like(t, float("nan"))
+
+
 def run_native(b, **kw) -> torch.Tensor:
+    kw.setdefault("out", nan_like(b.q))
     out = native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
                                     b.scale, **kw)
     torch.cuda.synchronize()
+    assert not torch.isnan(out.float()).any(), "an output row was left unwritten"
     return out
 
 
