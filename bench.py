@@ -19,6 +19,10 @@ Prints ONE JSON line:
                per-call HIP events
   us_per_call_warm   graph replays on one KV pool, never rotated (cache-warm
                where the working set fits the Infinity Cache; not `value`)
+  stream_probe the partial kernel's gather alone, no math (mxfa_stream_probe_launch),
+               at the kernel's pipeline depth and at 2-4 tiles in flight per
+               wave: microseconds and algorithmic GB/s, the access pattern's
+               ceiling on this device
   roofline     the dominant kernel, split_partial_kernel, alone: algorithmic
                bytes (KV + q + out + used block-table entries + lengths) / its
                average duration (HIP events around graph replays of
@@ -190,6 +194,24 @@ def measure_workload(name: str, spec: dict, device, steps: int, warmup: int) -> 
     us_partial = time_graph(partial, pools, steps, warmup, side)[0] if single else None
     kv = base.kv_bytes()
     alg = base.algorithmic_bytes()
+
+    # The streaming probe: the partial kernel's own gather (same ranges, grid,
+    # descriptors and loads) with no attention math, at the kernel's pipeline
+    # depth ("kernel") and at 2-4 tiles in flight per wave: the ceiling of the
+    # access pattern on this device.
+    probe = None
+    if (single and ns > 0 and base.k_cache.dtype in (torch.float16, torch.bfloat16)
+            and base.page_size >= 16 and base.head_dim in (64, 128)):
+        sink = torch.zeros(base.kv_heads, ns, 64, dtype=torch.int32, device=device)
+        probe = {}
+        for depth in (0, 2, 3, 4):
+            def run_probe(kc, vc, depth=depth):
+                native.stream_probe(base.q, kc, vc, base.block_table, base.cache_seqlens, ns,
+                                    sink=sink, tiles_in_flight=depth)
+
+            us = time_graph(run_probe, pools, steps, warmup, side)[0]
+            probe["kernel" if depth == 0 else f"tiles_in_flight_{depth}"] = {
+                "us": round(us, 3), "alg_gb_s": round(alg / (us * 1e-6) / 1e9, 1)}
     gbs = kv / (us_graph * 1e-6) / 1e9
     res = {
         "us_per_call": round(us_graph, 3),
@@ -206,6 +228,7 @@ def measure_workload(name: str, spec: dict, device, steps: int, warmup: int) -> 
         "partial_kernel_us": round(us_partial, 3) if us_partial else None,
         "partial_kernel_gb_s": round(alg / (us_partial * 1e-6) / 1e9, 1) if us_partial else None,
         "num_splits": ns,
+        "stream_probe": probe,
         "rotation_copies": len(pools),
         "timed_calls": timed_calls,
     }

@@ -294,9 +294,9 @@ int mxfa_split_decode_fp8_partial_launch(const void *q, int64_t q_stride_b, int6
  * per-tile buffer loads of K and V (q once per piece) as
  * mxfa_split_decode_partial_launch with the same arguments, but each wave
  * only XORs the words it loads; lane l of the wave of (kv head h, range r)
- * writes its XOR to sink[(h * R + r) * 64 + l], R = min(num_splits, total
- * 16-token tiles), so sink_bytes >= kv_heads * num_splits * 256. Nothing else
- * is written. tiles_in_flight: 0 for the decode kernel's own register sets
+ * writes its XOR to sink[(h * num_splits + r) * 64 + l] (sink_bytes >=
+ * kv_heads * num_splits * 256). Ranges r >= the total of 16-token tiles do not
+ * exist and are not written; nothing else is. tiles_in_flight: 0 for the decode kernel's own register sets
  * at this head dim, or 2..4 (tiles a wave holds in registers; loads go out
  * tiles_in_flight - 1 tiles ahead). 16-bit caches, head dim 64 or 128, page
  * size >= 16, num_splits > 0. Its time is the ceiling that the decode

@@ -552,6 +552,52 @@ __device__ __forceinline__ void zero_empty(const DecodeParams &p, const int32_t 
   }
 }
 
+// Batches of up to kWaveScanMax sequences skip the LDS tile scan: every wave
+// loads the lengths itself, one per lane, and scans the tile counts with DPP
+// (wave_tile_scan), so no wave waits on a barrier or an LDS round trip before
+// it looks for its range's first sequence.
+constexpr int kWaveScanMax = 64;
+
+// Lane b (< B) ends with its sequence's clamped length `len`, the exclusive
+// and inclusive tile prefix sums `excl` / `incl` (S_b and S_{b+1}); lanes past
+// the batch hold len 0 and excl = incl = the tile total, which is returned.
+// The length load needs only the preloaded leading arguments, so it is issued
+// before any wait on the parameter struct.
+template <bool kWindow>
+__device__ __forceinline__ int wave_tile_scan(const DecodeParams &p, const int32_t *seqlens, int B,
+                                              int &len, int &excl, int &incl) {
+  const int lane = threadIdx.x & 63;
+  const int raw = as_const(seqlens)[lane < B ? lane : B - 1];
+  int L = raw + p.seqlen_add;
+  L = L < 0 ? 0 : (L > p.max_len ? p.max_len : L);
+  L = lane < B ? L : 0;
+  const int n = kWindow ? (L > 0 ? tiles_of(L, p.ql, p.window_left) : 0) : (L + kTile - 1) / kTile;
+  wave_stamp_after(p, 8, n);
+  incl = wave_scan_incl(n);
+  excl = incl - n;
+  len = L;
+  return __builtin_amdgcn_readlane(incl, 63);
+}
+
+// zero_empty for the wave-local scan: the tile count of sequence b is lane b's
+// incl - excl (every wave holds the whole scan).
+template <int HD, int kThreads>
+__device__ __forceinline__ void zero_empty_wave(const DecodeParams &p, int tiles) {
+  const int kv0 = blockIdx.x * p.heads_per_wg;
+  const int kv1 = min(kv0 + p.heads_per_wg, p.hkv);
+  const int nh = (kv1 - kv0) * p.gq;
+  constexpr int F = HD / 4;  // 8-byte pieces per head row
+  for (int b = blockIdx.y; b < p.batch; b += gridDim.y) {
+    if (__builtin_amdgcn_readlane(tiles, b) != 0) continue;
+    char *row = p.out + b * p.o_sb + (int64_t)kv0 * p.gq * p.o_sh;
+    for (int i = threadIdx.x; i < p.ql * nh * F; i += kThreads) {
+      const int t = i / (nh * F), j = i % (nh * F);
+      *reinterpret_cast<uint2 *>(row + t * p.o_st + (j / F) * p.o_sh + (j % F) * 8) =
+          make_uint2(0u, 0u);
+    }
+  }
+}
+
 // Sum / max over the 4 DPP rows of the wave (lanes l, l^16, l^32, l^48); every
 // lane receives the result.
 __device__ __forceinline__ float rows_sum(float x) {
@@ -610,10 +656,11 @@ struct Tile {
 // only XORs the words it loaded into the returned value, with no attention
 // math and no output; other instantiations return 0.
 template <int HD, int HR, typename T, bool kF8, bool kLanePages, int NBUF, bool kExtras,
-          bool kSeq, bool kBalance = false, bool kProbe = false>
+          bool kSeq, bool kBalance = false, bool kProbe = false, bool kWaveLocal = false>
 __device__ __forceinline__ uint32_t run_range(const DecodeParams &p, const int32_t *s_tiles,
                                               int kvh, int rr, int lo, int hi, int stride,
-                                              float *lds_o, float *lds_lse, int pg_first = 0) {
+                                              float *lds_o, float *lds_lse, int pg_first = 0,
+                                              int wl_len = 0, int wl_excl = 0, int wl_incl = 0) {
   const int tstep = kSeq ? stride : 1;  // tile index step between the wave's tiles
   using E = Elem<T>;
   constexpr int NCH = HD / 32;               // MFMA steps over the head dim
@@ -688,7 +735,17 @@ __device__ __forceinline__ uint32_t run_range(const DecodeParams &p, const int32
   // sequence starts at its tile 0, so the first page id does not wait for the
   // length.
   int pb = 0, p_start = 0, p_end = hi;
-  if constexpr (!kSeq) {
+  // kWaveLocal (split kernel, B <= kWaveScanMax): the wave-local scan, lane b
+  // holding S_b = wl_excl, S_{b+1} = wl_incl and the length wl_len; s_tiles
+  // is not read.
+  constexpr bool wave_local = kWaveLocal && !kSeq;
+  if constexpr (wave_local) {
+    const int c = __builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < B && wl_excl <= lo));
+    pb = c - 1;
+    p_start = __builtin_amdgcn_readlane(wl_excl, pb);
+    p_end = __builtin_amdgcn_readlane(wl_incl, pb);
+    wave_stamp_after(p, 9, pb);
+  } else if constexpr (!kSeq) {
     int a = 0, n = B;  // s[a] <= lo < s[a + n]
     while (n > 63) {
       const int step = (n + 63) >> 6;
@@ -721,7 +778,8 @@ __device__ __forceinline__ uint32_t run_range(const DecodeParams &p, const int32
     pg_first = p_bt[min((lo - p_start) * kTile, p.max_len - 1) >> p.ps_log2];
     __builtin_amdgcn_sched_barrier(0);
   }
-  int p_len = seq_len_of(p.seqlens, pb, p.seqlen_add, p.max_len);
+  int p_len = wave_local ? __builtin_amdgcn_readlane(wl_len, pb)
+                         : seq_len_of(p.seqlens, pb, p.seqlen_add, p.max_len);
   int p_first = kExtras ? first_tile_of(p_len, p.ql, p.window_left) : 0;  // tile at p_start
 
   // Per-lane page ids are computed into a local array and copied to `lpg` at
@@ -753,9 +811,10 @@ __device__ __forceinline__ uint32_t run_range(const DecodeParams &p, const int32
         do {
           ++pb;
           p_start = p_end;
-          p_end = rfl(s_tiles[pb + 1]);
+          p_end = wave_local ? __builtin_amdgcn_readlane(wl_incl, pb) : rfl(s_tiles[pb + 1]);
         } while (t >= p_end);
-        p_len = seq_len_of(p.seqlens, pb, p.seqlen_add, p.max_len);
+        p_len = wave_local ? __builtin_amdgcn_readlane(wl_len, pb)
+                           : seq_len_of(p.seqlens, pb, p.seqlen_add, p.max_len);
         p_first = kExtras ? first_tile_of(p_len, p.ql, p.window_left) : 0;
         p_bt = as_const(p.bt + (int64_t)pb * p.bt_stride);
       }
@@ -1139,7 +1198,7 @@ __device__ __forceinline__ uint32_t run_range(const DecodeParams &p, const int32
 // kExtras: the call has a sliding window, soft-capping, ALiBi or sinks (the host
 // picks the instantiation; without them the kernel is the plain one).
 template <int HD, int HR, typename T, bool kF8, bool kLanePages, int NBUF, int WAVES,
-          bool kExtras>
+          bool kExtras, bool kWaveScan>
 __global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(const int32_t *seqlens,
                                                                         int batch,
                                                                         DecodeParams p) {
@@ -1148,11 +1207,22 @@ __global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(const int3
   __shared__ int s_wave_tot[WAVES];
 
   const unsigned long long t_entry = wave_clock();
-  const int NT = rfl(tile_prefix<kThreads, kExtras>(p, seqlens, batch, s_tiles, s_wave_tot));
-  zero_empty<HD, kThreads>(p, s_tiles);
   const int B = batch;
-  if (blockIdx.x == 0 && blockIdx.y == 0) {
-    for (int i = threadIdx.x; i <= B; i += kThreads) p.ws_s[i] = s_tiles[i];
+  // kWaveScan: the launcher's choice for B <= kWaveScanMax.
+  int wl_len = 0, wl_excl = 0, wl_incl = 0, NT;
+  if constexpr (kWaveScan) {
+    NT = rfl(wave_tile_scan<kExtras>(p, seqlens, B, wl_len, wl_excl, wl_incl));
+    zero_empty_wave<HD, kThreads>(p, wl_incl - wl_excl);
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64) {
+      if ((int)threadIdx.x < B) p.ws_s[threadIdx.x] = wl_excl;
+      if (threadIdx.x == 0) p.ws_s[B] = NT;
+    }
+  } else {
+    NT = rfl(tile_prefix<kThreads, kExtras>(p, seqlens, B, s_tiles, s_wave_tot));
+    zero_empty<HD, kThreads>(p, s_tiles);
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
+      for (int i = threadIdx.x; i <= B; i += kThreads) p.ws_s[i] = s_tiles[i];
+    }
   }
 
   const int wave = rfl(threadIdx.x >> 6);
@@ -1165,8 +1235,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(const int3
   const int lo = range_lo(rr, R, NT), hi = range_lo(rr + 1, R, NT);
   wave_stamp(p, 0, t_entry);
   wave_stamp(p, 1, wave_clock());
-  run_range<HD, HR, T, kF8, kLanePages, NBUF, kExtras, false, WAVES == 8>(
-      p, s_tiles, kvh, rr, lo, hi, 1, nullptr, nullptr);
+  run_range<HD, HR, T, kF8, kLanePages, NBUF, kExtras, false, WAVES == 8, false, kWaveScan>(
+      p, s_tiles, kvh, rr, lo, hi, 1, nullptr, nullptr, 0, wl_len, wl_excl, wl_incl);
   wave_stamp(p, 3, wave_clock());
   wave_stamp(p, 4, hi - lo);
   wave_stamp(p, 5, 1);
@@ -1177,16 +1247,20 @@ __global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(const int3
 // Streaming probe: split_partial_kernel's tile scan, ranges, launch shape and
 // per-tile loads (16-bit caches, page-uniform tiles, NBUF register sets) with
 // no attention math: each lane XORs the words it loads and writes that to
-// sink[(kvh * R + rr) * 64 + lane]. Its time is the ceiling the tile loop's
+// sink[(kvh * num_ranges + rr) * 64 + lane]. Its time is the ceiling the tile loop's
 // access pattern allows; it writes no output, workspace or prefix sums.
-template <int HD, typename T, int NBUF, int WAVES>
+template <int HD, typename T, int NBUF, int WAVES, bool kWaveScan>
 __global__ __launch_bounds__(WAVES * 64, 1) void stream_probe_kernel(const int32_t *seqlens,
                                                                        int batch, DecodeParams p,
                                                                        uint32_t *sink) {
   constexpr int kThreads = WAVES * 64;
   extern __shared__ int32_t s_tiles[];  // [B + 1]
   __shared__ int s_wave_tot[WAVES];
-  const int NT = rfl(tile_prefix<kThreads, false>(p, seqlens, batch, s_tiles, s_wave_tot));
+  int wl_len = 0, wl_excl = 0, wl_incl = 0, NT;
+  if constexpr (kWaveScan)
+    NT = rfl(wave_tile_scan<false>(p, seqlens, batch, wl_len, wl_excl, wl_incl));
+  else
+    NT = rfl(tile_prefix<kThreads, false>(p, seqlens, batch, s_tiles, s_wave_tot));
   const int wave = rfl(threadIdx.x >> 6);
   const int KH = p.heads_per_wg;
   const int kh = wave % KH, sub = wave / KH;
@@ -1195,9 +1269,10 @@ __global__ __launch_bounds__(WAVES * 64, 1) void stream_probe_kernel(const int32
   const int rr = blockIdx.y * p.subs + sub;
   if (sub >= p.subs || kvh >= p.hkv || rr >= R) return;
   const int lo = range_lo(rr, R, NT), hi = range_lo(rr + 1, R, NT);
-  const uint32_t x = run_range<HD, 1, T, false, false, NBUF, false, false, WAVES == 8, true>(
-      p, s_tiles, kvh, rr, lo, hi, 1, nullptr, nullptr);
-  sink[((int64_t)kvh * R + rr) * 64 + (threadIdx.x & 63)] = x;
+  const uint32_t x =
+      run_range<HD, 1, T, false, false, NBUF, false, false, WAVES == 8, true, kWaveScan>(
+          p, s_tiles, kvh, rr, lo, hi, 1, nullptr, nullptr, 0, wl_len, wl_excl, wl_incl);
+  sink[((int64_t)kvh * p.num_ranges + rr) * 64 + (threadIdx.x & 63)] = x;
 }
 
 // Merge of two partial states (max, weight, accumulator) in the base-2 domain.
@@ -1456,17 +1531,27 @@ constexpr int kNbuf = kRowBytes<HD, kF8> <= 64 ? 4 : kRowBytes<HD, kF8> <= 128 ?
 // Rows of the MFMA layout that hold used columns (4 columns per row).
 inline int head_rows(int cols) { return cols <= 4 ? 1 : cols <= 8 ? 2 : 4; }
 
-template <int HD, int HR, typename T, bool kF8, int WAVES, bool kExtras>
-static void launch_partial_x(const DecodeParams &p, const Grid &g, hipStream_t st) {
+template <int HD, int HR, typename T, bool kF8, int WAVES, bool kExtras, bool kWaveScan>
+static void launch_partial_s(const DecodeParams &p, const Grid &g, hipStream_t st) {
   dim3 grid(g.gx, g.gy);
-  const size_t lds = (size_t)(p.batch + 1) * sizeof(int32_t);
+  // The wave-local scan keeps nothing in LDS.
+  const size_t lds = kWaveScan ? 0 : (size_t)(p.batch + 1) * sizeof(int32_t);
   if (p.ps_log2 >= 4)
     hipLaunchKernelGGL(
-        (split_partial_kernel<HD, HR, T, kF8, false, kNbuf<HD, kF8>, WAVES, kExtras>), grid,
-        dim3(WAVES * 64), lds, st, p.seqlens, p.batch, p);
+        (split_partial_kernel<HD, HR, T, kF8, false, kNbuf<HD, kF8>, WAVES, kExtras, kWaveScan>),
+        grid, dim3(WAVES * 64), lds, st, p.seqlens, p.batch, p);
   else
-    hipLaunchKernelGGL((split_partial_kernel<HD, HR, T, kF8, true, 2, WAVES, kExtras>), grid,
-                       dim3(WAVES * 64), lds, st, p.seqlens, p.batch, p);
+    hipLaunchKernelGGL((split_partial_kernel<HD, HR, T, kF8, true, 2, WAVES, kExtras, kWaveScan>),
+                       grid, dim3(WAVES * 64), lds, st, p.seqlens, p.batch, p);
+}
+
+// Batches of up to kWaveScanMax sequences take the wave-local tile scan.
+template <int HD, int HR, typename T, bool kF8, int WAVES, bool kExtras>
+static void launch_partial_x(const DecodeParams &p, const Grid &g, hipStream_t st) {
+  if (p.batch <= kWaveScanMax)
+    launch_partial_s<HD, HR, T, kF8, WAVES, kExtras, true>(p, g, st);
+  else
+    launch_partial_s<HD, HR, T, kF8, WAVES, kExtras, false>(p, g, st);
 }
 
 template <int HD, int HR, typename T, bool kF8, int WAVES>
@@ -1575,27 +1660,34 @@ int launch_seq_hd(const DecodeParams &p, int dtype, bool fp8, hipStream_t st) {
 
 // Streaming probe launch (16-bit caches, page size >= 16): the decode
 // kernel's grid and waves; nbuf 0 takes the decode kernel's register sets.
-template <int HD, int WAVES>
-static int launch_probe_w(const DecodeParams &p, const Grid &g, int nbuf, uint32_t *sink,
+template <int HD, int WAVES, bool kWaveScan>
+static int launch_probe_s(const DecodeParams &p, const Grid &g, int nbuf, uint32_t *sink,
                           hipStream_t st) {
   dim3 grid(g.gx, g.gy);
-  const size_t lds = (size_t)(p.batch + 1) * sizeof(int32_t);
+  const size_t lds = kWaveScan ? 0 : (size_t)(p.batch + 1) * sizeof(int32_t);
   switch (nbuf == 0 ? kNbuf<HD, false> : nbuf) {
     case 2:
-      hipLaunchKernelGGL((stream_probe_kernel<HD, BF16, 2, WAVES>), grid, dim3(WAVES * 64), lds,
-                         st, p.seqlens, p.batch, p, sink);
+      hipLaunchKernelGGL((stream_probe_kernel<HD, BF16, 2, WAVES, kWaveScan>), grid,
+                         dim3(WAVES * 64), lds, st, p.seqlens, p.batch, p, sink);
       break;
     case 3:
-      hipLaunchKernelGGL((stream_probe_kernel<HD, BF16, 3, WAVES>), grid, dim3(WAVES * 64), lds,
-                         st, p.seqlens, p.batch, p, sink);
+      hipLaunchKernelGGL((stream_probe_kernel<HD, BF16, 3, WAVES, kWaveScan>), grid,
+                         dim3(WAVES * 64), lds, st, p.seqlens, p.batch, p, sink);
       break;
     case 4:
-      hipLaunchKernelGGL((stream_probe_kernel<HD, BF16, 4, WAVES>), grid, dim3(WAVES * 64), lds,
-                         st, p.seqlens, p.batch, p, sink);
+      hipLaunchKernelGGL((stream_probe_kernel<HD, BF16, 4, WAVES, kWaveScan>), grid,
+                         dim3(WAVES * 64), lds, st, p.seqlens, p.batch, p, sink);
       break;
     default: return MXFA_EUNSUPPORTED;
   }
   return hipGetLastError() == hipSuccess ? MXFA_OK : MXFA_ELAUNCH;
+}
+
+template <int HD, int WAVES>
+static int launch_probe_w(const DecodeParams &p, const Grid &g, int nbuf, uint32_t *sink,
+                          hipStream_t st) {
+  return p.batch <= kWaveScanMax ? launch_probe_s<HD, WAVES, true>(p, g, nbuf, sink, st)
+                                 : launch_probe_s<HD, WAVES, false>(p, g, nbuf, sink, st);
 }
 
 template <int HD>

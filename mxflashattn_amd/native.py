@@ -508,6 +508,20 @@ def token_chunks(q_len: int, per_launch: int, seqlen_add: int) -> list[tuple[int
 
 
 def _prepare(q, k_cache, v_cache, block_table, cache_seqlens, out, causal: bool = False):
+    q, block_table, cache_seqlens = _prepare_inputs(q, k_cache, v_cache, block_table,
+                                                    cache_seqlens, causal)
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    if out.shape != q.shape or out.dtype != q.dtype or out.stride(-1) != 1:
+        raise ValueError("out must match q's shape and dtype with a contiguous last dim")
+    if torch._debug_has_internal_overlap(out) == 1:
+        # Different workgroups write different rows; rows sharing memory would race.
+        raise ValueError("out must not have internally overlapping memory")
+    _require_device(q, out)
+    return q, block_table, cache_seqlens, out
+
+
+def _prepare_inputs(q, k_cache, v_cache, block_table, cache_seqlens, causal: bool = False):
     check_decode_shapes(q, k_cache, v_cache, causal)
     batch = q.shape[0]
     hd = q.shape[-1]
@@ -528,15 +542,7 @@ def _prepare(q, k_cache, v_cache, block_table, cache_seqlens, out, causal: bool 
         raise ValueError("block_table must be [batch, width >= 1]")
     if cache_seqlens.numel() != batch:
         raise ValueError("cache_seqlens must have one entry per sequence")
-    if out is None:
-        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-    if out.shape != q.shape or out.dtype != q.dtype or out.stride(-1) != 1:
-        raise ValueError("out must match q's shape and dtype with a contiguous last dim")
-    if torch._debug_has_internal_overlap(out) == 1:
-        # Different workgroups write different rows; rows sharing memory would race.
-        raise ValueError("out must not have internally overlapping memory")
-    _require_device(q, out)
-    return q, block_table, cache_seqlens, out
+    return q, block_table, cache_seqlens
 
 
 def _launch_multi(q, k_cache, v_cache, block_table, cache_seqlens, out, workspace, ws_bytes,
@@ -761,8 +767,8 @@ def stream_probe(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     current stream. Returns the sink, int32 [HKV, num_splits, 64], each lane's
     XOR of the words its wave loaded (only what the launch's ranges cover is
     written). ``tiles_in_flight`` 0 is the decode kernel's own pipeline depth."""
-    q, block_table, cache_seqlens, _ = _prepare(q, k_cache, v_cache, block_table,
-                                                cache_seqlens, None)
+    q, block_table, cache_seqlens = _prepare_inputs(q, k_cache, v_cache, block_table,
+                                                    cache_seqlens)
     hkv = k_cache.shape[2]
     if sink is None:
         sink = torch.empty(hkv, num_splits, 64, dtype=torch.int32, device=q.device)
