@@ -53,6 +53,10 @@ constexpr int kDppRowNewBcast0 = 0x150;
 constexpr int kDppRowShr0 = 0x110;
 constexpr int kDppRowBcast15 = 0x142;
 constexpr int kDppRowBcast31 = 0x143;
+// quad_perm:[1,0,3,2] and quad_perm:[2,3,0,1] (lane i of each group of four
+// takes lane i^1, then lane i^2).
+constexpr int kDppQuadSwap1 = 0xB1;
+constexpr int kDppQuadSwap2 = 0x4E;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

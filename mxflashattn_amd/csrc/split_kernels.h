@@ -287,6 +287,27 @@ struct Mfma<BF16> {
 // one dim per block; D = O[head][dim]. Element packing keeps k order: the low
 // half of the first register is token 4r.
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Dot product of two packed pairs of the element type, accumulated in fp32
+// (v_dot2c_f32_bf16 / v_dot2c_f32_f16).
+template <typename T>
+struct Dot2;
+template <>
+struct Dot2<BF16> {
+  static __device__ __forceinline__ float run(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
+                                           __builtin_bit_cast(bf16x2, b), c, false);
+  }
+};
+template <>
+struct Dot2<F16> {
+  static __device__ __forceinline__ float run(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c,
+                                  false);
+  }
+};
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 template <typename T>
@@ -656,7 +677,8 @@ struct Tile {
 // only XORs the words it loaded into the returned value, with no attention
 // math and no output; other instantiations return 0.
 template <int HD, int HR, typename T, bool kF8, bool kLanePages, int NBUF, bool kExtras,
-          bool kSeq, bool kBalance = false, bool kProbe = false, bool kWaveLocal = false>
+          bool kSeq, bool kBalance = false, bool kProbe = false, bool kWaveLocal = false,
+          int kValuG = 0>
 __device__ __forceinline__ uint32_t run_range(const DecodeParams &p, const int32_t *s_tiles,
                                               int kvh, int rr, int lo, int hi, int stride,
                                               float *lds_o, float *lds_lse, int pg_first = 0,
@@ -702,7 +724,13 @@ __device__ __forceinline__ uint32_t run_range(const DecodeParams &p, const int32
   // Lane offsets inside a tile: K in the MFMA A layout, V row-contiguous, q as
   // the MFMA B operand (columns >= GQ*QL read nothing). For fp8 caches step
   // 2m + s of lane row r covers dims 64m + 16r + 8s .. +7; q follows it.
-  const int k_off = col * (int)st + row * 16;
+  // kValuG > 0: QK on the VALU for the first kValuG columns (the rest are
+  // unused). Lane (r, c) then holds token 4r + c/4, 16-byte chunk c%4 of each
+  // 64-byte step: the same addresses per load instruction as the MFMA
+  // layout's token c, chunk r.
+  constexpr bool kValu = kValuG > 0 && !kF8 && !kLanePages && !kProbe;
+  const int k_off = kValu ? (4 * row + (col >> 2)) * (int)st + (col & 3) * 16
+                          : col * (int)st + row * 16;
   int v_off[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) v_off[u] = (4 * row + u) * (int)st + col * VB;
@@ -925,6 +953,7 @@ __device__ __forceinline__ uint32_t run_range(const DecodeParams &p, const int32
   float dsum = 0.f;     // partial denominator of column `col` over this row's tokens
   f32x4 oacc[VD];       // PV accumulators
   uint4 qf[NCH];
+  uint4 qv[kValu ? kValuG : 1][NCH];  // kValu: column g's chunk c%4 of each step, lane (r, c)
   auto clear_acc = [&]() {
 #pragma unroll
     for (int j = 0; j < VD; ++j) oacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1008,12 +1037,61 @@ __device__ __forceinline__ uint32_t run_range(const DecodeParams &p, const int32
       clear_acc();
 #pragma unroll
       for (int cc = 0; cc < NCH; ++cc) qf[cc] = s.q[cc];
+      if constexpr (kValu) {
+        // qf: lane (r', c') holds column c' chunk r'; column g chunk k sits in
+        // lane 16k + g (the LDS crossbar moves it; no LDS memory is used).
+#pragma unroll
+        for (int g = 0; g < kValuG; ++g) {
+          const int src = ((col & 3) * 16 + g) * 4;
+#pragma unroll
+          for (int cc = 0; cc < NCH; ++cc) {
+            qv[g][cc].x = __builtin_amdgcn_ds_bpermute(src, qf[cc].x);
+            qv[g][cc].y = __builtin_amdgcn_ds_bpermute(src, qf[cc].y);
+            qv[g][cc].z = __builtin_amdgcn_ds_bpermute(src, qf[cc].z);
+            qv[g][cc].w = __builtin_amdgcn_ds_bpermute(src, qf[cc].w);
+          }
+        }
+      }
       piece_from_start = (d.flags & kSeqStart) != 0;
       piece_first_in_range = (d.flags & kRangeStart) != 0;
     }
     // QK on the matrix cores; two accumulators halve the MFMA dependency chain.
     f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-    if constexpr (kF8) {
+    if constexpr (kValu) {
+      // QK on the VALU: per column g, the lane's 4 * NCH dot2 over its chunks
+      // of its token, summed over the four chunk lanes of the token (quad_perm
+      // [1,0,3,2] then [2,3,0,1]); lane (r, c) then holds the score of token
+      // 4r + c/4. Score element i of lane (r, h) (token 4r + i, column h) is
+      // lane (r, 4i)'s score of column h (row_newbcast:4i). The result is the
+      // MFMA layout, so the softmax and PV below are the same code.
+      float sg[kValuG];
+#pragma unroll
+      for (int g = 0; g < kValuG; ++g) {
+        float a = 0.f;
+#pragma unroll
+        for (int cc = 0; cc < NCH; ++cc) {
+          a = Dot2<T>::run(s.k[cc].x, qv[g][cc].x, a);
+          a = Dot2<T>::run(s.k[cc].y, qv[g][cc].y, a);
+          a = Dot2<T>::run(s.k[cc].z, qv[g][cc].z, a);
+          a = Dot2<T>::run(s.k[cc].w, qv[g][cc].w, a);
+        }
+        a += __int_as_float(
+            __builtin_amdgcn_update_dpp(0, __float_as_int(a), kDppQuadSwap1, 0xf, 0xf, false));
+        a += __int_as_float(
+            __builtin_amdgcn_update_dpp(0, __float_as_int(a), kDppQuadSwap2, 0xf, 0xf, false));
+        sg[g] = a;
+      }
+      static_for<4>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        float v = 0.f;
+#pragma unroll
+        for (int g = 0; g < kValuG; ++g) {
+          const float b = row_bcast<4 * i>(sg[g]);
+          v = col == g ? b : v;
+        }
+        acc0[i] = v;
+      });
+    } else if constexpr (kF8) {
 #pragma unroll
       for (int mm = 0; mm < NKL; ++mm) {
         acc0 = Mfma<T>::run(widen8<T>(s.k[mm].x, s.k[mm].y), qf[2 * mm], acc0);
@@ -1198,7 +1276,7 @@ __device__ __forceinline__ uint32_t run_range(const DecodeParams &p, const int32
 // kExtras: the call has a sliding window, soft-capping, ALiBi or sinks (the host
 // picks the instantiation; without them the kernel is the plain one).
 template <int HD, int HR, typename T, bool kF8, bool kLanePages, int NBUF, int WAVES,
-          bool kExtras, bool kWaveScan>
+          bool kExtras, bool kWaveScan, int kValuG>
 __global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(const int32_t *seqlens,
                                                                         int batch,
                                                                         DecodeParams p) {
@@ -1235,8 +1313,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(const int3
   const int lo = range_lo(rr, R, NT), hi = range_lo(rr + 1, R, NT);
   wave_stamp(p, 0, t_entry);
   wave_stamp(p, 1, wave_clock());
-  run_range<HD, HR, T, kF8, kLanePages, NBUF, kExtras, false, WAVES == 8, false, kWaveScan>(
-      p, s_tiles, kvh, rr, lo, hi, 1, nullptr, nullptr, 0, wl_len, wl_excl, wl_incl);
+  run_range<HD, HR, T, kF8, kLanePages, NBUF, kExtras, false, WAVES == 8, false, kWaveScan,
+            kValuG>(p, s_tiles, kvh, rr, lo, hi, 1, nullptr, nullptr, 0, wl_len, wl_excl, wl_incl);
   wave_stamp(p, 3, wave_clock());
   wave_stamp(p, 4, hi - lo);
   wave_stamp(p, 5, 1);
@@ -1531,55 +1609,91 @@ constexpr int kNbuf = kRowBytes<HD, kF8> <= 64 ? 4 : kRowBytes<HD, kF8> <= 128 ?
 // Rows of the MFMA layout that hold used columns (4 columns per row).
 inline int head_rows(int cols) { return cols <= 4 ? 1 : cols <= 8 ? 2 : 4; }
 
-template <int HD, int HR, typename T, bool kF8, int WAVES, bool kExtras, bool kWaveScan>
+template <int HD, int HR, typename T, bool kF8, int WAVES, bool kExtras, bool kWaveScan,
+          int kValuG>
 static void launch_partial_s(const DecodeParams &p, const Grid &g, hipStream_t st) {
   dim3 grid(g.gx, g.gy);
   // The wave-local scan keeps nothing in LDS.
   const size_t lds = kWaveScan ? 0 : (size_t)(p.batch + 1) * sizeof(int32_t);
   if (p.ps_log2 >= 4)
-    hipLaunchKernelGGL(
-        (split_partial_kernel<HD, HR, T, kF8, false, kNbuf<HD, kF8>, WAVES, kExtras, kWaveScan>),
-        grid, dim3(WAVES * 64), lds, st, p.seqlens, p.batch, p);
-  else
-    hipLaunchKernelGGL((split_partial_kernel<HD, HR, T, kF8, true, 2, WAVES, kExtras, kWaveScan>),
+    hipLaunchKernelGGL((split_partial_kernel<HD, HR, T, kF8, false, kNbuf<HD, kF8>, WAVES, kExtras,
+                                             kWaveScan, kValuG>),
                        grid, dim3(WAVES * 64), lds, st, p.seqlens, p.batch, p);
+  else  // per-lane page ids: QK stays on the matrix cores
+    hipLaunchKernelGGL(
+        (split_partial_kernel<HD, HR, T, kF8, true, 2, WAVES, kExtras, kWaveScan, 0>), grid,
+        dim3(WAVES * 64), lds, st, p.seqlens, p.batch, p);
 }
 
 // Batches of up to kWaveScanMax sequences take the wave-local tile scan.
-template <int HD, int HR, typename T, bool kF8, int WAVES, bool kExtras>
+template <int HD, int HR, typename T, bool kF8, int WAVES, bool kExtras, int kValuG>
 static void launch_partial_x(const DecodeParams &p, const Grid &g, hipStream_t st) {
   if (p.batch <= kWaveScanMax)
-    launch_partial_s<HD, HR, T, kF8, WAVES, kExtras, true>(p, g, st);
+    launch_partial_s<HD, HR, T, kF8, WAVES, kExtras, true, kValuG>(p, g, st);
   else
-    launch_partial_s<HD, HR, T, kF8, WAVES, kExtras, false>(p, g, st);
+    launch_partial_s<HD, HR, T, kF8, WAVES, kExtras, false, kValuG>(p, g, st);
 }
 
-template <int HD, int HR, typename T, bool kF8, int WAVES>
+template <int HD, int HR, typename T, bool kF8, int WAVES, int kValuG>
 static int launch_partial_w(const DecodeParams &p, const Grid &g, hipStream_t st) {
   if (p.window_left >= 0 || p.softcap > 0.f || p.sinks || p.alibi)
-    launch_partial_x<HD, HR, T, kF8, WAVES, true>(p, g, st);
+    launch_partial_x<HD, HR, T, kF8, WAVES, true, kValuG>(p, g, st);
   else
-    launch_partial_x<HD, HR, T, kF8, WAVES, false>(p, g, st);
+    launch_partial_x<HD, HR, T, kF8, WAVES, false, kValuG>(p, g, st);
   return hipGetLastError() == hipSuccess ? MXFA_OK : MXFA_ELAUNCH;
 }
 
 // The kernel is the grid's wave count; a grid the instantiations cannot run
 // (more waves than the row size has, or its heads and sub-ranges past the
 // waves) is refused: its extra kv heads would go uncomputed.
-template <int HD, int HR, typename T, bool kF8>
+template <int HD, int HR, typename T, bool kF8, int kValuG = 0>
 static int launch_partial_t(const DecodeParams &p, const Grid &g, hipStream_t st) {
   if (g.heads_per_wg * g.subs > g.waves) return MXFA_ELAUNCH;
   if constexpr (kMaxWaves<HD, kF8> == 8) {
-    if (g.waves == 8) return launch_partial_w<HD, HR, T, kF8, 8>(p, g, st);
+    if (g.waves == 8) return launch_partial_w<HD, HR, T, kF8, 8, kValuG>(p, g, st);
   }
   if (g.waves != 4) return MXFA_ELAUNCH;
-  return launch_partial_w<HD, HR, T, kF8, 4>(p, g, st);
+  return launch_partial_w<HD, HR, T, kF8, 4, kValuG>(p, g, st);
+}
+
+// Columns (query tokens x heads per kv head) whose QK runs on the VALU in
+// the split kernel: 0 for the matrix cores. Measured on MI355X (config-2
+// lengths, B 32, bf16, partial kernel under rocprof, VALU against MFMA): GQ 1
+// HD 128 423.0 / 427.9 us, GQ 2 HD 128 202.2 / 204.4, GQ 4 HD 128 103.5 /
+// 103.9; graph replays: GQ 1 HD 64 208.8 / 210.8, GQ 2 HD 256 218.1 / 223.2,
+// GQ 2 HD 64 109.0 / 109.1, GQ 4 HD 64 60.8 / 59.9, GQ 8 HD 128 61.8 / 59.5,
+// GQ 8 HD 64 42.8 / 33.7; as built here, config 3 (B 128, GQ 2 HD 64, fp16,
+// L <= 512) 18.67 / 17.82 and GQ 2 HD 64 109.3 / 109.1. With few columns the
+// MFMA computes 16 columns for one or two; with more, its few instructions per
+// tile beat the VALU's 4 x HD/32 dot2 per column; with 128-byte rows (eight
+// waves per CU, short pieces) the per-piece q exchange does not pay. 16-bit
+// caches with page-uniform tiles and head dims of 128 or more only.
+inline int valu_qk_columns(int cols, int hd) {
+  if (hd < 128) return 0;
+  if (cols <= 1) return 1;
+  if (cols <= 2) return 2;
+  if (cols <= 4 && hd == 128) return 4;
+  return 0;
 }
 
 template <int HD, typename T, bool kF8>
 static int launch_partial_hr(const DecodeParams &p, const Grid &g, hipStream_t st) {
-  switch (head_rows(p.gq * p.ql)) {
-    case 1: return launch_partial_t<HD, 1, T, kF8>(p, g, st);
+  const int cols = p.gq * p.ql;
+  switch (head_rows(cols)) {
+    case 1:
+      if constexpr (!kF8 && HD >= 128) {
+        if (p.ps_log2 >= 4) {
+          switch (valu_qk_columns(cols, HD)) {
+            case 1: return launch_partial_t<HD, 1, T, kF8, 1>(p, g, st);
+            case 2: return launch_partial_t<HD, 1, T, kF8, 2>(p, g, st);
+            case 4:
+              if constexpr (HD == 128) return launch_partial_t<HD, 1, T, kF8, 4>(p, g, st);
+              break;
+            default: break;
+          }
+        }
+      }
+      return launch_partial_t<HD, 1, T, kF8>(p, g, st);
     case 2: return launch_partial_t<HD, 2, T, kF8>(p, g, st);
     default: return launch_partial_t<HD, 4, T, kF8>(p, g, st);
   }
