@@ -22,8 +22,11 @@ INCLUDE_DIR = REPO_DIR / "include"
 LIB_DIR = PACKAGE_DIR / "_lib"
 LIB_NAME = "libmxfa_mi355x.so"
 LIB_PATH = LIB_DIR / LIB_NAME
-SOURCES = ("split_decode.hip", "split_hd64.hip", "split_hd128.hip", "split_hd256.hip",
-           "kv_append.hip")
+SOURCES = ("split_decode.hip", "split_hd64.hip", "split_hd64_ws.hip", "split_hd128.hip",
+           "split_hd128_ws.hip", "split_hd256.hip", "split_hd256_ws.hip", "kv_append.hip")
+# Comparison build: QK always on the matrix cores (the default build puts it on
+# the VALU for launches of few columns at head dims >= 128).
+QK_MFMA_LIB_PATH = PACKAGE_DIR / "_lib" / "qk_mfma" / "libmxfa_mi355x.so"
 ARCH = "gfx950"
 
 # Packed-fp32 VALU forms are disabled for every device pass: hipcc forms them
@@ -185,5 +188,9 @@ def build(verbose: bool = False, jobs: int | None = None, lib_path: Path = LIB_P
 
 
 if __name__ == "__main__":
-    path = build(verbose="-v" in sys.argv)
+    if "--qk-mfma" in sys.argv:
+        path = build(verbose="-v" in sys.argv, lib_path=QK_MFMA_LIB_PATH,
+                     extra=("-DMXFA_QK_ON_MFMA",), torch_op=False)
+    else:
+        path = build(verbose="-v" in sys.argv)
     print(path)

@@ -50,6 +50,12 @@ static int scratch_address(void **ptr) {
 int launch_partial_64(const DecodeParams &p, const Grid &g, int dtype, bool fp8, hipStream_t st);
 int launch_partial_128(const DecodeParams &p, const Grid &g, int dtype, bool fp8, hipStream_t st);
 int launch_partial_256(const DecodeParams &p, const Grid &g, int dtype, bool fp8, hipStream_t st);
+int launch_partial_64_ws(const DecodeParams &p, const Grid &g, int dtype, bool fp8,
+                         hipStream_t st);
+int launch_partial_128_ws(const DecodeParams &p, const Grid &g, int dtype, bool fp8,
+                          hipStream_t st);
+int launch_partial_256_ws(const DecodeParams &p, const Grid &g, int dtype, bool fp8,
+                          hipStream_t st);
 int launch_combine_64(const CombineParams &c, int dtype, hipStream_t st);
 int launch_combine_128(const CombineParams &c, int dtype, hipStream_t st);
 int launch_combine_256(const CombineParams &c, int dtype, hipStream_t st);
@@ -259,10 +265,17 @@ static DecodeParams make_params(const SplitArgs &a, const Grid &g) {
 static int launch_partial(const SplitArgs &a, hipStream_t st) {
   const Grid g = grid_for(a.hkv, a.num_splits, waves_for(a.hd * (a.fp8 ? 1 : 2), a.hkv));
   const DecodeParams p = make_params(a, g);
+  const bool ws = a.batch <= kWaveScanMax;  // the wave-local tile scan
   switch (a.hd) {
-    case 64: return launch_partial_64(p, g, a.dtype, a.fp8, st);
-    case 128: return launch_partial_128(p, g, a.dtype, a.fp8, st);
-    default: return launch_partial_256(p, g, a.dtype, a.fp8, st);
+    case 64:
+      return ws ? launch_partial_64_ws(p, g, a.dtype, a.fp8, st)
+                : launch_partial_64(p, g, a.dtype, a.fp8, st);
+    case 128:
+      return ws ? launch_partial_128_ws(p, g, a.dtype, a.fp8, st)
+                : launch_partial_128(p, g, a.dtype, a.fp8, st);
+    default:
+      return ws ? launch_partial_256_ws(p, g, a.dtype, a.fp8, st)
+                : launch_partial_256(p, g, a.dtype, a.fp8, st);
   }
 }
 

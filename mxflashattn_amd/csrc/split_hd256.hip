@@ -1,12 +1,13 @@
-// Instantiation unit of the split decode kernels for head dim 256 (the head
-// dims compile in parallel; the C ABI in split_decode.hip calls these).
+// Instantiation unit of the split decode kernels for head dim 256: the partial
+// kernel with the LDS tile scan, the per-sequence, combine and probe kernels
+// (the units compile in parallel; the C ABI in split_decode.hip calls these).
 #include "split_kernels.h"
 
 namespace mxfa {
 
 int launch_partial_256(const DecodeParams &p, const Grid &g, int dtype, bool fp8,
                        hipStream_t st) {
-  return launch_partial_hd<256>(p, g, dtype, fp8, st);
+  return launch_partial_hd<256, false>(p, g, dtype, fp8, st);
 }
 
 int launch_combine_256(const CombineParams &c, int dtype, hipStream_t st) {

@@ -1625,35 +1625,28 @@ static void launch_partial_s(const DecodeParams &p, const Grid &g, hipStream_t s
         dim3(WAVES * 64), lds, st, p.seqlens, p.batch, p);
 }
 
-// Batches of up to kWaveScanMax sequences take the wave-local tile scan.
-template <int HD, int HR, typename T, bool kF8, int WAVES, bool kExtras, int kValuG>
-static void launch_partial_x(const DecodeParams &p, const Grid &g, hipStream_t st) {
-  if (p.batch <= kWaveScanMax)
-    launch_partial_s<HD, HR, T, kF8, WAVES, kExtras, true, kValuG>(p, g, st);
-  else
-    launch_partial_s<HD, HR, T, kF8, WAVES, kExtras, false, kValuG>(p, g, st);
-}
-
-template <int HD, int HR, typename T, bool kF8, int WAVES, int kValuG>
+// kWaveScan (the wave-local tile scan) is the caller's choice, batch <=
+// kWaveScanMax; the two halves compile in separate units.
+template <int HD, int HR, typename T, bool kF8, int WAVES, bool kWaveScan, int kValuG>
 static int launch_partial_w(const DecodeParams &p, const Grid &g, hipStream_t st) {
   if (p.window_left >= 0 || p.softcap > 0.f || p.sinks || p.alibi)
-    launch_partial_x<HD, HR, T, kF8, WAVES, true, kValuG>(p, g, st);
+    launch_partial_s<HD, HR, T, kF8, WAVES, true, kWaveScan, kValuG>(p, g, st);
   else
-    launch_partial_x<HD, HR, T, kF8, WAVES, false, kValuG>(p, g, st);
+    launch_partial_s<HD, HR, T, kF8, WAVES, false, kWaveScan, kValuG>(p, g, st);
   return hipGetLastError() == hipSuccess ? MXFA_OK : MXFA_ELAUNCH;
 }
 
 // The kernel is the grid's wave count; a grid the instantiations cannot run
 // (more waves than the row size has, or its heads and sub-ranges past the
 // waves) is refused: its extra kv heads would go uncomputed.
-template <int HD, int HR, typename T, bool kF8, int kValuG = 0>
+template <int HD, int HR, typename T, bool kF8, bool kWaveScan, int kValuG = 0>
 static int launch_partial_t(const DecodeParams &p, const Grid &g, hipStream_t st) {
   if (g.heads_per_wg * g.subs > g.waves) return MXFA_ELAUNCH;
   if constexpr (kMaxWaves<HD, kF8> == 8) {
-    if (g.waves == 8) return launch_partial_w<HD, HR, T, kF8, 8, kValuG>(p, g, st);
+    if (g.waves == 8) return launch_partial_w<HD, HR, T, kF8, 8, kWaveScan, kValuG>(p, g, st);
   }
   if (g.waves != 4) return MXFA_ELAUNCH;
-  return launch_partial_w<HD, HR, T, kF8, 4, kValuG>(p, g, st);
+  return launch_partial_w<HD, HR, T, kF8, 4, kWaveScan, kValuG>(p, g, st);
 }
 
 // Columns (query tokens x heads per kv head) whose QK runs on the VALU in
@@ -1669,6 +1662,11 @@ static int launch_partial_t(const DecodeParams &p, const Grid &g, hipStream_t st
 // waves per CU, short pieces) the per-piece q exchange does not pay. 16-bit
 // caches with page-uniform tiles and head dims of 128 or more only.
 inline int valu_qk_columns(int cols, int hd) {
+#ifdef MXFA_QK_ON_MFMA
+  // Comparison build (python -m mxflashattn_amd._build --qk-mfma): QK always
+  // on the matrix cores.
+  return 0;
+#endif
   if (hd < 128) return 0;
   if (cols <= 1) return 1;
   if (cols <= 2) return 2;
@@ -1676,7 +1674,7 @@ inline int valu_qk_columns(int cols, int hd) {
   return 0;
 }
 
-template <int HD, typename T, bool kF8>
+template <int HD, typename T, bool kF8, bool kWaveScan>
 static int launch_partial_hr(const DecodeParams &p, const Grid &g, hipStream_t st) {
   const int cols = p.gq * p.ql;
   switch (head_rows(cols)) {
@@ -1684,31 +1682,32 @@ static int launch_partial_hr(const DecodeParams &p, const Grid &g, hipStream_t s
       if constexpr (!kF8 && HD >= 128) {
         if (p.ps_log2 >= 4) {
           switch (valu_qk_columns(cols, HD)) {
-            case 1: return launch_partial_t<HD, 1, T, kF8, 1>(p, g, st);
-            case 2: return launch_partial_t<HD, 1, T, kF8, 2>(p, g, st);
+            case 1: return launch_partial_t<HD, 1, T, kF8, kWaveScan, 1>(p, g, st);
+            case 2: return launch_partial_t<HD, 1, T, kF8, kWaveScan, 2>(p, g, st);
             case 4:
-              if constexpr (HD == 128) return launch_partial_t<HD, 1, T, kF8, 4>(p, g, st);
+              if constexpr (HD == 128) return launch_partial_t<HD, 1, T, kF8, kWaveScan, 4>(p, g, st);
               break;
             default: break;
           }
         }
       }
-      return launch_partial_t<HD, 1, T, kF8>(p, g, st);
-    case 2: return launch_partial_t<HD, 2, T, kF8>(p, g, st);
-    default: return launch_partial_t<HD, 4, T, kF8>(p, g, st);
+      return launch_partial_t<HD, 1, T, kF8, kWaveScan>(p, g, st);
+    case 2: return launch_partial_t<HD, 2, T, kF8, kWaveScan>(p, g, st);
+    default: return launch_partial_t<HD, 4, T, kF8, kWaveScan>(p, g, st);
   }
 }
 
 // Partial kernel for one head dim: dtype of q/out (MXFA_DTYPE_F16/BF16), fp8
-// caches or caches of that dtype.
-template <int HD>
+// caches or caches of that dtype; kWaveScan for batches of up to
+// kWaveScanMax sequences (the caller's choice).
+template <int HD, bool kWaveScan>
 int launch_partial_hd(const DecodeParams &p, const Grid &g, int dtype, bool fp8,
                       hipStream_t st) {
   if (dtype == MXFA_DTYPE_BF16)
-    return fp8 ? launch_partial_hr<HD, BF16, true>(p, g, st)
-               : launch_partial_hr<HD, BF16, false>(p, g, st);
-  return fp8 ? launch_partial_hr<HD, F16, true>(p, g, st)
-             : launch_partial_hr<HD, F16, false>(p, g, st);
+    return fp8 ? launch_partial_hr<HD, BF16, true, kWaveScan>(p, g, st)
+               : launch_partial_hr<HD, BF16, false, kWaveScan>(p, g, st);
+  return fp8 ? launch_partial_hr<HD, F16, true, kWaveScan>(p, g, st)
+             : launch_partial_hr<HD, F16, false, kWaveScan>(p, g, st);
 }
 
 // Per-sequence kernel (seq_decode_kernel): grid (ceil(HKV / KH), B) of
