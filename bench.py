@@ -40,7 +40,11 @@ Prints ONE JSON line:
   decode_step  config 5: decode tok/s of a 36-layer random-init Qwen3-4B-shaped
                model whose attention runs through the vLLM backend path
                (HIP-graph replayed steps), and attention's share of the step;
+               decode_step_eager the same steps launched from Python (vLLM's
+               enforce_eager, the reference's end-to-end mode);
                decode_step_fp8 is the same step with an fp8 KV cache
+  host_us_per_call  host time of one eager decode call through the public API,
+               the C++ operator and the binding (and with the operator off)
 """
 
 from __future__ import annotations
@@ -305,6 +309,56 @@ def cpu_baseline(name: str, spec: dict, reps: int) -> dict:
     return res
 
 
+def host_overhead(device, calls: int = 100) -> dict:
+    """Host microseconds per eager decode call (the time the call takes to
+    return; the launches are asynchronous) at config 2, whose 107 us of GPU
+    time per call keeps the host from ever waiting on the device:
+    ``api`` flash_attn_with_kvcache (its fast path into the C++ operator),
+    ``operator`` the C++ operator alone, ``binding`` native.paged_decode_split;
+    ``*_ctypes`` the same with the operator switched off (the ctypes path)."""
+    import mxflashattn_amd as mx
+    from mxflashattn_amd import native
+    from mxflashattn_amd.workloads import CONFIGS, make_paged_batch
+
+    b = make_paged_batch(**CONFIGS["config2_qwen3_4b"], device=device)
+    out = torch.empty_like(b.q)
+
+    def api():
+        mx.flash_attn_with_kvcache(b.q, b.k_cache, b.v_cache, cache_seqlens=b.cache_seqlens,
+                                   block_table=b.block_table, out=out)
+
+    def binding():
+        native.paged_decode_split(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
+                                  b.scale, out=out)
+
+    def timed(fn) -> float:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            fn()
+        host = time.perf_counter() - t0
+        torch.cuda.synchronize()
+        return round(host * 1e6 / calls, 2)
+
+    res = {"api": timed(api), "binding": timed(binding)}
+    op = native.torch_op()
+    if op is not None:
+        res["operator"] = timed(lambda: op.decode(b.q, b.k_cache, b.v_cache, b.block_table,
+                                                  b.cache_seqlens, b.scale, out, None, 0))
+    native.USE_TORCH_OP = False
+    try:
+        res["api_ctypes"] = timed(api)
+        res["binding_ctypes"] = timed(binding)
+    finally:
+        native.USE_TORCH_OP = True
+    res["calls"] = calls
+    del b
+    torch.cuda.empty_cache()
+    return res
+
+
 def load_traffic(workload: str) -> float | None:
     path = REPO / "profiles" / f"traffic_{workload}.json"
     if not path.exists():
@@ -362,6 +416,16 @@ def main() -> int:
             decode = {"error": repr(exc)}
         print(f"[bench] config5: {decode}", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
+    decode_eager = None
+    if not args.no_decode_step:
+        print("[bench] config5 decode step, eager", file=sys.stderr, flush=True)
+        try:
+            decode_eager = decode_step.run(device=device, eager=True)
+        except Exception as exc:
+            print(f"[bench] eager decode step failed: {exc!r}", file=sys.stderr, flush=True)
+            decode_eager = {"error": repr(exc)}
+        print(f"[bench] config5 eager: {decode_eager}", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
     decode_fp8 = None
     if not args.no_decode_step and not args.no_wide:
         print("[bench] config5 decode step, fp8 KV cache", file=sys.stderr, flush=True)
@@ -372,6 +436,10 @@ def main() -> int:
             decode_fp8 = {"error": repr(exc)}
         print(f"[bench] config5 fp8: {decode_fp8}", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
+
+    print("[bench] host time per eager call", file=sys.stderr, flush=True)
+    host = host_overhead(device)
+    print(f"[bench] host: {host}", file=sys.stderr, flush=True)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -437,7 +505,9 @@ def main() -> int:
         "cells": cells,
         "wide": wide,
         "decode_step": decode,
+        "decode_step_eager": decode_eager,
         "decode_step_fp8": decode_fp8,
+        "host_us_per_call": host,
     }
     summary = {args.workload: main_res, **cells}
     for name in sorted(summary):

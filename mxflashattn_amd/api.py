@@ -8,18 +8,23 @@ the reference's chain (vendor wheel, ATen extension, opt-in PyTorch path).
 
 from __future__ import annotations
 
+import math
 import os
 
 import torch
 
-from . import decode, fallback
-from .dispatch import dispatch
+from . import decode, fallback, native
+from .dispatch import BACKEND_MI355X, DispatchInfo, dispatch, record_dispatch
 from .validation import (
     validate_cumulative_lengths,
     validate_options,
     validate_qkv,
     validate_softmax_scale,
 )
+
+
+# The dispatch record of a call the fast path below takes (immutable, shared).
+_KVCACHE_MI355X = DispatchInfo(backend=BACKEND_MI355X, operation="flash_attn_with_kvcache")
 
 
 def _resolved_scale(head_dim: int, softmax_scale: float | None) -> float:
@@ -175,6 +180,30 @@ def flash_attn_with_kvcache(
     FlashAttention fork) is a tensor of q's shape, dtype and device that
     receives the result and is returned; the MI355X route writes into it
     directly, other backends copy their result into it."""
+    # The common decode call (one query token, a paged 16-bit cache with int32
+    # lengths and table, no appended k/v, default options) goes straight to the
+    # C++ operator, which makes the shape, dtype, device and layout checks the
+    # full path makes and launches on the current stream; anything it does not
+    # take (it returns None) continues below, where the same call gets the
+    # full validation, its error or another route.
+    if (k is None and v is None and isinstance(q, torch.Tensor)
+            and isinstance(block_table, torch.Tensor)
+            and isinstance(cache_seqlens, torch.Tensor)
+            and (out is None or isinstance(out, torch.Tensor)) and rotary_cos is None
+            and rotary_sin is None and not return_softmax_lse and softcap == 0
+            and alibi_slopes is None and window_size == (-1, -1)
+            and (softmax_scale is None or (type(softmax_scale) is float
+                                           and math.isfinite(softmax_scale)))
+            and q.is_cuda and q.ndim == 4 and q.shape[1] == 1 and q.shape[3] in (64, 128)
+            and os.environ.get("MXFLASHATTN_STRICT_VALIDATION", "0") != "1"):
+        op = native.torch_op() if native.USE_TORCH_OP else None
+        if op is not None:
+            scale = softmax_scale if softmax_scale is not None else float(q.shape[3] ** -0.5)
+            result = op.decode(q, k_cache, v_cache, block_table, cache_seqlens, scale, out,
+                               None, 0)
+            if result is not None:
+                record_dispatch(_KVCACHE_MI355X)
+                return out if out is not None else result
     validate_softmax_scale(softmax_scale)
     if rotary_cos is not None or rotary_sin is not None:
         raise NotImplementedError("rotary embeddings are not supported")

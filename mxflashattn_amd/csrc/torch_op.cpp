@@ -79,7 +79,8 @@ bool poison_outputs() {
 }
 
 void poison(void *stream, at::Tensor &out, at::Tensor *ws) {
-  if (!poison_outputs()) return;
+  // An output whose rows overlap is refused by the launch; it is not filled.
+  if (!poison_outputs() || at::has_internal_overlap(out) != at::MemOverlap::No) return;
   hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing((hipStream_t)stream, &status) != hipSuccess ||
       status != hipStreamCaptureStatusNone)

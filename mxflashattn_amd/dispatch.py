@@ -60,6 +60,10 @@ def _record(info: DispatchInfo) -> None:
     _state.dispatch_info = info
 
 
+# The public API's fast path records its (shared, immutable) DispatchInfo here.
+record_dispatch = _record
+
+
 def _native_extension() -> Any | None:
     try:
         return importlib.import_module("mxflashattn_amd._C")

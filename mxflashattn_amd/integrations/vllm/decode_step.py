@@ -11,7 +11,8 @@ the ``mi355x_split_decode`` kernels). The metadata object carries the fields
 vLLM's FlashAttention metadata carries for decode.
 
 As vLLM does for decode, a whole step (all layers and the logits) is captured
-once in a HIP graph and replayed; between replays the host-side model runner
+once in a HIP graph and replayed (``eager=True``: every step launched from
+Python instead, vLLM's ``enforce_eager``); between replays the host-side model runner
 advances the metadata (lengths, slots, positions) and picks the next tokens
 greedily. The prompt part of the KV cache is synthetic (random K/V, no
 prefill run): the decode step reads it exactly as it would read a real one.
@@ -240,13 +241,20 @@ def advance(state: DecodeState) -> None:
 def run(batch: int = 128, new_tokens: int = 256, shape: DecoderShape = QWEN3_4B,
         median: int = 1024, sigma: float = 1.0, lo: int = 16, hi: int = 8192,
         page_size: int = 16, device: torch.device | None = None, seed: int = 20261007,
-        kv_cache_dtype: str = "auto") -> dict:
-    """Decode ``new_tokens`` tokens for ``batch`` sequences; timing and share."""
+        kv_cache_dtype: str = "auto", eager: bool = False) -> dict:
+    """Decode ``new_tokens`` tokens for ``batch`` sequences; timing and share.
+
+    eager: every step is launched from Python (vLLM's ``enforce_eager=True``,
+    the mode of the reference's end-to-end runs) instead of replaying a
+    captured HIP graph."""
     device = device or torch.device("cuda", torch.cuda.current_device())
     model = DecoderModel(shape, device, seed=seed, kv_cache_dtype=kv_cache_dtype)
     prompt = lognormal_prompt_lengths(batch, median, sigma, lo, hi, seed)
     state = build_state(model, batch, prompt, new_tokens, page_size, seed)
     stream = torch.cuda.Stream(device)
+    if eager:
+        return _run_eager(model, state, batch, new_tokens, shape, prompt, stream,
+                          kv_cache_dtype, (median, sigma, lo, hi))
 
     def step():
         return model.step(state.tokens, state.positions, state.kv_caches, state.meta)
@@ -328,6 +336,91 @@ def run(batch: int = 128, new_tokens: int = 256, shape: DecoderShape = QWEN3_4B,
     }
 
 
+def _run_eager(model: DecoderModel, state: DecodeState, batch: int, new_tokens: int,
+               shape: DecoderShape, prompt: torch.Tensor, stream: torch.cuda.Stream,
+               kv_cache_dtype: str, dist: tuple) -> dict:
+    """Eager steps: the host launches every kernel of every layer, every step."""
+    import time
+
+    def step():
+        return model.step(state.tokens, state.positions, state.kv_caches, state.meta)
+
+    with torch.cuda.stream(stream):
+        logits = step()  # warm-up: the first decoded token (workspace sized here)
+        state.tokens.copy_(logits.argmax(-1))
+    torch.cuda.synchronize()
+    steps = new_tokens - 1
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        t0 = time.perf_counter()
+        start.record(stream)
+        for _ in range(steps):
+            advance(state)
+            logits = step()
+            state.tokens.copy_(logits.argmax(-1))
+        end.record(stream)
+        host_s = time.perf_counter() - t0
+    torch.cuda.synchronize()
+    step_ms = start.elapsed_time(end) / steps
+
+    # Attention alone, eager: the same two backend calls per layer, launched
+    # from Python; GPU time from events, host time per layer from the clock.
+    q_static = torch.randn(batch, shape.q_heads, shape.head_dim, device=model.device,
+                           dtype=model.dtype)
+    kv_static = torch.randn(batch, shape.kv_heads, shape.head_dim, device=model.device,
+                            dtype=model.dtype)
+    attn_static = torch.empty(batch, shape.q_heads * shape.head_dim, device=model.device,
+                              dtype=model.dtype)
+    reps = 20
+
+    def attention_layers():
+        for i in range(shape.layers):
+            model.attention(i, q_static, kv_static, kv_static, state.kv_caches[i], state.meta,
+                            attn_static)
+
+    a0 = torch.cuda.Event(enable_timing=True)
+    a1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        attention_layers()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        a0.record(stream)
+        for _ in range(reps):
+            attention_layers()
+        a1.record(stream)
+        attn_host_s = time.perf_counter() - t0
+    torch.cuda.synchronize()
+    attn_ms = a0.elapsed_time(a1) / reps
+    final_lens = state.meta.seq_lens.to(torch.int64)
+    kv_bytes_step = (int(final_lens.sum().item()) * shape.kv_heads * shape.head_dim * 2
+                     * state.kv_caches[0].element_size() * shape.layers)
+    median, sigma, lo, hi = dist
+    return {
+        "mode": "eager",
+        "decode_tok_s": round(batch / (step_ms * 1e-3), 1),
+        "step_ms": round(step_ms, 4),
+        "host_ms_per_step": round(host_s * 1e3 / steps, 4),
+        "attention_ms": round(attn_ms, 4),
+        "attention_share": round(attn_ms / step_ms, 4),
+        "attention_host_us_per_layer": round(attn_host_s * 1e6 / (reps * shape.layers), 2),
+        "attention_kv_gb_s": round(kv_bytes_step / (attn_ms * 1e-3) / 1e9, 1),
+        "batch": batch,
+        "kv_cache_dtype": "fp8_e4m3" if kv_cache_dtype.startswith("fp8") else "bf16",
+        "new_tokens": new_tokens,
+        "timed_steps": steps,
+        "layers": shape.layers,
+        "prompt_len": {"median": float(prompt.median()),
+                       "mean": round(float(prompt.float().mean()), 1),
+                       "min": int(prompt.min()), "max": int(prompt.max()),
+                       "distribution": f"lognormal(median {median}, sigma {sigma}) clipped "
+                                       f"[{lo}, {hi}]"},
+        "kv_tokens_at_end": int(final_lens.sum().item()),
+        "logits_finite": bool(torch.isfinite(logits.float()).all().item()),
+        "data": "synthetic (random-init weights, random prompt K/V, greedy tokens)",
+    }
+
+
 def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser(description=__doc__,
                                  formatter_class=argparse.RawTextHelpFormatter)
@@ -335,13 +428,15 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--new-tokens", type=int, default=256)
     ap.add_argument("--layers", type=int, default=QWEN3_4B.layers)
     ap.add_argument("--kv-cache-dtype", default="auto", choices=("auto", "fp8"))
+    ap.add_argument("--eager", action="store_true",
+                    help="launch every step from Python instead of replaying a HIP graph")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         print("decode_step needs a GPU", file=sys.stderr)
         return 2
     shape = DecoderShape(layers=args.layers)
     print(json.dumps(run(args.batch, args.new_tokens, shape,
-                         kv_cache_dtype=args.kv_cache_dtype)))
+                         kv_cache_dtype=args.kv_cache_dtype, eager=args.eager)))
     return 0
 
 

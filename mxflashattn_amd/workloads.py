@@ -99,6 +99,7 @@ def make_paged_batch(
     kv_dtype: torch.dtype | None = None,
     q_len: int = 1,
     window_left: int = -1,
+    packed: bool = False,
 ) -> PagedBatch:
     """Build one synthetic decode batch.
 
@@ -111,7 +112,11 @@ def make_paged_batch(
     nearest even; their dequantisation scales are 1). q_len > 1 gives every
     sequence that many query tokens (the last q_len positions of its length).
     window_left is recorded for the decode call (a sliding window) and changes
-    the bytes the call must read, not the data.
+    the bytes the call must read, not the data. packed (page_size 1): the keys
+    of all sequences are packed end to end, as flash_attn_varlen_func hands
+    them over ([total_tokens, HKV, HD] viewed as one-token pages), and table
+    row b is offset_b + arange(width) (past the sequence end it repeats the
+    last token, which the length never reaches).
     """
     device = torch.device(device)
     gen = torch.Generator(device=device)
@@ -126,17 +131,28 @@ def make_paged_batch(
         lens = torch.full((batch,), int(lengths), dtype=torch.int64)
     need = [(int(x) + page_size - 1) // page_size for x in lens]
     total_need = sum(need)
-    if num_pages is None:
-        num_pages = max(1, math.ceil(pool_factor * total_need))
-    if num_pages < total_need:
-        raise ValueError(f"pool of {num_pages} pages cannot hold {total_need} pages")
-    width = block_table_width or max(1, max(need) if need else 1)
-    perm = torch.randperm(num_pages, generator=torch.Generator().manual_seed(seed + 1))
-    table = torch.zeros((batch, width), dtype=torch.int32)
-    cursor = 0
-    for b, n in enumerate(need):
-        table[b, :n] = perm[cursor:cursor + n].to(torch.int32)
-        cursor += n
+    if packed:
+        if page_size != 1:
+            raise ValueError("packed keys are one-token pages (page_size 1)")
+        num_pages = max(1, total_need)
+        width = block_table_width or max(1, max(need) if need else 1)
+        starts = torch.cumsum(torch.tensor([0] + need[:-1], dtype=torch.int64), 0)
+        pos = torch.arange(width, dtype=torch.int64)[None, :]
+        last = (starts + torch.tensor(need, dtype=torch.int64) - 1).clamp(min=0)[:, None]
+        table = torch.minimum(starts[:, None] + pos, last).clamp(max=num_pages - 1)
+        table = table.to(torch.int32)
+    else:
+        if num_pages is None:
+            num_pages = max(1, math.ceil(pool_factor * total_need))
+        if num_pages < total_need:
+            raise ValueError(f"pool of {num_pages} pages cannot hold {total_need} pages")
+        width = block_table_width or max(1, max(need) if need else 1)
+        perm = torch.randperm(num_pages, generator=torch.Generator().manual_seed(seed + 1))
+        table = torch.zeros((batch, width), dtype=torch.int32)
+        cursor = 0
+        for b, n in enumerate(need):
+            table[b, :n] = perm[cursor:cursor + n].to(torch.int32)
+            cursor += n
 
     def randn(*shape: int) -> torch.Tensor:
         return torch.randn(*shape, generator=gen, device=device, dtype=torch.float32).to(dtype)
@@ -211,4 +227,9 @@ WIDE = {
     "wide_window1024_config2": dict(batch=32, q_heads=32, kv_heads=8, head_dim=128,
                                     dtype=torch.bfloat16, lengths=(1024, 8192),
                                     window_left=1023),
+    # Config 2 as flash_attn_varlen_func decode lays it out: the keys packed
+    # end to end and read as one-token pages (the per-lane page-id kernels).
+    "wide_varlen_config2": dict(batch=32, q_heads=32, kv_heads=8, head_dim=128,
+                                dtype=torch.bfloat16, lengths=(1024, 8192), page_size=1,
+                                packed=True),
 }
