@@ -1,5 +1,6 @@
 // Host-side torch operator in front of the C ABI (include/mxfa_mi355x.h): the
-// hot decode call without Python's per-argument marshalling.
+// hot decode call and the vLLM-form page append without Python's
+// per-argument marshalling.
 //
 // decode(q, k_cache, v_cache, block_table, cache_seqlens, scale, out,
 //        num_splits, seqlen_add) takes the common call (one query
@@ -206,6 +207,50 @@ py::object decode(const at::Tensor &q, const at::Tensor &k_cache, const at::Tens
   return py::cast(out);
 }
 
+// reshape_and_cache(key, value, key_cache, value_cache, slot_mapping): the
+// vLLM-form append of 16-bit caches (mxfa_reshape_and_cache_launch) for the
+// common call: key/value [T, HKV, HD] sharing strides with a contiguous last
+// dim, caches [pages, PS, HKV, HD] of their dtype sharing strides, int64
+// contiguous slots (at least T of them), every tensor on the current GPU.
+// Returns true once launched on torch's current stream; false (nothing
+// launched) for any other call, which the Python binding then takes.
+bool reshape_and_cache(const at::Tensor &key, const at::Tensor &value,
+                       const at::Tensor &key_cache, const at::Tensor &value_cache,
+                       const at::Tensor &slot_mapping) {
+  const at::ScalarType dt = key.scalar_type();
+  if (dt != at::kHalf && dt != at::kBFloat16) return false;
+  if (!key.is_cuda() || value.scalar_type() != dt || key_cache.scalar_type() != dt ||
+      value_cache.scalar_type() != dt || slot_mapping.scalar_type() != at::kLong)
+    return false;
+  if (key.dim() != 3 || !value.sizes().equals(key.sizes()) || !value.strides().equals(key.strides()) ||
+      key.stride(2) != 1)
+    return false;
+  if (key_cache.dim() != 4 || !value_cache.sizes().equals(key_cache.sizes()) ||
+      !value_cache.strides().equals(key_cache.strides()) || key_cache.stride(3) != 1)
+    return false;
+  if (key.size(1) != key_cache.size(2) || key.size(2) != key_cache.size(3)) return false;
+  if (slot_mapping.dim() != 1 || !slot_mapping.is_contiguous() ||
+      slot_mapping.size(0) < key.size(0))
+    return false;
+  const at::Device device = key.device();
+  if (value.device() != device || key_cache.device() != device ||
+      value_cache.device() != device || slot_mapping.device() != device ||
+      device.index() != c10::hip::current_device())
+    return false;
+  void *stream = (void *)c10::hip::getCurrentHIPStream(device.index()).stream();
+  const int rc = mxfa_reshape_and_cache_launch(
+      key.data_ptr(), value.data_ptr(), key.stride(0), key.stride(1), key_cache.data_ptr(),
+      value_cache.data_ptr(), key_cache.stride(0), key_cache.stride(1), key_cache.stride(2),
+      slot_mapping.data_ptr<int64_t>(), (int)key.size(0), (int)key.size(1), (int)key.size(2),
+      (int)key_cache.size(1), (int)key_cache.size(0),
+      dt == at::kBFloat16 ? MXFA_DTYPE_BF16 : MXFA_DTYPE_F16, stream);
+  if (rc == MXFA_EUNSUPPORTED || rc == MXFA_EINVAL) return false;  // nothing launched
+  if (rc != MXFA_OK)
+    throw std::runtime_error(std::string("mxfa_reshape_and_cache_launch failed (") +
+                             std::to_string(rc) + "): " + mxfa_strerror(rc));
+  return true;
+}
+
 }  // namespace
 
 PYBIND11_MODULE(_mxfa_torch, m) {
@@ -214,6 +259,8 @@ PYBIND11_MODULE(_mxfa_torch, m) {
         py::arg("block_table"), py::arg("cache_seqlens"), py::arg("scale"),
         py::arg("out") = py::none(), py::arg("num_splits") = py::none(),
         py::arg("seqlen_add") = 0);
+  m.def("reshape_and_cache", &reshape_and_cache, py::arg("key"), py::arg("value"),
+        py::arg("key_cache"), py::arg("value_cache"), py::arg("slot_mapping"));
   m.def("abi_version", &mxfa_abi_version);
   m.def("workspace_bytes", &workspace_bytes,
         "(bytes of live workspaces, bytes of workspaces replaced by larger ones)");

@@ -189,27 +189,37 @@ def decode_forward(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: A
         return result.reshape(n, -1), None
     layout = (inspect_layout(query, kv_cache, attn_metadata) if STRICT_LAYOUT
               else fast_layout(query, kv_cache, attn_metadata))
+    result = _paged_decode(query, kv_cache, attn_metadata, layout.batch_size,
+                           layout.num_actual_tokens, layout.max_query_len,
+                           softmax_scale=softmax_scale, causal=causal, out=out)
+    return result, layout
+
+
+def _paged_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: Any, batch: int,
+                  num_actual_tokens: int, max_query_len: int, *, softmax_scale: float,
+                  causal: bool, out: torch.Tensor | None) -> torch.Tensor:
+    """The checks and the call of decode_forward's default mode, once the
+    layout's batch, token count and query length are known; returns
+    [tokens, heads*dim]."""
     if not bool(attn_metadata.causal) and causal:
         raise DecoderAdapterBlocked("metadata_causal_flag_is_false")
     _no_cascade(attn_metadata)
-    if layout.max_query_len != 1:
+    if max_query_len != 1:
         raise DecoderAdapterBlocked(
-            f"only_single_token_decode_supported:max_query_len={layout.max_query_len}"
+            f"only_single_token_decode_supported:max_query_len={max_query_len}"
         )
     if kv_cache.dtype not in (torch.float16, torch.bfloat16):
         raise DecoderAdapterBlocked(f"kv_cache_dtype_not_supported:{kv_cache.dtype}")
     if query.shape[1] % kv_cache.shape[3]:
         raise DecoderAdapterBlocked("query_and_kv_head_counts_are_not_gqa_compatible")
-    key_cache, value_cache = kv_cache.unbind(0)
-    batch = layout.batch_size
-    q = query[: layout.num_actual_tokens].reshape(batch, 1, query.shape[1], query.shape[2])
+    q = query[:num_actual_tokens].reshape(batch, 1, query.shape[1], query.shape[2])
     result = flash_attn_with_kvcache(
-        q, key_cache, value_cache,
+        q, kv_cache[0], kv_cache[1],
         cache_seqlens=_int32_on(attn_metadata.seq_lens, query.device),
         block_table=_int32_on(attn_metadata.block_table, query.device),
         softmax_scale=softmax_scale, causal=causal, **_out_kw(out, q),
     )
-    return result.reshape(layout.num_actual_tokens, -1), layout
+    return result.reshape(num_actual_tokens, -1)
 
 
 def _out_kw(out: torch.Tensor | None, q: torch.Tensor) -> dict:
@@ -315,8 +325,22 @@ def forward_decode(query: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: A
             or alibi_slopes is not None):
         return _native_decode(query, kv_cache, attn_metadata, output, softmax_scale, k_scale,
                               v_scale, fp8, window_left, sinks, softcap, alibi_slopes)
-    result, _ = decode_forward(query, kv_cache, attn_metadata, softmax_scale=softmax_scale,
-                               causal=bool(attn_metadata.causal), out=output)
+    causal = bool(attn_metadata.causal)
+    if (STRICT_LAYOUT or os.getenv("MXFLASHATTN_GRAPH_DECODE", "0") == "1"
+            or _transparent_enabled()):
+        result, _ = decode_forward(query, kv_cache, attn_metadata, softmax_scale=softmax_scale,
+                                   causal=causal, out=output)
+    else:
+        # decode_forward's default mode with fast_layout's checks but without
+        # building the layout record, which this caller does not use.
+        _check_shapes(query, kv_cache, attn_metadata)
+        block_table = attn_metadata.block_table
+        if block_table.ndim != 2:
+            raise DecoderAdapterBlocked("block_table_rows_do_not_match_batch")
+        result = _paged_decode(query, kv_cache, attn_metadata, int(block_table.shape[0]),
+                               int(attn_metadata.num_actual_tokens),
+                               int(attn_metadata.max_query_len), softmax_scale=softmax_scale,
+                               causal=causal, out=output)
     info = get_last_dispatch_info()
     if info is None:
         raise RuntimeError("MXFlashAttn decoder returned without dispatch evidence")

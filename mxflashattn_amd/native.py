@@ -818,6 +818,13 @@ def reshape_and_cache(
 
     float8_e4m3fn caches store e4m3fn_rne(saturate(x / scale)) with the
     per-tensor k_scale / v_scale; 16-bit caches are a bit-exact copy."""
+    if USE_TORCH_OP and k_scale is None and v_scale is None:
+        op = torch_op()
+        # The common 16-bit call goes through the C++ operator; it launches
+        # nothing and returns False for any other call, taken below.
+        if op is not None and op.reshape_and_cache(key, value, key_cache, value_cache,
+                                                   slot_mapping):
+            return
     if key.dim() != 3 or value.shape != key.shape:
         raise ValueError("key/value must be [num_tokens, kv_heads, head_dim]")
     if key_cache.dim() != 4 or value_cache.shape != key_cache.shape:

@@ -122,3 +122,27 @@ def test_eager_decode_step_runs(device):
     assert res["mode"] == "eager" and res["logits_finite"]
     assert res["step_ms"] > 0 and 0 < res["attention_share"] <= 1.5
     assert res["attention_host_us_per_layer"] > 0 and res["timed_steps"] == 5
+
+
+def test_reshape_and_cache_operator_equals_ctypes_path(device, monkeypatch):
+    """The vLLM-form append through the C++ operator and through ctypes write
+    the same bytes; slots < 0 are skipped by both."""
+    g = torch.Generator().manual_seed(17)
+    pages, ps, hkv, hd = 40, 16, 8, 128
+    key = torch.randn(50, hkv, hd, generator=g).to(torch.bfloat16)
+    value = torch.randn(50, hkv, hd, generator=g).to(torch.bfloat16)
+    slots = torch.randperm(pages * ps, generator=g)[:50]
+    slots[[3, 17]] = -1
+    caches = []
+    for use_op in (True, False):
+        monkeypatch.setattr(native, "USE_TORCH_OP", use_op)
+        kc = torch.zeros(pages, ps, hkv, hd, dtype=torch.bfloat16, device=device)
+        vc = torch.zeros_like(kc)
+        native.reshape_and_cache(key.to(device), value.to(device), kc, vc, slots.to(device))
+        caches.append((kc, vc))
+    torch.cuda.synchronize()
+    assert torch.equal(caches[0][0], caches[1][0]) and torch.equal(caches[0][1], caches[1][1])
+    kc = caches[0][0].cpu().view(pages * ps, hkv, hd)
+    keep = slots >= 0
+    assert torch.equal(kc[slots[keep]], key[keep])
+    assert int((kc.abs().sum((1, 2)) > 0).sum()) == int(keep.sum())
