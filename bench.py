@@ -81,6 +81,8 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--no-decode-step", action="store_true", help="skip config 5")
     ap.add_argument("--no-wide", action="store_true",
                     help="skip the shapes beyond the reference's contract")
+    ap.add_argument("--no-host-overhead", action="store_true",
+                    help="skip the host-time-per-call section (config 2 launches)")
     ap.add_argument("--cpu-reps", type=int, default=15)
     return ap.parse_args()
 
@@ -437,9 +439,11 @@ def main() -> int:
         print(f"[bench] config5 fp8: {decode_fp8}", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
 
-    print("[bench] host time per eager call", file=sys.stderr, flush=True)
-    host = host_overhead(device)
-    print(f"[bench] host: {host}", file=sys.stderr, flush=True)
+    host = None
+    if not args.no_host_overhead:
+        print("[bench] host time per eager call", file=sys.stderr, flush=True)
+        host = host_overhead(device)
+        print(f"[bench] host: {host}", file=sys.stderr, flush=True)
 
     cpu = None
     if not args.no_cpu_baseline:

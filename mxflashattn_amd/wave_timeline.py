@@ -54,7 +54,11 @@ COMBINE_WORDS = 4
 def build() -> Path:
     from . import _build
 
-    return _build.build(lib_path=STAMPED_LIB, extra=("-DMXFA_WAVE_STAMPS",), torch_op=False)
+    # The stamps keep clock values live across the prologue: two fp8
+    # instantiations then hold 20 bytes per lane in scratch, which the
+    # shipped build refuses but a timing aid may carry.
+    return _build.build(lib_path=STAMPED_LIB, extra=("-DMXFA_WAVE_STAMPS",), torch_op=False,
+                        check_registers=False)
 
 
 def _summary(stamps, combine) -> dict:

@@ -113,6 +113,24 @@ def test_random_per_sequence_sweep(device, seed):
              per_sequence=True)
 
 
+# Every per-sequence case at head dim 256 in the seeds above. Built for two
+# waves per SIMD (a 256-register budget), the per-sequence kernel spilled
+# 65-201 VGPRs and returned wrong outputs on all of them (max error 0.6-3.6)
+# until a change that left its arithmetic alone but gave the compiler less to
+# keep live; the library ships one wave per SIMD there (no spills, and the
+# build now fails on any spill). They run again here by name.
+HD256_PER_SEQUENCE_SEEDS = (364, 377, 378, 379, 380, 381, 390, 396, 397, 400, 403, 406, 409, 418,
+                            421, 422, 437, 444, 448, 451, 453, 454, 457, 473)
+
+
+@pytest.mark.parametrize("seed", HD256_PER_SEQUENCE_SEEDS)
+def test_hd256_per_sequence_regression(device, seed):
+    c = draw(seed)
+    assert c["hd"] == 256
+    run_case(device, seed, extended=seed % 3 == 1, chunked_query=seed % 3 == 2,
+             per_sequence=True)
+
+
 @pytest.mark.parametrize("seed", range(480, 600))
 def test_random_odd_kv_heads_sweep(device, seed):
     run_case(device, seed, extended=seed % 4 == 1, chunked_query=seed % 4 == 2,
