@@ -22,8 +22,9 @@ INCLUDE_DIR = REPO_DIR / "include"
 LIB_DIR = PACKAGE_DIR / "_lib"
 LIB_NAME = "libmxfa_mi355x.so"
 LIB_PATH = LIB_DIR / LIB_NAME
-SOURCES = ("split_decode.hip", "split_hd64.hip", "split_hd64_ws.hip", "split_hd128.hip",
-           "split_hd128_ws.hip", "split_hd256.hip", "split_hd256_ws.hip", "kv_append.hip")
+SOURCES = ("split_decode.hip", "split_hd64.hip", "split_hd64_ws.hip", "split_hd64_ws4.hip",
+           "split_hd128.hip", "split_hd128_ws.hip", "split_hd128_ws4.hip", "split_hd256.hip",
+           "split_hd256_ws.hip", "split_hd256_ws4.hip", "kv_append.hip")
 # Comparison build: QK always on the matrix cores (the default build puts it on
 # the VALU for launches of few columns at head dims >= 128).
 QK_MFMA_LIB_PATH = PACKAGE_DIR / "_lib" / "qk_mfma" / "libmxfa_mi355x.so"
@@ -90,7 +91,16 @@ def _run(cmd: list[str]) -> str:
 # compiler's resource-usage remarks (one block per kernel) are the record.
 RESOURCE_REMARKS = "-Rpass-analysis=kernel-resource-usage"
 _REMARK = re.compile(r"remark:\s+(Function Name|VGPRs Spill|ScratchSize \[bytes/lane\]|VGPRs|"
-                     r"AGPRs|Occupancy \[waves/SIMD\]): (\S+)")
+                     r"AGPRs|Occupancy \[waves/SIMD\]|LDS Size \[bytes/block\]): (\S+)")
+
+# Static LDS each kernel family declares (the combine's reduction buffer; the
+# split kernels' per-wave tile totals), in bytes. More than that is a private
+# array the compiler moved into LDS, the same failure as scratch (a register
+# array indexed at run time) in another memory: it fails the build too.
+# Dynamic LDS (the tile prefix sums, the per-sequence kernel's pieces) is not
+# counted in the remark.
+STATIC_LDS_LIMITS = {"split_combine_kernel": 256 * 6 * 4}
+STATIC_LDS_DEFAULT = 64
 
 
 def resource_usage(remarks: str) -> dict[str, dict[str, str]]:
@@ -106,15 +116,26 @@ def resource_usage(remarks: str) -> dict[str, dict[str, str]]:
     return kernels
 
 
+def static_lds_limit(name: str) -> int:
+    for family, limit in STATIC_LDS_LIMITS.items():
+        if family in name:
+            return limit
+    return STATIC_LDS_DEFAULT
+
+
 def check_resource_usage(source: str, remarks: str) -> dict[str, dict[str, str]]:
-    """Raise when a kernel of ``source`` spills VGPRs or uses scratch memory."""
+    """Raise when a kernel of ``source`` spills VGPRs, uses scratch memory or
+    holds more static LDS than its family declares."""
     kernels = resource_usage(remarks)
     bad = [f"{name}: VGPR spills {u.get('VGPRs Spill')}, scratch "
-           f"{u.get('ScratchSize [bytes/lane]')} bytes/lane"
+           f"{u.get('ScratchSize [bytes/lane]')} bytes/lane, static LDS "
+           f"{u.get('LDS Size [bytes/block]')} bytes (limit {static_lds_limit(name)})"
            for name, u in kernels.items()
-           if u.get("VGPRs Spill", "0") != "0" or u.get("ScratchSize [bytes/lane]", "0") != "0"]
+           if u.get("VGPRs Spill", "0") != "0" or u.get("ScratchSize [bytes/lane]", "0") != "0"
+           or int(u.get("LDS Size [bytes/block]", "0")) > static_lds_limit(name)]
     if bad:
-        raise RuntimeError(f"{source}: kernels spill or use scratch memory:\n" + "\n".join(bad))
+        raise RuntimeError(f"{source}: kernels spill, use scratch memory or promote arrays to "
+                           "LDS:\n" + "\n".join(bad))
     return kernels
 
 

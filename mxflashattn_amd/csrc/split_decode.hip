@@ -56,6 +56,12 @@ int launch_partial_128_ws(const DecodeParams &p, const Grid &g, int dtype, bool 
                           hipStream_t st);
 int launch_partial_256_ws(const DecodeParams &p, const Grid &g, int dtype, bool fp8,
                           hipStream_t st);
+int launch_partial_64_ws4(const DecodeParams &p, const Grid &g, int dtype, bool fp8,
+                          hipStream_t st);
+int launch_partial_128_ws4(const DecodeParams &p, const Grid &g, int dtype, bool fp8,
+                           hipStream_t st);
+int launch_partial_256_ws4(const DecodeParams &p, const Grid &g, int dtype, bool fp8,
+                           hipStream_t st);
 int launch_combine_64(const CombineParams &c, int dtype, hipStream_t st);
 int launch_combine_128(const CombineParams &c, int dtype, hipStream_t st);
 int launch_combine_256(const CombineParams &c, int dtype, hipStream_t st);
@@ -265,17 +271,23 @@ static DecodeParams make_params(const SplitArgs &a, const Grid &g) {
 static int launch_partial(const SplitArgs &a, hipStream_t st) {
   const Grid g = grid_for(a.hkv, a.num_splits, waves_for(a.hd * (a.fp8 ? 1 : 2), a.hkv));
   const DecodeParams p = make_params(a, g);
-  const bool ws = a.batch <= kWaveScanMax;  // the wave-local tile scan
+  // The tile scan: inside each wave, one or four sequences per lane, or
+  // through LDS; four per lane is built for plain calls only.
+  int ws = wave_scan_per_lane(a.batch);
+  if (ws == 4 && !plain_call(p)) ws = 0;
   switch (a.hd) {
     case 64:
-      return ws ? launch_partial_64_ws(p, g, a.dtype, a.fp8, st)
-                : launch_partial_64(p, g, a.dtype, a.fp8, st);
+      return ws == 1   ? launch_partial_64_ws(p, g, a.dtype, a.fp8, st)
+             : ws == 4 ? launch_partial_64_ws4(p, g, a.dtype, a.fp8, st)
+                       : launch_partial_64(p, g, a.dtype, a.fp8, st);
     case 128:
-      return ws ? launch_partial_128_ws(p, g, a.dtype, a.fp8, st)
-                : launch_partial_128(p, g, a.dtype, a.fp8, st);
+      return ws == 1   ? launch_partial_128_ws(p, g, a.dtype, a.fp8, st)
+             : ws == 4 ? launch_partial_128_ws4(p, g, a.dtype, a.fp8, st)
+                       : launch_partial_128(p, g, a.dtype, a.fp8, st);
     default:
-      return ws ? launch_partial_256_ws(p, g, a.dtype, a.fp8, st)
-                : launch_partial_256(p, g, a.dtype, a.fp8, st);
+      return ws == 1   ? launch_partial_256_ws(p, g, a.dtype, a.fp8, st)
+             : ws == 4 ? launch_partial_256_ws4(p, g, a.dtype, a.fp8, st)
+                       : launch_partial_256(p, g, a.dtype, a.fp8, st);
   }
 }
 

@@ -7,7 +7,7 @@ namespace mxfa {
 
 int launch_partial_64(const DecodeParams &p, const Grid &g, int dtype, bool fp8,
                        hipStream_t st) {
-  return launch_partial_hd<64, false>(p, g, dtype, fp8, st);
+  return launch_partial_hd<64, 0>(p, g, dtype, fp8, st);
 }
 
 int launch_combine_64(const CombineParams &c, int dtype, hipStream_t st) {

@@ -574,42 +574,131 @@ __device__ __forceinline__ void zero_empty(const DecodeParams &p, const int32_t 
 }
 
 // Batches of up to kWaveScanMax sequences skip the LDS tile scan: every wave
-// loads the lengths itself, one per lane, and scans the tile counts with DPP
-// (wave_tile_scan), so no wave waits on a barrier or an LDS round trip before
-// it looks for its range's first sequence.
-constexpr int kWaveScanMax = 64;
-
-// Lane b (< B) ends with its sequence's clamped length `len`, the exclusive
-// and inclusive tile prefix sums `excl` / `incl` (S_b and S_{b+1}); lanes past
-// the batch hold len 0 and excl = incl = the tile total, which is returned.
-// The length load needs only the preloaded leading arguments, so it is issued
-// before any wait on the parameter struct.
-template <bool kWindow>
-__device__ __forceinline__ int wave_tile_scan(const DecodeParams &p, const int32_t *seqlens, int B,
-                                              int &len, int &excl, int &incl) {
-  const int lane = threadIdx.x & 63;
-  const int raw = as_const(seqlens)[lane < B ? lane : B - 1];
-  int L = raw + p.seqlen_add;
-  L = L < 0 ? 0 : (L > p.max_len ? p.max_len : L);
-  L = lane < B ? L : 0;
-  const int n = kWindow ? (L > 0 ? tiles_of(L, p.ql, p.window_left) : 0) : (L + kTile - 1) / kTile;
-  wave_stamp_after(p, 8, n);
-  incl = wave_scan_incl(n);
-  excl = incl - n;
-  len = L;
-  return __builtin_amdgcn_readlane(incl, 63);
+// loads the lengths itself, kPer consecutive sequences per lane, and scans the
+// tile counts with DPP (wave_tile_scan), so no wave waits on a barrier or an
+// LDS round trip before it looks for its range's first sequence. One sequence
+// per lane up to 64 sequences, four up to 256: the four-per-lane scan costs
+// 0.2 us more per call at B <= 64 (measured on MI355X), so each batch size
+// takes the smaller one. kWaveScan template arguments: 0 (the LDS scan), 1, 4.
+constexpr int kWaveScanMax1 = 64;
+constexpr int kWaveScanMax = 4 * 64;
+inline int wave_scan_per_lane(int batch) {
+  return batch <= kWaveScanMax1 ? 1 : batch <= kWaveScanMax ? 4 : 0;
 }
 
-// zero_empty for the wave-local scan: the tile count of sequence b is lane b's
-// incl - excl (every wave holds the whole scan).
-template <int HD, int kThreads>
-__device__ __forceinline__ void zero_empty_wave(const DecodeParams &p, int tiles) {
+// The wave-local scan state. Lane l holds sequences b = kPer * l + j (j <
+// kPer): the clamped lengths len0.., the exclusive tile prefix sums pre0..
+// (S_b), and incl = S_{b+1} of its last one. Sequences past the batch count
+// length 0, so their S is the tile total. Every query takes a wave-uniform
+// sequence b < B. Named fields rather than arrays: an array indexed by j is
+// kept in memory (private, or LDS by promotion), not in registers.
+template <int kPer>
+struct WaveScan;
+
+template <>
+struct WaveScan<1> {
+  int len0 = 0, pre0 = 0, incl = 0;
+  __device__ __forceinline__ int start(int b) const { return __builtin_amdgcn_readlane(pre0, b); }
+  __device__ __forceinline__ int end(int b) const { return __builtin_amdgcn_readlane(incl, b); }
+  __device__ __forceinline__ int length(int b) const { return __builtin_amdgcn_readlane(len0, b); }
+  // The sequence holding tile t (0 <= t < tile total): the largest b < B with
+  // S_b <= t; the lanes that pass form a prefix (S is nondecreasing).
+  __device__ __forceinline__ int find(int t, int B) const {
+    const int lane = threadIdx.x & 63;
+    return __builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < B && pre0 <= t)) - 1;
+  }
+};
+
+template <>
+struct WaveScan<4> {
+  int len0 = 0, len1 = 0, len2 = 0, len3 = 0;
+  int pre0 = 0, pre1 = 0, pre2 = 0, pre3 = 0;
+  int incl = 0;
+
+  __device__ __forceinline__ static int sel(int j, int a0, int a1, int a2, int a3) {
+    return j == 0 ? a0 : j == 1 ? a1 : j == 2 ? a2 : a3;
+  }
+  __device__ __forceinline__ int start(int b) const {
+    return __builtin_amdgcn_readlane(sel(b & 3, pre0, pre1, pre2, pre3), b >> 2);
+  }
+  __device__ __forceinline__ int end(int b) const {
+    return __builtin_amdgcn_readlane(sel(b & 3, pre1, pre2, pre3, incl), b >> 2);
+  }
+  __device__ __forceinline__ int length(int b) const {
+    return __builtin_amdgcn_readlane(sel(b & 3, len0, len1, len2, len3), b >> 2);
+  }
+  // As above: the last lane whose first S passes holds b, and of its own S
+  // those that pass form a prefix too (entries past the batch hold the total,
+  // which none do).
+  __device__ __forceinline__ int find(int t, int B) const {
+    const int lane = threadIdx.x & 63;
+    const int l =
+        __builtin_popcountll(__builtin_amdgcn_ballot_w64(4 * lane < B && pre0 <= t)) - 1;
+    const int j = (__builtin_amdgcn_readlane(pre1, l) <= t ? 1 : 0) +
+                  (__builtin_amdgcn_readlane(pre2, l) <= t ? 1 : 0) +
+                  (__builtin_amdgcn_readlane(pre3, l) <= t ? 1 : 0);
+    return 4 * l + j;
+  }
+};
+
+// Clamped length of sequence b (0 past the batch), and the tile count of a length.
+__device__ __forceinline__ int clamp_len(const DecodeParams &p, int raw, int b, int B) {
+  int L = raw + p.seqlen_add;
+  L = L < 0 ? 0 : (L > p.max_len ? p.max_len : L);
+  return b < B ? L : 0;
+}
+template <bool kWindow>
+__device__ __forceinline__ int tile_count(const DecodeParams &p, int L) {
+  return kWindow ? (L > 0 ? tiles_of(L, p.ql, p.window_left) : 0) : (L + kTile - 1) / kTile;
+}
+
+// Fills `w` for the batch and returns the tile total. The length loads need
+// only the preloaded leading arguments, so they are issued (together) before
+// any wait on the parameter struct.
+template <bool kWindow>
+__device__ __forceinline__ int wave_tile_scan(const DecodeParams &p, const int32_t *seqlens, int B,
+                                              WaveScan<1> &w) {
+  const int b = threadIdx.x & 63;
+  w.len0 = clamp_len(p, as_const(seqlens)[b < B ? b : B - 1], b, B);
+  const int n = tile_count<kWindow>(p, w.len0);
+  wave_stamp_after(p, 8, n);
+  w.incl = wave_scan_incl(n);
+  w.pre0 = w.incl - n;
+  return __builtin_amdgcn_readlane(w.incl, 63);
+}
+template <bool kWindow>
+__device__ __forceinline__ int wave_tile_scan(const DecodeParams &p, const int32_t *seqlens, int B,
+                                              WaveScan<4> &w) {
+  const int b0 = 4 * (threadIdx.x & 63);
+  const int r0 = as_const(seqlens)[b0 < B ? b0 : B - 1];
+  const int r1 = as_const(seqlens)[b0 + 1 < B ? b0 + 1 : B - 1];
+  const int r2 = as_const(seqlens)[b0 + 2 < B ? b0 + 2 : B - 1];
+  const int r3 = as_const(seqlens)[b0 + 3 < B ? b0 + 3 : B - 1];
+  w.len0 = clamp_len(p, r0, b0, B);
+  w.len1 = clamp_len(p, r1, b0 + 1, B);
+  w.len2 = clamp_len(p, r2, b0 + 2, B);
+  w.len3 = clamp_len(p, r3, b0 + 3, B);
+  const int n0 = tile_count<kWindow>(p, w.len0), n1 = tile_count<kWindow>(p, w.len1);
+  const int n2 = tile_count<kWindow>(p, w.len2), n3 = tile_count<kWindow>(p, w.len3);
+  const int run = n0 + n1 + n2 + n3;  // this lane's tiles
+  wave_stamp_after(p, 8, run);
+  w.incl = wave_scan_incl(run);
+  w.pre0 = w.incl - run;
+  w.pre1 = w.pre0 + n0;
+  w.pre2 = w.pre1 + n1;
+  w.pre3 = w.pre2 + n2;
+  return __builtin_amdgcn_readlane(w.incl, 63);
+}
+
+// zero_empty for the wave-local scan (every wave holds the whole scan).
+template <int HD, int kThreads, int kPer>
+__device__ __forceinline__ void zero_empty_wave(const DecodeParams &p, const WaveScan<kPer> &w) {
   const int kv0 = blockIdx.x * p.heads_per_wg;
   const int kv1 = min(kv0 + p.heads_per_wg, p.hkv);
   const int nh = (kv1 - kv0) * p.gq;
   constexpr int F = HD / 4;  // 8-byte pieces per head row
   for (int b = blockIdx.y; b < p.batch; b += gridDim.y) {
-    if (__builtin_amdgcn_readlane(tiles, b) != 0) continue;
+    if (w.end(b) != w.start(b)) continue;
     char *row = p.out + b * p.o_sb + (int64_t)kv0 * p.gq * p.o_sh;
     for (int i = threadIdx.x; i < p.ql * nh * F; i += kThreads) {
       const int t = i / (nh * F), j = i % (nh * F);
@@ -617,6 +706,23 @@ __device__ __forceinline__ void zero_empty_wave(const DecodeParams &p, int tiles
           make_uint2(0u, 0u);
     }
   }
+}
+
+// The prefix sums s[0..B] into the workspace (workgroup (0, 0), first wave).
+__device__ __forceinline__ void store_prefix_wave(const DecodeParams &p, const WaveScan<1> &w,
+                                                  int B, int NT) {
+  const int b = threadIdx.x & 63;
+  if (b < B) p.ws_s[b] = w.pre0;
+  if (b == 0) p.ws_s[B] = NT;
+}
+__device__ __forceinline__ void store_prefix_wave(const DecodeParams &p, const WaveScan<4> &w,
+                                                  int B, int NT) {
+  const int b0 = 4 * (threadIdx.x & 63);
+  if (b0 < B) p.ws_s[b0] = w.pre0;
+  if (b0 + 1 < B) p.ws_s[b0 + 1] = w.pre1;
+  if (b0 + 2 < B) p.ws_s[b0 + 2] = w.pre2;
+  if (b0 + 3 < B) p.ws_s[b0 + 3] = w.pre3;
+  if (b0 == 0) p.ws_s[B] = NT;
 }
 
 // Sum / max over the 4 DPP rows of the wave (lanes l, l^16, l^32, l^48); every
@@ -677,12 +783,12 @@ struct Tile {
 // only XORs the words it loaded into the returned value, with no attention
 // math and no output; other instantiations return 0.
 template <int HD, int HR, typename T, bool kF8, bool kLanePages, int NBUF, bool kExtras,
-          bool kSeq, bool kBalance = false, bool kProbe = false, bool kWaveLocal = false,
+          bool kSeq, bool kBalance = false, bool kProbe = false, int kWaveLocal = 0,
           int kValuG = 0>
 __device__ __forceinline__ uint32_t run_range(const DecodeParams &p, const int32_t *s_tiles,
                                               int kvh, int rr, int lo, int hi, int stride,
                                               float *lds_o, float *lds_lse, int pg_first = 0,
-                                              int wl_len = 0, int wl_excl = 0, int wl_incl = 0) {
+                                              WaveScan<kWaveLocal == 4 ? 4 : 1> wsc = {}) {
   const int tstep = kSeq ? stride : 1;  // tile index step between the wave's tiles
   using E = Elem<T>;
   constexpr int NCH = HD / 32;               // MFMA steps over the head dim
@@ -763,15 +869,13 @@ __device__ __forceinline__ uint32_t run_range(const DecodeParams &p, const int32
   // sequence starts at its tile 0, so the first page id does not wait for the
   // length.
   int pb = 0, p_start = 0, p_end = hi;
-  // kWaveLocal (split kernel, B <= kWaveScanMax): the wave-local scan, lane b
-  // holding S_b = wl_excl, S_{b+1} = wl_incl and the length wl_len; s_tiles
-  // is not read.
-  constexpr bool wave_local = kWaveLocal && !kSeq;
+  // kWaveLocal (split kernel, 1 or 4 sequences per lane): the wave-local scan wsc
+  // gives the prefix sums and lengths; s_tiles is not read.
+  constexpr bool wave_local = kWaveLocal != 0 && !kSeq;
   if constexpr (wave_local) {
-    const int c = __builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < B && wl_excl <= lo));
-    pb = c - 1;
-    p_start = __builtin_amdgcn_readlane(wl_excl, pb);
-    p_end = __builtin_amdgcn_readlane(wl_incl, pb);
+    pb = wsc.find(lo, B);
+    p_start = wsc.start(pb);
+    p_end = wsc.end(pb);
     wave_stamp_after(p, 9, pb);
   } else if constexpr (!kSeq) {
     int a = 0, n = B;  // s[a] <= lo < s[a + n]
@@ -806,8 +910,7 @@ __device__ __forceinline__ uint32_t run_range(const DecodeParams &p, const int32
     pg_first = p_bt[min((lo - p_start) * kTile, p.max_len - 1) >> p.ps_log2];
     __builtin_amdgcn_sched_barrier(0);
   }
-  int p_len = wave_local ? __builtin_amdgcn_readlane(wl_len, pb)
-                         : seq_len_of(p.seqlens, pb, p.seqlen_add, p.max_len);
+  int p_len = wave_local ? wsc.length(pb) : seq_len_of(p.seqlens, pb, p.seqlen_add, p.max_len);
   int p_first = kExtras ? first_tile_of(p_len, p.ql, p.window_left) : 0;  // tile at p_start
 
   // Per-lane page ids are computed into a local array and copied to `lpg` at
@@ -839,10 +942,9 @@ __device__ __forceinline__ uint32_t run_range(const DecodeParams &p, const int32
         do {
           ++pb;
           p_start = p_end;
-          p_end = wave_local ? __builtin_amdgcn_readlane(wl_incl, pb) : rfl(s_tiles[pb + 1]);
+          p_end = wave_local ? wsc.end(pb) : rfl(s_tiles[pb + 1]);
         } while (t >= p_end);
-        p_len = wave_local ? __builtin_amdgcn_readlane(wl_len, pb)
-                           : seq_len_of(p.seqlens, pb, p.seqlen_add, p.max_len);
+        p_len = wave_local ? wsc.length(pb) : seq_len_of(p.seqlens, pb, p.seqlen_add, p.max_len);
         p_first = kExtras ? first_tile_of(p_len, p.ql, p.window_left) : 0;
         p_bt = as_const(p.bt + (int64_t)pb * p.bt_stride);
       }
@@ -1276,7 +1378,7 @@ __device__ __forceinline__ uint32_t run_range(const DecodeParams &p, const int32
 // kExtras: the call has a sliding window, soft-capping, ALiBi or sinks (the host
 // picks the instantiation; without them the kernel is the plain one).
 template <int HD, int HR, typename T, bool kF8, bool kLanePages, int NBUF, int WAVES,
-          bool kExtras, bool kWaveScan, int kValuG>
+          bool kExtras, int kWaveScan, int kValuG>
 __global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(const int32_t *seqlens,
                                                                         int batch,
                                                                         DecodeParams p) {
@@ -1286,15 +1388,14 @@ __global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(const int3
 
   const unsigned long long t_entry = wave_clock();
   const int B = batch;
-  // kWaveScan: the launcher's choice for B <= kWaveScanMax.
-  int wl_len = 0, wl_excl = 0, wl_incl = 0, NT;
-  if constexpr (kWaveScan) {
-    NT = rfl(wave_tile_scan<kExtras>(p, seqlens, B, wl_len, wl_excl, wl_incl));
-    zero_empty_wave<HD, kThreads>(p, wl_incl - wl_excl);
-    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64) {
-      if ((int)threadIdx.x < B) p.ws_s[threadIdx.x] = wl_excl;
-      if (threadIdx.x == 0) p.ws_s[B] = NT;
-    }
+  // kWaveScan: the launcher's choice, sequences per lane of the wave-local
+  // scan (wave_scan_per_lane), or 0 for the LDS scan.
+  WaveScan<kWaveScan == 4 ? 4 : 1> wsc;
+  int NT;
+  if constexpr (kWaveScan != 0) {
+    NT = rfl(wave_tile_scan<kExtras>(p, seqlens, B, wsc));
+    zero_empty_wave<HD, kThreads>(p, wsc);
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64) store_prefix_wave(p, wsc, B, NT);
   } else {
     NT = rfl(tile_prefix<kThreads, kExtras>(p, seqlens, B, s_tiles, s_wave_tot));
     zero_empty<HD, kThreads>(p, s_tiles);
@@ -1314,7 +1415,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(const int3
   wave_stamp(p, 0, t_entry);
   wave_stamp(p, 1, wave_clock());
   run_range<HD, HR, T, kF8, kLanePages, NBUF, kExtras, false, WAVES == 8, false, kWaveScan,
-            kValuG>(p, s_tiles, kvh, rr, lo, hi, 1, nullptr, nullptr, 0, wl_len, wl_excl, wl_incl);
+            kValuG>(p, s_tiles, kvh, rr, lo, hi, 1, nullptr, nullptr, 0, wsc);
   wave_stamp(p, 3, wave_clock());
   wave_stamp(p, 4, hi - lo);
   wave_stamp(p, 5, 1);
@@ -1327,16 +1428,17 @@ __global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(const int3
 // no attention math: each lane XORs the words it loads and writes that to
 // sink[(kvh * num_ranges + rr) * 64 + lane]. Its time is the ceiling the tile loop's
 // access pattern allows; it writes no output, workspace or prefix sums.
-template <int HD, typename T, int NBUF, int WAVES, bool kWaveScan>
+template <int HD, typename T, int NBUF, int WAVES, int kWaveScan>
 __global__ __launch_bounds__(WAVES * 64, 1) void stream_probe_kernel(const int32_t *seqlens,
                                                                        int batch, DecodeParams p,
                                                                        uint32_t *sink) {
   constexpr int kThreads = WAVES * 64;
   extern __shared__ int32_t s_tiles[];  // [B + 1]
   __shared__ int s_wave_tot[WAVES];
-  int wl_len = 0, wl_excl = 0, wl_incl = 0, NT;
-  if constexpr (kWaveScan)
-    NT = rfl(wave_tile_scan<false>(p, seqlens, batch, wl_len, wl_excl, wl_incl));
+  WaveScan<kWaveScan == 4 ? 4 : 1> wsc;
+  int NT;
+  if constexpr (kWaveScan != 0)
+    NT = rfl(wave_tile_scan<false>(p, seqlens, batch, wsc));
   else
     NT = rfl(tile_prefix<kThreads, false>(p, seqlens, batch, s_tiles, s_wave_tot));
   const int wave = rfl(threadIdx.x >> 6);
@@ -1349,7 +1451,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void stream_probe_kernel(const int32
   const int lo = range_lo(rr, R, NT), hi = range_lo(rr + 1, R, NT);
   const uint32_t x =
       run_range<HD, 1, T, false, false, NBUF, false, false, WAVES == 8, true, kWaveScan>(
-          p, s_tiles, kvh, rr, lo, hi, 1, nullptr, nullptr, 0, wl_len, wl_excl, wl_incl);
+          p, s_tiles, kvh, rr, lo, hi, 1, nullptr, nullptr, 0, wsc);
   sink[((int64_t)kvh * p.num_ranges + rr) * 64 + (threadIdx.x & 63)] = x;
 }
 
@@ -1609,37 +1711,53 @@ constexpr int kNbuf = kRowBytes<HD, kF8> <= 64 ? 4 : kRowBytes<HD, kF8> <= 128 ?
 // Rows of the MFMA layout that hold used columns (4 columns per row).
 inline int head_rows(int cols) { return cols <= 4 ? 1 : cols <= 8 ? 2 : 4; }
 
-template <int HD, int HR, typename T, bool kF8, int WAVES, bool kExtras, bool kWaveScan,
+template <int HD, int HR, typename T, bool kF8, int WAVES, bool kExtras, int kWaveScan,
           int kValuG>
-static void launch_partial_s(const DecodeParams &p, const Grid &g, hipStream_t st) {
+static int launch_partial_s(const DecodeParams &p, const Grid &g, hipStream_t st) {
   dim3 grid(g.gx, g.gy);
   // The wave-local scan keeps nothing in LDS.
   const size_t lds = kWaveScan ? 0 : (size_t)(p.batch + 1) * sizeof(int32_t);
-  if (p.ps_log2 >= 4)
+  if (p.ps_log2 >= 4) {
     hipLaunchKernelGGL((split_partial_kernel<HD, HR, T, kF8, false, kNbuf<HD, kF8>, WAVES, kExtras,
                                              kWaveScan, kValuG>),
                        grid, dim3(WAVES * 64), lds, st, p.seqlens, p.batch, p);
-  else  // per-lane page ids: QK stays on the matrix cores
-    hipLaunchKernelGGL(
-        (split_partial_kernel<HD, HR, T, kF8, true, 2, WAVES, kExtras, kWaveScan, 0>), grid,
-        dim3(WAVES * 64), lds, st, p.seqlens, p.batch, p);
+  } else {  // per-lane page ids: QK stays on the matrix cores
+    if constexpr (kWaveScan == 4)
+      return MXFA_EUNSUPPORTED;  // not instantiated (plain_call)
+    else
+      hipLaunchKernelGGL(
+          (split_partial_kernel<HD, HR, T, kF8, true, 2, WAVES, kExtras, kWaveScan, 0>), grid,
+          dim3(WAVES * 64), lds, st, p.seqlens, p.batch, p);
+  }
+  return hipGetLastError() == hipSuccess ? MXFA_OK : MXFA_ELAUNCH;
 }
 
-// kWaveScan (the wave-local tile scan) is the caller's choice, batch <=
-// kWaveScanMax; the two halves compile in separate units.
-template <int HD, int HR, typename T, bool kF8, int WAVES, bool kWaveScan, int kValuG>
+// A call with no window, cap, sinks or ALiBi on page-uniform tiles: the only
+// calls the four-sequences-per-lane scan is built for (the others, past 64
+// sequences, keep the LDS scan), so its instantiations stay few.
+inline bool plain_call(const DecodeParams &p) {
+  return p.window_left < 0 && !(p.softcap > 0.f) && !p.sinks && !p.alibi && p.ps_log2 >= 4;
+}
+
+// kWaveScan (the wave-local tile scan, 1 or 4 sequences per lane, or 0) is
+// the caller's choice (wave_scan_per_lane, plain_call); the three compile in
+// separate units.
+template <int HD, int HR, typename T, bool kF8, int WAVES, int kWaveScan, int kValuG>
 static int launch_partial_w(const DecodeParams &p, const Grid &g, hipStream_t st) {
-  if (p.window_left >= 0 || p.softcap > 0.f || p.sinks || p.alibi)
-    launch_partial_s<HD, HR, T, kF8, WAVES, true, kWaveScan, kValuG>(p, g, st);
-  else
-    launch_partial_s<HD, HR, T, kF8, WAVES, false, kWaveScan, kValuG>(p, g, st);
-  return hipGetLastError() == hipSuccess ? MXFA_OK : MXFA_ELAUNCH;
+  const bool extras = p.window_left >= 0 || p.softcap > 0.f || p.sinks || p.alibi;
+  if constexpr (kWaveScan == 4) {
+    if (extras) return MXFA_EUNSUPPORTED;  // not instantiated (plain_call)
+    return launch_partial_s<HD, HR, T, kF8, WAVES, false, kWaveScan, kValuG>(p, g, st);
+  } else {
+    return extras ? launch_partial_s<HD, HR, T, kF8, WAVES, true, kWaveScan, kValuG>(p, g, st)
+                  : launch_partial_s<HD, HR, T, kF8, WAVES, false, kWaveScan, kValuG>(p, g, st);
+  }
 }
 
 // The kernel is the grid's wave count; a grid the instantiations cannot run
 // (more waves than the row size has, or its heads and sub-ranges past the
 // waves) is refused: its extra kv heads would go uncomputed.
-template <int HD, int HR, typename T, bool kF8, bool kWaveScan, int kValuG = 0>
+template <int HD, int HR, typename T, bool kF8, int kWaveScan, int kValuG = 0>
 static int launch_partial_t(const DecodeParams &p, const Grid &g, hipStream_t st) {
   if (g.heads_per_wg * g.subs > g.waves) return MXFA_ELAUNCH;
   if constexpr (kMaxWaves<HD, kF8> == 8) {
@@ -1674,7 +1792,7 @@ inline int valu_qk_columns(int cols, int hd) {
   return 0;
 }
 
-template <int HD, typename T, bool kF8, bool kWaveScan>
+template <int HD, typename T, bool kF8, int kWaveScan>
 static int launch_partial_hr(const DecodeParams &p, const Grid &g, hipStream_t st) {
   const int cols = p.gq * p.ql;
   switch (head_rows(cols)) {
@@ -1698,9 +1816,9 @@ static int launch_partial_hr(const DecodeParams &p, const Grid &g, hipStream_t s
 }
 
 // Partial kernel for one head dim: dtype of q/out (MXFA_DTYPE_F16/BF16), fp8
-// caches or caches of that dtype; kWaveScan for batches of up to
-// kWaveScanMax sequences (the caller's choice).
-template <int HD, bool kWaveScan>
+// caches or caches of that dtype; kWaveScan the sequences per lane of the
+// wave-local scan, or 0 (the caller's choice).
+template <int HD, int kWaveScan>
 int launch_partial_hd(const DecodeParams &p, const Grid &g, int dtype, bool fp8,
                       hipStream_t st) {
   if (dtype == MXFA_DTYPE_BF16)
@@ -1773,7 +1891,7 @@ int launch_seq_hd(const DecodeParams &p, int dtype, bool fp8, hipStream_t st) {
 
 // Streaming probe launch (16-bit caches, page size >= 16): the decode
 // kernel's grid and waves; nbuf 0 takes the decode kernel's register sets.
-template <int HD, int WAVES, bool kWaveScan>
+template <int HD, int WAVES, int kWaveScan>
 static int launch_probe_s(const DecodeParams &p, const Grid &g, int nbuf, uint32_t *sink,
                           hipStream_t st) {
   dim3 grid(g.gx, g.gy);
@@ -1799,8 +1917,11 @@ static int launch_probe_s(const DecodeParams &p, const Grid &g, int nbuf, uint32
 template <int HD, int WAVES>
 static int launch_probe_w(const DecodeParams &p, const Grid &g, int nbuf, uint32_t *sink,
                           hipStream_t st) {
-  return p.batch <= kWaveScanMax ? launch_probe_s<HD, WAVES, true>(p, g, nbuf, sink, st)
-                                 : launch_probe_s<HD, WAVES, false>(p, g, nbuf, sink, st);
+  switch (wave_scan_per_lane(p.batch)) {
+    case 1: return launch_probe_s<HD, WAVES, 1>(p, g, nbuf, sink, st);
+    case 4: return launch_probe_s<HD, WAVES, 4>(p, g, nbuf, sink, st);
+    default: return launch_probe_s<HD, WAVES, 0>(p, g, nbuf, sink, st);
+  }
 }
 
 template <int HD>

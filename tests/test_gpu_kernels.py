@@ -461,7 +461,8 @@ def test_maximum_batch(device):
         assert max_err(run_native(b, **kw), expected) <= TOL[torch.float16]
 
 
-@pytest.mark.parametrize("batch", [63, 64, 65, 257, 513, 1024, 4032, 4033, 4353])
+@pytest.mark.parametrize("batch", [63, 64, 65, 127, 128, 129, 255, 256, 257, 513, 1024, 4032,
+                                   4033, 4353])
 @pytest.mark.parametrize("kv_heads,head_dim,dtype", [(2, 128, torch.bfloat16),
                                                      (8, 64, torch.float16)],
                          ids=["4wave", "8wave"])
@@ -473,8 +474,10 @@ def test_batches_past_one_length_per_thread(device, batch, kv_heads, head_dim, d
     # needs two rounds of eight per thread in the four-wave kernel. The
     # search for a range's first sequence settles up to 63 candidates in one
     # round: 63, 64 and 65 sequences sit around that, 4032 and 4033 around
-    # the step of 63 that still leaves two rounds. A window takes the
-    # extended instantiation's tile count.
+    # the step of 63 that still leaves two rounds. Up to 256 sequences the
+    # split kernel scans inside each wave instead, four sequences per lane:
+    # 127-129 fill lanes 31-32 partly and wholly, 255-257 sit around its end.
+    # A window takes the extended instantiation's tile count.
     g = torch.Generator().manual_seed(batch + head_dim)
     lengths = torch.randint(0, 48, (batch,), generator=g)
     lengths[batch // 3] = 0

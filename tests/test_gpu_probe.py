@@ -59,11 +59,15 @@ def expected_per_kv_head(b, num_splits: int) -> np.ndarray:
 
 CASES = [
     # (batch, q_heads, kv_heads, head_dim, page_size, max_len): 4-wave 256-byte
-    # rows, 4-wave and 8-wave 128-byte rows, two sub-ranges per workgroup.
+    # rows, 4-wave and 8-wave 128-byte rows, two sub-ranges per workgroup; the
+    # wave-local scan with four sequences per lane (130) and the LDS scan past
+    # its 256 (300).
     (7, 32, 8, 128, 16, 3000),
     (9, 32, 4, 64, 16, 4000),
     (6, 16, 8, 64, 64, 2500),
     (5, 8, 2, 128, 32, 1500),
+    (130, 16, 8, 64, 16, 600),
+    (300, 8, 2, 128, 16, 400),
 ]
 
 
