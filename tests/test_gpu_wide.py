@@ -806,3 +806,34 @@ def test_graph_replays_of_a_chunked_causal_query_follow_the_lengths(device):
         b.cache_seqlens = lens.clone()
         assert max_err(out, port_expected(b, True, -1, None, 0.0, slopes)) \
             <= TOL[torch.bfloat16], (i, new)
+
+
+# Batches of 65 to 256 sequences take the wave-local tile scan with four
+# sequences per lane on plain calls (and the LDS scan with a window, cap,
+# sinks or ALiBi): every head dim, several GQ, both 16-bit types and fp8,
+# with empty sequences at lane edges and inside a lane, against the fp64
+# oracle, at the heuristic's split count and a few others.
+@pytest.mark.parametrize("batch", [65, 130, 256])
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("gq,dtype,fp8", [(1, torch.bfloat16, False), (4, torch.float16, False),
+                                          (8, torch.bfloat16, False), (4, torch.bfloat16, True)],
+                         ids=["gq1-bf16", "gq4-f16", "gq8-bf16", "gq4-fp8"])
+def test_four_sequences_per_lane_scan(device, batch, head_dim, gq, dtype, fp8):
+    g = torch.Generator().manual_seed(batch * 7 + head_dim + gq)
+    lengths = torch.randint(1, 90, (batch,), generator=g)
+    lengths[[0, 3, 4, batch // 2, batch - 1]] = 0  # lane 0's first and 1's first, mid, last
+    lengths[5] = 16  # a sequence ending on a tile edge
+    b = make_paged_batch(batch, 2 * gq, 2, head_dim, dtype, lengths, seed=batch + gq).to(device)
+    if fp8:
+        k8, v8 = fp8_caches(b, device)
+        expected = fp8_expected(b, k8, v8, 1.0, 1.0)
+    else:
+        k8, v8 = b.k_cache, b.v_cache
+        expected = f64_expected(b)
+    empty = b.cache_seqlens.cpu() == 0
+    for ns in (None, 3, 100, 1000):
+        kw = {} if ns is None else dict(num_splits=ns)
+        got = decode(b, k8, v8, **kw)
+        assert torch.isfinite(got.float()).all()
+        assert max_err(got, expected) <= TOL[dtype], (ns, max_err(got, expected))
+        assert not got.cpu()[empty].any(), ns
