@@ -262,6 +262,7 @@ static DecodeParams make_params(const SplitArgs &a, const Grid &g) {
   p.max_len = a.btw * a.ps;
   p.num_pages = a.num_pages;
   p.num_ranges = a.num_splits;
+  p.grid_y = g.gy;
 #ifdef MXFA_WAVE_STAMPS
   p.stamps = g_wave_stamps;
 #endif

@@ -134,6 +134,8 @@ struct DecodeParams {
   int max_len;  // block_table_width * page_size
   int num_pages;
   int num_ranges;
+  int grid_y;  // workgroups along y of the split kernel's grid (gridDim.y, read from here
+               // with the other fields rather than from the dispatch's own arguments)
 #ifdef MXFA_WAVE_STAMPS
   unsigned long long *stamps;  // profiling builds: kStampWords words per wave (see wave_stamp)
 #endif
@@ -554,23 +556,28 @@ __device__ __forceinline__ int tile_prefix(const DecodeParams &p, const int32_t 
   return total;
 }
 
+// Zero output rows of sequence b for this workgroup's kv heads [kv0, kv1):
+// thread i writes 8-byte piece i % F of rows i / F, i / F + kThreads / F, ...
+// of every query token (F = HD / 4 pieces per row; no run-time division, so
+// nothing is set up before the caller knows a sequence is empty).
+template <int HD, int kThreads>
+__device__ __forceinline__ void zero_rows(const DecodeParams &p, int b, int kv0, int nh) {
+  constexpr int F = HD / 4;
+  static_assert(kThreads % F == 0, "whole rows per pass");
+  char *row = p.out + b * p.o_sb + (int64_t)kv0 * p.gq * p.o_sh + (threadIdx.x % F) * 8;
+  for (int t = 0; t < p.ql; ++t)
+    for (int h = threadIdx.x / F; h < nh; h += kThreads / F)
+      *reinterpret_cast<uint2 *>(row + t * p.o_st + h * p.o_sh) = make_uint2(0u, 0u);
+}
+
 // Empty sequences (no tiles) get zero output; sequence b is cleared by the
-// workgroups with blockIdx.y == b % gridDim.y, each for its own kv heads.
+// workgroups with blockIdx.y == b % grid_y, each for its own kv heads.
 template <int HD, int kThreads>
 __device__ __forceinline__ void zero_empty(const DecodeParams &p, const int32_t *s) {
   const int kv0 = blockIdx.x * p.heads_per_wg;
-  const int kv1 = min(kv0 + p.heads_per_wg, p.hkv);
-  const int nh = (kv1 - kv0) * p.gq;
-  constexpr int F = HD / 4;  // 8-byte pieces per head row
-  for (int b = blockIdx.y; b < p.batch; b += gridDim.y) {
-    if (s[b + 1] != s[b]) continue;
-    char *row = p.out + b * p.o_sb + (int64_t)kv0 * p.gq * p.o_sh;
-    for (int i = threadIdx.x; i < p.ql * nh * F; i += kThreads) {
-      const int t = i / (nh * F), j = i % (nh * F);
-      *reinterpret_cast<uint2 *>(row + t * p.o_st + (j / F) * p.o_sh + (j % F) * 8) =
-          make_uint2(0u, 0u);
-    }
-  }
+  const int nh = (min(kv0 + p.heads_per_wg, p.hkv) - kv0) * p.gq;
+  for (int b = blockIdx.y; b < p.batch; b += p.grid_y)
+    if (s[b + 1] == s[b]) zero_rows<HD, kThreads>(p, b, kv0, nh);
 }
 
 // Batches of up to kWaveScanMax sequences skip the LDS tile scan: every wave
@@ -694,18 +701,9 @@ __device__ __forceinline__ int wave_tile_scan(const DecodeParams &p, const int32
 template <int HD, int kThreads, int kPer>
 __device__ __forceinline__ void zero_empty_wave(const DecodeParams &p, const WaveScan<kPer> &w) {
   const int kv0 = blockIdx.x * p.heads_per_wg;
-  const int kv1 = min(kv0 + p.heads_per_wg, p.hkv);
-  const int nh = (kv1 - kv0) * p.gq;
-  constexpr int F = HD / 4;  // 8-byte pieces per head row
-  for (int b = blockIdx.y; b < p.batch; b += gridDim.y) {
-    if (w.end(b) != w.start(b)) continue;
-    char *row = p.out + b * p.o_sb + (int64_t)kv0 * p.gq * p.o_sh;
-    for (int i = threadIdx.x; i < p.ql * nh * F; i += kThreads) {
-      const int t = i / (nh * F), j = i % (nh * F);
-      *reinterpret_cast<uint2 *>(row + t * p.o_st + (j / F) * p.o_sh + (j % F) * 8) =
-          make_uint2(0u, 0u);
-    }
-  }
+  const int nh = (min(kv0 + p.heads_per_wg, p.hkv) - kv0) * p.gq;
+  for (int b = blockIdx.y; b < p.batch; b += p.grid_y)
+    if (w.end(b) == w.start(b)) zero_rows<HD, kThreads>(p, b, kv0, nh);
 }
 
 // The prefix sums s[0..B] into the workspace (workgroup (0, 0), first wave).
@@ -1395,7 +1393,6 @@ __global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(const int3
   if constexpr (kWaveScan != 0) {
     NT = rfl(wave_tile_scan<kExtras>(p, seqlens, B, wsc));
     zero_empty_wave<HD, kThreads>(p, wsc);
-    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64) store_prefix_wave(p, wsc, B, NT);
   } else {
     NT = rfl(tile_prefix<kThreads, kExtras>(p, seqlens, B, s_tiles, s_wave_tot));
     zero_empty<HD, kThreads>(p, s_tiles);
@@ -1416,6 +1413,12 @@ __global__ __launch_bounds__(WAVES * 64, 1) void split_partial_kernel(const int3
   wave_stamp(p, 1, wave_clock());
   run_range<HD, HR, T, kF8, kLanePages, NBUF, kExtras, false, WAVES == 8, false, kWaveScan,
             kValuG>(p, s_tiles, kvh, rr, lo, hi, 1, nullptr, nullptr, 0, wsc);
+  // The prefix sums for the combine, by the first wave of workgroup (0, 0)
+  // (which always has a range) once its own range is done: the pointer is
+  // read from the parameter block only here, off the prologue.
+  if constexpr (kWaveScan != 0) {
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64) store_prefix_wave(p, wsc, B, NT);
+  }
   wave_stamp(p, 3, wave_clock());
   wave_stamp(p, 4, hi - lo);
   wave_stamp(p, 5, 1);
