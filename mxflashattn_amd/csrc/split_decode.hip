@@ -270,7 +270,11 @@ static DecodeParams make_params(const SplitArgs &a, const Grid &g) {
 }
 
 static int launch_partial(const SplitArgs &a, hipStream_t st) {
-  const Grid g = grid_for(a.hkv, a.num_splits, waves_for(a.hd * (a.fp8 ? 1 : 2), a.hkv));
+  Grid g = grid_for(a.hkv, a.num_splits, waves_for(a.hd * (a.fp8 ? 1 : 2), a.hkv));
+  // The host's bound on tiles per range: every sequence at the table's
+  // capacity (the lengths are on the device).
+  const int64_t cap_tiles = ((int64_t)a.btw * a.ps + kTile - 1) / kTile;
+  g.short_ranges = (int64_t)a.batch * cap_tiles <= (int64_t)kShortRangeTiles * a.num_splits;
   const DecodeParams p = make_params(a, g);
   // The tile scan: inside each wave, one or four sequences per lane, or
   // through LDS; four per lane is built for plain calls only.

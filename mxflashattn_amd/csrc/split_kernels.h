@@ -145,6 +145,7 @@ struct DecodeParams {
 // heads_per_wg x subs are used (kv head, sub-range); gx x gy workgroups.
 struct Grid {
   int waves, heads_per_wg, subs, gx, gy;
+  bool short_ranges = false;  // host's bound on tiles per range <= kShortRangeTiles
 };
 
 struct CombineParams {
@@ -1711,6 +1712,19 @@ inline Grid grid_for(int hkv, int num_splits, int waves) {
 template <int HD, bool kF8>
 constexpr int kNbuf = kRowBytes<HD, kF8> <= 64 ? 4 : kRowBytes<HD, kF8> <= 128 ? 3 : 2;
 
+// Eight-wave workgroups of 128-byte rows (two waves per SIMD) take two
+// register sets instead of three when the host's bound on tiles per range is
+// small: the shorter pipeline fill and drain pay more than the third set's
+// bytes in flight there, and less over long ranges. Graph replays on MI355X,
+// three sets against two: config 3 (B 128, 8 tiles per range) 17.56 / 17.35
+// us, B 32 GQ4 HD64 with L <= 2048 19.59 / 19.14, the GQ4 HD64 cell (42 tiles)
+// 60.13 / 59.88, fp8 HD128 at config 2 (42 tiles) 61.65 / 61.37; the GQ2 HD64
+// cell (84 tiles) 108.62 / 109.19. Four-wave workgroups (one wave per SIMD)
+// keep three sets everywhere (GQ8 HD64 33.76 / 34.26 with two).
+constexpr int kShortRangeTiles = 64;
+template <int HD, bool kF8, int WAVES>
+constexpr bool kTwoSetsShort = kRowBytes<HD, kF8> == 128 && WAVES == 8;
+
 // Rows of the MFMA layout that hold used columns (4 columns per row).
 inline int head_rows(int cols) { return cols <= 4 ? 1 : cols <= 8 ? 2 : 4; }
 
@@ -1721,6 +1735,14 @@ static int launch_partial_s(const DecodeParams &p, const Grid &g, hipStream_t st
   // The wave-local scan keeps nothing in LDS.
   const size_t lds = kWaveScan ? 0 : (size_t)(p.batch + 1) * sizeof(int32_t);
   if (p.ps_log2 >= 4) {
+    if constexpr (kTwoSetsShort<HD, kF8, WAVES>) {
+      if (g.short_ranges) {
+        hipLaunchKernelGGL((split_partial_kernel<HD, HR, T, kF8, false, 2, WAVES, kExtras,
+                                                 kWaveScan, kValuG>),
+                           grid, dim3(WAVES * 64), lds, st, p.seqlens, p.batch, p);
+        return hipGetLastError() == hipSuccess ? MXFA_OK : MXFA_ELAUNCH;
+      }
+    }
     hipLaunchKernelGGL((split_partial_kernel<HD, HR, T, kF8, false, kNbuf<HD, kF8>, WAVES, kExtras,
                                              kWaveScan, kValuG>),
                        grid, dim3(WAVES * 64), lds, st, p.seqlens, p.batch, p);
