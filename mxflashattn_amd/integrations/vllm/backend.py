@@ -4,11 +4,16 @@ Every attention call through the plugin can record a small JSON event naming
 the path that served it. Events are kept in memory and, when
 MXFLASHATTN_DISPATCH_LOG (or a sibling of MXFLASHATTN_PLUGIN_IMPORT_LOG) names
 a file, appended to it as JSON lines; MXFLASHATTN_DISPATCH_SAMPLE=N keeps only
-every N-th line so the write cost stays off the hot path.
+every N-th line so the write cost stays off the hot path. The in-memory buffer
+keeps the most recent MXFLASHATTN_DISPATCH_EVENTS_MAX events (65,536 by
+default): a server records one per layer per step, which an unbounded list
+(the reference's) turns into a leak over a long run; the log file, when set,
+keeps every line.
 """
 
 from __future__ import annotations
 
+import collections
 import json
 import os
 import threading
@@ -17,7 +22,8 @@ import torch
 
 from ... import api
 
-DISPATCH_EVENTS: list[dict[str, str]] = []
+DISPATCH_EVENTS_MAX = int(os.getenv("MXFLASHATTN_DISPATCH_EVENTS_MAX", "65536") or 65536)
+DISPATCH_EVENTS: collections.deque[dict[str, str]] = collections.deque(maxlen=DISPATCH_EVENTS_MAX)
 _LOCK = threading.Lock()
 _JSON_CACHE: dict[tuple[tuple[str, str], ...], str] = {}
 _counter = 0

@@ -3,6 +3,7 @@ tests/test_vllm_official_split_fallback.py of the reference, for the parts that
 do not need vLLM installed): shape guards, the compat wrapper's hand-back,
 dispatch events and the backend registration result."""
 
+import collections
 import json
 
 import pytest
@@ -250,6 +251,22 @@ def test_dispatch_log_sampling(monkeypatch, tmp_path):
     lines = [json.loads(x) for x in log.read_text().splitlines()]
     assert [x["i"] for x in lines] == ["0", "3", "6"]
     assert len(backend.get_dispatch_events()) == 7
+
+
+def test_dispatch_event_buffer_keeps_the_most_recent(monkeypatch, tmp_path):
+    # One event per layer per step: the in-memory buffer is bounded (oldest
+    # dropped), while the log file, when set, keeps every line.
+    assert backend.DISPATCH_EVENTS.maxlen == backend.DISPATCH_EVENTS_MAX == 65536
+    log = tmp_path / "events.jsonl"
+    monkeypatch.setenv("MXFLASHATTN_DISPATCH_LOG", str(log))
+    monkeypatch.delenv("MXFLASHATTN_DISPATCH_SAMPLE", raising=False)
+    monkeypatch.setattr(backend, "DISPATCH_EVENTS", collections.deque(maxlen=4))
+    for i in range(10):
+        backend.record_event({"path": "mi355x_split_decode", "i": str(i)})
+    assert [e["i"] for e in backend.get_dispatch_events()] == ["6", "7", "8", "9"]
+    assert len(log.read_text().splitlines()) == 10
+    backend.clear_dispatch_events()
+    assert backend.get_dispatch_events() == []
 
 
 def test_plugin_import_log_names_the_dispatch_log(monkeypatch, tmp_path):
