@@ -137,6 +137,22 @@ def test_random_odd_kv_heads_sweep(device, seed):
              per_sequence=seed % 4 == 3, hkv_choices=(5, 6, 7, 9, 10, 12))
 
 
+# Batches of 65 to 256 sequences: the tile scan runs inside each wave with
+# four sequences per lane on plain calls with pages of at least 16 tokens, and
+# through LDS otherwise (a window, cap, sinks or ALiBi, or smaller pages).
+@pytest.mark.parametrize("seed", range(600, 630))
+def test_random_large_batch_sweep(device, seed):
+    run_case(device, seed, extended=seed % 3 == 1, large_batch=True)
+
+
+def redraw_large_batch(c: dict, seed: int) -> dict:
+    """The case redrawn with 65 to 256 mostly short sequences (empty ones among them)."""
+    r = random.Random(40_000 + seed)
+    batch = r.randint(65, 256)
+    lengths = [r.choice([0, 1, r.randint(2, 40), r.randint(40, 200)]) for _ in range(batch)]
+    return dict(c, batch=batch, lengths=lengths)
+
+
 def chunked(c: dict, seed: int) -> dict:
     """The case as a causal query past the kernel's 16 columns (GQ >= 2)."""
     r = random.Random(30_000 + seed)
@@ -146,8 +162,11 @@ def chunked(c: dict, seed: int) -> dict:
 
 
 def run_case(device, seed: int, extended: bool, chunked_query: bool = False,
-             per_sequence: bool = False, hkv_choices: tuple = (1, 2, 3, 4, 8)):
+             per_sequence: bool = False, hkv_choices: tuple = (1, 2, 3, 4, 8),
+             large_batch: bool = False):
     c = draw(seed, hkv_choices)
+    if large_batch:
+        c = redraw_large_batch(c, seed)
     if chunked_query:
         c = chunked(c, seed)
     if per_sequence:
