@@ -19,5 +19,8 @@ Modules:
 
 How each function is pinned (golden vectors, closed forms, invariants) is
 listed in tests/test_oracle.py; every function here has at least one check
-that a dropped term, swapped index or transposed operand would fail.
+that a dropped term, swapped index or transposed operand would fail. The
+golden vectors of the reference's own build (tests/golden/, written by
+tests/golden/make_golden.py from oracle/_ref) pin reference_port and the C
+oracle where the reference is absent (tests/test_golden.py).
 """
