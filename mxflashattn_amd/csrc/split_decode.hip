@@ -300,16 +300,23 @@ static int launch_partial(const SplitArgs &a, hipStream_t st) {
 // about num_splits / batch + 1 pieces; enough piece groups G (a power of two)
 // that they fold in one step of eight loads, then as many rows as fit in the
 // block's kCombineThreads / G chunk threads (at most the next power of two of
-// the rows per sequence).
-static int combine_heads_per_block(int batch, int hq, int hd, int num_splits) {
+// the rows per sequence). Where one row's chunks leave too few groups for
+// that (few sequences, many ranges), each row's chunks are split over
+// chunk_parts blocks.
+static void combine_shape(int batch, int hq, int hd, int num_splits, CombineParams &c) {
   const int ch = hd / 4;
   const int pieces = (num_splits + batch - 1) / batch + 1;
   int groups = 1;
   while (groups * ch < kCombineThreads && groups * 8 < pieces) groups *= 2;
   int h = kCombineThreads / (groups * ch);
   if (h < 1) h = 1;
+  // One head per block and still more than eight pieces per thread: split
+  // the head's chunks over more blocks, each with more piece groups.
+  int parts = 1;
+  while (h == 1 && parts < ch && kCombineThreads / (ch / parts) * 8 < pieces) parts *= 2;
   while (h > 1 && h / 2 >= hq) h /= 2;
-  return h;
+  c.heads_per_block = h;
+  c.chunk_parts = parts;
 }
 
 static int launch_combine(void *ws, void *out, const float *sinks, int64_t o_sb, int64_t o_st,
@@ -330,7 +337,7 @@ static int launch_combine(void *ws, void *out, const float *sinks, int64_t o_sb,
   c.gq = hq / hkv;
   c.ql = ql;
   c.num_ranges = ns;
-  c.heads_per_block = combine_heads_per_block(batch, hq * ql, hd, ns);
+  combine_shape(batch, hq * ql, hd, ns, c);
   c.sinks = sinks;
 #ifdef MXFA_WAVE_STAMPS
   c.stamps = g_wave_stamps ? g_wave_stamps + kStampCombineBase : nullptr;

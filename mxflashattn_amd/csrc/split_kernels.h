@@ -160,6 +160,7 @@ struct CombineParams {
   int ql;
   int num_ranges;
   int heads_per_block;  // a power of two; heads_per_block * HD / 4 <= kCombineThreads
+  int chunk_parts;      // a power of two <= HD / 4; heads_per_block is 1 when above 1
   const float *sinks;   // as DecodeParams::sinks
 #ifdef MXFA_WAVE_STAMPS
   unsigned long long *stamps;  // profiling builds: kStampCombineWords words per block
@@ -1475,19 +1476,22 @@ __device__ __forceinline__ void lse_fold(float &M, float &W, float4 &A, float m2
 }
 
 // LSE combine: one block of kCombineThreads per (sequence b, H consecutive
-// query heads), H = heads_per_block (host choice). The block's CB = H * HD/4
-// float4 chunks are split over G = kCombineThreads / CB piece groups: thread
-// (g, c) folds pieces ra+g, ra+g+G, ... of chunk c, eight loads in flight per
-// step; the G groups then merge through an LDS tree and the output is rounded
-// once. The fold order depends on H only (a host choice), never on timing.
-// Blocks whose sequence lies inside one range (written by the partial kernel)
-// or is empty (zero-filled there) leave at once.
+// query heads), H = heads_per_block (host choice), or, with X = chunk_parts > 1
+// (then H = 1), per (sequence, head, 1/X of the head's HD/4 float4 chunks).
+// The block's CB = H * HD/4 / X chunks are split over G = kCombineThreads / CB
+// piece groups: thread (g, c) folds pieces ra+g, ra+g+G, ... of chunk c, eight
+// loads in flight per step; the G groups then merge through an LDS tree and
+// the output is rounded once. Splitting a head's chunks over X blocks gives a
+// sequence of many pieces (few sequences, many ranges) X times the groups, so
+// its pieces come in one step. The fold order depends on H and X only (host
+// choices), never on timing. Blocks whose sequence lies inside one range
+// (written by the partial kernel) or is empty (zero-filled there) leave at once.
 constexpr int kCombineThreads = 256;
 
 template <int HD, typename T>
 __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(
     const int32_t *ws_s, const float *ws_o, const float *ws_lse, int batch, int nblk, int H,
-    int hq, int ql, int gq, int ns, CombineParams p) {
+    int X, int hq, int ql, int gq, int ns, CombineParams p) {
   using E = Elem<T>;
   constexpr int CH = HD / 4;  // float4 chunks per head
   constexpr int kUnroll = 8;
@@ -1495,14 +1499,16 @@ __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(
   // Everything up to the piece loads comes from the leading arguments (the
   // CombineParams fields of the same names, preloaded into SGPRs): the
   // prefix sums are read at once and the pieces right after them.
-  const int b = blockIdx.x / nblk;  // nblk = ceil(nv / H) blocks per sequence
+  const int b = blockIdx.x / nblk;  // nblk = ceil(nv / H) * X blocks per sequence
   const int NT = ws_s[batch];
   const int sb = ws_s[b], se = ws_s[b + 1];
-  const int CB = H * CH;
+  const int CC = CH / X;  // chunks of a head in this block
+  const int CB = H * CC;
   const int groups = kCombineThreads / CB;
   const int nv = hq * ql;  // (query token, head) rows per sequence
-  const int vh = (blockIdx.x % nblk) * H + (threadIdx.x % CB) / CH;
-  const int cc = threadIdx.x % CH;
+  const int hb = blockIdx.x % nblk;
+  const int vh = (hb / X) * H + (threadIdx.x % CB) / CC;
+  const int cc = (hb % X) * CC + threadIdx.x % CC;
   const int g = threadIdx.x / CB;
   block_stamp_after(p, 0, g);
   block_stamp_after(p, 1, NT + sb + se);
@@ -1962,17 +1968,21 @@ int launch_probe_hd(const DecodeParams &p, const Grid &g, int nbuf, uint32_t *si
 
 template <int HD>
 int launch_combine_hd(const CombineParams &c, int dtype, hipStream_t st) {
-  // One block per (sequence, heads_per_block rows of (query token, head)).
-  const int nblk = (c.hq * c.ql + c.heads_per_block - 1) / c.heads_per_block;
+  // One block per (sequence, heads_per_block rows of (query token, head),
+  // 1/chunk_parts of the head dim).
+  if (c.chunk_parts < 1 || (HD / 4) % c.chunk_parts || (c.chunk_parts > 1 && c.heads_per_block != 1))
+    return MXFA_ELAUNCH;
+  const int nblk =
+      (c.hq * c.ql + c.heads_per_block - 1) / c.heads_per_block * c.chunk_parts;
   dim3 grid(c.batch * nblk);
   if (dtype == MXFA_DTYPE_BF16)
     hipLaunchKernelGGL((split_combine_kernel<HD, BF16>), grid, dim3(kCombineThreads), 0, st,
-                       c.ws_s, c.ws_o, c.ws_lse, c.batch, nblk, c.heads_per_block, c.hq, c.ql,
-                       c.gq, c.num_ranges, c);
+                       c.ws_s, c.ws_o, c.ws_lse, c.batch, nblk, c.heads_per_block,
+                       c.chunk_parts, c.hq, c.ql, c.gq, c.num_ranges, c);
   else
     hipLaunchKernelGGL((split_combine_kernel<HD, F16>), grid, dim3(kCombineThreads), 0, st,
-                       c.ws_s, c.ws_o, c.ws_lse, c.batch, nblk, c.heads_per_block, c.hq, c.ql,
-                       c.gq, c.num_ranges, c);
+                       c.ws_s, c.ws_o, c.ws_lse, c.batch, nblk, c.heads_per_block,
+                       c.chunk_parts, c.hq, c.ql, c.gq, c.num_ranges, c);
   return hipGetLastError() == hipSuccess ? MXFA_OK : MXFA_ELAUNCH;
 }
 

@@ -391,6 +391,31 @@ def test_partial_then_combine_equals_one_launch(device):
     assert max_err(one[keep], oracle_out(sub)) <= TOL[torch.bfloat16]
 
 
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("lengths", [[40000], [20000, 7, 3000]], ids=["one", "three"])
+def test_few_sequences_many_ranges(device, head_dim, lengths):
+    # Few sequences over many ranges: hundreds to thousands of pieces per
+    # (sequence, head), so the combine splits each head's chunks over 1 to 16
+    # blocks to fold them in one step (or several, past that). Every split
+    # count against the oracle, and the two stages against one launch.
+    dtype = torch.float16 if head_dim == 128 else torch.bfloat16
+    batch = len(lengths)
+    b = make_paged_batch(batch, 8, 2, head_dim, dtype, torch.tensor(lengths),
+                         seed=70 + head_dim + batch).to(device)
+    expected = oracle_out(b)
+    for ns in (60, 100, 300, 700, 2000):
+        one = run_native(b, num_splits=ns)
+        assert max_err(one, expected) <= TOL[dtype], ns
+        ws = torch.empty(native.workspace_size(batch, 8, head_dim, ns), dtype=torch.uint8,
+                         device=device)
+        out = torch.full_like(b.q, float("nan"))
+        native.split_decode_partial(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens,
+                                    b.scale, out, ws, ns)
+        native.split_decode_combine(ws, out, 2, ns)
+        torch.cuda.synchronize()
+        assert torch.equal(out, one), ns
+
+
 @pytest.mark.parametrize("ns", [None, native.SPLITS_PER_SEQUENCE], ids=["split", "per_seq"])
 def test_graph_replays_match_eager(device, ns):
     # One decode call captured in a HIP graph (the workspace allocated by an
