@@ -160,7 +160,7 @@ struct CombineParams {
   int ql;
   int num_ranges;
   int heads_per_block;  // a power of two; heads_per_block * HD / 4 <= kCombineThreads
-  int chunk_parts;      // a power of two <= HD / 4; heads_per_block is 1 when above 1
+  int chunk_parts;      // a power of two <= HD / 32; heads_per_block is 1 when above 1
   const float *sinks;   // as DecodeParams::sinks
 #ifdef MXFA_WAVE_STAMPS
   unsigned long long *stamps;  // profiling builds: kStampCombineWords words per block
@@ -1970,7 +1970,7 @@ template <int HD>
 int launch_combine_hd(const CombineParams &c, int dtype, hipStream_t st) {
   // One block per (sequence, heads_per_block rows of (query token, head),
   // 1/chunk_parts of the head dim).
-  if (c.chunk_parts < 1 || (HD / 4) % c.chunk_parts || (c.chunk_parts > 1 && c.heads_per_block != 1))
+  if (c.chunk_parts < 1 || (HD / 32) % c.chunk_parts || (c.chunk_parts > 1 && c.heads_per_block != 1))
     return MXFA_ELAUNCH;
   const int nblk =
       (c.hq * c.ql + c.heads_per_block - 1) / c.heads_per_block * c.chunk_parts;

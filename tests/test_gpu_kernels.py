@@ -395,7 +395,7 @@ def test_partial_then_combine_equals_one_launch(device):
 @pytest.mark.parametrize("lengths", [[40000], [20000, 7, 3000]], ids=["one", "three"])
 def test_few_sequences_many_ranges(device, head_dim, lengths):
     # Few sequences over many ranges: hundreds to thousands of pieces per
-    # (sequence, head), so the combine splits each head's chunks over 1 to 16
+    # (sequence, head), so the combine splits each head's chunks over 1 to 8
     # blocks to fold them in one step (or several, past that). Every split
     # count against the oracle, and the two stages against one launch.
     dtype = torch.float16 if head_dim == 128 else torch.bfloat16
