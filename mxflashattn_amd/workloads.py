@@ -227,6 +227,12 @@ WIDE = {
     "wide_window1024_config2": dict(batch=32, q_heads=32, kv_heads=8, head_dim=128,
                                     dtype=torch.bfloat16, lengths=(1024, 8192),
                                     window_left=1023),
+    # One long sequence (a single long-context request): every range holds a
+    # piece of it, so the combine folds hundreds of pieces per head.
+    "wide_one_seq_128k_d128": dict(batch=1, q_heads=32, kv_heads=8, head_dim=128,
+                                   dtype=torch.bfloat16, lengths=131072),
+    "wide_one_seq_64k_d256": dict(batch=1, q_heads=16, kv_heads=2, head_dim=256,
+                                  dtype=torch.bfloat16, lengths=65536),
     # Config 2 as flash_attn_varlen_func decode lays it out: the keys packed
     # end to end and read as one-token pages (the per-lane page-id kernels).
     "wide_varlen_config2": dict(batch=32, q_heads=32, kv_heads=8, head_dim=128,
