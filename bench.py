@@ -23,6 +23,10 @@ Prints ONE JSON line:
                at the kernel's pipeline depth and at 2-4 tiles in flight per
                wave: microseconds and algorithmic GB/s, the access pattern's
                ceiling on this device
+  read_ceiling the plain streaming read (mxfa_stream_read_launch) of the same
+               byte counts as config 2, GQ8 HD64 and config 3, best over
+               layouts, bytes in flight and workgroups per CU: the device's
+               read rate with no access pattern at all
   roofline     the dominant kernel, split_partial_kernel, alone: algorithmic
                bytes (KV + q + out + used block-table entries + lengths) / its
                average duration (HIP events around graph replays of
@@ -83,6 +87,8 @@ def parse_args() -> argparse.Namespace:
                     help="skip the shapes beyond the reference's contract")
     ap.add_argument("--no-host-overhead", action="store_true",
                     help="skip the host-time-per-call section (config 2 launches)")
+    ap.add_argument("--no-read-ceiling", action="store_true",
+                    help="skip the plain streaming-read ceiling")
     ap.add_argument("--cpu-reps", type=int, default=15)
     return ap.parse_args()
 
@@ -161,6 +167,55 @@ def time_graph(fn, pools, calls: int, warmup: int, stream, rounds: int = 10) -> 
     del graph
     per_call = [a.elapsed_time(b) * 1e3 / calls for a, b in events]
     return statistics.median(per_call), calls * rounds
+
+
+# Plain streaming read settings: (layout, KB per wave step, workgroups per CU).
+READ_SETTINGS = [(layout, depth, wgs) for layout in (0, 1) for depth in (4, 8, 16)
+                 for wgs in (1, 2)]
+
+
+def read_ceiling(device, sizes: dict[str, int], calls: int = 64) -> dict:
+    """The device's plain read rate at each named byte count.
+
+    mxfa_stream_read_launch reads the bytes once with no other work, at every
+    READ_SETTINGS combination; each setting is timed like the decode calls
+    (graph replays, median of 10 regions), rotating over disjoint slices of
+    one buffer that cover >= ROTATE_BYTES, as the KV pools do. Byte counts
+    are rounded up to a multiple of 16. Reported: the best setting's GB/s
+    (bytes / us) and every setting's.
+    """
+    from mxflashattn_amd import native
+
+    cus = native.num_cus(device.index or 0)
+    plans = {}
+    for name, nbytes in sizes.items():
+        nbytes = (int(nbytes) + 15) // 16 * 16
+        stride = (nbytes + 4095) // 4096 * 4096
+        copies = max(2, math.ceil(ROTATE_BYTES / nbytes))
+        plans[name] = (nbytes, stride, copies)
+    buf = torch.empty(max(s * c for _, s, c in plans.values()), dtype=torch.uint8, device=device)
+    sink = torch.empty(max(w for _, _, w in READ_SETTINGS) * cus * 256, dtype=torch.int32,
+                       device=device)
+    side = torch.cuda.Stream(device)
+    out = {}
+    for name, (nbytes, stride, copies) in plans.items():
+        views = [(buf[i * stride:i * stride + nbytes],) for i in range(copies)]
+        rates = {}
+        for layout, depth, wgs in READ_SETTINGS:
+            def run(view, layout=layout, depth=depth, wgs=wgs):
+                native.stream_read(view, nbytes, layout=layout, depth=depth,
+                                   workgroups=wgs * cus, sink=sink)
+
+            us = time_graph(run, views, calls, 2, side)[0]
+            rates[f"layout{layout}_{depth}kb_{wgs}wg"] = (round(nbytes / (us * 1e-6) / 1e9, 1),
+                                                          round(us, 3))
+        best = max(rates, key=lambda k: rates[k][0])
+        out[name] = {"bytes": nbytes, "best_gb_s": rates[best][0], "best_us": rates[best][1],
+                     "best_setting": best,
+                     "gb_s_by_setting": {k: v[0] for k, v in rates.items()}}
+    del buf
+    torch.cuda.empty_cache()
+    return out
 
 
 def measure_workload(name: str, spec: dict, device, steps: int, warmup: int) -> dict:
@@ -406,6 +461,16 @@ def main() -> int:
             wide[name] = measure_workload(name, wspec, device, 64, 10)
             print(f"[bench] {name}: {wide[name]}", file=sys.stderr, flush=True)
 
+    ceiling = None
+    if not args.no_read_ceiling:
+        sizes = {args.workload: main_res["algorithmic_bytes"]}
+        for name in ("cell_gq8_d64", "config3_highbatch_gq2_d64"):
+            if name in cells:
+                sizes[name] = cells[name]["algorithmic_bytes"]
+        print("[bench] plain read ceiling", file=sys.stderr, flush=True)
+        ceiling = read_ceiling(device, sizes)
+        print(f"[bench] read ceiling: {ceiling}", file=sys.stderr, flush=True)
+
     decode = None
     if not args.no_decode_step:
         from mxflashattn_amd.integrations.vllm import decode_step
@@ -504,7 +569,14 @@ def main() -> int:
             # between them) against the same peak.
             "call_achieved": main_res["alg_gb_s"],
             "call_frac": round(main_res["alg_gb_s"] / HBM_PEAK_GBS, 4),
+            # The plain read of the same byte count with no other work
+            # (mxfa_stream_read_launch, best setting): what this device
+            # streams, against which `achieved` is a fraction too.
+            "read_ceiling_gb_s": ceiling[args.workload]["best_gb_s"] if ceiling else None,
+            "frac_of_read_ceiling": (round(achieved / ceiling[args.workload]["best_gb_s"], 4)
+                                     if ceiling else None),
         },
+        "read_ceiling": ceiling,
         "cpu_baseline": cpu,
         "cells": cells,
         "wide": wide,

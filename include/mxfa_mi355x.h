@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define MXFA_ABI_VERSION 11
+#define MXFA_ABI_VERSION 12
 
 /* Return codes. */
 #define MXFA_OK 0
@@ -316,6 +316,22 @@ int mxfa_stream_probe_launch(const void *q, int64_t q_stride_b, int64_t q_stride
                              int kv_heads, int head_dim, int page_size, int block_table_width,
                              int num_pages, int dtype, int num_splits, int tiles_in_flight,
                              void *stream);
+
+/*
+ * Plain streaming read (a measurement aid; no counterpart in the reference,
+ * whose bandwidth probe is the paged one above): reads [buf, buf + bytes)
+ * once with 16-byte non-temporal buffer loads and no other work, the read
+ * ceiling of the device at a given byte count. `workgroups` workgroups of four
+ * waves; each wave reads chunks of `depth` KB (depth 4, 8 or 16: 16-byte loads
+ * per lane in flight). layout 0: wave w reads the w-th of 4 * workgroups equal
+ * contiguous slices; layout 1: the waves take consecutive chunks in turn.
+ * Lane l of wave w writes the XOR of the words it read to sink[64 w + l]
+ * (sink_bytes >= workgroups * 1024). buf 16-byte aligned, bytes a positive
+ * multiple of 16. Returns MXFA_EINVAL, MXFA_EUNSUPPORTED (depth) or
+ * MXFA_EWORKSPACE (sink) before launching anything.
+ */
+int mxfa_stream_read_launch(const void *buf, uint64_t bytes, int layout, int depth,
+                            int workgroups, uint32_t *sink, size_t sink_bytes, void *stream);
 
 /*
  * vLLM-style paged append: for token t with slot = slot_mapping[t] >= 0,

@@ -24,7 +24,7 @@ LIB_NAME = "libmxfa_mi355x.so"
 LIB_PATH = LIB_DIR / LIB_NAME
 SOURCES = ("split_decode.hip", "split_hd64.hip", "split_hd64_ws.hip", "split_hd64_ws4.hip",
            "split_hd128.hip", "split_hd128_ws.hip", "split_hd128_ws4.hip", "split_hd256.hip",
-           "split_hd256_ws.hip", "split_hd256_ws4.hip", "kv_append.hip")
+           "split_hd256_ws.hip", "split_hd256_ws4.hip", "kv_append.hip", "stream_read.hip")
 # Comparison build: QK always on the matrix cores (the default build puts it on
 # the VALU for launches of few columns at head dims >= 128).
 QK_MFMA_LIB_PATH = PACKAGE_DIR / "_lib" / "qk_mfma" / "libmxfa_mi355x.so"

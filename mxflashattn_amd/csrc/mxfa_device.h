@@ -1,6 +1,6 @@
 // Device helpers shared by the gfx950 kernels: element types (exact widening
-// of 16-bit halves, fp32 -> fp16/bf16 rounding), the DPP row broadcast and
-// nontemporal loads.
+// of 16-bit halves, fp32 -> fp16/bf16 rounding), the DPP row broadcast,
+// nontemporal loads and raw buffer descriptors.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -76,6 +76,21 @@ __device__ __forceinline__ uint4 load_stream16(const void *p) {
 __device__ __forceinline__ uint2 load_stream8(const void *p) {
   const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t *>(p));
   return make_uint2(v.x, v.y);
+}
+
+// Raw buffer descriptors: loads at byte offsets at or past `bytes` return
+// zeros and touch no memory.
+constexpr uint32_t kSrdWord3 = 0x00020000u;  // raw 32-bit buffer, gfx9 family
+constexpr int kAuxStream = 2;                // nt: no temporal reuse expected
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_srd(const char *base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(base), (short)0, bytes, kSrdWord3);
+}
+
+template <int Aux>
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, int off) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, Aux);
+  return make_uint4(v.x, v.y, v.z, v.w);
 }
 
 }  // namespace mxfa

@@ -88,8 +88,6 @@ constexpr float kRescaleLog2 = 8.0f;
 // LDS: 16000 sequences keep a workgroup within 64 KB.
 constexpr int kMaxBatch = 16000;
 constexpr int kMaxCols = 16;      // query tokens x heads per kv head: the 16 MFMA columns
-constexpr uint32_t kSrdWord3 = 0x00020000u;  // raw 32-bit buffer, gfx9 family
-constexpr int kAuxStream = 2;                // nt: no temporal reuse expected
 constexpr int kOffOut = 0x40000000;          // a lane offset no descriptor covers
 
 // Tile flags.
@@ -264,10 +262,6 @@ __device__ __forceinline__ int range_of(int t, int R, int NT) {
   return (int)(x / NT);
 }
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_srd(const char *base, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(base), (short)0, bytes, kSrdWord3);
-}
-
 template <typename T>
 struct Mfma;
 template <>
@@ -373,12 +367,6 @@ __device__ __forceinline__ uint4 widen8(uint32_t w0, uint32_t w1) {
 // 16-bit element j of a V fragment word list, paired from two tokens.
 __device__ __forceinline__ uint32_t pair_halves(uint32_t lo_tok, uint32_t hi_tok, int odd) {
   return __builtin_amdgcn_perm(hi_tok, lo_tok, odd ? 0x07060302u : 0x05040100u);
-}
-
-template <int Aux>
-__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, int off) {
-  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, Aux);
-  return make_uint4(v.x, v.y, v.z, v.w);
 }
 
 // BYTES contiguous bytes of one lane (4, 8, 16 or 32), as words.

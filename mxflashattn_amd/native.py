@@ -24,7 +24,7 @@ LIB_PATH = Path(
     os.environ.get("MXFLASHATTN_AMD_LIB")
     or Path(__file__).resolve().parent / "_lib" / "libmxfa_mi355x.so"
 )
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 MXFA_OK = 0
 MXFA_EUNSUPPORTED = -1
@@ -80,6 +80,7 @@ EXPORTED_SYMBOLS = (
     "mxfa_split_decode_fp8_partial_launch",
     "mxfa_split_decode_multi_launch",
     "mxfa_stream_probe_launch",
+    "mxfa_stream_read_launch",
     "mxfa_reshape_and_cache_launch",
     "mxfa_reshape_and_cache_fp8_launch",
     "mxfa_append_kv_launch",
@@ -125,6 +126,7 @@ _SIGNATURES = {
         [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _p, _sz, _i, _i, _i, _i, _i,
          _i, _i, _i, _i, _i, _p],
     ),
+    "mxfa_stream_read_launch": (_i, [_p, ctypes.c_uint64, _i, _i, _i, _p, _sz, _p]),
     "mxfa_split_decode_combine_launch": (
         _i,
         [_p, _sz, _p, _i64, _i64, _i, _i, _i, _i, _i, _i, _p],
@@ -782,6 +784,33 @@ def stream_probe(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
         k_cache.shape[1], block_table.shape[1], k_cache.shape[0], _dtype_code(q), int(num_splits),
         int(tiles_in_flight), _stream_handle(q.device))
     _check(rc, "mxfa_stream_probe_launch")
+    return sink
+
+
+def stream_read(buf: torch.Tensor, nbytes: int | None = None, *, layout: int = 0,
+                depth: int = 8, workgroups: int | None = None,
+                sink: torch.Tensor | None = None) -> torch.Tensor:
+    """The plain streaming read (mxfa_stream_read_launch): one pass over the
+    first ``nbytes`` bytes of ``buf`` (a contiguous GPU tensor; all of it by
+    default) with no other work, on the current stream. ``workgroups``
+    defaults to one per CU. Returns the sink, int32 [workgroups * 256], each
+    lane's XOR of the words it read."""
+    if buf.device.type != "cuda" or not buf.is_contiguous():
+        raise ValueError("buf must be a contiguous tensor on a GPU")
+    total = buf.numel() * buf.element_size()
+    nbytes = total if nbytes is None else int(nbytes)
+    if nbytes > total:
+        raise ValueError(f"nbytes {nbytes} exceeds the buffer's {total} bytes")
+    if workgroups is None:
+        workgroups = num_cus(buf.device.index or 0)
+    if sink is None:
+        sink = torch.empty(workgroups * 256, dtype=torch.int32, device=buf.device)
+    if sink.dtype != torch.int32 or not sink.is_contiguous() or sink.device != buf.device:
+        raise ValueError("sink must be a contiguous int32 tensor on buf's device")
+    rc = library().mxfa_stream_read_launch(buf.data_ptr(), nbytes, int(layout), int(depth),
+                                           int(workgroups), sink.data_ptr(), sink.numel() * 4,
+                                           _stream_handle(buf.device))
+    _check(rc, "mxfa_stream_read_launch")
     return sink
 
 

@@ -44,7 +44,7 @@ def test_library_loads_and_reports_header_abi(lib):
 
 def test_every_header_function_is_exported_and_bound(lib):
     declared = header_functions()
-    assert len(declared) == len(set(declared)) == 16
+    assert len(declared) == len(set(declared)) == 17
     for name in declared:
         assert hasattr(lib, name), name
     assert set(declared) == set(native.EXPORTED_SYMBOLS) == set(native._SIGNATURES)
@@ -345,6 +345,19 @@ def probe_args(**over):
 ])
 def test_stream_probe_rejects_before_launching(lib, over, code):
     assert lib.mxfa_stream_probe_launch(*probe_args(**over)) == code
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(buf=None), -2), (dict(buf=FAKE + 8), -2), (dict(nbytes=0), -2), (dict(nbytes=1000), -2),
+    (dict(layout=2), -2), (dict(layout=-1), -2), (dict(workgroups=0), -2), (dict(depth=2), -1),
+    (dict(depth=32), -1), (dict(sink=None), -3), (dict(sink=FAKE + 2), -3),
+    (dict(sink_bytes=4 * 1024 - 4), -3),
+])
+def test_stream_read_rejects_before_launching(lib, over, code):
+    a = dict(buf=FAKE, nbytes=1 << 20, layout=0, depth=8, workgroups=4, sink=FAKE,
+             sink_bytes=4 * 1024, stream=None)
+    a.update(over)
+    assert lib.mxfa_stream_read_launch(*a.values()) == code
 
 
 def test_decode_workspace_boundary_is_exact(lib):

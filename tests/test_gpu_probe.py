@@ -97,3 +97,30 @@ def test_probe_refuses_shapes_it_does_not_walk(device):
     b = make_paged_batch(2, 8, 2, 256, torch.bfloat16, torch.tensor([5, 9]), seed=3).to(device)
     with pytest.raises(native.UnsupportedConfig, match="mxfa_stream_probe_launch"):
         native.stream_probe(b.q, b.k_cache, b.v_cache, b.block_table, b.cache_seqlens, 4)
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("depth", [4, 8, 16])
+@pytest.mark.parametrize("workgroups", [1, 7, 512])
+def test_stream_read_reads_every_word_once(device, layout, depth, workgroups):
+    # mxfa_stream_read_launch: the XOR of the sink equals the XOR of every
+    # 32-bit word of the bytes read, for byte counts that leave a partial last
+    # chunk, more waves than chunks, and one word past a slice boundary.
+    g = torch.Generator().manual_seed(depth * 10 + layout)
+    data = torch.randint(-2**31, 2**31 - 1, (3 * 2**20 // 4 + 100,), dtype=torch.int32,
+                         generator=g)
+    buf = data.to(device)
+    for nbytes in (16, 1040, 3 * 2**20 + 400, buf.numel() * 4):
+        sink = native.stream_read(buf, nbytes, layout=layout, depth=depth, workgroups=workgroups)
+        torch.cuda.synchronize()
+        got = int(np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32)))
+        want = int(np.bitwise_xor.reduce(data[:nbytes // 4].numpy().view(np.uint32)))
+        assert got == want, (nbytes, got, want)
+
+
+def test_stream_read_refuses_bad_arguments(device):
+    buf = torch.zeros(1024, dtype=torch.int32, device=device)
+    with pytest.raises(native.UnsupportedConfig, match="mxfa_stream_read_launch"):
+        native.stream_read(buf, depth=2)
+    with pytest.raises(ValueError):
+        native.stream_read(buf, 4097)
