@@ -24,11 +24,15 @@ namespace mxfa {
 
 template <int kDepth>
 __global__ __launch_bounds__(256) void stream_read_kernel(const char *buf, uint64_t bytes,
-                                                          int layout, uint32_t *sink) {
+                                                          uint64_t slice, int layout,
+                                                          uint32_t *sink) {
   constexpr uint32_t kChunk = 64u * 16u * kDepth;  // bytes a wave reads per step
   const int lane = threadIdx.x & 63;
   const uint64_t waves = (uint64_t)gridDim.x * 4;
-  const uint64_t w = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  // The wave index through readfirstlane: the compiler then knows it is the
+  // same in every lane, so each chunk's descriptor is built in scalar
+  // registers (a per-lane one would wrap every load in a loop over lanes).
+  const uint64_t w = (uint64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   uint32_t x = 0;
   auto step = [&](uint64_t off, uint64_t end) {
     const uint64_t left = end - off;
@@ -39,8 +43,7 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const char *buf, uint6
 #pragma unroll
     for (int i = 0; i < kDepth; ++i) x ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
   };
-  if (layout == 0) {
-    const uint64_t slice = ((bytes + waves - 1) / waves + 15) & ~(uint64_t)15;
+  if (layout == 0) {  // slice: bytes per wave, a multiple of 16 (host)
     const uint64_t lo = w * slice < bytes ? w * slice : bytes;
     const uint64_t hi = bytes - lo < slice ? bytes : lo + slice;
     for (uint64_t off = lo; off < hi; off += kChunk) step(off, hi);
@@ -64,13 +67,15 @@ extern "C" int mxfa_stream_read_launch(const void *buf, uint64_t bytes, int layo
   if (!sink || ((uintptr_t)sink & 3u) || sink_bytes / 1024 < (size_t)workgroups)
     return MXFA_EWORKSPACE;
   const char *b = static_cast<const char *>(buf);
+  const uint64_t waves = (uint64_t)workgroups * 4;
+  const uint64_t slice = ((bytes + waves - 1) / waves + 15) & ~(uint64_t)15;
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid(workgroups), block(256);
   if (depth == 4)
-    hipLaunchKernelGGL(stream_read_kernel<4>, grid, block, 0, st, b, bytes, layout, sink);
+    hipLaunchKernelGGL(stream_read_kernel<4>, grid, block, 0, st, b, bytes, slice, layout, sink);
   else if (depth == 8)
-    hipLaunchKernelGGL(stream_read_kernel<8>, grid, block, 0, st, b, bytes, layout, sink);
+    hipLaunchKernelGGL(stream_read_kernel<8>, grid, block, 0, st, b, bytes, slice, layout, sink);
   else
-    hipLaunchKernelGGL(stream_read_kernel<16>, grid, block, 0, st, b, bytes, layout, sink);
+    hipLaunchKernelGGL(stream_read_kernel<16>, grid, block, 0, st, b, bytes, slice, layout, sink);
   return hipGetLastError() == hipSuccess ? MXFA_OK : MXFA_ELAUNCH;
 }
