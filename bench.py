@@ -89,6 +89,9 @@ def parse_args() -> argparse.Namespace:
                     help="skip the host-time-per-call section (config 2 launches)")
     ap.add_argument("--no-read-ceiling", action="store_true",
                     help="skip the plain streaming-read ceiling")
+    ap.add_argument("--read-ceiling-bytes", default=None,
+                    help="only measure the plain read ceiling at these comma-separated "
+                         "byte counts and print it as one JSON line")
     ap.add_argument("--cpu-reps", type=int, default=15)
     return ap.parse_args()
 
@@ -441,6 +444,10 @@ def main() -> int:
 
     native.library()  # fail loudly when the HIP library is missing
     device = torch.device("cuda", 0)
+    if args.read_ceiling_bytes:
+        sizes = {f"{int(n)}_bytes": int(n) for n in args.read_ceiling_bytes.split(",")}
+        print(json.dumps({"read_ceiling": read_ceiling(device, sizes)}))
+        return 0
     spec = {**CONFIGS, **CELLS, **WIDE}[args.workload]
     print(f"[bench] workload {args.workload}: steps={args.steps} warmup={args.warmup}",
           file=sys.stderr, flush=True)
